@@ -1,0 +1,334 @@
+#!/usr/bin/env python3
+"""Benchmark of the trnfft_amd HIP FFT path on one MI355X.
+
+Headline (the BASELINE metric): batched fp32 c2c FFT, 4096 signals x N=1024,
+one step = one forward FFT of one batch plus one inverse FFT of another batch, with inputs
+resident in HBM and the buffer sets rotated over > 1 GiB so no launch reads data left in the
+256 MB Infinity Cache by the previous one.  Reported:
+  value      GFLOP/s (5 N log2 N per transform) of the whole timed region
+  roofline   the c2c kernel's algorithmic bytes per launch / its average launch duration
+             (HIP events on the launch stream) against 8 TB/s
+  cpu_baseline  the reference's pytorch path (its literal per-k radix-2 loop, restated in
+             oracle/) timed on this host's cores on the same workload
+  secondary  the other BASELINE configs (STFT, Bluestein, fft2, four-step N=2^20, GEMMs):
+             kernel time, GFLOP/s, algorithmic GB/s and fraction of 8 TB/s
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import re
+import subprocess
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+FP32_PEAK = 157.3e12  # MI355X dense fp32 (matrix), flop/s
+
+
+def make_c2c_input(batch: int, n: int, seed: int = 42):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(batch, n, generator=g), torch.randn(batch, n, generator=g)
+
+
+def make_stft_input(batch: int, length: int, seed: int = 42, sr: int = 16000) -> torch.Tensor:
+    """Sum of 3 random-frequency sinusoids + N(0, 0.1) noise per waveform."""
+    g = torch.Generator().manual_seed(seed)
+    t = torch.arange(length, dtype=torch.float64) / sr
+    f = 50.0 + (7950.0 - 50.0) * torch.rand(batch, 3, 1, generator=g, dtype=torch.float64)
+    a = 0.1 + 0.9 * torch.rand(batch, 3, 1, generator=g, dtype=torch.float64)
+    ph = 2 * math.pi * torch.rand(batch, 3, 1, generator=g, dtype=torch.float64)
+    x = (a * torch.sin(2 * math.pi * f * t + ph)).sum(dim=1)
+    x = x + 0.1 * torch.randn(batch, length, generator=g, dtype=torch.float64)
+    return x.float()
+
+
+def flops_fft(n: int, batch: int) -> float:
+    return 5.0 * n * math.log2(n) * batch
+
+
+class EventTimer:
+    """Per-launch HIP event pairs on the launch stream; returns mean/median launch duration."""
+
+    def __init__(self):
+        self.pairs = []
+
+    def record(self, fn):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        self.pairs.append((s, e))
+
+    def durations_s(self):
+        torch.cuda.synchronize()
+        return [s.elapsed_time(e) * 1e-3 for s, e in self.pairs]
+
+
+def _median(v):
+    v = sorted(v)
+    return v[len(v) // 2]
+
+
+def _traffic_from_profiles(kernel_tag: str):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/*.md), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_pmc.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+# ---------------------------------------------------------------------------------------------
+# headline: batched c2c N=1024
+# ---------------------------------------------------------------------------------------------
+
+
+def bench_headline(steps: int, warmup: int):
+    import trnfft_amd
+    from trnfft_amd import _lib
+    from trnfft_amd.plan import native_plan
+
+    batch, n = 4096, 1024
+    dev = torch.device("cuda", torch.cuda.current_device())
+    plane = batch * n * 4
+    sets = max(4, math.ceil((1.25 * 2**30) / (4 * plane)))  # in+out (2 planes each) per set > 1.25 GiB total
+    re, im = make_c2c_input(batch, n)
+    ins = []
+    for s in range(sets):
+        # distinct data per set (rolled copies of the seeded batch)
+        r = torch.roll(re, shifts=s, dims=0).to(dev)
+        i = torch.roll(im, shifts=s, dims=0).to(dev)
+        ins.append((r, i))
+    outs = [(torch.empty_like(ins[0][0]), torch.empty_like(ins[0][0])) for _ in range(sets)]
+    pf = native_plan(_lib.KIND_C2C, n, False, dev.index)
+    pi = native_plan(_lib.KIND_C2C, n, True, dev.index)
+    lib = _lib.lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    args_f = [
+        (pf.handle, batch, ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+         ctypes.c_void_p(c.data_ptr()), ctypes.c_void_p(d.data_ptr()), None, stream)
+        for (a, b), (c, d) in zip(ins, outs)
+    ]
+    # inverse of another set's input (same work, and its data is not the just-written output)
+    args_i = [
+        (pi.handle, batch, ctypes.c_void_p(ins[(k + sets // 2) % sets][0].data_ptr()),
+         ctypes.c_void_p(ins[(k + sets // 2) % sets][1].data_ptr()),
+         ctypes.c_void_p(outs[(k + sets // 2) % sets][0].data_ptr()),
+         ctypes.c_void_p(outs[(k + sets // 2) % sets][1].data_ptr()), None, stream)
+        for k in range(sets)
+    ]
+    execute = lib.tfa_execute
+
+    def step(k):
+        rc = execute(*args_f[k % sets])
+        rc |= execute(*args_i[k % sets])
+        if rc:
+            _lib.check(rc, "tfa_execute")
+
+    for k in range(warmup):
+        step(k)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        step(k)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    # per-launch kernel durations (separate pass, event pairs around each launch)
+    timer = EventTimer()
+    for k in range(max(20, min(steps, 200))):
+        timer.record(lambda k=k: execute(*args_f[k % sets]))
+        timer.record(lambda k=k: execute(*args_i[k % sets]))
+    d = timer.durations_s()
+    t_launch = sum(d) / len(d)
+
+    # correctness of what was timed: last forward output vs a fresh transform of the same input
+    chk = trnfft_amd.fft(trnfft_amd.ComplexTensor(ins[0][0], ins[0][1]))
+    execute(*args_f[0])
+    torch.cuda.synchronize()
+    assert torch.equal(chk.real, outs[0][0]) and torch.equal(chk.imag, outs[0][1])
+
+    flops_step = 2 * flops_fft(n, batch)
+    bytes_launch = 2 * 2 * plane  # read re+im, write re+im
+    return {
+        "wall_s": wall,
+        "ms_per_step": wall / steps * 1e3,
+        "value": flops_step * steps / wall / 1e9,
+        "t_launch_s": t_launch,
+        "t_launch_median_s": _median(d),
+        "bytes_launch": bytes_launch,
+        "buffer_sets": sets,
+    }
+
+
+# ---------------------------------------------------------------------------------------------
+# secondary configs (each: kernel time with events, median over launches)
+# ---------------------------------------------------------------------------------------------
+
+
+def _time_launches(fn, reps=30, warm=3):
+    for _ in range(warm):
+        fn()
+    timer = EventTimer()
+    for _ in range(reps):
+        timer.record(fn)
+    d = timer.durations_s()
+    return _median(d)
+
+
+def bench_secondary():
+    import trnfft_amd
+    from trnfft_amd import ComplexTensor
+
+    dev = torch.device("cuda", torch.cuda.current_device())
+    out = {}
+
+    def rec(name, t, flops, nbytes, note=""):
+        out[name] = {
+            "ms": round(t * 1e3, 4),
+            "gflops": round(flops / t / 1e9, 1),
+            "gbps": round(nbytes / t / 1e9, 1),
+            "frac_hbm": round(nbytes / t / HBM_PEAK, 4),
+        }
+        if note:
+            out[name]["note"] = note
+
+    # C2: STFT 64 x 160000, n_fft 512, hop 256
+    x = make_stft_input(64, 160000).to(dev)
+    t = _time_launches(lambda: trnfft_amd.stft(x, n_fft=512, hop_length=256))
+    rec("c2_stft_64x160000_nfft512", t, 40064 * 5 * 512 * 9, 64 * 160000 * 4 + 2 * 64 * 257 * 626 * 4,
+        "includes output allocation per call")
+    del x
+    # C3: Bluestein
+    for n, b in [(1000, 1024), (4099, 256)]:
+        re, im = make_c2c_input(b, n)
+        xc = ComplexTensor(re.to(dev), im.to(dev))
+        t = _time_launches(lambda: trnfft_amd.fft(xc))
+        rec(f"c3_bluestein_{b}x{n}", t, flops_fft(n, b), 4 * b * n * 4)
+    # C4b: four-step N = 2^20, batch 16
+    re, im = make_c2c_input(16, 1 << 20)
+    xc = ComplexTensor(re.to(dev), im.to(dev))
+    t = _time_launches(lambda: trnfft_amd.fft(xc), reps=20)
+    rec("c4b_fourstep_16x2^20", t, flops_fft(1 << 20, 16), 4 * 16 * (1 << 20) * 4,
+        "two HBM passes; algorithmic bytes = one read + one write")
+    del xc
+    # C4a: fft2 32 x 2048 x 2048 real
+    g = torch.Generator().manual_seed(42)
+    img = torch.rand(32, 2048, 2048, generator=g).to(dev)
+    t = _time_launches(lambda: trnfft_amd.fft2(img), reps=5, warm=1)
+    rec("c4a_fft2_32x2048x2048", t, 32 * 5 * 2048 * 2048 * 22, 32 * 2048 * 2048 * (4 + 8))
+    del img
+    torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------------------------------------
+# CPU baseline: the reference's pytorch path (literal per-k radix-2 loop) on host cores
+# ---------------------------------------------------------------------------------------------
+
+
+def bench_cpu_baseline(reps: int = 3):
+    sys.path.insert(0, ROOT)
+    import oracle
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    batch, n = 4096, 1024
+    re, im = make_c2c_input(batch, n)
+    oracle.cooley_tukey_loop(re[:64], im[:64], False)  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fr, fi = oracle.cooley_tukey_loop(re, im, False)
+        oracle.cooley_tukey_loop(fr, fi, True)
+        times.append(time.perf_counter() - t0)
+    t = _median(times)
+    try:
+        model = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        model = next((l.split(":", 1)[1].strip() for l in model.splitlines() if l.startswith("Model name")), "")
+    except Exception:
+        model = ""
+    return {
+        "value": round(2 * flops_fft(n, batch) / t / 1e9, 4),
+        "unit": "GFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"full workload 4096x{n} fft+ifft, reference radix-2 per-k loop (oracle.cooley_tukey_loop, "
+        f"trnfft/fft_core.py:53-117), torch CPU fp32, median of {reps}, {t:.2f} s/step; host: {model}",
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU only (requested --gpus {args.gpus}): every config here is a batch "
+            "of independent transforms; see DESIGN.md for how the path shards across GPUs",
+            file=sys.stderr,
+        )
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    head = bench_headline(args.steps, args.warmup)
+    achieved = head["bytes_launch"] / head["t_launch_s"]
+    result = {
+        "metric": "batched c2c FFT GFLOP/s (5N·log2N) + % peak HBM GB/s, fp32, N=1024..2^20",
+        "value": round(head["value"], 1),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: N(0,1) re/im, seed 42, 4096x1024 (BASELINE config 1)",
+        "config": {
+            "workload": "batched c2c FFT, 4096 x N=1024 fp32 split re/im; step = forward fft of one batch + "
+            "inverse fft of another, buffers rotated over >1 GiB",
+            "n": 1024,
+            "batch": 4096,
+            "buffer_sets": head["buffer_sets"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "c2c_lds_kernel<1024>",
+            "achieved": round(achieved / 1e9, 1),
+            "peak": 8000.0,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK, 4),
+            "traffic": _traffic_from_profiles("c2c_lds_n1024"),
+            "t_launch_us": round(head["t_launch_s"] * 1e6, 3),
+            "t_launch_median_us": round(head["t_launch_median_s"] * 1e6, 3),
+            "bytes_per_launch": head["bytes_launch"],
+        },
+    }
+    if not args.no_secondary:
+        result["secondary"] = bench_secondary()
+    if not args.no_cpu:
+        result["cpu_baseline"] = bench_cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

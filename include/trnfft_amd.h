@@ -1,0 +1,115 @@
+/*
+ * trnfft_amd.h — C ABI of the MI355X (gfx950) FFT backend for trnfft.
+ *
+ * Plain C: raw device pointers, sizes and an opaque stream handle; no torch types.  Data is in
+ * trnfft's split layout (ComplexTensor, trnfft/complex.py:16-33): two contiguous row-major
+ * fp32 planes, re and im, batch rows of length n.  All entry points return TFA_OK (0) or a
+ * negative status; tfa_last_error() gives the calling thread's message for the last failure.
+ *
+ * Ownership: the caller owns every input, output and workspace buffer (device memory, e.g. from
+ * the PyTorch caching allocator).  A plan owns its device tables (twiddles, Bluestein chirp and
+ * filter spectrum, DFT matrix) and is immutable after creation, so tfa_execute* may be called
+ * concurrently on one plan from several threads/streams.  A plan is bound to the device that was
+ * current at creation.
+ */
+#ifndef TRNFFT_AMD_H
+#define TRNFFT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct tfa_plan tfa_plan;
+typedef void* tfa_stream; /* hipStream_t; NULL = the null stream */
+
+/* Status codes (the Python layer maps them to exceptions). */
+#define TFA_OK 0
+#define TFA_ERR_INVALID (-1)     /* bad argument                      -> ValueError          */
+#define TFA_ERR_UNSUPPORTED (-2) /* size or kind not implemented      -> NotImplementedError */
+#define TFA_ERR_HIP (-3)         /* HIP runtime / launch failure      -> RuntimeError        */
+
+/* Plan kinds. */
+#define TFA_KIND_C2C 0       /* power-of-two n (Stockham in LDS; four-step above 16384)     */
+#define TFA_KIND_BLUESTEIN 1 /* any n >= 2, chirp-z over a power-of-two m >= 2n-1            */
+#define TFA_KIND_DFT_GEMM 2  /* n <= 256, X = x @ W on the matrix cores                      */
+#define TFA_KIND_STFT 3      /* framed, windowed onesided/twosided transform of real signals */
+
+/* STFT flags. */
+#define TFA_STFT_CENTER 1     /* reflect-pad n_fft/2 on both sides (pad_mode="reflect") */
+#define TFA_STFT_NORMALIZED 2 /* scale by 1/sqrt(n_fft)                                 */
+#define TFA_STFT_ONESIDED 4   /* keep bins 0..n_fft/2                                   */
+
+typedef struct tfa_plan_desc {
+  int32_t kind;    /* TFA_KIND_* */
+  int32_t inverse; /* 0: forward, sign -1, unscaled; 1: inverse, sign +1, scaled 1/n */
+  int64_t n;       /* transform length (STFT: n_fft) */
+  int64_t hop;     /* STFT only: hop_length */
+  int32_t flags;   /* STFT only: TFA_STFT_* */
+  int32_t reserved;
+} tfa_plan_desc;
+
+/*
+ * Create a plan.  Replaces the reference's per-call plan lookup plus table construction:
+ * trnfft/plan.py:34-46 (create_plan: algorithm choice, Bluestein m = 1 << (2n-2).bit_length()),
+ * trnfft/fft_core.py:86-88 (radix-2 twiddles), :1316-1345 (Bluestein chirp, with the same
+ * fp32 angle expression sign*pi*k*k/n, and filter h), :239-243 (DFT matrix).
+ */
+int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc);
+
+/* Release a plan and its device tables (trnfft/plan.py:49-50 clear_plan_cache drops them). */
+void tfa_plan_destroy(tfa_plan* plan);
+
+/* Device workspace (bytes) tfa_execute needs for `batch` rows; 0 when none. */
+int tfa_plan_workspace_size(const tfa_plan* plan, int64_t batch, size_t* bytes);
+
+/* Padded length m of a Bluestein plan (n for the other kinds). */
+int64_t tfa_plan_padded_n(const tfa_plan* plan);
+
+/*
+ * Batched 1-D transform along the last axis: out[b, k] = sum_j in[b, j] W^(j k) (x 1/n when
+ * inverse).  in_im may be NULL for real input (imaginary part zero, trnfft/complex.py:27-28).
+ * Out-of-place, or in place with out_* == in_*.  Replaces trnfft/fft_core.py:22-50 (fft_core),
+ * which dispatches to _cooley_tukey (:53-117, power-of-two n), _bluestein (:1285-1376, other n)
+ * and, for TFA_KIND_DFT_GEMM plans, _fft_via_gemm (:221-251).
+ */
+int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const float* in_im,
+                float* out_re, float* out_im, void* workspace, tfa_stream stream);
+
+/*
+ * Short-time Fourier transform of `batch` real signals of `num_samples` samples each.  Frames
+ * of n_fft samples every hop, after reflect padding when TFA_STFT_CENTER; each frame is
+ * multiplied by window (device pointer, n_fft floats, already centre-padded to n_fft) and
+ * transformed; output planes are (batch, n_bins, n_frames) row-major with n_bins = n_fft/2+1
+ * when TFA_STFT_ONESIDED else n_fft.  Replaces trnfft/api.py:291-365 (stft).
+ */
+int tfa_stft_frames(const tfa_plan* plan, int64_t num_samples, int64_t* n_frames);
+int tfa_stft_execute(const tfa_plan* plan, int64_t batch, int64_t num_samples, const float* signal,
+                     const float* window, float* out_re, float* out_im, tfa_stream stream);
+
+/*
+ * Complex GEMM on split planes, C = A @ B (b_trans = 0) or C = A @ B^T (b_trans = 1), plus an
+ * optional complex bias broadcast over rows (bias_re/bias_im NULL for none).  A is (m, k) with
+ * row stride lda; B is (k, n) with row stride ldb, or (n, k) when b_trans; C is (m, n) with row
+ * stride ldc.  Replaces trnfft/nki/dispatch.py:74-84 (complex_gemm) and :91-102
+ * (complex_linear: y = x @ W^T with W (out, in)), whose kernels are :121-200 and :267-345, and
+ * the bias add of trnfft/nn.py:46-48.
+ */
+int tfa_complex_gemm(int64_t m, int64_t n, int64_t k, const float* a_re, const float* a_im,
+                     int64_t lda, const float* b_re, const float* b_im, int64_t ldb, int32_t b_trans,
+                     const float* bias_re, const float* bias_im, float* c_re, float* c_im,
+                     int64_t ldc, tfa_stream stream);
+
+/* Thread-local message describing the last failure on this thread ("" if none). */
+const char* tfa_last_error(void);
+
+/* ABI version, (major << 16) | minor. */
+int32_t tfa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRNFFT_AMD_H */

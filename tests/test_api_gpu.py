@@ -1,0 +1,118 @@
+"""GPU parity of the API layer: rfft/irfft/hfft, fft2/fftn/ifftn, stft/istft vs the oracle."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import trnfft_amd
+from conftest import rel_l2, tol_pow2
+from trnfft_amd import ComplexTensor
+
+pytestmark = pytest.mark.gpu
+
+
+def test_rfft_irfft():
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(3, 128, generator=g)
+    got = trnfft_amd.rfft(x.cuda())
+    ref = oracle.rfft(x)
+    assert got.shape == (3, 65)
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(128)
+    back = trnfft_amd.irfft(got, n=128)
+    ref_back = oracle.irfft(ref, n=128)
+    assert rel_l2(back, torch.zeros_like(back), ref_back, torch.zeros_like(ref_back)) <= tol_pow2(128)
+
+
+def test_hfft_ihfft_roundtrip():
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(32, generator=g)
+    y = trnfft_amd.hfft(trnfft_amd.ihfft(x.cuda(), n=32), n=32)
+    np.testing.assert_allclose(y.cpu().numpy(), x.numpy(), atol=1e-4)
+    e = np.fft.ihfft(x.numpy(), n=32)
+    z = trnfft_amd.ihfft(x, n=32)
+    np.testing.assert_allclose(z.real.numpy(), e.real, atol=1e-5)
+    np.testing.assert_allclose(z.imag.numpy(), e.imag, atol=1e-5)
+
+
+@pytest.mark.parametrize("shape", [(8, 8), (3, 64, 32), (2, 256, 512)])
+def test_fft2_vs_oracle(shape):
+    rng = np.random.default_rng(42)
+    x = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
+    got = trnfft_amd.fft2(x.cuda())
+    ref = oracle.fft2(x)
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(shape[-1] * shape[-2])
+
+
+def test_fftn_ifftn():
+    rng = np.random.default_rng(42)
+    x = torch.from_numpy(rng.standard_normal((4, 8, 16)).astype(np.float32))
+    got = trnfft_amd.fftn(x.cuda())
+    ref = oracle.fftn(x)
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(512)
+    back = trnfft_amd.ifftn(got)
+    assert rel_l2(back.real, back.imag, x, torch.zeros_like(x)) <= 2 * tol_pow2(512)
+    got0 = trnfft_amd.fftn(x.cuda(), dim=(0,))
+    ref0 = oracle.fftn(x, dim=(0,))
+    assert rel_l2(got0.real, got0.imag, *ref0) <= tol_pow2(4)
+
+
+def test_fft2_config4a_one_image_and_parseval():
+    # BASELINE config 4a at full shape (32 x 2048 x 2048, U[0,1)): oracle on one image, Parseval on all
+    g = torch.Generator().manual_seed(42)
+    x = torch.rand(32, 2048, 2048, generator=g)
+    got = trnfft_amd.fft2(x.cuda())
+    ref = oracle.fft2(x[5])
+    assert rel_l2(got.real[5], got.imag[5], *ref) <= tol_pow2(2048)
+    e_t = (x.double() ** 2).sum()
+    e_f = (got.real.double() ** 2 + got.imag.double() ** 2).sum().cpu() / (2048 * 2048)
+    assert abs(e_t - e_f) / e_t < 1e-5
+
+
+@pytest.mark.parametrize("n_fft,hop,center,normalized,onesided", [
+    (512, 256, True, False, True),
+    (256, 64, True, False, True),
+    (128, 32, False, False, True),
+    (64, 16, True, True, False),
+])
+def test_stft_vs_oracle(n_fft, hop, center, normalized, onesided):
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(3, 4000, generator=g)
+    got = trnfft_amd.stft(x.cuda(), n_fft=n_fft, hop_length=hop, center=center, normalized=normalized, onesided=onesided)
+    ref = oracle.stft(x, n_fft=n_fft, hop_length=hop, center=center, normalized=normalized, onesided=onesided)
+    assert got.shape == ref[0].shape
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(n_fft)
+
+
+def test_stft_config2_full_size():
+    # 64 x 160000 samples, 3 sinusoids + N(0, 0.1) noise, n_fft 512, hop 256
+    from bench import make_stft_input
+
+    x = make_stft_input(64, 160000, seed=42)
+    got = trnfft_amd.stft(x.cuda(), n_fft=512, hop_length=256)
+    assert got.shape == (64, 257, 626)
+    ref = oracle.stft(x, n_fft=512, hop_length=256)
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(512)
+
+
+def test_istft_roundtrip():
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(4, 1024, generator=g)
+    spec = trnfft_amd.stft(x.cuda(), n_fft=256, hop_length=64)
+    y = trnfft_amd.istft(spec, n_fft=256, hop_length=64, length=1024)
+    np.testing.assert_allclose(y.cpu().numpy(), x.numpy(), atol=1e-3)
+    ref = oracle.istft((spec.real.cpu(), spec.imag.cpu()), n_fft=256, hop_length=64, length=1024)
+    assert float((y.cpu() - ref).abs().max()) < 1e-4
+
+
+def test_stft_single_tone():
+    sr, freq, n_fft = 1000, 100, 256
+    t = torch.arange(0, 1.0, 1.0 / sr)
+    s = torch.sin(2 * np.pi * freq * t)
+    res = trnfft_amd.stft(s.cuda(), n_fft=n_fft, hop_length=64, center=False)
+    peak = res.abs().mean(dim=-1).argmax().item()
+    assert abs(peak - int(freq * n_fft / sr)) <= 1

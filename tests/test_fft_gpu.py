@@ -1,0 +1,125 @@
+"""GPU parity: power-of-two c2c (LDS Stockham and four-step) and Bluestein vs the CPU oracle.
+
+Tolerances (relative L2 over both planes): 1e-6*log2(n) for power-of-two transforms and
+1e-5*log2(n) for Bluestein; inputs seeded as the reference's tests (seed 42, re then im).
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import trnfft_amd
+from conftest import rel_l2, seeded_complex, tol_bluestein, tol_pow2
+from trnfft_amd import ComplexTensor
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "bluestein_vectors.npz")
+
+
+def _gpu_fft(re, im, inverse=False):
+    x = ComplexTensor(re.cuda(), im.cuda())
+    y = trnfft_amd.ifft(x) if inverse else trnfft_amd.fft(x)
+    torch.cuda.synchronize()
+    return y.real.cpu(), y.imag.cpu()
+
+
+@pytest.mark.parametrize("n", [1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192, 16384])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_pow2_lds_vs_oracle(n, inverse):
+    batch = max(3, min(257, (1 << 16) // n))  # ragged batch: not a multiple of the per-block count
+    re, im = seeded_complex(batch, n, seed=n)
+    got = _gpu_fft(re, im, inverse)
+    ref = oracle.fft_core(re, im, inverse)
+    assert rel_l2(*got, *ref) <= tol_pow2(n), (n, inverse)
+
+
+@pytest.mark.parametrize("n", [1 << 15, 1 << 16, 1 << 17, 1 << 18, 1 << 20])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_pow2_fourstep_vs_oracle(n, inverse):
+    re, im = seeded_complex(2, n, seed=n)
+    got = _gpu_fft(re, im, inverse)
+    ref = oracle.fft_core(re, im, inverse)
+    assert rel_l2(*got, *ref) <= tol_pow2(n), (n, inverse)
+
+
+def test_config1_batched_1024_roundtrip():
+    # 4096 x 1024, forward then inverse, each against the oracle
+    re, im = seeded_complex(4096, 1024)
+    x = ComplexTensor(re.cuda(), im.cuda())
+    X = trnfft_amd.fft(x)
+    ref = oracle.fft_core(re, im, False)
+    assert rel_l2(X.real, X.imag, *ref) <= tol_pow2(1024)
+    back = trnfft_amd.ifft(X)
+    ref_back = oracle.fft_core(ref[0], ref[1], True)
+    assert rel_l2(back.real, back.imag, *ref_back) <= tol_pow2(1024)
+    assert rel_l2(back.real, back.imag, re, im) <= 2 * tol_pow2(1024)
+
+
+def test_config4b_large_n_properties():
+    # BASELINE config 4b at full size (16 x 2^20): oracle on one row, round trip + Parseval on all
+    n = 1 << 20
+    re, im = seeded_complex(16, n)
+    x = ComplexTensor(re.cuda(), im.cuda())
+    X = trnfft_amd.fft(x)
+    ref0 = oracle.fft_core(re[:1], im[:1], False)
+    assert rel_l2(X.real[:1], X.imag[:1], *ref0) <= tol_pow2(n)
+    e_t = (re.double() ** 2 + im.double() ** 2).sum()
+    e_f = (X.real.double() ** 2 + X.imag.double() ** 2).sum().cpu() / n
+    assert abs(e_t - e_f) / e_t < 1e-5
+    back = trnfft_amd.ifft(X)
+    assert rel_l2(back.real, back.imag, re, im) <= 2 * tol_pow2(n)
+
+
+def test_real_input_and_known_answers():
+    n = 16
+    x = torch.zeros(n)
+    x[0] = 1.0
+    y = trnfft_amd.fft(x)  # CPU tensor in, CPU result out
+    assert y.real.device.type == "cpu"
+    np.testing.assert_allclose(y.real.numpy(), np.ones(n), atol=1e-6)
+    np.testing.assert_allclose(y.imag.numpy(), np.zeros(n), atol=1e-6)
+    g = torch.Generator().manual_seed(42)
+    r = torch.randn(5, 1024, generator=g)
+    got = trnfft_amd.fft(r.cuda())
+    ref = oracle.fft_core(r, torch.zeros_like(r), False)
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(1024)
+    z = trnfft_amd.fft(torch.tensor([1.0, 2.0, 3.0, 4.0]), n=8)
+    e = np.fft.fft([1, 2, 3, 4, 0, 0, 0, 0])
+    np.testing.assert_allclose(z.real.numpy(), e.real, atol=1e-5)
+    np.testing.assert_allclose(z.imag.numpy(), e.imag, atol=1e-5)
+
+
+def test_leading_dims_and_empty_batch():
+    re, im = seeded_complex(6, 256)
+    x = ComplexTensor(re.reshape(2, 3, 256).cuda(), im.reshape(2, 3, 256).cuda())
+    y = trnfft_amd.fft(x)
+    assert y.shape == (2, 3, 256)
+    ref = oracle.fft_core(re, im, False)
+    assert rel_l2(y.real.reshape(6, 256), y.imag.reshape(6, 256), *ref) <= tol_pow2(256)
+    e = trnfft_amd.fft(ComplexTensor(torch.zeros(0, 64, device="cuda"), torch.zeros(0, 64, device="cuda")))
+    assert e.shape == (0, 64)
+
+
+@pytest.mark.parametrize("direction", ["fft", "ifft"])
+def test_bluestein_vs_reference_golden(direction):
+    d = np.load(GOLDEN)
+    for n, _b in d["cases"]:
+        re = torch.from_numpy(d[f"n{n}_in_re"])
+        im = torch.from_numpy(d[f"n{n}_in_im"])
+        got = _gpu_fft(re, im, direction == "ifft")
+        err = rel_l2(*got, d[f"n{n}_{direction}_re"], d[f"n{n}_{direction}_im"])
+        assert err <= tol_bluestein(int(n)), (int(n), direction, err)
+
+
+@pytest.mark.parametrize("n,batch", [(1000, 1024), (4099, 256), (3, 5), (17, 33), (8193, 4), (20000, 2)])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_bluestein_vs_oracle(n, batch, inverse):
+    re, im = seeded_complex(batch, n, seed=n)
+    got = _gpu_fft(re, im, inverse)
+    ref = oracle.fft_core(re, im, inverse)
+    assert rel_l2(*got, *ref) <= tol_bluestein(n), (n, inverse)

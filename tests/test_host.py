@@ -1,0 +1,121 @@
+"""Host-side logic that runs without a GPU: C ABI exports and argument errors, plan selection,
+backend dispatch semantics, ComplexTensor arithmetic (reference tests/test_complex.py)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import trnfft_amd
+from trnfft_amd import ComplexTensor, _lib
+from trnfft_amd.plan import FFTAlgorithm
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "trnfft_amd.h")
+
+
+def _declared_symbols() -> set[str]:
+    text = open(HEADER).read()
+    return set(re.findall(r"\b(tfa_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    declared = _declared_symbols()
+    assert declared == set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.tfa_abi_version() >> 16 == 1
+
+
+def test_abi_rejects_bad_arguments_without_gpu():
+    lib = _lib.lib()
+    h = ctypes.c_void_p()
+    assert lib.tfa_plan_create(ctypes.byref(h), None) == _lib.TFA_ERR_INVALID
+    desc = _lib.PlanDesc(kind=_lib.KIND_C2C, inverse=0, n=0, hop=0, flags=0, reserved=0)
+    assert lib.tfa_plan_create(ctypes.byref(h), ctypes.byref(desc)) == _lib.TFA_ERR_INVALID
+    assert b"length" in lib.tfa_last_error()
+    assert lib.tfa_execute(None, 1, None, None, None, None, None, None) == _lib.TFA_ERR_INVALID
+    with pytest.raises(ValueError):
+        _lib.check(_lib.TFA_ERR_INVALID, "x")
+
+
+def test_create_plan_matches_reference_choice():
+    # trnfft/plan.py:34-46
+    trnfft_amd.clear_plan_cache()
+    p = trnfft_amd.create_plan(1024)
+    assert p.algorithm == FFTAlgorithm.COOLEY_TUKEY and p.padded_n is None and p.is_power_of_2
+    for n, m in [(1000, 2048), (4099, 16384), (997, 2048), (4097, 16384), (7, 16)]:
+        p = trnfft_amd.create_plan(n, inverse=True)
+        assert p.algorithm == FFTAlgorithm.BLUESTEIN and p.padded_n == m and p.inverse
+    assert trnfft_amd.create_plan(1000, True) is trnfft_amd.create_plan(1000, True)
+
+
+def test_backend_selection_semantics():
+    assert trnfft_amd.get_backend() == "auto"
+    with pytest.raises(AssertionError):
+        trnfft_amd.set_backend("nki")
+    trnfft_amd.set_backend("pytorch")
+    try:
+        with pytest.raises(RuntimeError, match="pytorch"):
+            trnfft_amd.fft(torch.randn(8))
+    finally:
+        trnfft_amd.set_backend("auto")
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU behaviour")
+def test_fails_loudly_without_gpu():
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        trnfft_amd.fft(torch.randn(4, 64))
+    with pytest.raises(RuntimeError):
+        trnfft_amd.set_backend("hip")
+
+
+def test_precision_modes():
+    assert trnfft_amd.get_precision() == "fast"
+    with pytest.raises(ValueError):
+        trnfft_amd.set_precision("bogus")
+    from trnfft_amd.precision import _resolve
+
+    assert _resolve(None) == "fast"
+    with pytest.raises(NotImplementedError):
+        _resolve("double")
+
+
+class TestComplexTensor:
+    def test_from_real_and_complex(self):
+        x = ComplexTensor(torch.tensor([1.0, 2.0, 3.0]))
+        assert x.imag.sum().item() == 0.0
+        z = torch.complex(torch.tensor([1.0, 2.0]), torch.tensor([3.0, 4.0]))
+        y = ComplexTensor(z)
+        np.testing.assert_allclose(y.real.numpy(), [1.0, 2.0])
+        np.testing.assert_allclose(y.imag.numpy(), [3.0, 4.0])
+
+    def test_arithmetic(self):
+        a = ComplexTensor(torch.tensor([1.0]), torch.tensor([2.0]))
+        b = ComplexTensor(torch.tensor([3.0]), torch.tensor([4.0]))
+        c = a * b
+        assert c.real.item() == -5.0 and c.imag.item() == 10.0
+        d = a + b
+        assert d.real.item() == 4.0 and d.imag.item() == 6.0
+        e = b - a
+        assert e.real.item() == 2.0 and e.imag.item() == 2.0
+        f = -a
+        assert f.real.item() == -1.0
+        g = a.conj()
+        assert g.imag.item() == -2.0
+        assert abs(ComplexTensor(torch.tensor([3.0]), torch.tensor([4.0])).abs().item() - 5.0) < 1e-6
+
+    def test_views_are_contiguous_copies(self):
+        x = ComplexTensor(torch.randn(3, 4), torch.randn(3, 4))
+        t = x.transpose(0, 1)
+        assert t.shape == (4, 3) and t.real.is_contiguous()
+        assert x.reshape(12).shape == (12,)
+        assert x[1].shape == (4,)
+        with pytest.raises(AssertionError):
+            ComplexTensor(torch.randn(2), torch.randn(3))

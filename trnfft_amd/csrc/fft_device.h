@@ -1,0 +1,255 @@
+// Device building blocks: complex helpers, in-register small DFTs and the LDS-resident
+// Stockham transform used by every FFT kernel in this library.
+//
+// Conventions: DIR = -1 is the forward transform (W = exp(-2*pi*i/N)), DIR = +1 the inverse
+// (unscaled; callers apply 1/N).  A transform of length N held by T = N/E threads keeps
+// x[tid + T*e] in register e of thread tid on entry and X[tid + T*e] there on exit.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "fft_shape.h"
+
+namespace tfa {
+
+__device__ __forceinline__ float2 cadd(float2 a, float2 b) { return make_float2(a.x + b.x, a.y + b.y); }
+__device__ __forceinline__ float2 csub(float2 a, float2 b) { return make_float2(a.x - b.x, a.y - b.y); }
+__device__ __forceinline__ float2 cmul(float2 a, float2 b) {
+  return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
+}
+__device__ __forceinline__ float2 cscale(float2 a, float s) { return make_float2(a.x * s, a.y * s); }
+
+// a * (DIR * i)
+template <int DIR>
+__device__ __forceinline__ float2 mul_diri(float2 a) {
+  return DIR < 0 ? make_float2(a.y, -a.x) : make_float2(-a.y, a.x);
+}
+
+// constexpr sin/cos (Taylor series after reduction to [-pi/4, pi/4]); used only to fold
+// compile-time twiddle constants of the in-register DFTs.
+constexpr double kPi = 3.14159265358979323846264338327950288;
+constexpr double taylor_sin(double x) {
+  double term = x, sum = x;
+  for (int k = 1; k < 14; ++k) {
+    term *= -x * x / ((2 * k) * (2 * k + 1));
+    sum += term;
+  }
+  return sum;
+}
+constexpr double taylor_cos(double x) {
+  double term = 1.0, sum = 1.0;
+  for (int k = 1; k < 14; ++k) {
+    term *= -x * x / ((2 * k - 1) * (2 * k));
+    sum += term;
+  }
+  return sum;
+}
+// cos(2*pi*k/r), sin(2*pi*k/r) for integer k, r: reduce by octant so the series converges fast.
+constexpr double cos2pi(int k, int r) {
+  k = ((k % r) + r) % r;
+  // angle = 2*pi*k/r in [0, 2*pi); use symmetry on 8*k/r
+  double a = 2.0 * kPi * k / r;
+  if (a > kPi) a -= 2.0 * kPi;
+  double s = 1.0;
+  if (a > kPi / 2) { a = kPi - a; s = -1.0; }
+  else if (a < -kPi / 2) { a = -kPi - a; s = -1.0; }
+  return s * taylor_cos(a);
+}
+constexpr double sin2pi(int k, int r) {
+  k = ((k % r) + r) % r;
+  double a = 2.0 * kPi * k / r;
+  if (a > kPi) a -= 2.0 * kPi;
+  if (a > kPi / 2) a = kPi - a;
+  else if (a < -kPi / 2) a = -kPi - a;
+  return taylor_sin(a);
+}
+
+// v * W_R^K with W_R = exp(DIR*2*pi*i/R); trivial angles use adds/negations only.
+template <int K, int R, int DIR>
+__device__ __forceinline__ float2 twiddle_const(float2 v) {
+  constexpr int k = ((K % R) + R) % R;
+  if constexpr (k == 0) {
+    return v;
+  } else if constexpr (2 * k == R) {
+    return make_float2(-v.x, -v.y);
+  } else if constexpr (4 * k == R) {
+    return mul_diri<DIR>(v);
+  } else if constexpr (4 * k == 3 * R) {
+    return mul_diri<-DIR>(v);
+  } else if constexpr (8 * k == R || 8 * k == 3 * R || 8 * k == 5 * R || 8 * k == 7 * R) {
+    constexpr float h = 0.707106781186547524400844362104849f;
+    constexpr float c = (8 * k == R || 8 * k == 7 * R) ? h : -h;
+    constexpr float s = (float)DIR * ((8 * k == R || 8 * k == 3 * R) ? h : -h);
+    // (c + i s)(x + i y) with |c| = |s| = h: h-scaled sums
+    if constexpr (c > 0 && s > 0) return make_float2((v.x - v.y) * h, (v.x + v.y) * h);
+    else if constexpr (c > 0 && s < 0) return make_float2((v.x + v.y) * h, (v.y - v.x) * h);
+    else if constexpr (c < 0 && s > 0) return make_float2(-(v.x + v.y) * h, (v.x - v.y) * h);
+    else return make_float2((v.y - v.x) * h, -(v.x + v.y) * h);
+  } else {
+    constexpr float c = (float)cos2pi(k, R);
+    constexpr float s = (float)((double)DIR * sin2pi(k, R));
+    return make_float2(v.x * c - v.y * s, v.x * s + v.y * c);
+  }
+}
+
+// In-register DFT of length R on a[0..R) (natural order in and out).
+template <int R, int DIR>
+struct Dft;
+
+template <int DIR>
+struct Dft<1, DIR> {
+  __device__ __forceinline__ static void run(float2*) {}
+};
+
+template <int DIR>
+struct Dft<2, DIR> {
+  __device__ __forceinline__ static void run(float2* a) {
+    float2 t = a[0];
+    a[0] = cadd(t, a[1]);
+    a[1] = csub(t, a[1]);
+  }
+};
+
+template <int DIR>
+struct Dft<4, DIR> {
+  __device__ __forceinline__ static void run(float2* a) {
+    float2 t0 = cadd(a[0], a[2]);
+    float2 t1 = csub(a[0], a[2]);
+    float2 t2 = cadd(a[1], a[3]);
+    float2 t3 = mul_diri<DIR>(csub(a[1], a[3]));
+    a[0] = cadd(t0, t2);
+    a[2] = csub(t0, t2);
+    a[1] = cadd(t1, t3);
+    a[3] = csub(t1, t3);
+  }
+};
+
+// R = R1 * R2: DFT_R2 over the stride-R1 subsequences, twiddle W_R^{l q}, then DFT_R1.
+template <int R1, int R2, int DIR>
+struct DftSplit {
+  static constexpr int R = R1 * R2;
+  template <int L, int Q>
+  __device__ __forceinline__ static void tw(float2 (&b)[R1][R2]) {
+    if constexpr (L < R1) {
+      if constexpr (Q < R2) {
+        b[L][Q] = twiddle_const<L * Q, R, DIR>(b[L][Q]);
+        tw<L, Q + 1>(b);
+      } else {
+        tw<L + 1, 0>(b);
+      }
+    }
+  }
+  __device__ __forceinline__ static void run(float2* a) {
+    float2 b[R1][R2];
+#pragma unroll
+    for (int l = 0; l < R1; ++l) {
+#pragma unroll
+      for (int m = 0; m < R2; ++m) b[l][m] = a[l + R1 * m];
+      Dft<R2, DIR>::run(b[l]);
+    }
+    tw<0, 0>(b);
+#pragma unroll
+    for (int q = 0; q < R2; ++q) {
+      float2 c[R1];
+#pragma unroll
+      for (int l = 0; l < R1; ++l) c[l] = b[l][q];
+      Dft<R1, DIR>::run(c);
+#pragma unroll
+      for (int p = 0; p < R1; ++p) a[q + R2 * p] = c[p];
+    }
+  }
+};
+
+template <int DIR>
+struct Dft<8, DIR> {
+  __device__ __forceinline__ static void run(float2* a) { DftSplit<2, 4, DIR>::run(a); }
+};
+template <int DIR>
+struct Dft<16, DIR> {
+  __device__ __forceinline__ static void run(float2* a) { DftSplit<4, 4, DIR>::run(a); }
+};
+template <int DIR>
+struct Dft<32, DIR> {
+  __device__ __forceinline__ static void run(float2* a) { DftSplit<4, 8, DIR>::run(a); }
+};
+
+// Synchronisation between the LDS write and read halves of a pass exchange.  When a transform
+// lives inside one wavefront (T <= 64) program order within the wave suffices and only the
+// compiler must be kept from moving LDS accesses across the exchange.
+template <bool WAVE_LOCAL>
+__device__ __forceinline__ void exchange_sync() {
+  if constexpr (WAVE_LOCAL) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  } else {
+    __syncthreads();
+  }
+}
+
+// LDS-resident Stockham FFT of one length-N transform held by T = N/E threads.
+//   v:    registers, x[tid + T*e] on entry, X[tid + T*e] on exit
+//   lre/lim: this transform's LDS scratch, lds_pad(N) floats each
+//   tw:   the plan's twiddle table for (N, E, DIR) (layout from make_shape)
+template <int N, int E, int DIR, bool WAVE_LOCAL>
+struct LdsFft {
+  static constexpr LdsShape S = make_shape(N, E);
+  static constexpr int T = N / E;
+
+  template <int P>
+  __device__ __forceinline__ static void pass(float2 (&v)[E], float* lre, float* lim,
+                                              const float2* __restrict__ tw, int tid) {
+    if constexpr (P < S.npass) {
+      constexpr int R = S.radix[P];
+      constexpr int NB = E / R;
+      constexpr int LS = S.ls[P];
+      constexpr bool LAST = (P == S.npass - 1);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int j = tid + b * T;
+        const int k = j & (LS - 1);
+        float2 w[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) w[r] = v[b + r * NB];
+        if constexpr (P > 0) {
+          const float4* t4 = reinterpret_cast<const float4*>(tw + S.twoff[P] + k * R);
+#pragma unroll
+          for (int r2 = 0; r2 < R / 2; ++r2) {
+            float4 q = t4[r2];
+            if (r2 > 0) w[2 * r2] = cmul(w[2 * r2], make_float2(q.x, q.y));
+            w[2 * r2 + 1] = cmul(w[2 * r2 + 1], make_float2(q.z, q.w));
+          }
+        }
+        Dft<R, DIR>::run(w);
+        if constexpr (LAST) {
+#pragma unroll
+          for (int u = 0; u < R; ++u) v[b + u * NB] = w[u];
+        } else {
+          const int base = (j - k) * R + k;
+#pragma unroll
+          for (int u = 0; u < R; ++u) {
+            const int idx = lds_pad(base + u * LS);
+            lre[idx] = w[u].x;
+            lim[idx] = w[u].y;
+          }
+        }
+      }
+      if constexpr (!LAST) {
+        exchange_sync<WAVE_LOCAL>();
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int idx = lds_pad(tid + T * e);
+          v[e] = make_float2(lre[idx], lim[idx]);
+        }
+        exchange_sync<WAVE_LOCAL>();
+        pass<P + 1>(v, lre, lim, tw, tid);
+      }
+    }
+  }
+
+  __device__ __forceinline__ static void run(float2 (&v)[E], float* lre, float* lim,
+                                             const float2* __restrict__ tw, int tid) {
+    pass<0>(v, lre, lim, tw, tid);
+  }
+};
+
+}  // namespace tfa

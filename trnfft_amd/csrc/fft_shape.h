@@ -1,0 +1,55 @@
+// Compile-time shape of the LDS-resident Stockham FFT, shared by the device kernels and the
+// host code that builds their twiddle tables (both must agree on pass order and table layout).
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace tfa {
+
+constexpr int kMaxPasses = 8;
+
+__host__ __device__ constexpr int ilog2(long long n) {
+  int l = 0;
+  while ((1LL << l) < n) ++l;
+  return l;
+}
+
+// Complex elements each thread keeps in registers for a length-N transform.  A transform of
+// length N is handled by T = N / E threads; every pass but the last is radix E.
+__host__ __device__ constexpr int lds_epth(int n) {
+  return n <= 16 ? n : (n == 32 || n == 64) ? 8 : 16;
+}
+
+struct LdsShape {
+  int n, e, t, npass;
+  int radix[kMaxPasses];
+  int ls[kMaxPasses];       // product of the radices of the earlier passes
+  int twoff[kMaxPasses + 1];  // offset (in complex entries) of each pass's twiddle block
+};
+
+// Pass p (p >= 1) multiplies input r of a butterfly with in-transform position k (k < ls[p])
+// by W_{ls[p]*radix[p]}^{r*k}; its block holds ls[p] rows of radix[p] entries (entry r = 0 is 1).
+__host__ __device__ constexpr LdsShape make_shape(int n, int e) {
+  LdsShape s{};
+  s.n = n;
+  s.e = e;
+  s.t = n / e;
+  int rem = n, p = 0, ls = 1, off = 0;
+  while (rem > 1) {
+    int r = rem >= e ? e : rem;
+    s.radix[p] = r;
+    s.ls[p] = ls;
+    s.twoff[p] = off;
+    if (p > 0) off += ls * r;
+    ls *= r;
+    rem /= r;
+    ++p;
+  }
+  s.npass = p;
+  s.twoff[p] = off;
+  return s;
+}
+
+// LDS word index with one pad word per 16 to keep the strided pass writes bank-conflict free.
+__host__ __device__ constexpr int lds_pad(int i) { return i + (i >> 4); }
+
+}  // namespace tfa

@@ -1,0 +1,98 @@
+// Launch interfaces of the device kernels (host side) plus small device helpers shared by them.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "fft_device.h"
+
+namespace tfa {
+
+// Per-workgroup LDS budget of gfx950 (160 KiB per CU, all of it addressable by one workgroup).
+constexpr long long kLdsBytes = 163840;
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Remap the
+// linear block index so that consecutive tiles run on the same XCD at about the same time:
+// tiles that share HBM cache lines then meet in one L2 instead of eight.
+__device__ __forceinline__ long long xcd_tile_remap(long long i, long long g) {
+  const long long per = g / 8;
+  if (i >= per * 8) return i;
+  return (i % 8) * per + i / 8;
+}
+
+// Thread layout of the batched LDS kernels for transform length N: T threads per transform,
+// XF transforms per workgroup (at least 256 threads per workgroup), PADN LDS floats per plane
+// per transform (1 when the transform needs no exchange).
+template <int N>
+struct C2cThreads {
+  static constexpr int E = lds_epth(N);
+  static constexpr int T = N / E;
+  static constexpr int XF = T >= 256 ? 1 : 256 / T;
+  static constexpr int THREADS = XF * T;
+  static constexpr LdsShape S = make_shape(N, E);
+  static constexpr int PADN = S.npass > 1 ? lds_pad(N) : 1;
+};
+
+struct C2cArgs {
+  const float* in_re;
+  const float* in_im;  // nullptr: real input (imaginary part zero)
+  float* out_re;
+  float* out_im;
+  const float2* tw;
+  long long batch;
+  float scale;
+  int dir;
+  hipStream_t stream;
+};
+hipError_t launch_c2c_lds(int n, const C2cArgs& a);
+
+struct FourStepArgs {
+  const float* in_re;
+  const float* in_im;  // nullptr: real input
+  float* t_re;         // workspace, batch * n1 * n2 floats each
+  float* t_im;
+  float* out_re;
+  float* out_im;
+  const float2* tw1;  // LDS-FFT table for length n1
+  const float2* tw2;  // LDS-FFT table for length n2
+  const float2* tw_lo;  // W_N^j, j < 2^lo_bits
+  const float2* tw_hi;  // W_N^(j << lo_bits)
+  int n1, n2, lo_bits;
+  long long batch;
+  float scale;
+  int dir;
+  hipStream_t stream;
+};
+hipError_t launch_fourstep(const FourStepArgs& a);
+
+struct BluesteinArgs {
+  const float* in_re;
+  const float* in_im;  // nullptr: real input
+  float* out_re;
+  float* out_im;
+  const float2* chirp;  // n entries, exp(sign*i*pi*k^2/n) with the angle rounded as in fp32
+  const float2* hs;     // m entries, FFT_m(h) / m
+  const float2* tw_f;   // LDS-FFT tables for length m, forward and inverse (fused path)
+  const float2* tw_i;
+  int n, m;
+  long long batch;
+  float scale;
+  hipStream_t stream;
+};
+hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a);
+hipError_t launch_bluestein_pre(const BluesteinArgs& a, float* y_re, float* y_im);
+hipError_t launch_bluestein_mul(const BluesteinArgs& a, float* y_re, float* y_im);
+hipError_t launch_bluestein_post(const BluesteinArgs& a, const float* y_re, const float* y_im);
+
+struct StftArgs {
+  const float* signal;  // (batch, length)
+  const float* window;  // n_fft
+  float* out_re;        // (batch, n_bins, n_frames)
+  float* out_im;
+  const float2* tw;  // LDS-FFT table for n_fft, forward
+  int length, hop, pad, n_frames, n_bins;
+  long long batch;
+  float scale;
+  hipStream_t stream;
+};
+hipError_t launch_stft(int n_fft, const StftArgs& a);
+
+}  // namespace tfa

@@ -1,0 +1,383 @@
+// Host side of the C ABI (include/trnfft_amd.h): plan construction (algorithm choice and device
+// tables), workspace sizing and execution dispatch.
+#include <cmath>
+#include <complex>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/trnfft_amd.h"
+#include "kernels.h"
+
+using tfa::LdsShape;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(TFA_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool is_pow2(int64_t n) { return n > 0 && (n & (n - 1)) == 0; }
+
+// Largest power-of-two transform one workgroup keeps in LDS.
+constexpr int64_t kMaxLdsN = 16384;
+// Largest power-of-two transform of the two-pass four-step path (4096 x 4096).
+constexpr int64_t kMaxFourStepN = int64_t(1) << 24;
+
+// exp(dir * 2*pi*i * num / den), num reduced mod den first; computed in fp64, rounded to fp32.
+float2 unit_root(int64_t num, int64_t den, int dir) {
+  num %= den;
+  if (num < 0) num += den;
+  const double a = 2.0 * M_PI * (double)num / (double)den;
+  return make_float2((float)std::cos(a), (float)(dir * std::sin(a)));
+}
+
+// Twiddle table of the LDS Stockham transform of length n (layout of tfa::make_shape).
+std::vector<float2> lds_table(int n, int dir) {
+  const LdsShape s = tfa::make_shape(n, tfa::lds_epth(n));
+  std::vector<float2> t((size_t)s.twoff[s.npass] + 2, make_float2(1.0f, 0.0f));
+  for (int p = 1; p < s.npass; ++p) {
+    const int r = s.radix[p], ls = s.ls[p];
+    for (int k = 0; k < ls; ++k)
+      for (int q = 0; q < r; ++q) t[(size_t)s.twoff[p] + k * r + q] = unit_root((int64_t)q * k, (int64_t)ls * r, dir);
+  }
+  return t;
+}
+
+struct DevBuf {
+  void* p = nullptr;
+};
+
+// Power-of-two transform tables for one direction: LDS path (n <= kMaxLdsN) or four-step.
+struct C2cTables {
+  int64_t n = 0;
+  int dir = -1;
+  bool fourstep = false;
+  float2* tw = nullptr;  // LDS path
+  int n1 = 0, n2 = 0, lo_bits = 0;
+  float2 *tw1 = nullptr, *tw2 = nullptr, *tw_lo = nullptr, *tw_hi = nullptr;
+};
+
+}  // namespace
+
+struct tfa_plan {
+  tfa_plan_desc d{};
+  int device = 0;
+  int64_t m = 0;  // padded length (Bluestein), else n
+  C2cTables fwd, inv;  // C2C uses the one for its direction; Bluestein uses both (length m)
+  bool blue_fused = false;
+  float2* chirp = nullptr;
+  float2* hs = nullptr;
+  float* w_re = nullptr;  // DFT-GEMM matrix
+  float* w_im = nullptr;
+  std::vector<void*> allocs;
+
+  ~tfa_plan() {
+    for (void* p : allocs) (void)hipFree(p);
+  }
+
+  template <class T>
+  int upload(const std::vector<T>& h, T** out) {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, h.size() * sizeof(T) + 16);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(plan table)");
+    allocs.push_back(p);
+    e = hipMemcpy(p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy(plan table)");
+    *out = static_cast<T*>(p);
+    return TFA_OK;
+  }
+
+  int build_c2c(int64_t n, int dir, C2cTables* t) {
+    t->n = n;
+    t->dir = dir;
+    if (n <= kMaxLdsN) {
+      t->fourstep = false;
+      return upload(lds_table((int)n, dir), &t->tw);
+    }
+    if (n > kMaxFourStepN) return fail(TFA_ERR_UNSUPPORTED, "power-of-two length above 2^24 not supported");
+    t->fourstep = true;
+    const int lg = tfa::ilog2(n);
+    t->n1 = 1 << (lg / 2);      // column transform length (strided)
+    t->n2 = (int)(n / t->n1);   // row transform length (contiguous), n2 >= n1
+    t->lo_bits = (lg + 1) / 2;
+    int rc;
+    if ((rc = upload(lds_table(t->n1, dir), &t->tw1))) return rc;
+    if ((rc = upload(lds_table(t->n2, dir), &t->tw2))) return rc;
+    std::vector<float2> lo((size_t)1 << t->lo_bits), hi((size_t)(n >> t->lo_bits));
+    for (size_t j = 0; j < lo.size(); ++j) lo[j] = unit_root((int64_t)j, n, dir);
+    for (size_t j = 0; j < hi.size(); ++j) hi[j] = unit_root((int64_t)j << t->lo_bits, n, dir);
+    if ((rc = upload(lo, &t->tw_lo))) return rc;
+    return upload(hi, &t->tw_hi);
+  }
+};
+
+namespace {
+
+size_t c2c_workspace(const C2cTables& t, int64_t batch) {
+  return t.fourstep ? (size_t)2 * sizeof(float) * (size_t)batch * (size_t)t.n : 0;
+}
+
+int run_c2c(const C2cTables& t, int64_t batch, const float* in_re, const float* in_im, float* out_re,
+            float* out_im, void* ws, float scale, hipStream_t s) {
+  hipError_t e;
+  if (!t.fourstep) {
+    tfa::C2cArgs a{in_re, in_im, out_re, out_im, t.tw, batch, scale, t.dir, s};
+    e = tfa::launch_c2c_lds((int)t.n, a);
+  } else {
+    if (!ws) return fail(TFA_ERR_INVALID, "four-step transform needs a workspace");
+    float* t_re = static_cast<float*>(ws);
+    float* t_im = t_re + (size_t)batch * (size_t)t.n;
+    tfa::FourStepArgs a{in_re, in_im, t_re, t_im, out_re, out_im, t.tw1, t.tw2, t.tw_lo, t.tw_hi,
+                        t.n1, t.n2, t.lo_bits, batch, scale, t.dir, s};
+    e = tfa::launch_fourstep(a);
+  }
+  return e == hipSuccess ? TFA_OK : hip_fail(e, "c2c launch");
+}
+
+// Host fp64 radix-2 FFT (forward, in place) used only to build the Bluestein filter spectrum.
+void host_fft(std::vector<std::complex<double>>& a) {
+  const size_t n = a.size();
+  for (size_t i = 1, j = 0; i < n; ++i) {
+    size_t bit = n >> 1;
+    for (; j & bit; bit >>= 1) j ^= bit;
+    j ^= bit;
+    if (i < j) std::swap(a[i], a[j]);
+  }
+  for (size_t len = 2; len <= n; len <<= 1) {
+    for (size_t k = 0; k < len / 2; ++k) {
+      const double ang = -2.0 * M_PI * (double)k / (double)len;
+      const std::complex<double> w(std::cos(ang), std::sin(ang));
+      for (size_t i = k; i < n; i += len) {
+        const std::complex<double> u = a[i], v = a[i + len / 2] * w;
+        a[i] = u + v;
+        a[i + len / 2] = u - v;
+      }
+    }
+  }
+}
+
+// The reference's chirp, trnfft/fft_core.py:1316-1320: angle = sign * pi * k * k / n evaluated
+// in fp32 exactly as torch does it (fp32(sign*pi) * k, * k, true division by n, each rounded
+// to fp32), then cos/sin of that fp32 angle.  Reproducing the fp32 angle is required for parity:
+// its rounding moves the reference's result ~1e-4 (n=1000) from the exact DFT.
+std::vector<float2> reference_chirp(int64_t n, int sign) {
+  std::vector<float2> c((size_t)n);
+  volatile float spi = (float)(sign * M_PI);
+  const float fn = (float)n;
+  for (int64_t k = 0; k < n; ++k) {
+    const float kf = (float)k;
+    volatile float a1 = spi * kf;
+    volatile float a2 = a1 * kf;
+    volatile float a3 = a2 / fn;
+    const double a = (double)a3;
+    c[(size_t)k] = make_float2((float)std::cos(a), (float)std::sin(a));
+  }
+  return c;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t tfa_abi_version(void) { return (1 << 16) | 0; }
+
+const char* tfa_last_error(void) { return g_last_error.c_str(); }
+
+int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
+  if (!out || !desc) return fail(TFA_ERR_INVALID, "null argument");
+  *out = nullptr;
+  const int64_t n = desc->n;
+  if (n < 1) return fail(TFA_ERR_INVALID, "transform length must be >= 1");
+  tfa_plan* p = new (std::nothrow) tfa_plan();
+  if (!p) return fail(TFA_ERR_INVALID, "out of host memory");
+  p->d = *desc;
+  p->m = n;
+  hipError_t he = hipGetDevice(&p->device);
+  if (he != hipSuccess) {
+    delete p;
+    return hip_fail(he, "hipGetDevice");
+  }
+  const int dir = desc->inverse ? 1 : -1;
+  int rc = TFA_OK;
+  switch (desc->kind) {
+    case TFA_KIND_C2C:
+      if (!is_pow2(n)) {
+        rc = fail(TFA_ERR_INVALID, "TFA_KIND_C2C needs a power-of-two length");
+        break;
+      }
+      rc = p->build_c2c(n, dir, dir < 0 ? &p->fwd : &p->inv);
+      break;
+    case TFA_KIND_BLUESTEIN: {
+      if (n < 2) {
+        rc = fail(TFA_ERR_INVALID, "Bluestein needs n >= 2");
+        break;
+      }
+      // trnfft/plan.py:42: m = 1 << (2n-2).bit_length()
+      int64_t v = 2 * n - 2, bits = 0;
+      while (v) { ++bits; v >>= 1; }
+      const int64_t m = int64_t(1) << bits;
+      p->m = m;
+      if (m > kMaxFourStepN) {
+        rc = fail(TFA_ERR_UNSUPPORTED, "Bluestein padded length above 2^24 not supported");
+        break;
+      }
+      p->blue_fused = m <= kMaxLdsN;
+      if ((rc = p->build_c2c(m, -1, &p->fwd))) break;
+      if ((rc = p->build_c2c(m, 1, &p->inv))) break;
+      const std::vector<float2> chirp = reference_chirp(n, dir);
+      // h = conj(chirp) circularly wrapped (trnfft/fft_core.py:1337-1345); H = FFT_m(h) / m
+      std::vector<std::complex<double>> h((size_t)m, {0.0, 0.0});
+      for (int64_t i = 0; i < n; ++i) {
+        const std::complex<double> hc(chirp[(size_t)i].x, -(double)chirp[(size_t)i].y);
+        h[(size_t)i] = hc;
+        if (i > 0) h[(size_t)(m - i)] = hc;
+      }
+      host_fft(h);
+      std::vector<float2> hs((size_t)m);
+      for (int64_t i = 0; i < m; ++i)
+        hs[(size_t)i] = make_float2((float)(h[(size_t)i].real() / (double)m), (float)(h[(size_t)i].imag() / (double)m));
+      if ((rc = p->upload(chirp, &p->chirp))) break;
+      rc = p->upload(hs, &p->hs);
+      break;
+    }
+    case TFA_KIND_STFT:
+      if (!is_pow2(n) || n < 16 || n > 4096) {
+        rc = fail(TFA_ERR_UNSUPPORTED, "fused STFT needs a power-of-two n_fft in [16, 4096]");
+        break;
+      }
+      if (desc->hop < 1) {
+        rc = fail(TFA_ERR_INVALID, "hop_length must be >= 1");
+        break;
+      }
+      rc = p->build_c2c(n, -1, &p->fwd);
+      break;
+    case TFA_KIND_DFT_GEMM:
+      rc = fail(TFA_ERR_UNSUPPORTED, "plan kind not implemented yet");
+      break;
+    default:
+      rc = fail(TFA_ERR_INVALID, "unknown plan kind");
+  }
+  if (rc != TFA_OK) {
+    delete p;
+    return rc;
+  }
+  *out = p;
+  return TFA_OK;
+}
+
+void tfa_plan_destroy(tfa_plan* plan) { delete plan; }
+
+int64_t tfa_plan_padded_n(const tfa_plan* plan) { return plan ? plan->m : 0; }
+
+int tfa_plan_workspace_size(const tfa_plan* plan, int64_t batch, size_t* bytes) {
+  if (!plan || !bytes || batch < 0) return fail(TFA_ERR_INVALID, "bad argument");
+  *bytes = 0;
+  switch (plan->d.kind) {
+    case TFA_KIND_C2C:
+      *bytes = c2c_workspace(plan->d.inverse ? plan->inv : plan->fwd, batch);
+      break;
+    case TFA_KIND_BLUESTEIN:
+      if (!plan->blue_fused)
+        *bytes = (size_t)2 * sizeof(float) * (size_t)batch * (size_t)plan->m + c2c_workspace(plan->fwd, batch);
+      break;
+    default:
+      break;
+  }
+  return TFA_OK;
+}
+
+int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const float* in_im,
+                float* out_re, float* out_im, void* workspace, tfa_stream stream) {
+  if (!plan) return fail(TFA_ERR_INVALID, "null plan");
+  if (batch < 0) return fail(TFA_ERR_INVALID, "negative batch");
+  if (batch == 0) return TFA_OK;
+  if (!in_re || !out_re || !out_im) return fail(TFA_ERR_INVALID, "null data pointer");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
+    return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n = plan->d.n;
+  const float scale = plan->d.inverse ? (float)(1.0 / (double)n) : 1.0f;
+  switch (plan->d.kind) {
+    case TFA_KIND_C2C:
+      return run_c2c(plan->d.inverse ? plan->inv : plan->fwd, batch, in_re, in_im, out_re, out_im,
+                     workspace, scale, s);
+    case TFA_KIND_BLUESTEIN: {
+      tfa::BluesteinArgs a{in_re, in_im, out_re, out_im, plan->chirp, plan->hs, plan->fwd.tw,
+                           plan->inv.tw, (int)n, (int)plan->m, batch, scale, s};
+      hipError_t e;
+      if (plan->blue_fused) {
+        e = tfa::launch_bluestein_fused((int)plan->m, a);
+        return e == hipSuccess ? TFA_OK : hip_fail(e, "bluestein launch");
+      }
+      if (!workspace) return fail(TFA_ERR_INVALID, "staged Bluestein needs a workspace");
+      float* y_re = static_cast<float*>(workspace);
+      float* y_im = y_re + (size_t)batch * (size_t)plan->m;
+      void* inner_ws = y_im + (size_t)batch * (size_t)plan->m;
+      if ((e = tfa::launch_bluestein_pre(a, y_re, y_im)) != hipSuccess) return hip_fail(e, "bluestein pre");
+      int rc = run_c2c(plan->fwd, batch, y_re, y_im, y_re, y_im, inner_ws, 1.0f, s);
+      if (rc) return rc;
+      if ((e = tfa::launch_bluestein_mul(a, y_re, y_im)) != hipSuccess) return hip_fail(e, "bluestein mul");
+      rc = run_c2c(plan->inv, batch, y_re, y_im, y_re, y_im, inner_ws, 1.0f, s);
+      if (rc) return rc;
+      if ((e = tfa::launch_bluestein_post(a, y_re, y_im)) != hipSuccess) return hip_fail(e, "bluestein post");
+      return TFA_OK;
+    }
+    default:
+      return fail(TFA_ERR_UNSUPPORTED, "plan kind not executable with tfa_execute");
+  }
+}
+
+int tfa_stft_frames(const tfa_plan* plan, int64_t num_samples, int64_t* n_frames) {
+  if (!plan || !n_frames || plan->d.kind != TFA_KIND_STFT) return fail(TFA_ERR_INVALID, "not an STFT plan");
+  const int64_t n_fft = plan->d.n;
+  const int64_t padded = (plan->d.flags & TFA_STFT_CENTER) ? num_samples + 2 * (n_fft / 2) : num_samples;
+  if (padded < n_fft) return fail(TFA_ERR_INVALID, "signal shorter than n_fft");
+  *n_frames = 1 + (padded - n_fft) / plan->d.hop;
+  return TFA_OK;
+}
+
+int tfa_stft_execute(const tfa_plan* plan, int64_t batch, int64_t num_samples, const float* signal,
+                     const float* window, float* out_re, float* out_im, tfa_stream stream) {
+  if (!plan || plan->d.kind != TFA_KIND_STFT) return fail(TFA_ERR_INVALID, "not an STFT plan");
+  if (batch < 0) return fail(TFA_ERR_INVALID, "negative batch");
+  if (batch == 0) return TFA_OK;
+  if (!signal || !window || !out_re || !out_im) return fail(TFA_ERR_INVALID, "null data pointer");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
+    return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  const int64_t n_fft = plan->d.n;
+  const bool center = plan->d.flags & TFA_STFT_CENTER;
+  const int64_t pad = center ? n_fft / 2 : 0;
+  if (center && num_samples <= pad) return fail(TFA_ERR_INVALID, "reflect padding needs more samples than n_fft/2");
+  if (num_samples > INT32_MAX / 2) return fail(TFA_ERR_UNSUPPORTED, "signal too long");
+  int64_t frames = 0;
+  int rc = tfa_stft_frames(plan, num_samples, &frames);
+  if (rc) return rc;
+  const int n_bins = (plan->d.flags & TFA_STFT_ONESIDED) ? (int)(n_fft / 2 + 1) : (int)n_fft;
+  const float scale = (plan->d.flags & TFA_STFT_NORMALIZED) ? (float)(1.0 / std::sqrt((double)n_fft)) : 1.0f;
+  tfa::StftArgs a{signal, window, out_re, out_im, plan->fwd.tw, (int)num_samples, (int)plan->d.hop,
+                  (int)pad, (int)frames, n_bins, batch, scale, static_cast<hipStream_t>(stream)};
+  hipError_t e = tfa::launch_stft((int)n_fft, a);
+  return e == hipSuccess ? TFA_OK : hip_fail(e, "stft launch");
+}
+
+int tfa_complex_gemm(int64_t m, int64_t n, int64_t k, const float* a_re, const float* a_im,
+                     int64_t lda, const float* b_re, const float* b_im, int64_t ldb, int32_t b_trans,
+                     const float* bias_re, const float* bias_im, float* c_re, float* c_im,
+                     int64_t ldc, tfa_stream stream) {
+  (void)m; (void)n; (void)k; (void)a_re; (void)a_im; (void)lda; (void)b_re; (void)b_im; (void)ldb;
+  (void)b_trans; (void)bias_re; (void)bias_im; (void)c_re; (void)c_im; (void)ldc; (void)stream;
+  return fail(TFA_ERR_UNSUPPORTED, "complex gemm not implemented yet");
+}
+
+}  // extern "C"

@@ -1,0 +1,154 @@
+"""Backend dispatch (interface of trnfft/nki/dispatch.py:50-102, with "hip" in place of "nki").
+
+    "auto"    — HIP if the native library loads and a gfx950 GPU is visible
+    "pytorch" — do not use this backend (the caller's own pytorch path runs instead)
+    "hip"     — always HIP (RuntimeError at selection time if unavailable)
+
+This package is the HIP dispatch target only: every compute entry point raises RuntimeError
+when ``_use_hip()`` is False.  There is no CPU fallback inside it; trnfft keeps its own pytorch
+path and consults ``_use_hip()`` before delegating here (see INTEGRATION.md at the repo root).
+
+CPU inputs are moved to the current GPU and results moved back, as the reference's NKI path
+does with its XLA device (trnfft/nki/dispatch.py:423-428, trnfft/nki/autograd.py:58-60).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+
+import torch
+
+from . import _lib
+from .complex import ComplexTensor
+
+HAS_HIP = _lib.library_present()
+
+_backend = "auto"
+
+
+def set_backend(backend: str):
+    """Set dispatch backend: 'auto', 'pytorch', or 'hip' (trnfft/nki/dispatch.py:53-59)."""
+    global _backend
+    assert backend in ("auto", "pytorch", "hip")
+    if backend == "hip" and not _hip_ready():
+        raise RuntimeError(
+            "HIP backend requires libtrnfft_amd.so (python -m trnfft_amd.csrc.build) and a gfx950 GPU"
+        )
+    _backend = backend
+
+
+def get_backend() -> str:
+    return _backend
+
+
+@functools.lru_cache(maxsize=1)
+def _hip_ready() -> bool:
+    if not HAS_HIP:
+        return False
+    try:
+        _lib.lib()
+    except OSError:
+        return False
+    if not torch.cuda.is_available():
+        return False
+    try:
+        arch = torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName
+    except Exception:
+        return False
+    return arch.startswith("gfx950")
+
+
+def _use_hip() -> bool:
+    if _backend == "hip":
+        return True
+    if _backend == "pytorch":
+        return False
+    return _hip_ready()
+
+
+def _require_hip(what: str) -> None:
+    if not _use_hip():
+        if _backend == "pytorch":
+            raise RuntimeError(
+                f"trnfft_amd.{what}: backend is 'pytorch'; the pytorch path belongs to trnfft itself "
+                "(trnfft_amd only executes the HIP target)"
+            )
+        raise RuntimeError(
+            f"trnfft_amd.{what}: HIP backend unavailable (needs libtrnfft_amd.so built for gfx950 and a "
+            "visible gfx950 GPU); no CPU fallback exists in this package"
+        )
+    _lib.lib()
+
+
+def target_device(*tensors: torch.Tensor) -> torch.device:
+    """Device to run on: the inputs' GPU, or the current GPU for CPU inputs."""
+    for t in tensors:
+        if t is not None and t.is_cuda:
+            return t.device
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def to_device_f32(t: torch.Tensor | None, dev: torch.device) -> torch.Tensor | None:
+    """Contiguous fp32 copy of t on dev (no copy when it already is one)."""
+    if t is None:
+        return None
+    if t.dtype != torch.float32:
+        raise TypeError(f"the HIP backend computes in fp32; got {t.dtype}")
+    return t.to(dev, non_blocking=False).contiguous()
+
+
+def stream_handle(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _gemm(a_re, a_im, b_re, b_im, b_trans: bool, bias_re=None, bias_im=None, what="complex_gemm"):
+    _require_hip(what)
+    dev = target_device(a_re, b_re)
+    out_dev = a_re.device
+    a_re, a_im = to_device_f32(a_re, dev), to_device_f32(a_im, dev)
+    b_re, b_im = to_device_f32(b_re, dev), to_device_f32(b_im, dev)
+    bias_re, bias_im = to_device_f32(bias_re, dev), to_device_f32(bias_im, dev)
+    lead = a_re.shape[:-1]
+    k = a_re.shape[-1]
+    m = 1
+    for s in lead:
+        m *= s
+    if b_trans:
+        n, kb = b_re.shape
+    else:
+        kb, n = b_re.shape
+    if kb != k:
+        raise ValueError(f"{what}: inner dimensions differ ({k} vs {kb})")
+    c_re = torch.empty(*lead, n, device=dev, dtype=torch.float32)
+    c_im = torch.empty(*lead, n, device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_complex_gemm(
+            m, n, k, ptr(a_re), ptr(a_im), k, ptr(b_re), ptr(b_im), b_re.shape[1], int(b_trans),
+            ptr(bias_re), ptr(bias_im), ptr(c_re), ptr(c_im), n, stream_handle(dev),
+        )
+    _lib.check(rc, what)
+    out = ComplexTensor._wrap(c_re, c_im)
+    return out if out_dev == dev else out.to(out_dev)
+
+
+def complex_gemm(a: ComplexTensor, b: ComplexTensor) -> ComplexTensor:
+    """C = A @ B on the MFMA complex GEMM (trnfft/nki/dispatch.py:74-84)."""
+    if a.real.dim() != 2 or b.real.dim() != 2:
+        raise ValueError("complex_gemm expects 2-D operands")
+    return _gemm(a.real, a.imag, b.real, b.imag, False)
+
+
+def complex_linear(
+    x: ComplexTensor,
+    w_real: torch.Tensor,
+    w_imag: torch.Tensor,
+    bias_real: torch.Tensor | None = None,
+    bias_imag: torch.Tensor | None = None,
+) -> ComplexTensor:
+    """y = x @ W^T (+ bias) with W (out, in) (trnfft/nki/dispatch.py:91-102, trnfft/nn.py:46-48)."""
+    return _gemm(x.real, x.imag, w_real, w_imag, True, bias_real, bias_imag, what="complex_linear")

@@ -1,0 +1,99 @@
+"""1-D FFT entry point on the HIP kernels (contract of trnfft/fft_core.py:22-50).
+
+``fft_core(x, inverse, plan, precision)`` transforms the last dimension of a ComplexTensor,
+treating every leading dimension as batch, and returns new tensors:
+
+* n == 1: a clone (trnfft/fft_core.py:41-42);
+* power-of-two n: the LDS-resident Stockham kernel (n <= 16384) or the two-pass four-step
+  kernel pair (n > 16384), replacing the radix-2 ``_cooley_tukey`` (:53-117) and the NKI
+  Stockham/butterfly chain (:548-1238);
+* any other n: the fused Bluestein kernel, replacing ``_bluestein`` (:1285-1376), with the chirp
+  built from the reference's fp32 angle expression so results agree with the reference;
+* ``_fft_via_gemm`` (:221-251): DFT as one complex GEMM on the matrix cores, taken when
+  n <= ``_DFT_GEMM_THRESHOLD`` (0 by default: the Stockham kernel is faster on MI355X; the
+  reference only routes here on its NKI backend).
+
+Inverse transforms are scaled by 1/n inside the kernels, as the reference scales after its loop.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .complex import ComplexTensor
+from .dispatch import _require_hip, ptr, stream_handle, target_device, to_device_f32
+from .plan import FFTAlgorithm, FFTPlan, create_plan, native_plan
+from .precision import _resolve
+
+# n at or below which power-of-two transforms run as a DFT-GEMM (trnfft/fft_core.py:138 uses
+# 256 on NKI); 0 keeps every length on the Stockham kernel.
+_DFT_GEMM_THRESHOLD = 0
+
+
+def fft_core(
+    x: ComplexTensor,
+    inverse: bool = False,
+    plan: FFTPlan | None = None,
+    precision: str | None = None,
+) -> ComplexTensor:
+    """Compute the 1-D FFT along the last dimension on the GPU."""
+    _resolve(precision)
+    n = x.shape[-1]
+    if n == 1:
+        return x.clone()
+    if plan is None:
+        plan = create_plan(n, inverse=inverse)
+    _require_hip("fft_core")
+    if plan.algorithm == FFTAlgorithm.COOLEY_TUKEY and n <= _DFT_GEMM_THRESHOLD:
+        return _fft_via_gemm(x, inverse)
+    return execute_1d(x.real, x.imag, inverse)
+
+
+def execute_1d(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> ComplexTensor:
+    """Run the batched transform of the last dimension; ``im=None`` means real input."""
+    n = re.shape[-1]
+    dev = target_device(re, im)
+    out_dev = re.device
+    re = to_device_f32(re, dev)
+    im = to_device_f32(im, dev)
+    if n == 1:
+        out = ComplexTensor._wrap(re.clone(), im.clone() if im is not None else torch.zeros_like(re))
+        return out if out_dev == dev else out.to(out_dev)
+    batch = re.numel() // n if n else 0
+    kind = _lib.KIND_C2C if (n & (n - 1)) == 0 else _lib.KIND_BLUESTEIN
+    plan = native_plan(kind, n, inverse, dev.index)
+    out_re = torch.empty_like(re)
+    out_im = torch.empty_like(re)
+    ws = None
+    ws_bytes = plan.workspace_bytes(batch)
+    if ws_bytes:
+        ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_execute(
+            plan.handle, batch, ptr(re), ptr(im), ptr(out_re), ptr(out_im), ptr(ws), stream_handle(dev)
+        )
+    _lib.check(rc, "tfa_execute")
+    out = ComplexTensor._wrap(out_re, out_im)
+    return out if out_dev == dev else out.to(out_dev)
+
+
+def _fft_via_gemm(x: ComplexTensor, inverse: bool) -> ComplexTensor:
+    """X = x @ W with the exact DFT matrix, on the matrix-core DFT-GEMM kernel (n <= 256)."""
+    re, im = x.real, x.imag
+    n = re.shape[-1]
+    dev = target_device(re, im)
+    out_dev = re.device
+    re = to_device_f32(re, dev)
+    im = to_device_f32(im, dev)
+    batch = re.numel() // n
+    plan = native_plan(_lib.KIND_DFT_GEMM, n, inverse, dev.index)
+    out_re = torch.empty_like(re)
+    out_im = torch.empty_like(re)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_execute(
+            plan.handle, batch, ptr(re), ptr(im), ptr(out_re), ptr(out_im), ptr(None), stream_handle(dev)
+        )
+    _lib.check(rc, "tfa_execute(dft_gemm)")
+    out = ComplexTensor._wrap(out_re, out_im)
+    return out if out_dev == dev else out.to(out_dev)
