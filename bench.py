@@ -139,11 +139,16 @@ def bench_headline(steps: int, warmup: int):
     for k in range(warmup):
         step(k)
     torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    ev0.record()
     for k in range(steps):
         step(k)
+    ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    t_region_launch = ev0.elapsed_time(ev1) * 1e-3 / (2 * steps)
 
     # per-launch kernel durations (separate pass, event pairs around each launch)
     timer = EventTimer()
@@ -151,7 +156,7 @@ def bench_headline(steps: int, warmup: int):
         timer.record(lambda k=k: execute(*args_f[k % sets]))
         timer.record(lambda k=k: execute(*args_i[k % sets]))
     d = timer.durations_s()
-    t_launch = sum(d) / len(d)
+    t_launch = t_region_launch
 
     # correctness of what was timed: last forward output vs a fresh transform of the same input
     chk = trnfft_amd.fft(trnfft_amd.ComplexTensor(ins[0][0], ins[0][1]))
@@ -159,9 +164,26 @@ def bench_headline(steps: int, warmup: int):
     torch.cuda.synchronize()
     assert torch.equal(chk.real, outs[0][0]) and torch.equal(chk.imag, outs[0][1])
 
+    # plain device copy of the same bytes (32 MiB in, 32 MiB out per launch, same rotation): the
+    # achievable-bandwidth reference, and the known-size kernel that calibrates rocprof counters
+    csrc = [torch.cat([a.reshape(-1), b.reshape(-1)]) for a, b in ins]
+    cdst = [torch.empty_like(csrc[0]) for _ in range(sets)]
+    for k in range(warmup):
+        cdst[k % sets].copy_(csrc[k % sets])
+    torch.cuda.synchronize()
+    reps = max(20, min(2 * steps, 400))
+    ev0.record()
+    for k in range(reps):
+        cdst[k % sets].copy_(csrc[(k + 3) % sets])
+    ev1.record()
+    torch.cuda.synchronize()
+    t_copy = ev0.elapsed_time(ev1) * 1e-3 / reps
+    del csrc, cdst
+
     flops_step = 2 * flops_fft(n, batch)
     bytes_launch = 2 * 2 * plane  # read re+im, write re+im
     return {
+        "t_copy_s": t_copy,
         "wall_s": wall,
         "ms_per_step": wall / steps * 1e3,
         "value": flops_step * steps / wall / 1e9,
@@ -318,8 +340,10 @@ def main(argv=None):
             "frac": round(achieved / HBM_PEAK, 4),
             "traffic": _traffic_from_profiles("c2c_lds_n1024"),
             "t_launch_us": round(head["t_launch_s"] * 1e6, 3),
-            "t_launch_median_us": round(head["t_launch_median_s"] * 1e6, 3),
+            "t_launch_isolated_median_us": round(head["t_launch_median_s"] * 1e6, 3),
             "bytes_per_launch": head["bytes_launch"],
+            "copy_gbps": round(head["bytes_launch"] / head["t_copy_s"] / 1e9, 1),
+            "frac_of_copy": round(head["t_copy_s"] / head["t_launch_s"], 4),
         },
     }
     if not args.no_secondary:

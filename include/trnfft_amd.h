@@ -36,6 +36,7 @@ typedef void* tfa_stream; /* hipStream_t; NULL = the null stream */
 #define TFA_KIND_BLUESTEIN 1 /* any n >= 2, chirp-z over a power-of-two m >= 2n-1            */
 #define TFA_KIND_DFT_GEMM 2  /* n <= 256, X = x @ W on the matrix cores                      */
 #define TFA_KIND_STFT 3      /* framed, windowed onesided/twosided transform of real signals */
+#define TFA_KIND_FFT2 4      /* 2-D transform over the last two axes (n = last, n2 = second to last) */
 
 /* STFT flags. */
 #define TFA_STFT_CENTER 1     /* reflect-pad n_fft/2 on both sides (pad_mode="reflect") */
@@ -49,6 +50,7 @@ typedef struct tfa_plan_desc {
   int64_t hop;     /* STFT only: hop_length */
   int32_t flags;   /* STFT only: TFA_STFT_* */
   int32_t reserved;
+  int64_t n2;      /* FFT2 only: length of the second-to-last axis */
 } tfa_plan_desc;
 
 /*
@@ -74,9 +76,21 @@ int64_t tfa_plan_padded_n(const tfa_plan* plan);
  * Out-of-place, or in place with out_* == in_*.  Replaces trnfft/fft_core.py:22-50 (fft_core),
  * which dispatches to _cooley_tukey (:53-117, power-of-two n), _bluestein (:1285-1376, other n)
  * and, for TFA_KIND_DFT_GEMM plans, _fft_via_gemm (:221-251).
+ * TFA_KIND_FFT2 plans: `batch` arrays of (n2, n) each, transformed over both axes (x 1/(n n2)
+ * when inverse), power-of-two 16 <= n <= 2048 and 16 <= n2 <= 4096, output must not alias the
+ * input; replaces trnfft/api.py:105-139 (fft2 -> fftn over (-2, -1)).
  */
 int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const float* in_im,
                 float* out_re, float* out_im, void* workspace, tfa_stream stream);
+
+/*
+ * Batched 1-D transform along a strided axis, in place allowed: data viewed as (outer, n, stride)
+ * row-major, each of the outer*stride columns transformed along its n elements (element stride
+ * `stride`).  TFA_KIND_C2C plans with n <= 4096 only.  Replaces the transpose-copy + contiguous
+ * FFT + transpose-back of trnfft/api.py:496-516 (_fft_along_dim) used by fft2/fftn/ifftn.
+ */
+int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, const float* in_re,
+                        const float* in_im, float* out_re, float* out_im, tfa_stream stream);
 
 /*
  * Short-time Fourier transform of `batch` real signals of `num_samples` samples each.  Frames

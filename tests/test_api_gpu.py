@@ -116,3 +116,55 @@ def test_stft_single_tone():
     res = trnfft_amd.stft(s.cuda(), n_fft=n_fft, hop_length=64, center=False)
     peak = res.abs().mean(dim=-1).argmax().item()
     assert abs(peak - int(freq * n_fft / sr)) <= 1
+
+
+@pytest.mark.parametrize("shape,dim", [
+    ((6, 16, 12), None),        # 12 is not a power of two: transpose + Bluestein path on that axis
+    ((3, 40, 8), (0, 1)),       # ragged column tiles (stride 8 < tile width)
+    ((5, 128, 3), (1,)),        # stride 3
+    ((2, 4096, 17), (1,)),      # longest strided axis
+    ((4, 8, 2, 16), (0, 2)),
+])
+def test_fftn_strided_axes_vs_oracle(shape, dim):
+    rng = np.random.default_rng(7)
+    re = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
+    im = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
+    got = trnfft_amd.fftn(ComplexTensor(re.cuda(), im.cuda()), dim=dim)
+    ref = oracle.fftn((re, im), dim=dim)
+    dims = range(len(shape)) if dim is None else dim
+    total = 1
+    for d in dims:
+        total *= shape[d]
+    assert rel_l2(got.real, got.imag, *ref) <= 1e-5 * math.log2(total)
+    back = trnfft_amd.ifftn(got, dim=dim)
+    assert rel_l2(back.real, back.imag, re, im) <= 1e-5 * math.log2(total)
+
+
+@pytest.mark.parametrize("n_fft,hop,length,batch_shape", [
+    (16, 4, 301, (2,)),
+    (4096, 1024, 20000, (1,)),
+    (512, 200, 9999, (2, 3)),
+    (1024, 256, 5000, ()),
+])
+def test_stft_edge_shapes(n_fft, hop, length, batch_shape):
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(*batch_shape, length, generator=g)
+    got = trnfft_amd.stft(x.cuda(), n_fft=n_fft, hop_length=hop)
+    ref = oracle.stft(x, n_fft=n_fft, hop_length=hop)
+    assert got.shape == ref[0].shape
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(n_fft)
+
+
+@pytest.mark.parametrize("shape", [(2, 16, 16), (1, 4096, 16), (3, 16, 2048), (2, 512, 1024), (1, 128, 64)])
+def test_fft2_two_pass_complex_and_inverse(shape):
+    rng = np.random.default_rng(11)
+    re = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
+    im = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
+    got = trnfft_amd.fft2(ComplexTensor(re.cuda(), im.cuda()))
+    ref = oracle.fft2((re, im))
+    n = shape[-1] * shape[-2]
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(n)
+    back = trnfft_amd.ifftn(got, dim=(-2, -1))
+    ref_back = oracle.ifftn(ref, dim=(-2, -1))
+    assert rel_l2(back.real, back.imag, *ref_back) <= tol_pow2(n)
+    assert rel_l2(back.real, back.imag, re, im) <= 2 * tol_pow2(n)

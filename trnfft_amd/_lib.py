@@ -21,6 +21,7 @@ KIND_C2C = 0
 KIND_BLUESTEIN = 1
 KIND_DFT_GEMM = 2
 KIND_STFT = 3
+KIND_FFT2 = 4
 
 STFT_CENTER = 1
 STFT_NORMALIZED = 2
@@ -33,6 +34,7 @@ EXPORTS = (
     "tfa_plan_workspace_size",
     "tfa_plan_padded_n",
     "tfa_execute",
+    "tfa_execute_strided",
     "tfa_stft_frames",
     "tfa_stft_execute",
     "tfa_complex_gemm",
@@ -49,6 +51,7 @@ class PlanDesc(ctypes.Structure):
         ("hop", ctypes.c_int64),
         ("flags", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+        ("n2", ctypes.c_int64),
     ]
 
 
@@ -70,6 +73,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tfa_plan_padded_n.restype = _i64
     lib.tfa_execute.argtypes = [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.tfa_execute.restype = ctypes.c_int
+    lib.tfa_execute_strided.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp]
+    lib.tfa_execute_strided.restype = ctypes.c_int
     lib.tfa_stft_frames.argtypes = [_vp, _i64, ctypes.POINTER(_i64)]
     lib.tfa_stft_frames.restype = ctypes.c_int
     lib.tfa_stft_execute.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp]

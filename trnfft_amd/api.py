@@ -14,7 +14,7 @@ import torch
 from . import _lib
 from .complex import ComplexTensor
 from .dispatch import _require_hip, ptr, stream_handle, target_device, to_device_f32
-from .fft_core import execute_1d, fft_core
+from .fft_core import execute_1d, execute_fft2, execute_strided, fft2_ok, fft_core, strided_ok
 from .plan import native_plan
 from .precision import _resolve
 
@@ -137,7 +137,21 @@ def _fftn(input, s, dim, inverse: bool) -> ComplexTensor:
     if s is not None:
         for size, d in zip(s, dim):
             x = _resize_dim_real(x, d, size) if real_in else _resize_dim(x, d, size)
-    for d in dim:
+    if ndim >= 2 and sorted(dim) == [ndim - 2, ndim - 1] and fft2_ok(x.shape[-2], x.shape[-1]):
+        # both trailing axes at once: the two-pass 2-D kernels (the 1-D transforms of the two
+        # axes commute; only rounding differs from the reference's dim -2 then dim -1 order)
+        _resolve(None)
+        _require_hip("fft2")
+        if real_in:
+            return execute_fft2(x.contiguous(), None, inverse)
+        return execute_fft2(x.real, x.imag, inverse)
+    order = list(dim)
+    if real_in and (ndim - 1) in order:
+        # real input: transform the contiguous last axis first (it reads only the real plane);
+        # the axes' 1-D transforms commute, so only rounding differs from the given order
+        order.remove(ndim - 1)
+        order.insert(0, ndim - 1)
+    for d in order:
         x = _fft_along_dim(x, d, inverse=inverse)
     return x
 
@@ -268,6 +282,10 @@ def stft(
             plan.handle, batch, length, ptr(x), ptr(win), ptr(out_re), ptr(out_im), stream_handle(dev)
         )
     _lib.check(rc, "tfa_stft_execute")
+    if center and x.dim() == 2 and x.shape[0] == 1:
+        # the reference squeezes a (1, L) signal to 1-D after padding (trnfft/api.py:313-315),
+        # so its result has no batch axis; keep that shape for drop-in compatibility
+        out_re, out_im = out_re[0], out_im[0]
     out = ComplexTensor._wrap(out_re, out_im)
     return out if out_dev == dev else out.to(out_dev)
 
@@ -383,14 +401,30 @@ def _resize_dim_real(x: torch.Tensor, dim: int, n: int) -> torch.Tensor:
 
 
 def _fft_along_dim(x, dim: int, inverse: bool) -> ComplexTensor:
-    """1-D FFT along `dim` of a ComplexTensor or real tensor (trnfft/api.py:496-516)."""
+    """1-D FFT along `dim` of a ComplexTensor or real tensor (trnfft/api.py:496-516).
+
+    The last axis runs the contiguous kernels; another power-of-two axis (n <= 4096) runs the
+    strided kernel in place of the reference's transpose / FFT / transpose-back copies; other
+    lengths along a non-last axis keep the transpose round trip.
+    """
     real_in = _is_real_tensor(x)
-    ndim = x.dim() if real_in else len(x.shape)
+    shape = tuple(x.shape)
+    ndim = len(shape)
     dim = dim % ndim
+    n = shape[dim]
     if dim == ndim - 1:
         if real_in:
             return _real_1d(x, inverse)
         return fft_core(x, inverse=inverse)
+    stride = 1
+    for s_ in shape[dim + 1 :]:
+        stride *= s_
+    if strided_ok(n, stride):
+        _resolve(None)
+        _require_hip("fftn")
+        if real_in:
+            return execute_strided(x.contiguous(), None, dim, inverse)
+        return execute_strided(x.real, x.imag, dim, inverse)
     if real_in:
         moved = x.transpose(dim, -1).contiguous()
         res = _real_1d(moved, inverse)

@@ -190,7 +190,9 @@ __device__ __forceinline__ void exchange_sync() {
 //   v:    registers, x[tid + T*e] on entry, X[tid + T*e] on exit
 //   lre/lim: this transform's LDS scratch, lds_pad(N) floats each
 //   tw:   the plan's twiddle table for (N, E, DIR) (layout from make_shape)
-template <int N, int E, int DIR, bool WAVE_LOCAL>
+// SPLIT: exchange the real and imaginary planes one after the other through `lre` alone (lim
+// unused): half the LDS per transform, twice the synchronisations.
+template <int N, int E, int DIR, bool WAVE_LOCAL, bool SPLIT = false>
 struct LdsFft {
   static constexpr LdsShape S = make_shape(N, E);
   static constexpr int T = N / E;
@@ -203,45 +205,106 @@ struct LdsFft {
       constexpr int NB = E / R;
       constexpr int LS = S.ls[P];
       constexpr bool LAST = (P == S.npass - 1);
+      // the pass's LDS write index is linear in u when the radix (first pass) or the span LS
+      // (later passes) is a multiple of the 16-word padding period
+      constexpr bool LIN_W = (LS == 1) ? (R % 16 == 0) : (LS % 16 == 0);
+      float2 w[NB][R];
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const int j = tid + b * T;
         const int k = j & (LS - 1);
-        float2 w[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) w[r] = v[b + r * NB];
+        for (int r = 0; r < R; ++r) w[b][r] = v[b + r * NB];
         if constexpr (P > 0) {
           const float4* t4 = reinterpret_cast<const float4*>(tw + S.twoff[P] + k * R);
 #pragma unroll
           for (int r2 = 0; r2 < R / 2; ++r2) {
             float4 q = t4[r2];
-            if (r2 > 0) w[2 * r2] = cmul(w[2 * r2], make_float2(q.x, q.y));
-            w[2 * r2 + 1] = cmul(w[2 * r2 + 1], make_float2(q.z, q.w));
+            if (r2 > 0) w[b][2 * r2] = cmul(w[b][2 * r2], make_float2(q.x, q.y));
+            w[b][2 * r2 + 1] = cmul(w[b][2 * r2 + 1], make_float2(q.z, q.w));
           }
         }
-        Dft<R, DIR>::run(w);
+        Dft<R, DIR>::run(w[b]);
         if constexpr (LAST) {
 #pragma unroll
-          for (int u = 0; u < R; ++u) v[b + u * NB] = w[u];
-        } else {
-          const int base = (j - k) * R + k;
-#pragma unroll
-          for (int u = 0; u < R; ++u) {
-            const int idx = lds_pad(base + u * LS);
-            lre[idx] = w[u].x;
-            lim[idx] = w[u].y;
-          }
+          for (int u = 0; u < R; ++u) v[b + u * NB] = w[b][u];
+        } else if constexpr (!SPLIT) {
+          store_pass<R, LS, LIN_W>(w[b], lre, lim, j, k, 2);
         }
       }
       if constexpr (!LAST) {
-        exchange_sync<WAVE_LOCAL>();
+        if constexpr (!SPLIT) {
+          exchange_sync<WAVE_LOCAL>();
+          load_pass(v, lre, lim, tid, 2);
+          exchange_sync<WAVE_LOCAL>();
+        } else {
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-          const int idx = lds_pad(tid + T * e);
-          v[e] = make_float2(lre[idx], lim[idx]);
+          for (int plane = 0; plane < 2; ++plane) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+              const int j = tid + b * T;
+              store_pass<R, LS, LIN_W>(w[b], lre, lre, j, j & (LS - 1), plane);
+            }
+            exchange_sync<WAVE_LOCAL>();
+            load_pass(v, lre, lre, tid, plane);
+            exchange_sync<WAVE_LOCAL>();
+          }
         }
-        exchange_sync<WAVE_LOCAL>();
         pass<P + 1>(v, lre, lim, tw, tid);
+      }
+    }
+  }
+
+  // which: 0 = real plane into a, 1 = imaginary plane into a, 2 = real into a and imag into b
+  template <int R, int LS, bool LIN_W>
+  __device__ __forceinline__ static void store_pass(const float2 (&w)[R], float* a, float* b, int j, int k,
+                                                    int which) {
+    if constexpr (LIN_W) {
+      // padded index = base + compile-time offset per u (immediate-offset LDS stores)
+      const int base = LS == 1 ? j * (R + R / 16) : lds_pad((j - k) * R) + k + (k >> 4);
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        const int off = LS == 1 ? u + (u >> 4) : u * (LS + LS / 16);
+        if (which == 2) {
+          a[base + off] = w[u].x;
+          b[base + off] = w[u].y;
+        } else {
+          a[base + off] = which ? w[u].y : w[u].x;
+        }
+      }
+    } else {
+      const int base = (j - k) * R + k;
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        const int idx = lds_pad(base + u * LS);
+        if (which == 2) {
+          a[idx] = w[u].x;
+          b[idx] = w[u].y;
+        } else {
+          a[idx] = which ? w[u].y : w[u].x;
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ static void load_pass(float2 (&v)[E], const float* a, const float* b, int tid,
+                                                   int which) {
+    if constexpr (T % 16 == 0) {
+      const int rb = tid + (tid >> 4);
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int idx = rb + e * (T + T / 16);
+        if (which == 2) v[e] = make_float2(a[idx], b[idx]);
+        else if (which == 0) v[e].x = a[idx];
+        else v[e].y = a[idx];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int idx = lds_pad(tid + T * e);
+        if (which == 2) v[e] = make_float2(a[idx], b[idx]);
+        else if (which == 0) v[e].x = a[idx];
+        else v[e].y = a[idx];
       }
     }
   }

@@ -14,9 +14,12 @@ __host__ __device__ constexpr int ilog2(long long n) {
 }
 
 // Complex elements each thread keeps in registers for a length-N transform.  A transform of
-// length N is handled by T = N / E threads; every pass but the last is radix E.
+// length N is handled by T = N / E threads; every pass but the last is radix E.  The choice per N
+// comes from a launch-shape sweep of the batched kernel on MI355X (64 MiB per launch, buffers
+// rotated past the Infinity Cache): 512 and 4096 are fastest at E = 32 (2 passes for 512),
+// the other lengths at E = 16 (1024 = 16*16*4, 2048 = 16*16*8, 4 or 2 transforms per block).
 __host__ __device__ constexpr int lds_epth(int n) {
-  return n <= 16 ? n : (n == 32 || n == 64) ? 8 : 16;
+  return n <= 16 ? n : (n == 32 || n == 64) ? 8 : (n == 512 || n == 4096) ? 32 : 16;
 }
 
 struct LdsShape {

@@ -18,6 +18,11 @@ __device__ __forceinline__ long long xcd_tile_remap(long long i, long long g) {
   return (i % 8) * per + i / 8;
 }
 
+// Streaming (non-temporal) global accesses: every element of a batched transform is read once
+// and written once, so it should not displace other lines in L2 / the Infinity Cache.
+__device__ __forceinline__ float ld_stream(const float* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st_stream(float* p, float v) { __builtin_nontemporal_store(v, p); }
+
 // Thread layout of the batched LDS kernels for transform length N: T threads per transform,
 // XF transforms per workgroup (at least 256 threads per workgroup), PADN LDS floats per plane
 // per transform (1 when the transform needs no exchange).
@@ -43,6 +48,25 @@ struct C2cArgs {
   hipStream_t stream;
 };
 hipError_t launch_c2c_lds(int n, const C2cArgs& a);
+
+struct StridedArgs {
+  const float* in_re;
+  const float* in_im;  // nullptr: real input
+  float* out_re;       // may equal in_re (in place)
+  float* out_im;
+  const float2* tw;     // LDS-FFT table for length n1
+  const float2* tw_lo;  // four-step twiddle tables (TWIDDLE only)
+  const float2* tw_hi;
+  long long outer;   // independent (n1 x stride) blocks
+  long long stride;  // element stride of the transformed axis = number of columns
+  int lo_bits;
+  unsigned nmask;  // (n1 * n2) - 1 for the four-step twiddle
+  float scale;     // applied when !twiddle
+  int dir;
+  bool twiddle;
+  hipStream_t stream;
+};
+hipError_t launch_strided(int n1, const StridedArgs& a);
 
 struct FourStepArgs {
   const float* in_re;
@@ -94,5 +118,39 @@ struct StftArgs {
   hipStream_t stream;
 };
 hipError_t launch_stft(int n_fft, const StftArgs& a);
+
+struct Fft2Args {
+  const float* in_re;
+  const float* in_im;  // nullptr: real input
+  float* out_re;       // must not alias the input
+  float* out_im;
+  const float2* tw_w;   // LDS-FFT table for length w
+  const float2* tw_hr;  // LDS-FFT table for length h/8
+  const float2* tw_h;   // W_h^i, i < h
+  long long batch, h, w;
+  float scale;  // applied in pass 2 (1/(h*w) for the inverse)
+  int dir;
+  hipStream_t stream;
+};
+hipError_t launch_fft2(const Fft2Args& a);
+
+struct GemmArgs {
+  long long m, n, k;
+  const float* a_re;
+  const float* a_im;
+  long long lda;
+  const float* b_re;
+  const float* b_im;
+  long long ldb;
+  int b_trans;
+  const float* bias_re;  // nullable
+  const float* bias_im;
+  float* c_re;
+  float* c_im;
+  long long ldc;
+  float alpha;
+  hipStream_t stream;
+};
+hipError_t launch_cgemm(const GemmArgs& a);
 
 }  // namespace tfa

@@ -3,8 +3,11 @@
 //  * c2c_lds_kernel: one launch per batch; each transform of length N <= 16384 stays in
 //    registers + LDS for all its passes (replaces the reference's per-stage launches,
 //    trnfft/fft_core.py:53-117 on CPU and :1063-1238 on the NKI path).
-//  * fourstep_col_kernel / fourstep_row_kernel: N = N1*N2 > 16384 in two HBM passes
-//    (column FFTs with the W_N^{n2*k1} twiddle fused into their store, then row FFTs whose
+//  * strided_kernel: transform along a non-contiguous axis (element stride S), C adjacent
+//    columns per workgroup; replaces the transpose copies of trnfft/api.py:496-516 for fftn/fft2
+//    and is the column pass of the four-step path.
+//  * four-step (strided_kernel with twiddle + fourstep_row_kernel): N = N1*N2 > 16384 in two HBM
+//    passes (column FFTs with the W_N^{n2*k1} twiddle fused into their store, then row FFTs whose
 //    output is transposed through LDS so the strided store stays coalesced).  This is the
 //    single-GPU form of the reference's row-column decomposition, trnfft/nki/multicore.py:151-219.
 #include "kernels.h"
@@ -14,26 +17,35 @@ namespace tfa {
 // ---------------------------------------------------------------------------------------------
 // LDS-resident batched transform
 // ---------------------------------------------------------------------------------------------
-template <int N, int DIR, bool REAL_IN>
+// TAIL = false: every transform slot of the grid is inside the batch (no guards at all; the
+// guard-free instruction stream measured fastest).  TAIL = true: one workgroup for the ragged
+// remainder, slots past the batch end neither load nor store.
+template <int N, int DIR, bool REAL_IN, bool TAIL>
 __global__ __launch_bounds__(C2cThreads<N>::THREADS) void c2c_lds_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re,
-    float* out_im, const float2* __restrict__ tw, long long batch, float scale) {
+    float* out_im, const float2* __restrict__ tw, long long first, long long batch, float scale) {
   using C = C2cThreads<N>;
   constexpr int E = C::E, T = C::T;
   __shared__ float lre[C::XF * C::PADN];
   __shared__ float lim[C::XF * C::PADN];
   const int tid = threadIdx.x & (T - 1);
   const int xf = threadIdx.x / T;
-  const long long b = (long long)blockIdx.x * C::XF + xf;
-  const bool valid = b < batch;
+  const long long b = first + (long long)blockIdx.x * C::XF + xf;
+  const bool valid = !TAIL || b < batch;
   const size_t base = (size_t)b * N;
-
+  // one base pointer per plane; element e is at a compile-time offset T*e (immediate offsets)
+  const float* pr = in_re + base + tid;
+  const float* pi = REAL_IN ? nullptr : in_im + base + tid;
+  // inverse: the 1/n factor is applied to the input (exact for power-of-two n), keeping the
+  // store sequence free of multiplies
+  const float sc = DIR < 0 ? 1.0f : scale;
   float2 v[E];
   if (valid) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const size_t i = base + tid + T * e;
-      v[e] = make_float2(in_re[i], REAL_IN ? 0.0f : in_im[i]);
+      const float xr = ld_stream(pr + T * e);
+      const float xi = REAL_IN ? 0.0f : ld_stream(pi + T * e);
+      v[e] = DIR < 0 ? make_float2(xr, xi) : make_float2(xr * sc, xi * sc);
     }
   } else {
 #pragma unroll
@@ -41,11 +53,12 @@ __global__ __launch_bounds__(C2cThreads<N>::THREADS) void c2c_lds_kernel(
   }
   LdsFft<N, E, DIR, (T <= 64)>::run(v, lre + xf * C::PADN, lim + xf * C::PADN, tw, tid);
   if (valid) {
+    float* qr = out_re + base + tid;
+    float* qi = out_im + base + tid;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const size_t i = base + tid + T * e;
-      out_re[i] = v[e].x * scale;
-      out_im[i] = v[e].y * scale;
+      st_stream(qr + T * e, v[e].x);
+      st_stream(qi + T * e, v[e].y);
     }
   }
 }
@@ -53,9 +66,13 @@ __global__ __launch_bounds__(C2cThreads<N>::THREADS) void c2c_lds_kernel(
 template <int N, int DIR, bool REAL_IN>
 static hipError_t launch_c2c_lds_t(const C2cArgs& a) {
   using C = C2cThreads<N>;
-  const long long blocks = (a.batch + C::XF - 1) / C::XF;
-  hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN>), dim3((unsigned)blocks), dim3(C::THREADS),
-                     0, a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.batch, a.scale);
+  const long long full = a.batch / C::XF;
+  if (full > 0)
+    hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN, false>), dim3((unsigned)full), dim3(C::THREADS), 0,
+                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, 0LL, a.batch, a.scale);
+  if (full * C::XF < a.batch)
+    hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN, true>), dim3(1), dim3(C::THREADS), 0, a.stream, a.in_re,
+                       a.in_im, a.out_re, a.out_im, a.tw, full * C::XF, a.batch, a.scale);
   return hipGetLastError();
 }
 
@@ -99,46 +116,50 @@ __host__ __device__ constexpr int fourstep_tile(int l) {
   return c;
 }
 
-// Column pass: FFT over n1 of each column n2 (stride N2), times W_N^{n2*k1}, stored in place
-// layout tmp[k1*N2 + n2].  One workgroup = C adjacent columns of one batch entry.
-template <int N1, int DIR, bool REAL_IN>
-__global__ __launch_bounds__(fourstep_tile(N1) * (N1 / lds_epth(N1))) void fourstep_col_kernel(
-    const float* __restrict__ in_re, const float* __restrict__ in_im, float* __restrict__ t_re,
-    float* __restrict__ t_im, const float2* __restrict__ tw, const float2* __restrict__ tw_lo,
-    const float2* __restrict__ tw_hi, int n2_len, int lo_bits, long long batch) {
+// Strided-axis transform: x viewed as (outer, N1, S) row-major; transform along the N1 axis
+// (element stride S) for every (outer, column) pair.  One workgroup = C adjacent columns of one
+// outer block, so each load/store instruction covers C consecutive floats.  With TWIDDLE the
+// result k1 of column c is multiplied by W_Ntot^(c*k1) (the four-step column pass, with S = N2).
+template <int N1, int DIR, bool REAL_IN, bool TWIDDLE>
+__global__ __launch_bounds__(fourstep_tile(N1) * (N1 / lds_epth(N1))) void strided_kernel(
+    const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re, float* out_im,
+    const float2* __restrict__ tw, const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi,
+    long long stride, int tiles_per_block, int lo_bits, unsigned nmask, float scale) {
   constexpr int E = lds_epth(N1), T = N1 / E, C = fourstep_tile(N1);
   constexpr int PADN = lds_pad(N1) + 1;
   __shared__ float lre[C * PADN];
   __shared__ float lim[C * PADN];
   const int c = threadIdx.x % C;  // column within tile (fast across lanes: coalesced)
   const int t = threadIdx.x / C;
-  const int tiles_per_row = n2_len / C;
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
-  const long long b = tile / tiles_per_row;
-  const int n2 = (int)(tile % tiles_per_row) * C + c;
-  const size_t N = (size_t)N1 * n2_len;
-  const size_t base = (size_t)b * N + n2;
+  const long long b = tile / tiles_per_block;
+  const long long col = (tile % tiles_per_block) * C + c;
+  const bool valid = col < stride;
+  const size_t base = (size_t)b * N1 * stride + col;
 
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const size_t i = base + (size_t)(t + T * e) * n2_len;
-    v[e] = make_float2(in_re[i], REAL_IN ? 0.0f : in_im[i]);
+    const size_t i = base + (size_t)(t + T * e) * stride;
+    v[e] = valid ? make_float2(ld_stream(in_re + i), REAL_IN ? 0.0f : ld_stream(in_im + i)) : make_float2(0.0f, 0.0f);
   }
   LdsFft<N1, E, DIR, false>::run(v, lre + c * PADN, lim + c * PADN, tw, t);
-  const unsigned nmask = (unsigned)(N - 1);
+  if (!valid) return;
   const unsigned lomask = (1u << lo_bits) - 1;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int k1 = t + T * e;
-    const unsigned m = ((unsigned)n2 * (unsigned)k1) & nmask;
-    const float2 w = cmul(tw_lo[m & lomask], tw_hi[m >> lo_bits]);
-    const float2 y = cmul(v[e], w);
-    const size_t i = base + (size_t)k1 * n2_len;
-    t_re[i] = y.x;
-    t_im[i] = y.y;
+    float2 y = v[e];
+    if constexpr (TWIDDLE) {
+      const unsigned m = ((unsigned)col * (unsigned)k1) & nmask;
+      y = cmul(y, cmul(tw_lo[m & lomask], tw_hi[m >> lo_bits]));
+    } else {
+      y = cscale(y, scale);
+    }
+    const size_t i = base + (size_t)k1 * stride;
+    st_stream(out_re + i, y.x);
+    st_stream(out_im + i, y.y);
   }
-  (void)batch;
 }
 
 // Row pass: FFT over n2 of each row k1 of tmp (contiguous), output X[k1 + N1*k2] for C
@@ -192,20 +213,44 @@ __global__ __launch_bounds__(fourstep_tile(N2) * (N2 / lds_epth(N2))) void fours
   (void)batch;
 }
 
-template <int N1, int DIR>
-static hipError_t launch_col_t(const FourStepArgs& a, bool real_in) {
+template <int N1, int DIR, bool TWIDDLE>
+static hipError_t launch_strided_t(const StridedArgs& a) {
   constexpr int C = fourstep_tile(N1), T = N1 / lds_epth(N1);
-  if (a.n2 % C) return hipErrorInvalidValue;
-  const long long blocks = a.batch * (a.n2 / C);
-  if (real_in)
-    hipLaunchKernelGGL((fourstep_col_kernel<N1, DIR, true>), dim3((unsigned)blocks), dim3(C * T), 0,
-                       a.stream, a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, a.n2,
-                       a.lo_bits, a.batch);
+  const long long tiles = (a.stride + C - 1) / C;
+  const long long blocks = a.outer * tiles;
+  if (a.in_im == nullptr)
+    hipLaunchKernelGGL((strided_kernel<N1, DIR, true, TWIDDLE>), dim3((unsigned)blocks), dim3(C * T), 0,
+                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.tw_lo, a.tw_hi, a.stride,
+                       (int)tiles, a.lo_bits, a.nmask, a.scale);
   else
-    hipLaunchKernelGGL((fourstep_col_kernel<N1, DIR, false>), dim3((unsigned)blocks), dim3(C * T), 0,
-                       a.stream, a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, a.n2,
-                       a.lo_bits, a.batch);
+    hipLaunchKernelGGL((strided_kernel<N1, DIR, false, TWIDDLE>), dim3((unsigned)blocks), dim3(C * T), 0,
+                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.tw_lo, a.tw_hi, a.stride,
+                       (int)tiles, a.lo_bits, a.nmask, a.scale);
   return hipGetLastError();
+}
+
+template <int DIR, bool TWIDDLE>
+static hipError_t launch_strided_dir(int n1, const StridedArgs& a) {
+  switch (n1) {
+    case 2: return launch_strided_t<2, DIR, TWIDDLE>(a);
+    case 4: return launch_strided_t<4, DIR, TWIDDLE>(a);
+    case 8: return launch_strided_t<8, DIR, TWIDDLE>(a);
+    case 16: return launch_strided_t<16, DIR, TWIDDLE>(a);
+    case 32: return launch_strided_t<32, DIR, TWIDDLE>(a);
+    case 64: return launch_strided_t<64, DIR, TWIDDLE>(a);
+    case 128: return launch_strided_t<128, DIR, TWIDDLE>(a);
+    case 256: return launch_strided_t<256, DIR, TWIDDLE>(a);
+    case 512: return launch_strided_t<512, DIR, TWIDDLE>(a);
+    case 1024: return launch_strided_t<1024, DIR, TWIDDLE>(a);
+    case 2048: return launch_strided_t<2048, DIR, TWIDDLE>(a);
+    case 4096: return launch_strided_t<4096, DIR, TWIDDLE>(a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_strided(int n1, const StridedArgs& a) {
+  if (a.dir < 0) return a.twiddle ? launch_strided_dir<-1, true>(n1, a) : launch_strided_dir<-1, false>(n1, a);
+  return a.twiddle ? launch_strided_dir<1, true>(n1, a) : launch_strided_dir<1, false>(n1, a);
 }
 
 template <int N2, int DIR>
@@ -216,20 +261,6 @@ static hipError_t launch_row_t(const FourStepArgs& a) {
   hipLaunchKernelGGL((fourstep_row_kernel<N2, DIR>), dim3((unsigned)blocks), dim3(C * T), 0,
                      a.stream, a.t_re, a.t_im, a.out_re, a.out_im, a.tw2, a.n1, a.batch, a.scale);
   return hipGetLastError();
-}
-
-template <int DIR>
-static hipError_t launch_col_dir(const FourStepArgs& a, bool real_in) {
-  switch (a.n1) {
-    case 64: return launch_col_t<64, DIR>(a, real_in);
-    case 128: return launch_col_t<128, DIR>(a, real_in);
-    case 256: return launch_col_t<256, DIR>(a, real_in);
-    case 512: return launch_col_t<512, DIR>(a, real_in);
-    case 1024: return launch_col_t<1024, DIR>(a, real_in);
-    case 2048: return launch_col_t<2048, DIR>(a, real_in);
-    case 4096: return launch_col_t<4096, DIR>(a, real_in);
-    default: return hipErrorInvalidValue;
-  }
 }
 
 template <int DIR>
@@ -247,8 +278,9 @@ static hipError_t launch_row_dir(const FourStepArgs& a) {
 }
 
 hipError_t launch_fourstep(const FourStepArgs& a) {
-  const bool real_in = a.in_im == nullptr;
-  hipError_t e = a.dir < 0 ? launch_col_dir<-1>(a, real_in) : launch_col_dir<1>(a, real_in);
+  StridedArgs col{a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, a.batch, a.n2,
+                  a.lo_bits, (unsigned)((long long)a.n1 * a.n2 - 1), 1.0f, a.dir, true, a.stream};
+  hipError_t e = launch_strided(a.n1, col);
   if (e != hipSuccess) return e;
   return a.dir < 0 ? launch_row_dir<-1>(a) : launch_row_dir<1>(a);
 }

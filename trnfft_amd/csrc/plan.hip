@@ -76,6 +76,8 @@ struct tfa_plan {
   bool blue_fused = false;
   float2* chirp = nullptr;
   float2* hs = nullptr;
+  C2cTables col;          // FFT2: LDS table for n2/8 (pass 2)
+  float2* tw_h = nullptr;  // FFT2: W_{n2}^i, i < n2
   float* w_re = nullptr;  // DFT-GEMM matrix
   float* w_im = nullptr;
   std::vector<void*> allocs;
@@ -260,9 +262,37 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       }
       rc = p->build_c2c(n, -1, &p->fwd);
       break;
-    case TFA_KIND_DFT_GEMM:
-      rc = fail(TFA_ERR_UNSUPPORTED, "plan kind not implemented yet");
+    case TFA_KIND_FFT2: {
+      const int64_t h = desc->n2;
+      if (!is_pow2(n) || n < 16 || n > 2048 || !is_pow2(h) || h < 16 || h > 4096) {
+        rc = fail(TFA_ERR_UNSUPPORTED, "FFT2 plans need power-of-two 16 <= n <= 2048 and 16 <= n2 <= 4096");
+        break;
+      }
+      if ((rc = p->build_c2c(n, dir, &p->fwd))) break;
+      if ((rc = p->build_c2c(h / 8, dir, &p->col))) break;
+      std::vector<float2> th((size_t)h);
+      for (int64_t i = 0; i < h; ++i) th[(size_t)i] = unit_root(i, h, dir);
+      rc = p->upload(th, &p->tw_h);
       break;
+    }
+    case TFA_KIND_DFT_GEMM: {
+      if (n > 4096) {
+        rc = fail(TFA_ERR_UNSUPPORTED, "DFT-GEMM plans are limited to n <= 4096");
+        break;
+      }
+      // exact DFT matrix: phase (k*j mod n) in integers, angle in fp64 (the reference builds
+      // it from an fp32 angle, trnfft/fft_core.py:239-243, which costs ~2e-5 relative at n=256)
+      std::vector<float> wr((size_t)(n * n)), wi((size_t)(n * n));
+      for (int64_t k = 0; k < n; ++k)
+        for (int64_t j = 0; j < n; ++j) {
+          const float2 w = unit_root((k * j) % n, n, dir);
+          wr[(size_t)(k * n + j)] = w.x;
+          wi[(size_t)(k * n + j)] = w.y;
+        }
+      if ((rc = p->upload(wr, &p->w_re))) break;
+      rc = p->upload(wi, &p->w_im);
+      break;
+    }
     default:
       rc = fail(TFA_ERR_INVALID, "unknown plan kind");
   }
@@ -332,9 +362,44 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
       if ((e = tfa::launch_bluestein_post(a, y_re, y_im)) != hipSuccess) return hip_fail(e, "bluestein post");
       return TFA_OK;
     }
+    case TFA_KIND_FFT2: {
+      if (in_re == out_re || (in_im && in_im == out_im)) return fail(TFA_ERR_INVALID, "FFT2 output must not alias the input");
+      const int64_t h = plan->d.n2;
+      const float s2 = plan->d.inverse ? (float)(1.0 / ((double)n * (double)h)) : 1.0f;
+      tfa::Fft2Args f{in_re, in_im, out_re, out_im, plan->fwd.tw, plan->col.tw, plan->tw_h, batch, h, n, s2, plan->fwd.dir, s};
+      hipError_t e = tfa::launch_fft2(f);
+      return e == hipSuccess ? TFA_OK : hip_fail(e, "fft2 launch");
+    }
+    case TFA_KIND_DFT_GEMM: {
+      if (!in_im) return fail(TFA_ERR_INVALID, "DFT-GEMM needs both input planes");
+      // X = x @ W (W symmetric, so x @ W^T), scaled 1/n when inverse
+      tfa::GemmArgs g{batch, n, n, in_re, in_im, n, plan->w_re, plan->w_im, n, 1, nullptr, nullptr,
+                      out_re, out_im, n, scale, s};
+      hipError_t e = tfa::launch_cgemm(g);
+      return e == hipSuccess ? TFA_OK : hip_fail(e, "dft-gemm launch");
+    }
     default:
       return fail(TFA_ERR_UNSUPPORTED, "plan kind not executable with tfa_execute");
   }
+}
+
+int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, const float* in_re,
+                        const float* in_im, float* out_re, float* out_im, tfa_stream stream) {
+  if (!plan) return fail(TFA_ERR_INVALID, "null plan");
+  if (outer < 0 || stride < 1) return fail(TFA_ERR_INVALID, "bad outer/stride");
+  if (plan->d.kind != TFA_KIND_C2C || plan->d.n > 4096 || plan->d.n < 2)
+    return fail(TFA_ERR_UNSUPPORTED, "strided transforms need a power-of-two C2C plan with 2 <= n <= 4096");
+  if (outer == 0) return TFA_OK;
+  if (!in_re || !out_re || !out_im) return fail(TFA_ERR_INVALID, "null data pointer");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
+    return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  const C2cTables& t = plan->d.inverse ? plan->inv : plan->fwd;
+  const float scale = plan->d.inverse ? (float)(1.0 / (double)plan->d.n) : 1.0f;
+  tfa::StridedArgs a{in_re, in_im, out_re, out_im, t.tw, nullptr, nullptr, outer, stride, 0, 0u, scale,
+                     t.dir, false, static_cast<hipStream_t>(stream)};
+  hipError_t e = tfa::launch_strided((int)plan->d.n, a);
+  return e == hipSuccess ? TFA_OK : hip_fail(e, "strided launch");
 }
 
 int tfa_stft_frames(const tfa_plan* plan, int64_t num_samples, int64_t* n_frames) {
@@ -375,9 +440,16 @@ int tfa_complex_gemm(int64_t m, int64_t n, int64_t k, const float* a_re, const f
                      int64_t lda, const float* b_re, const float* b_im, int64_t ldb, int32_t b_trans,
                      const float* bias_re, const float* bias_im, float* c_re, float* c_im,
                      int64_t ldc, tfa_stream stream) {
-  (void)m; (void)n; (void)k; (void)a_re; (void)a_im; (void)lda; (void)b_re; (void)b_im; (void)ldb;
-  (void)b_trans; (void)bias_re; (void)bias_im; (void)c_re; (void)c_im; (void)ldc; (void)stream;
-  return fail(TFA_ERR_UNSUPPORTED, "complex gemm not implemented yet");
+  if (m < 0 || n < 0 || k < 0) return fail(TFA_ERR_INVALID, "negative dimension");
+  if (m == 0 || n == 0) return TFA_OK;
+  if (!a_re || !a_im || !b_re || !b_im || !c_re || !c_im) return fail(TFA_ERR_INVALID, "null data pointer");
+  if ((bias_re == nullptr) != (bias_im == nullptr)) return fail(TFA_ERR_INVALID, "bias needs both planes or neither");
+  if (lda < k || ldc < n || ldb < (b_trans ? k : n)) return fail(TFA_ERR_INVALID, "leading dimension too small");
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return fail(TFA_ERR_UNSUPPORTED, "dimension above 2^31");
+  tfa::GemmArgs g{m, n, k, a_re, a_im, lda, b_re, b_im, ldb, b_trans ? 1 : 0, bias_re, bias_im,
+                  c_re, c_im, ldc, 1.0f, static_cast<hipStream_t>(stream)};
+  hipError_t e = tfa::launch_cgemm(g);
+  return e == hipSuccess ? TFA_OK : hip_fail(e, "complex gemm launch");
 }
 
 }  // extern "C"

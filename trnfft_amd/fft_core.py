@@ -78,6 +78,72 @@ def execute_1d(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> Comp
     return out if out_dev == dev else out.to(out_dev)
 
 
+# longest power-of-two axis the strided kernel transforms in place of a transpose round trip
+_STRIDED_MAX_N = 4096
+
+
+def execute_strided(re: torch.Tensor, im: torch.Tensor | None, dim: int, inverse: bool) -> ComplexTensor:
+    """Transform along a non-last axis `dim` without moving it (power-of-two n <= 4096).
+
+    The contiguous tensor is viewed as (outer, n, stride); every column is transformed along
+    its n elements by the strided kernel (replaces trnfft/api.py:496-516's transposes).
+    """
+    shape = re.shape
+    n = shape[dim]
+    dev = target_device(re, im)
+    out_dev = re.device
+    re = to_device_f32(re, dev)
+    im = to_device_f32(im, dev)
+    outer = 1
+    for s_ in shape[:dim]:
+        outer *= s_
+    stride = 1
+    for s_ in shape[dim + 1 :]:
+        stride *= s_
+    plan = native_plan(_lib.KIND_C2C, n, inverse, dev.index)
+    out_re = torch.empty_like(re)
+    out_im = torch.empty_like(re)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_execute_strided(
+            plan.handle, outer, stride, ptr(re), ptr(im), ptr(out_re), ptr(out_im), stream_handle(dev)
+        )
+    _lib.check(rc, "tfa_execute_strided")
+    out = ComplexTensor._wrap(out_re, out_im)
+    return out if out_dev == dev else out.to(out_dev)
+
+
+def fft2_ok(h: int, w: int) -> bool:
+    """Shapes the two-pass 2-D kernels take: power-of-two 16 <= w <= 2048, 16 <= h <= 4096."""
+    def p2(v):
+        return v > 0 and (v & (v - 1)) == 0
+
+    return p2(h) and p2(w) and 16 <= w <= 2048 and 16 <= h <= 4096
+
+
+def execute_fft2(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> ComplexTensor:
+    """2-D transform over the last two axes (two HBM passes; replaces trnfft/api.py:105-139)."""
+    h, w = re.shape[-2], re.shape[-1]
+    dev = target_device(re, im)
+    out_dev = re.device
+    re = to_device_f32(re, dev)
+    im = to_device_f32(im, dev)
+    batch = re.numel() // (h * w) if re.numel() else 0
+    plan = native_plan(_lib.KIND_FFT2, w, inverse, dev.index, n2=h)
+    out_re = torch.empty(re.shape, dtype=torch.float32, device=dev)
+    out_im = torch.empty_like(out_re)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_execute(
+            plan.handle, batch, ptr(re), ptr(im), ptr(out_re), ptr(out_im), ptr(None), stream_handle(dev)
+        )
+    _lib.check(rc, "tfa_execute(fft2)")
+    out = ComplexTensor._wrap(out_re, out_im)
+    return out if out_dev == dev else out.to(out_dev)
+
+
+def strided_ok(n: int, stride: int) -> bool:
+    return 2 <= n <= _STRIDED_MAX_N and (n & (n - 1)) == 0 and stride >= 1
+
+
 def _fft_via_gemm(x: ComplexTensor, inverse: bool) -> ComplexTensor:
     """X = x @ W with the exact DFT matrix, on the matrix-core DFT-GEMM kernel (n <= 256)."""
     re, im = x.real, x.imag

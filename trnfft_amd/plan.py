@@ -69,14 +69,14 @@ def clear_plan_cache():
 class NativePlan:
     """Owner of one ``tfa_plan`` (device tables) created on a given device."""
 
-    __slots__ = ("handle", "kind", "n", "inverse", "device", "padded_n", "hop", "flags")
+    __slots__ = ("handle", "kind", "n", "inverse", "device", "padded_n", "hop", "flags", "n2")
 
-    def __init__(self, kind: int, n: int, inverse: bool, device: int, hop: int = 0, flags: int = 0):
+    def __init__(self, kind: int, n: int, inverse: bool, device: int, hop: int = 0, flags: int = 0, n2: int = 0):
         import torch
 
         self.kind, self.n, self.inverse, self.device = kind, n, inverse, device
-        self.hop, self.flags = hop, flags
-        desc = _lib.PlanDesc(kind=kind, inverse=int(bool(inverse)), n=n, hop=hop, flags=flags, reserved=0)
+        self.hop, self.flags, self.n2 = hop, flags, n2
+        desc = _lib.PlanDesc(kind=kind, inverse=int(bool(inverse)), n=n, hop=hop, flags=flags, reserved=0, n2=n2)
         handle = ctypes.c_void_p()
         lib = _lib.lib()
         with torch.cuda.device(device):
@@ -101,14 +101,14 @@ class NativePlan:
             pass
 
 
-def native_plan(kind: int, n: int, inverse: bool, device: int, hop: int = 0, flags: int = 0) -> NativePlan:
-    key = (kind, n, bool(inverse), device, hop, flags)
+def native_plan(kind: int, n: int, inverse: bool, device: int, hop: int = 0, flags: int = 0, n2: int = 0) -> NativePlan:
+    key = (kind, n, bool(inverse), device, hop, flags, n2)
     p = _native_cache.get(key)
     if p is not None:
         return p
     with _lock:
         p = _native_cache.get(key)
         if p is None:
-            p = NativePlan(kind, n, inverse, device, hop, flags)
+            p = NativePlan(kind, n, inverse, device, hop, flags, n2)
             _native_cache[key] = p
     return p
