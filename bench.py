@@ -130,9 +130,12 @@ def bench_headline(steps: int, warmup: int):
     ]
     execute = lib.tfa_execute
 
-    def step(k):
-        rc = execute(*args_f[k % sets])
-        rc |= execute(*args_i[k % sets])
+    def step(k, strm=None):
+        af, ai = args_f[k % sets], args_i[k % sets]
+        if strm is not None:
+            af, ai = af[:-1] + (strm,), ai[:-1] + (strm,)
+        rc = execute(*af)
+        rc |= execute(*ai)
         if rc:
             _lib.check(rc, "tfa_execute")
 
@@ -141,10 +144,33 @@ def bench_headline(steps: int, warmup: int):
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
+
+    # eager: one C-ABI call per launch from Python
     t0 = time.perf_counter()
     ev0.record()
     for k in range(steps):
         step(k)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_eager = time.perf_counter() - t0
+    t_eager_launch = ev0.elapsed_time(ev1) * 1e-3 / (2 * steps)
+
+    # graph: the same K steps captured once into a HIP graph and replayed (no host work between
+    # launches); this is the timed region reported as `value`
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            strm = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for k in range(steps):
+                step(k, strm)
+    torch.cuda.current_stream().wait_stream(cap)
+    graph.replay()  # warm-up replay
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    graph.replay()
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -158,11 +184,16 @@ def bench_headline(steps: int, warmup: int):
     d = timer.durations_s()
     t_launch = t_region_launch
 
-    # correctness of what was timed: last forward output vs a fresh transform of the same input
-    chk = trnfft_amd.fft(trnfft_amd.ComplexTensor(ins[0][0], ins[0][1]))
-    execute(*args_f[0])
+    # correctness of what was timed: the last step's two outputs (written after every other
+    # access to those buffers in the graph) equal fresh eager transforms, bit for bit
+    kf, ki = (steps - 1) % sets, (steps - 1 + sets // 2) % sets
+    chk = trnfft_amd.fft(trnfft_amd.ComplexTensor(ins[kf][0], ins[kf][1]))
+    chk_i = trnfft_amd.ifft(trnfft_amd.ComplexTensor(ins[ki][0], ins[ki][1]))
+    graph.replay()
     torch.cuda.synchronize()
-    assert torch.equal(chk.real, outs[0][0]) and torch.equal(chk.imag, outs[0][1])
+    assert torch.equal(chk.real, outs[kf][0]) and torch.equal(chk.imag, outs[kf][1])
+    assert torch.equal(chk_i.real, outs[ki][0]) and torch.equal(chk_i.imag, outs[ki][1])
+    del graph
 
     # plain device copy of the same bytes (32 MiB in, 32 MiB out per launch, same rotation): the
     # achievable-bandwidth reference, and the known-size kernel that calibrates rocprof counters
@@ -184,6 +215,8 @@ def bench_headline(steps: int, warmup: int):
     bytes_launch = 2 * 2 * plane  # read re+im, write re+im
     return {
         "t_copy_s": t_copy,
+        "wall_eager_s": wall_eager,
+        "t_eager_launch_s": t_eager_launch,
         "wall_s": wall,
         "ms_per_step": wall / steps * 1e3,
         "value": flops_step * steps / wall / 1e9,
@@ -210,47 +243,96 @@ def _time_launches(fn, reps=30, warm=3):
 
 
 def bench_secondary():
-    import trnfft_amd
-    from trnfft_amd import ComplexTensor
+    from trnfft_amd import _lib
+    from trnfft_amd.plan import native_plan
 
     dev = torch.device("cuda", torch.cuda.current_device())
+    L = _lib.lib()
+    strm = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def P(t):
+        return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+    def chk(rc):
+        if rc:
+            _lib.check(rc, "secondary")
+
     out = {}
 
-    def rec(name, t, flops, nbytes, note=""):
-        out[name] = {
-            "ms": round(t * 1e3, 4),
-            "gflops": round(flops / t / 1e9, 1),
-            "gbps": round(nbytes / t / 1e9, 1),
-            "frac_hbm": round(nbytes / t / HBM_PEAK, 4),
-        }
+    def rec(name, t, flops, nbytes, kind="hbm", note=""):
+        r = {"ms": round(t * 1e3, 4), "gflops": round(flops / t / 1e9, 1), "gbps": round(nbytes / t / 1e9, 1)}
+        if kind == "hbm":
+            r["frac_hbm"] = round(nbytes / t / HBM_PEAK, 4)
+        else:
+            r["frac_fp32_mfma"] = round(flops / t / FP32_PEAK, 4)
         if note:
-            out[name]["note"] = note
+            r["note"] = note
+        out[name] = r
 
-    # C2: STFT 64 x 160000, n_fft 512, hop 256
+    # C2: STFT 64 x 160000, n_fft 512, hop 256 (center, reflect, periodic Hann, onesided)
     x = make_stft_input(64, 160000).to(dev)
-    t = _time_launches(lambda: trnfft_amd.stft(x, n_fft=512, hop_length=256))
-    rec("c2_stft_64x160000_nfft512", t, 40064 * 5 * 512 * 9, 64 * 160000 * 4 + 2 * 64 * 257 * 626 * 4,
-        "includes output allocation per call")
-    del x
-    # C3: Bluestein
+    win = torch.hann_window(512).to(dev)
+    pl = native_plan(_lib.KIND_STFT, 512, False, dev.index, hop=256, flags=_lib.STFT_CENTER | _lib.STFT_ONESIDED)
+    o_re = torch.empty(64, 257, 626, device=dev)
+    o_im = torch.empty_like(o_re)
+    t = _time_launches(lambda: chk(L.tfa_stft_execute(pl.handle, 64, 160000, P(x), P(win), P(o_re), P(o_im), strm)))
+    rec("c2_stft_64x160000_nfft512", t, 40064 * 5 * 512 * 9, 64 * 160000 * 4 + 2 * 64 * 257 * 626 * 4)
+    del x, o_re, o_im
+    # C3: Bluestein (fused, one launch)
     for n, b in [(1000, 1024), (4099, 256)]:
         re, im = make_c2c_input(b, n)
-        xc = ComplexTensor(re.to(dev), im.to(dev))
-        t = _time_launches(lambda: trnfft_amd.fft(xc))
+        re, im = re.to(dev), im.to(dev)
+        yr, yi = torch.empty_like(re), torch.empty_like(re)
+        pl = native_plan(_lib.KIND_BLUESTEIN, n, False, dev.index)
+        t = _time_launches(lambda: chk(L.tfa_execute(pl.handle, b, P(re), P(im), P(yr), P(yi), None, strm)))
         rec(f"c3_bluestein_{b}x{n}", t, flops_fft(n, b), 4 * b * n * 4)
     # C4b: four-step N = 2^20, batch 16
     re, im = make_c2c_input(16, 1 << 20)
-    xc = ComplexTensor(re.to(dev), im.to(dev))
-    t = _time_launches(lambda: trnfft_amd.fft(xc), reps=20)
+    re, im = re.to(dev), im.to(dev)
+    yr, yi = torch.empty_like(re), torch.empty_like(re)
+    pl = native_plan(_lib.KIND_C2C, 1 << 20, False, dev.index)
+    ws = torch.empty(pl.workspace_bytes(16) // 4, device=dev)
+    t = _time_launches(lambda: chk(L.tfa_execute(pl.handle, 16, P(re), P(im), P(yr), P(yi), P(ws), strm)), reps=20)
     rec("c4b_fourstep_16x2^20", t, flops_fft(1 << 20, 16), 4 * 16 * (1 << 20) * 4,
-        "two HBM passes; algorithmic bytes = one read + one write")
-    del xc
-    # C4a: fft2 32 x 2048 x 2048 real
+        note="two HBM passes; algorithmic bytes = one read + one write")
+    del re, im, yr, yi, ws
+    # C4a: fft2 32 x 2048 x 2048 real, U[0, 1)
     g = torch.Generator().manual_seed(42)
     img = torch.rand(32, 2048, 2048, generator=g).to(dev)
-    t = _time_launches(lambda: trnfft_amd.fft2(img), reps=5, warm=1)
-    rec("c4a_fft2_32x2048x2048", t, 32 * 5 * 2048 * 2048 * 22, 32 * 2048 * 2048 * (4 + 8))
-    del img
+    yr = torch.empty_like(img)
+    yi = torch.empty_like(img)
+    pl = native_plan(_lib.KIND_FFT2, 2048, False, dev.index, n2=2048)
+    t = _time_launches(lambda: chk(L.tfa_execute(pl.handle, 32, P(img), None, P(yr), P(yi), None, strm)), reps=5, warm=1)
+    rec("c4a_fft2_32x2048x2048", t, 32 * 5 * 2048 * 2048 * 22, 32 * 2048 * 2048 * (4 + 8),
+        note="two HBM passes; algorithmic bytes = real read + complex write")
+    del img, yr, yi
+    # C5a: ComplexLinear 8192 x 1024 -> 1024 (Kaiming-uniform U(+-1/32) weights, zero bias)
+    g = torch.Generator().manual_seed(42)
+    xr = torch.randn(8192, 1024, generator=g).to(dev)
+    xi = torch.randn(8192, 1024, generator=g).to(dev)
+    wr = (torch.rand(1024, 1024, generator=g) * 2 - 1).div_(32).to(dev)
+    wi = (torch.rand(1024, 1024, generator=g) * 2 - 1).div_(32).to(dev)
+    br = torch.zeros(1024, device=dev)
+    bi = torch.zeros(1024, device=dev)
+    yr = torch.empty(8192, 1024, device=dev)
+    yi = torch.empty_like(yr)
+    t = _time_launches(lambda: chk(L.tfa_complex_gemm(8192, 1024, 1024, P(xr), P(xi), 1024, P(wr), P(wi), 1024, 1,
+                                                       P(br), P(bi), P(yr), P(yi), 1024, strm)))
+    rec("c5a_complex_linear_8192x1024x1024", t, 8.0 * 8192 * 1024 * 1024, 142614528, kind="mfma")
+    del xr, xi, yr, yi
+    # C5b: DFT-as-GEMM, 65536 x N=256 forward
+    re, im = make_c2c_input(65536, 256)
+    re, im = re.to(dev), im.to(dev)
+    yr, yi = torch.empty_like(re), torch.empty_like(re)
+    pl = native_plan(_lib.KIND_DFT_GEMM, 256, False, dev.index)
+    t = _time_launches(lambda: chk(L.tfa_execute(pl.handle, 65536, P(re), P(im), P(yr), P(yi), None, strm)))
+    rec("c5b_dft_gemm_65536x256", t, 8.0 * 65536 * 256 * 256, 268959744, kind="mfma",
+        note="flops = 8*M*N*N of the complex GEMM (the FFT-equivalent is 671 MFLOP)")
+    # same shape on the Stockham kernel, for comparison
+    pl = native_plan(_lib.KIND_C2C, 256, False, dev.index)
+    t = _time_launches(lambda: chk(L.tfa_execute(pl.handle, 65536, P(re), P(im), P(yr), P(yi), None, strm)))
+    rec("c5b_stockham_65536x256", t, flops_fft(256, 65536), 4 * 65536 * 256 * 4)
+    del re, im, yr, yi
     torch.cuda.empty_cache()
     return out
 
@@ -324,9 +406,10 @@ def main(argv=None):
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: N(0,1) re/im, seed 42, 4096x1024 (BASELINE config 1)",
+        "value_eager": round(2 * flops_fft(1024, 4096) * args.steps / head["wall_eager_s"] / 1e9, 1),
         "config": {
             "workload": "batched c2c FFT, 4096 x N=1024 fp32 split re/im; step = forward fft of one batch + "
-            "inverse fft of another, buffers rotated over >1 GiB",
+            "inverse fft of another, buffers rotated over >1 GiB; K steps replayed as one HIP graph",
             "n": 1024,
             "batch": 4096,
             "buffer_sets": head["buffer_sets"],
@@ -341,6 +424,7 @@ def main(argv=None):
             "traffic": _traffic_from_profiles("c2c_lds_n1024"),
             "t_launch_us": round(head["t_launch_s"] * 1e6, 3),
             "t_launch_isolated_median_us": round(head["t_launch_median_s"] * 1e6, 3),
+            "t_launch_eager_us": round(head["t_eager_launch_s"] * 1e6, 3),
             "bytes_per_launch": head["bytes_launch"],
             "copy_gbps": round(head["bytes_launch"] / head["t_copy_s"] / 1e9, 1),
             "frac_of_copy": round(head["t_copy_s"] / head["t_launch_s"], 4),

@@ -221,9 +221,21 @@ def stft_num_frames(length: int, n_fft: int, hop_length: int, center: bool = Tru
     return 1 + (padded - n_fft) // hop_length
 
 
-def _effective_window(window: torch.Tensor | None, n_fft: int, win_length: int, dtype) -> torch.Tensor:
+_default_windows: dict[tuple, torch.Tensor] = {}
+
+
+def _effective_window(window: torch.Tensor | None, n_fft: int, win_length: int, dtype, device=None) -> torch.Tensor:
     if window is None:
-        window = torch.hann_window(win_length, dtype=dtype)
+        # default periodic Hann (torch.hann_window, as the reference), built once per device so
+        # later calls (including ones under HIP-graph capture) make no host-to-device copy
+        key = (win_length, n_fft, dtype, str(device))
+        cached = _default_windows.get(key)
+        if cached is not None:
+            return cached
+        w = _effective_window(torch.hann_window(win_length, dtype=dtype), n_fft, win_length, dtype)
+        w = w.to(device) if device is not None else w
+        _default_windows[key] = w
+        return w
     if win_length < n_fft:
         padded = torch.zeros(n_fft, dtype=window.dtype, device=window.device)
         offset = (n_fft - win_length) // 2
@@ -254,8 +266,8 @@ def stft(
         win_length = n_fft
     _resolve(None)
     _require_hip("stft")
-    win = _effective_window(window, n_fft, win_length, input.dtype)
     dev = target_device(input)
+    win = _effective_window(window, n_fft, win_length, input.dtype, dev)
     out_dev = input.device
     x = to_device_f32(input, dev)
     win = to_device_f32(win, dev)
