@@ -192,7 +192,10 @@ __device__ __forceinline__ void exchange_sync() {
 //   tw:   the plan's twiddle table for (N, E, DIR) (layout from make_shape)
 // SPLIT: exchange the real and imaginary planes one after the other through `lre` alone (lim
 // unused): half the LDS per transform, twice the synchronisations.
-template <int N, int E, int DIR, bool WAVE_LOCAL, bool SPLIT = false>
+// IL: `lre` holds lds_pad(N) interleaved float2 (re, im) entries (lim unused): one 64-bit LDS
+// access per element instead of two 32-bit ones (gfx950 serves a 64-lane ds_read_b64 of
+// consecutive float2 in the cycles of a ds_read_b32, so this halves LDS time as well).
+template <int N, int E, int DIR, bool WAVE_LOCAL, bool SPLIT = false, bool IL = false>
 struct LdsFft {
   static constexpr LdsShape S = make_shape(N, E);
   static constexpr int T = N / E;
@@ -229,13 +232,13 @@ struct LdsFft {
 #pragma unroll
           for (int u = 0; u < R; ++u) v[b + u * NB] = w[b][u];
         } else if constexpr (!SPLIT) {
-          store_pass<R, LS, LIN_W>(w[b], lre, lim, j, k, 2);
+          store_pass<R, LS, LIN_W>(w[b], lre, lim, j, k, IL ? 3 : 2);
         }
       }
       if constexpr (!LAST) {
         if constexpr (!SPLIT) {
           exchange_sync<WAVE_LOCAL>();
-          load_pass(v, lre, lim, tid, 2);
+          load_pass(v, lre, lim, tid, IL ? 3 : 2);
           exchange_sync<WAVE_LOCAL>();
         } else {
 #pragma unroll
@@ -255,7 +258,8 @@ struct LdsFft {
     }
   }
 
-  // which: 0 = real plane into a, 1 = imaginary plane into a, 2 = real into a and imag into b
+  // which: 0 = real plane into a, 1 = imaginary plane into a, 2 = real into a and imag into b,
+  //        3 = interleaved float2 entries in a
   template <int R, int LS, bool LIN_W>
   __device__ __forceinline__ static void store_pass(const float2 (&w)[R], float* a, float* b, int j, int k,
                                                     int which) {
@@ -265,7 +269,9 @@ struct LdsFft {
 #pragma unroll
       for (int u = 0; u < R; ++u) {
         const int off = LS == 1 ? u + (u >> 4) : u * (LS + LS / 16);
-        if (which == 2) {
+        if (which == 3) {
+          reinterpret_cast<float2*>(a)[base + off] = w[u];
+        } else if (which == 2) {
           a[base + off] = w[u].x;
           b[base + off] = w[u].y;
         } else {
@@ -277,7 +283,9 @@ struct LdsFft {
 #pragma unroll
       for (int u = 0; u < R; ++u) {
         const int idx = lds_pad(base + u * LS);
-        if (which == 2) {
+        if (which == 3) {
+          reinterpret_cast<float2*>(a)[idx] = w[u];
+        } else if (which == 2) {
           a[idx] = w[u].x;
           b[idx] = w[u].y;
         } else {
@@ -294,7 +302,8 @@ struct LdsFft {
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int idx = rb + e * (T + T / 16);
-        if (which == 2) v[e] = make_float2(a[idx], b[idx]);
+        if (which == 3) v[e] = reinterpret_cast<const float2*>(a)[idx];
+        else if (which == 2) v[e] = make_float2(a[idx], b[idx]);
         else if (which == 0) v[e].x = a[idx];
         else v[e].y = a[idx];
       }
@@ -302,7 +311,8 @@ struct LdsFft {
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const int idx = lds_pad(tid + T * e);
-        if (which == 2) v[e] = make_float2(a[idx], b[idx]);
+        if (which == 3) v[e] = reinterpret_cast<const float2*>(a)[idx];
+        else if (which == 2) v[e] = make_float2(a[idx], b[idx]);
         else if (which == 0) v[e].x = a[idx];
         else v[e].y = a[idx];
       }

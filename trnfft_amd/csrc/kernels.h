@@ -22,6 +22,11 @@ __device__ __forceinline__ long long xcd_tile_remap(long long i, long long g) {
 // and written once, so it should not displace other lines in L2 / the Infinity Cache.
 __device__ __forceinline__ float ld_stream(const float* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_stream(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ float4 ld_stream4(const float4* p) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v r = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(p));
+  return make_float4(r.x, r.y, r.z, r.w);
+}
 
 // Thread layout of the batched LDS kernels for transform length N: T threads per transform,
 // XF transforms per workgroup (at least 256 threads per workgroup), PADN LDS floats per plane

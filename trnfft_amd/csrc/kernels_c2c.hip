@@ -120,12 +120,12 @@ __host__ __device__ constexpr int fourstep_tile(int l) {
 // (element stride S) for every (outer, column) pair.  One workgroup = C adjacent columns of one
 // outer block, so each load/store instruction covers C consecutive floats.  With TWIDDLE the
 // result k1 of column c is multiplied by W_Ntot^(c*k1) (the four-step column pass, with S = N2).
-template <int N1, int DIR, bool REAL_IN, bool TWIDDLE>
-__global__ __launch_bounds__(fourstep_tile(N1) * (N1 / lds_epth(N1))) void strided_kernel(
+template <int N1, int DIR, bool REAL_IN, bool TWIDDLE, int C = fourstep_tile(N1)>
+__global__ __launch_bounds__(C * (N1 / lds_epth(N1))) void strided_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re, float* out_im,
     const float2* __restrict__ tw, const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi,
     long long stride, int tiles_per_block, int lo_bits, unsigned nmask, float scale) {
-  constexpr int E = lds_epth(N1), T = N1 / E, C = fourstep_tile(N1);
+  constexpr int E = lds_epth(N1), T = N1 / E;
   constexpr int PADN = lds_pad(N1) + 1;
   __shared__ float lre[C * PADN];
   __shared__ float lim[C * PADN];
@@ -164,12 +164,12 @@ __global__ __launch_bounds__(fourstep_tile(N1) * (N1 / lds_epth(N1))) void strid
 
 // Row pass: FFT over n2 of each row k1 of tmp (contiguous), output X[k1 + N1*k2] for C
 // adjacent rows, transposed through LDS so each store covers C consecutive k1.
-template <int N2, int DIR>
-__global__ __launch_bounds__(fourstep_tile(N2) * (N2 / lds_epth(N2))) void fourstep_row_kernel(
+template <int N2, int DIR, int C = fourstep_tile(N2)>
+__global__ __launch_bounds__(C * (N2 / lds_epth(N2))) void fourstep_row_kernel(
     const float* __restrict__ t_re, const float* __restrict__ t_im, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ tw, int n1_len, long long batch,
     float scale) {
-  constexpr int E = lds_epth(N2), T = N2 / E, C = fourstep_tile(N2);
+  constexpr int E = lds_epth(N2), T = N2 / E;
   constexpr int PADN = lds_pad(N2) + 1;
   constexpr int THREADS = C * T;
   __shared__ float lre[C * PADN];

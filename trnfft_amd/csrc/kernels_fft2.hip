@@ -86,10 +86,10 @@ __host__ __device__ constexpr int fft2_tile(int hr) {
   return c;
 }
 
-template <int HR, int DIR>
-__global__ __launch_bounds__(fft2_tile(HR) * (HR / lds_epth(HR))) void fft2_pass2_kernel(
+template <int HR, int DIR, int C = fft2_tile(HR)>
+__global__ __launch_bounds__(C * (HR / lds_epth(HR))) void fft2_pass2_kernel(
     float* re, float* im, const float2* __restrict__ tw, int W, int tiles_per_group, float scale) {
-  constexpr int E = lds_epth(HR), T = HR / E, C = fft2_tile(HR);
+  constexpr int E = lds_epth(HR), T = HR / E;
   constexpr int PADN = lds_pad(HR) + 1;
   __shared__ float lre[C * PADN];
   __shared__ float lim[C * PADN];
