@@ -232,14 +232,41 @@ def bench_headline(steps: int, warmup: int):
 # ---------------------------------------------------------------------------------------------
 
 
-def _time_launches(fn, reps=30, warm=3):
-    for _ in range(warm):
-        fn()
-    timer = EventTimer()
-    for _ in range(reps):
-        timer.record(fn)
-    d = timer.durations_s()
-    return _median(d)
+ROTATE_BYTES = 1.25 * 2**30  # > 4x the 256 MB Infinity Cache
+
+
+def _n_sets(set_bytes: int) -> int:
+    """Buffer sets to rotate so that consecutive launches never find their data in the MALL."""
+    return max(1, math.ceil(ROTATE_BYTES / set_bytes))
+
+
+def _time_rot(fn, n_sets: int, reps: int = 30, warm: int = 3) -> float:
+    """Average launch duration of fn(k, stream) over `reps` back-to-back launches (k = buffer set
+    k % n_sets), captured once into a HIP graph and timed with HIP events around one replay, so
+    host launch overhead neither adds to nor starves the timed kernels."""
+    cur = torch.cuda.current_stream()
+    for k in range(warm):
+        fn(k % n_sets, ctypes.c_void_p(cur.cuda_stream))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(cur)
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for k in range(reps):
+                fn(k % n_sets, h)
+    cur.wait_stream(cap)
+    graph.replay()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    del graph
+    return ev0.elapsed_time(ev1) * 1e-3 / reps
 
 
 def bench_secondary():
@@ -248,7 +275,6 @@ def bench_secondary():
 
     dev = torch.device("cuda", torch.cuda.current_device())
     L = _lib.lib()
-    strm = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
     def P(t):
         return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
@@ -257,56 +283,71 @@ def bench_secondary():
         if rc:
             _lib.check(rc, "secondary")
 
+    def rolled(t, n):
+        """n distinct device copies of t (rows rolled), each a buffer set's input."""
+        return [torch.roll(t, shifts=k, dims=0).to(dev) for k in range(n)]
+
     out = {}
 
-    def rec(name, t, flops, nbytes, kind="hbm", note=""):
+    def rec(name, t, flops, nbytes, kind="hbm", note="", sets=None):
         r = {"ms": round(t * 1e3, 4), "gflops": round(flops / t / 1e9, 1), "gbps": round(nbytes / t / 1e9, 1)}
         if kind == "hbm":
             r["frac_hbm"] = round(nbytes / t / HBM_PEAK, 4)
         else:
             r["frac_fp32_mfma"] = round(flops / t / FP32_PEAK, 4)
+        if sets is not None:
+            r["buffer_sets"] = sets
         if note:
             r["note"] = note
         out[name] = r
 
     # C2: STFT 64 x 160000, n_fft 512, hop 256 (center, reflect, periodic Hann, onesided)
-    x = make_stft_input(64, 160000).to(dev)
+    nbytes = 64 * 160000 * 4 + 2 * 64 * 257 * 626 * 4
+    S = _n_sets(nbytes)
+    xs = rolled(make_stft_input(64, 160000), S)
     win = torch.hann_window(512).to(dev)
     pl = native_plan(_lib.KIND_STFT, 512, False, dev.index, hop=256, flags=_lib.STFT_CENTER | _lib.STFT_ONESIDED)
-    o_re = torch.empty(64, 257, 626, device=dev)
-    o_im = torch.empty_like(o_re)
-    t = _time_launches(lambda: chk(L.tfa_stft_execute(pl.handle, 64, 160000, P(x), P(win), P(o_re), P(o_im), strm)))
-    rec("c2_stft_64x160000_nfft512", t, 40064 * 5 * 512 * 9, 64 * 160000 * 4 + 2 * 64 * 257 * 626 * 4)
-    del x, o_re, o_im
+    os_ = [(torch.empty(64, 257, 626, device=dev), torch.empty(64, 257, 626, device=dev)) for _ in range(S)]
+    t = _time_rot(lambda k, st: chk(L.tfa_stft_execute(pl.handle, 64, 160000, P(xs[k]), P(win), P(os_[k][0]),
+                                                   P(os_[k][1]), st)), S)
+    rec("c2_stft_64x160000_nfft512", t, 40064 * 5 * 512 * 9, nbytes, sets=S)
+    del xs, os_
     # C3: Bluestein (fused, one launch)
     for n, b in [(1000, 1024), (4099, 256)]:
+        nbytes = 4 * b * n * 4
+        S = _n_sets(nbytes)
         re, im = make_c2c_input(b, n)
-        re, im = re.to(dev), im.to(dev)
-        yr, yi = torch.empty_like(re), torch.empty_like(re)
+        ins = list(zip(rolled(re, S), rolled(im, S)))
+        outs = [(torch.empty(b, n, device=dev), torch.empty(b, n, device=dev)) for _ in range(S)]
         pl = native_plan(_lib.KIND_BLUESTEIN, n, False, dev.index)
-        t = _time_launches(lambda: chk(L.tfa_execute(pl.handle, b, P(re), P(im), P(yr), P(yi), None, strm)))
-        rec(f"c3_bluestein_{b}x{n}", t, flops_fft(n, b), 4 * b * n * 4)
-    # C4b: four-step N = 2^20, batch 16
+        t = _time_rot(lambda k, st: chk(L.tfa_execute(pl.handle, b, P(ins[k][0]), P(ins[k][1]), P(outs[k][0]),
+                                                  P(outs[k][1]), None, st)), S)
+        rec(f"c3_bluestein_{b}x{n}", t, flops_fft(n, b), nbytes, sets=S)
+        del ins, outs
+    # C4b: four-step N = 2^20, batch 16 (the workspace is written and read within one call)
+    nbytes = 4 * 16 * (1 << 20) * 4
+    S = _n_sets(nbytes)
     re, im = make_c2c_input(16, 1 << 20)
-    re, im = re.to(dev), im.to(dev)
-    yr, yi = torch.empty_like(re), torch.empty_like(re)
+    ins = list(zip(rolled(re, S), rolled(im, S)))
+    outs = [(torch.empty(16, 1 << 20, device=dev), torch.empty(16, 1 << 20, device=dev)) for _ in range(S)]
     pl = native_plan(_lib.KIND_C2C, 1 << 20, False, dev.index)
     ws = torch.empty(pl.workspace_bytes(16) // 4, device=dev)
-    t = _time_launches(lambda: chk(L.tfa_execute(pl.handle, 16, P(re), P(im), P(yr), P(yi), P(ws), strm)), reps=20)
-    rec("c4b_fourstep_16x2^20", t, flops_fft(1 << 20, 16), 4 * 16 * (1 << 20) * 4,
+    t = _time_rot(lambda k, st: chk(L.tfa_execute(pl.handle, 16, P(ins[k][0]), P(ins[k][1]), P(outs[k][0]),
+                                              P(outs[k][1]), P(ws), st)), S, reps=20)
+    rec("c4b_fourstep_16x2^20", t, flops_fft(1 << 20, 16), nbytes, sets=S,
         note="two HBM passes; algorithmic bytes = one read + one write")
-    del re, im, yr, yi, ws
-    # C4a: fft2 32 x 2048 x 2048 real, U[0, 1)
+    del ins, outs, ws
+    # C4a: fft2 32 x 2048 x 2048 real, U[0, 1) (1.5 GiB per set: no rotation needed)
     g = torch.Generator().manual_seed(42)
     img = torch.rand(32, 2048, 2048, generator=g).to(dev)
     yr = torch.empty_like(img)
     yi = torch.empty_like(img)
     pl = native_plan(_lib.KIND_FFT2, 2048, False, dev.index, n2=2048)
-    t = _time_launches(lambda: chk(L.tfa_execute(pl.handle, 32, P(img), None, P(yr), P(yi), None, strm)), reps=5, warm=1)
-    rec("c4a_fft2_32x2048x2048", t, 32 * 5 * 2048 * 2048 * 22, 32 * 2048 * 2048 * (4 + 8),
+    t = _time_rot(lambda k, st: chk(L.tfa_execute(pl.handle, 32, P(img), None, P(yr), P(yi), None, st)), 1, reps=5, warm=1)
+    rec("c4a_fft2_32x2048x2048", t, 32 * 5 * 2048 * 2048 * 22, 32 * 2048 * 2048 * (4 + 8), sets=1,
         note="two HBM passes; algorithmic bytes = real read + complex write")
     del img, yr, yi
-    # C5a: ComplexLinear 8192 x 1024 -> 1024 (Kaiming-uniform U(+-1/32) weights, zero bias)
+    # C5a: ComplexLinear 8192 x 1024 -> 1024 (Kaiming-uniform U(+-1/32) weights, zero bias); MFMA-bound
     g = torch.Generator().manual_seed(42)
     xr = torch.randn(8192, 1024, generator=g).to(dev)
     xi = torch.randn(8192, 1024, generator=g).to(dev)
@@ -316,23 +357,42 @@ def bench_secondary():
     bi = torch.zeros(1024, device=dev)
     yr = torch.empty(8192, 1024, device=dev)
     yi = torch.empty_like(yr)
-    t = _time_launches(lambda: chk(L.tfa_complex_gemm(8192, 1024, 1024, P(xr), P(xi), 1024, P(wr), P(wi), 1024, 1,
-                                                       P(br), P(bi), P(yr), P(yi), 1024, strm)))
+    t = _time_rot(lambda k, st: chk(L.tfa_complex_gemm(8192, 1024, 1024, P(xr), P(xi), 1024, P(wr), P(wi), 1024, 1,
+                                                   P(br), P(bi), P(yr), P(yi), 1024, st)), 1)
     rec("c5a_complex_linear_8192x1024x1024", t, 8.0 * 8192 * 1024 * 1024, 142614528, kind="mfma")
     del xr, xi, yr, yi
-    # C5b: DFT-as-GEMM, 65536 x N=256 forward
+    # C5b: DFT-as-GEMM, 65536 x N=256 forward, and the same shape on the Stockham kernel
+    nbytes = 4 * 65536 * 256 * 4
+    S = _n_sets(nbytes)
     re, im = make_c2c_input(65536, 256)
-    re, im = re.to(dev), im.to(dev)
-    yr, yi = torch.empty_like(re), torch.empty_like(re)
+    ins = list(zip(rolled(re, S), rolled(im, S)))
+    outs = [(torch.empty(65536, 256, device=dev), torch.empty(65536, 256, device=dev)) for _ in range(S)]
     pl = native_plan(_lib.KIND_DFT_GEMM, 256, False, dev.index)
-    t = _time_launches(lambda: chk(L.tfa_execute(pl.handle, 65536, P(re), P(im), P(yr), P(yi), None, strm)))
-    rec("c5b_dft_gemm_65536x256", t, 8.0 * 65536 * 256 * 256, 268959744, kind="mfma",
+    t = _time_rot(lambda k, st: chk(L.tfa_execute(pl.handle, 65536, P(ins[k][0]), P(ins[k][1]), P(outs[k][0]),
+                                              P(outs[k][1]), None, st)), S)
+    rec("c5b_dft_gemm_65536x256", t, 8.0 * 65536 * 256 * 256, 268959744, kind="mfma", sets=S,
         note="flops = 8*M*N*N of the complex GEMM (the FFT-equivalent is 671 MFLOP)")
-    # same shape on the Stockham kernel, for comparison
     pl = native_plan(_lib.KIND_C2C, 256, False, dev.index)
-    t = _time_launches(lambda: chk(L.tfa_execute(pl.handle, 65536, P(re), P(im), P(yr), P(yi), None, strm)))
-    rec("c5b_stockham_65536x256", t, flops_fft(256, 65536), 4 * 65536 * 256 * 4)
-    del re, im, yr, yi
+    t = _time_rot(lambda k, st: chk(L.tfa_execute(pl.handle, 65536, P(ins[k][0]), P(ins[k][1]), P(outs[k][0]),
+                                              P(outs[k][1]), None, st)), S)
+    rec("c5b_stockham_65536x256", t, flops_fft(256, 65536), nbytes, sets=S)
+    del ins, outs
+    # rfft / irfft as r2c / c2r kernels, 4096 rows x N=1024 (the headline shape, real signals)
+    b, n = 4096, 1024
+    nbytes = b * n * 4 + 2 * b * (n // 2 + 1) * 4
+    S = _n_sets(nbytes)
+    re, im = make_c2c_input(b, n)
+    xs = rolled(re, S)
+    bins = [(torch.empty(b, n // 2 + 1, device=dev), torch.empty(b, n // 2 + 1, device=dev)) for _ in range(S)]
+    pl = native_plan(_lib.KIND_REAL, n, False, dev.index)
+    t = _time_rot(lambda k, st: chk(L.tfa_execute(pl.handle, b, P(xs[k]), None, P(bins[k][0]), P(bins[k][1]), None,
+                                              st)), S)
+    rec("rfft_r2c_4096x1024", t, flops_fft(n, b) / 2, nbytes, sets=S, note="flops = 2.5 N log2 N per row")
+    pl = native_plan(_lib.KIND_REAL, n, True, dev.index)
+    t = _time_rot(lambda k, st: chk(L.tfa_execute(pl.handle, b, P(bins[k][0]), P(bins[k][1]), P(xs[(k + 1) % S]),
+                                              None, None, st)), S)
+    rec("irfft_c2r_4096x1024", t, flops_fft(n, b) / 2, nbytes, sets=S, note="flops = 2.5 N log2 N per row")
+    del xs, bins
     torch.cuda.empty_cache()
     return out
 

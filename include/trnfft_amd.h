@@ -37,6 +37,7 @@ typedef void* tfa_stream; /* hipStream_t; NULL = the null stream */
 #define TFA_KIND_DFT_GEMM 2  /* n <= 256, X = x @ W on the matrix cores                      */
 #define TFA_KIND_STFT 3      /* framed, windowed onesided/twosided transform of real signals */
 #define TFA_KIND_FFT2 4      /* 2-D transform over the last two axes (n = last, n2 = second to last) */
+#define TFA_KIND_REAL 5      /* real rows: forward r2c (n real -> n/2+1 bins), inverse c2r; power-of-two 4 <= n <= 32768 */
 
 /* STFT flags. */
 #define TFA_STFT_CENTER 1     /* reflect-pad n_fft/2 on both sides (pad_mode="reflect") */
@@ -79,6 +80,13 @@ int64_t tfa_plan_padded_n(const tfa_plan* plan);
  * TFA_KIND_FFT2 plans: `batch` arrays of (n2, n) each, transformed over both axes (x 1/(n n2)
  * when inverse), power-of-two 16 <= n <= 2048 and 16 <= n2 <= 4096, output must not alias the
  * input; replaces trnfft/api.py:105-139 (fft2 -> fftn over (-2, -1)).
+ * TFA_KIND_REAL plans, forward (replaces trnfft/api.py:38-46, rfft): in_re = (batch, n) real
+ * rows, in_im must be NULL, out_re/out_im = (batch, n/2+1) bins.  Inverse (replaces
+ * trnfft/api.py:49-68, irfft with its default n = 2*(bins-1)): in_re/in_im = (batch, n/2+1)
+ * bins, out_re = (batch, n) real rows scaled 1/n, out_im unused (may be NULL); the imaginary
+ * parts of bins 0 and n/2 are ignored, as the reference's real part of the Hermitian-completed
+ * inverse ignores them.  The real rows (input of the forward, output of the inverse) must be
+ * 8-byte aligned; out-of-place only.
  */
 int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const float* in_im,
                 float* out_re, float* out_im, void* workspace, tfa_stream stream);

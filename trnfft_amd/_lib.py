@@ -22,6 +22,7 @@ KIND_BLUESTEIN = 1
 KIND_DFT_GEMM = 2
 KIND_STFT = 3
 KIND_FFT2 = 4
+KIND_REAL = 5
 
 STFT_CENTER = 1
 STFT_NORMALIZED = 2

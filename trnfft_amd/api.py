@@ -14,7 +14,17 @@ import torch
 from . import _lib
 from .complex import ComplexTensor
 from .dispatch import _require_hip, ptr, stream_handle, target_device, to_device_f32
-from .fft_core import execute_1d, execute_fft2, execute_strided, fft2_ok, fft_core, strided_ok
+from .fft_core import (
+    execute_1d,
+    execute_c2r,
+    execute_fft2,
+    execute_r2c,
+    execute_strided,
+    fft2_ok,
+    fft_core,
+    real_ok,
+    strided_ok,
+)
 from .plan import native_plan
 from .precision import _resolve
 
@@ -59,6 +69,10 @@ def rfft(input: torch.Tensor, n: int | None = None) -> ComplexTensor:
     if n is not None:
         input = _resize_real(input, n)
     n = input.shape[-1]
+    if real_ok(n):
+        _resolve(None)
+        _require_hip("rfft")
+        return execute_r2c(input)
     result = _real_1d(input, inverse=False)
     half = n // 2 + 1
     return ComplexTensor(result.real[..., :half], result.imag[..., :half])
@@ -68,6 +82,10 @@ def irfft(input: ComplexTensor, n: int | None = None) -> torch.Tensor:
     """Inverse of rfft via the Hermitian-completed spectrum (trnfft/api.py:49-68)."""
     if n is None:
         n = 2 * (input.shape[-1] - 1)
+    if n == 2 * (input.shape[-1] - 1) and real_ok(n):
+        _resolve(None)
+        _require_hip("irfft")
+        return execute_c2r(input.real, input.imag, n)
     dev = input.real.device
     full_re = torch.zeros(*input.shape[:-1], n, dtype=input.dtype, device=dev)
     full_im = torch.zeros(*input.shape[:-1], n, dtype=input.dtype, device=dev)

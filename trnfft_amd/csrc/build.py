@@ -14,7 +14,15 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 LIB = os.path.join(PKG, "libtrnfft_amd.so")
-SOURCES = ["plan.hip", "kernels_c2c.hip", "kernels_bluestein.hip", "kernels_stft.hip", "kernels_gemm.hip", "kernels_fft2.hip"]
+SOURCES = [
+    "plan.hip",
+    "kernels_c2c.hip",
+    "kernels_bluestein.hip",
+    "kernels_stft.hip",
+    "kernels_gemm.hip",
+    "kernels_fft2.hip",
+    "kernels_real.hip",
+]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -22,6 +22,14 @@ __host__ __device__ constexpr int lds_epth(int n) {
   return n <= 16 ? n : (n == 32 || n == 64) ? 8 : (n == 512 || n == 4096) ? 32 : 16;
 }
 
+// Elements per thread of the real-row kernels (r2c / c2r over a half-length h complex transform),
+// from a launch-shape sweep on MI355X (4M real samples per launch, buffers rotated past the
+// Infinity Cache): small transforms want E = 4 (more lanes per row segment), mid sizes E = 8
+// (one wavefront per transform up to h = 512), the largest E = 32 (fewest workgroup barriers).
+__host__ __device__ constexpr int real_epth(int h, bool inverse) {
+  return h <= 2 ? h : h >= 8192 ? 32 : (h <= (inverse ? 64 : 256)) ? 4 : 8;
+}
+
 struct LdsShape {
   int n, e, t, npass;
   int radix[kMaxPasses];

@@ -124,6 +124,20 @@ struct StftArgs {
 };
 hipError_t launch_stft(int n_fft, const StftArgs& a);
 
+struct RealArgs {
+  const float* in_re;  // forward: (batch, n) real rows; inverse: (batch, n/2+1) bins
+  const float* in_im;  // inverse only
+  float* out_re;       // forward: (batch, n/2+1) bins; inverse: (batch, n) real rows
+  float* out_im;       // forward only
+  const float2* tw;    // LDS-FFT table for length n/2 in the plan's direction
+  const float2* twr;   // W_n^k = exp(-2 pi i k / n), k < n/2
+  long long batch;
+  float scale;  // inverse: 1/n
+  bool inverse;
+  hipStream_t stream;
+};
+hipError_t launch_real(int n, const RealArgs& a);
+
 struct Fft2Args {
   const float* in_re;
   const float* in_im;  // nullptr: real input

@@ -1,0 +1,180 @@
+// Real-input forward (r2c) and real-output inverse (c2r) transforms of power-of-two length
+// N = 2H, 4 <= N <= 32768, through one complex transform of half length.
+//
+// The reference computes rfft as a full length-N complex transform of (x, 0) and slices bins
+// 0..N/2 (trnfft/api.py:38-46), and irfft by materialising the Hermitian-completed length-N
+// spectrum and taking the real part of its inverse (trnfft/api.py:49-68).  Here:
+//   r2c: z[m] = x[2m] + i x[2m+1] (the real row read as H float2), Z = FFT_H(z), then
+//        X[k] = E[k] + W_N^k O[k],  E[k] = (Z[k] + conj Z[H-k]) / 2,  O[k] = (Z[k] - conj Z[H-k]) / 2i,
+//        for k = 0..H-1, and X[H] = Re Z[0] - Im Z[0].
+//   c2r: Z[k] = (X[k] + conj X[H-k]) + i W_N^-k (X[k] - conj X[H-k]), scaled by 1/N, for k < H
+//        (Im X[0] and Im X[H] are dropped: they only feed the imaginary part the reference
+//        discards), z = IFFT_H(Z) unnormalised, x[2m] = Re z[m], x[2m+1] = Im z[m].
+// Half the HBM bytes of the complex formulation and half its arithmetic.
+#include "kernels.h"
+
+namespace tfa {
+
+template <int H, int E_, int THR = 256>
+struct RealCfg {
+  static constexpr int E = E_;
+  static constexpr int T = H / E;
+  static constexpr int XF = T >= THR ? 1 : THR / T;  // transforms per workgroup
+  static constexpr int THREADS = XF * T;
+  static constexpr int PADR = lds_pad(H) + 1;  // room for bins 0..H
+};
+
+__device__ __forceinline__ float2 ld_stream2(const float2* p) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  const f2v r = __builtin_nontemporal_load(reinterpret_cast<const f2v*>(p));
+  return make_float2(r.x, r.y);
+}
+__device__ __forceinline__ void st_stream2(float2* p, float2 v) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  f2v r;
+  r.x = v.x;
+  r.y = v.y;
+  __builtin_nontemporal_store(r, reinterpret_cast<f2v*>(p));
+}
+
+// x: (batch, 2H) real rows; out: (batch, H+1) bins.  twr[k] = W_N^k = exp(-2 pi i k / N), k < H.
+template <int H, bool TAIL, int E_ = real_epth(H, false), int THR = 256>
+__global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
+    const float* __restrict__ x, float* __restrict__ out_re, float* __restrict__ out_im,
+    const float2* __restrict__ tw, const float2* __restrict__ twr, long long first, long long batch) {
+  using C = RealCfg<H, E_, THR>;
+  constexpr int E = C::E, T = C::T;
+  constexpr bool WL = T <= 64;
+  __shared__ float lre[C::XF * C::PADR];
+  __shared__ float lim[C::XF * C::PADR];
+  const int tid = threadIdx.x % T;
+  const int xf = threadIdx.x / T;
+  const long long b = first + (long long)blockIdx.x * C::XF + xf;
+  const bool valid = !TAIL || b < batch;
+  float* mre = lre + xf * C::PADR;
+  float* mim = lim + xf * C::PADR;
+  const float2* src = reinterpret_cast<const float2*>(x + (size_t)b * (2 * H)) + tid;
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = valid ? ld_stream2(src + T * e) : make_float2(0.0f, 0.0f);
+  LdsFft<H, E, -1, WL>::run(v, mre, mim, tw, tid);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    mre[lds_pad(tid + T * e)] = v[e].x;
+    mim[lds_pad(tid + T * e)] = v[e].y;
+  }
+  exchange_sync<WL>();
+  if (!valid) return;
+  float* qr = out_re + (size_t)b * (H + 1) + tid;
+  float* qi = out_im + (size_t)b * (H + 1) + tid;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int k = tid + T * e;
+    const int r = lds_pad((H - k) & (H - 1));
+    const float2 a = v[e];
+    const float2 c = make_float2(mre[r], -mim[r]);  // conj Z[H-k]
+    const float2 ev = make_float2(0.5f * (a.x + c.x), 0.5f * (a.y + c.y));
+    const float2 od = make_float2(0.5f * (a.y - c.y), -0.5f * (a.x - c.x));  // (a - c) / 2i
+    const float2 y = cadd(ev, cmul(twr[k], od));
+    st_stream(qr + T * e, y.x);
+    st_stream(qi + T * e, y.y);
+  }
+  if (tid == 0) {
+    st_stream(qr + H, v[0].x - v[0].y);
+    st_stream(qi + H, 0.0f);
+  }
+}
+
+// in: (batch, H+1) bins; x: (batch, 2H) real rows.  tw: inverse LDS table of length H.
+template <int H, bool TAIL, int E_ = real_epth(H, true), int THR = 256>
+__global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
+    const float* __restrict__ in_re, const float* __restrict__ in_im, float* __restrict__ x,
+    const float2* __restrict__ tw, const float2* __restrict__ twr, long long first, long long batch, float scale) {
+  using C = RealCfg<H, E_, THR>;
+  constexpr int E = C::E, T = C::T;
+  constexpr bool WL = T <= 64;
+  __shared__ float lre[C::XF * C::PADR];
+  __shared__ float lim[C::XF * C::PADR];
+  const int tid = threadIdx.x % T;
+  const int xf = threadIdx.x / T;
+  const long long b = first + (long long)blockIdx.x * C::XF + xf;
+  const bool valid = !TAIL || b < batch;
+  float* mre = lre + xf * C::PADR;
+  float* mim = lim + xf * C::PADR;
+  const float* pr = in_re + (size_t)b * (H + 1) + tid;
+  const float* pi = in_im + (size_t)b * (H + 1) + tid;
+  float2 a[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    a[e] = valid ? make_float2(ld_stream(pr + T * e), ld_stream(pi + T * e)) : make_float2(0.0f, 0.0f);
+    mre[lds_pad(tid + T * e)] = a[e].x;
+    mim[lds_pad(tid + T * e)] = a[e].y;
+  }
+  if (tid == 0) {
+    mre[lds_pad(H)] = valid ? ld_stream(pr + H) : 0.0f;  // Im X[H] is never read
+    a[0].y = 0.0f;                                       // Im X[0] drops out
+  }
+  exchange_sync<WL>();
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int k = tid + T * e;
+    const int r = lds_pad(H - k);
+    const float2 c = make_float2(mre[r], k == 0 ? 0.0f : -mim[r]);  // conj X[H-k]
+    const float2 sum = cadd(a[e], c);
+    const float2 dif = cmul(csub(a[e], c), make_float2(twr[k].x, -twr[k].y));  // x W_N^-k
+    v[e] = make_float2((sum.x - dif.y) * scale, (sum.y + dif.x) * scale);         // sum + i dif
+  }
+  exchange_sync<WL>();  // the transform below reuses this transform's LDS
+  LdsFft<H, E, 1, WL>::run(v, mre, mim, tw, tid);
+  if (!valid) return;
+  float2* dst = reinterpret_cast<float2*>(x + (size_t)b * (2 * H)) + tid;
+#pragma unroll
+  for (int e = 0; e < E; ++e) st_stream2(dst + T * e, v[e]);
+}
+
+template <int H>
+static hipError_t launch_real_h(const RealArgs& a) {
+  if (a.inverse) {
+    using C = RealCfg<H, real_epth(H, true)>;
+    const long long full = a.batch / C::XF;
+    if (full > 0)
+      hipLaunchKernelGGL((c2r_kernel<H, false>), dim3((unsigned)full), dim3(C::THREADS), 0, a.stream, a.in_re,
+                         a.in_im, a.out_re, a.tw, a.twr, 0LL, a.batch, a.scale);
+    if (full * C::XF < a.batch)
+      hipLaunchKernelGGL((c2r_kernel<H, true>), dim3(1), dim3(C::THREADS), 0, a.stream, a.in_re, a.in_im, a.out_re,
+                         a.tw, a.twr, full * C::XF, a.batch, a.scale);
+  } else {
+    using C = RealCfg<H, real_epth(H, false)>;
+    const long long full = a.batch / C::XF;
+    if (full > 0)
+      hipLaunchKernelGGL((r2c_kernel<H, false>), dim3((unsigned)full), dim3(C::THREADS), 0, a.stream, a.in_re,
+                         a.out_re, a.out_im, a.tw, a.twr, 0LL, a.batch);
+    if (full * C::XF < a.batch)
+      hipLaunchKernelGGL((r2c_kernel<H, true>), dim3(1), dim3(C::THREADS), 0, a.stream, a.in_re, a.out_re,
+                         a.out_im, a.tw, a.twr, full * C::XF, a.batch);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_real(int n, const RealArgs& a) {
+  switch (n) {
+    case 4: return launch_real_h<2>(a);
+    case 8: return launch_real_h<4>(a);
+    case 16: return launch_real_h<8>(a);
+    case 32: return launch_real_h<16>(a);
+    case 64: return launch_real_h<32>(a);
+    case 128: return launch_real_h<64>(a);
+    case 256: return launch_real_h<128>(a);
+    case 512: return launch_real_h<256>(a);
+    case 1024: return launch_real_h<512>(a);
+    case 2048: return launch_real_h<1024>(a);
+    case 4096: return launch_real_h<2048>(a);
+    case 8192: return launch_real_h<4096>(a);
+    case 16384: return launch_real_h<8192>(a);
+    case 32768: return launch_real_h<16384>(a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace tfa

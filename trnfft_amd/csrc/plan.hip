@@ -41,8 +41,8 @@ float2 unit_root(int64_t num, int64_t den, int dir) {
 }
 
 // Twiddle table of the LDS Stockham transform of length n (layout of tfa::make_shape).
-std::vector<float2> lds_table(int n, int dir) {
-  const LdsShape s = tfa::make_shape(n, tfa::lds_epth(n));
+std::vector<float2> lds_table(int n, int dir, int e = 0) {
+  const LdsShape s = tfa::make_shape(n, e ? e : tfa::lds_epth(n));
   std::vector<float2> t((size_t)s.twoff[s.npass] + 2, make_float2(1.0f, 0.0f));
   for (int p = 1; p < s.npass; ++p) {
     const int r = s.radix[p], ls = s.ls[p];
@@ -78,6 +78,7 @@ struct tfa_plan {
   float2* hs = nullptr;
   C2cTables col;          // FFT2: LDS table for n2/8 (pass 2)
   float2* tw_h = nullptr;  // FFT2: W_{n2}^i, i < n2
+  float2* twr = nullptr;  // REAL: W_n^k, k < n/2
   float* w_re = nullptr;  // DFT-GEMM matrix
   float* w_im = nullptr;
   std::vector<void*> allocs;
@@ -275,6 +276,21 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       rc = p->upload(th, &p->tw_h);
       break;
     }
+    case TFA_KIND_REAL: {
+      if (!is_pow2(n) || n < 4 || n > 2 * kMaxLdsN) {
+        rc = fail(TFA_ERR_UNSUPPORTED, "real-input plans need a power-of-two n in [4, 32768]");
+        break;
+      }
+      // half-length transform table for the real kernels' own elements-per-thread choice
+      C2cTables* t = dir < 0 ? &p->fwd : &p->inv;
+      t->n = n / 2;
+      t->dir = dir;
+      if ((rc = p->upload(lds_table((int)(n / 2), dir, tfa::real_epth((int)(n / 2), dir > 0)), &t->tw))) break;
+      std::vector<float2> tr((size_t)(n / 2));
+      for (int64_t k = 0; k < n / 2; ++k) tr[(size_t)k] = unit_root(k, n, -1);
+      rc = p->upload(tr, &p->twr);
+      break;
+    }
     case TFA_KIND_DFT_GEMM: {
       if (n > 4096) {
         rc = fail(TFA_ERR_UNSUPPORTED, "DFT-GEMM plans are limited to n <= 4096");
@@ -330,7 +346,8 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
   if (!plan) return fail(TFA_ERR_INVALID, "null plan");
   if (batch < 0) return fail(TFA_ERR_INVALID, "negative batch");
   if (batch == 0) return TFA_OK;
-  if (!in_re || !out_re || !out_im) return fail(TFA_ERR_INVALID, "null data pointer");
+  const bool c2r = plan->d.kind == TFA_KIND_REAL && plan->d.inverse;
+  if (!in_re || !out_re || (!out_im && !c2r)) return fail(TFA_ERR_INVALID, "null data pointer");
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
     return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
@@ -369,6 +386,18 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
       tfa::Fft2Args f{in_re, in_im, out_re, out_im, plan->fwd.tw, plan->col.tw, plan->tw_h, batch, h, n, s2, plan->fwd.dir, s};
       hipError_t e = tfa::launch_fft2(f);
       return e == hipSuccess ? TFA_OK : hip_fail(e, "fft2 launch");
+    }
+    case TFA_KIND_REAL: {
+      const float* rows = c2r ? out_re : in_re;
+      if (reinterpret_cast<uintptr_t>(rows) % 8 != 0) return fail(TFA_ERR_INVALID, "real rows must be 8-byte aligned");
+      if (c2r ? !in_im : in_im != nullptr)
+        return fail(TFA_ERR_INVALID, c2r ? "c2r needs both input planes" : "r2c takes real input (in_im must be NULL)");
+      if (in_re == out_re || (c2r && in_im == out_re) || (!c2r && in_re == out_im))
+        return fail(TFA_ERR_INVALID, "real transforms are out-of-place only");
+      const C2cTables& t = c2r ? plan->inv : plan->fwd;
+      tfa::RealArgs a{in_re, in_im, out_re, out_im, t.tw, plan->twr, batch, scale, c2r, s};
+      hipError_t e = tfa::launch_real((int)n, a);
+      return e == hipSuccess ? TFA_OK : hip_fail(e, "real transform launch");
     }
     case TFA_KIND_DFT_GEMM: {
       if (!in_im) return fail(TFA_ERR_INVALID, "DFT-GEMM needs both input planes");

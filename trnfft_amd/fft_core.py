@@ -78,6 +78,55 @@ def execute_1d(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> Comp
     return out if out_dev == dev else out.to(out_dev)
 
 
+# real-row transforms through a half-length complex transform: power-of-two n in this range
+_REAL_MIN_N, _REAL_MAX_N = 4, 32768
+
+
+def real_ok(n: int) -> bool:
+    return _REAL_MIN_N <= n <= _REAL_MAX_N and (n & (n - 1)) == 0
+
+
+def _aligned8(t: torch.Tensor) -> torch.Tensor:
+    return t if t.data_ptr() % 8 == 0 else t.clone()
+
+
+def execute_r2c(x: torch.Tensor) -> ComplexTensor:
+    """Bins 0..n/2 of the transform of real rows (the last dimension), n a power of two in
+    [4, 32768]: one half-length complex transform per row (replaces trnfft/api.py:38-46, which
+    runs a full complex transform of (x, 0) and slices)."""
+    n = x.shape[-1]
+    dev = target_device(x, None)
+    out_dev = x.device
+    x = _aligned8(to_device_f32(x, dev).contiguous())
+    batch = x.numel() // n
+    plan = native_plan(_lib.KIND_REAL, n, False, dev.index)
+    shape = (*x.shape[:-1], n // 2 + 1)
+    out_re = torch.empty(shape, dtype=torch.float32, device=dev)
+    out_im = torch.empty(shape, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_execute(plan.handle, batch, ptr(x), None, ptr(out_re), ptr(out_im), None, stream_handle(dev))
+    _lib.check(rc, "tfa_execute")
+    out = ComplexTensor._wrap(out_re, out_im)
+    return out if out_dev == dev else out.to(out_dev)
+
+
+def execute_c2r(re: torch.Tensor, im: torch.Tensor, n: int) -> torch.Tensor:
+    """Real rows of length n from bins 0..n/2 (n = 2*(bins-1), a power of two in [4, 32768]),
+    scaled 1/n (replaces trnfft/api.py:49-68's Hermitian completion + complex inverse + .real)."""
+    assert re.shape[-1] == n // 2 + 1
+    dev = target_device(re, im)
+    out_dev = re.device
+    re = to_device_f32(re, dev).contiguous()
+    im = to_device_f32(im, dev).contiguous()
+    batch = re.numel() // (n // 2 + 1)
+    plan = native_plan(_lib.KIND_REAL, n, True, dev.index)
+    out = torch.empty((*re.shape[:-1], n), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_execute(plan.handle, batch, ptr(re), ptr(im), ptr(out), None, None, stream_handle(dev))
+    _lib.check(rc, "tfa_execute")
+    return out if out_dev == dev else out.to(out_dev)
+
+
 # longest power-of-two axis the strided kernel transforms in place of a transpose round trip
 _STRIDED_MAX_N = 4096
 
