@@ -124,6 +124,25 @@ int tfa_complex_gemm(int64_t m, int64_t n, int64_t k, const float* a_re, const f
                      const float* bias_re, const float* bias_im, float* c_re, float* c_im,
                      int64_t ldc, tfa_stream stream);
 
+/* Operand ops of tfa_complex_gemm_ex (BLAS-style, plus conjugation without transpose). */
+#define TFA_OP_N 0 /* op(X) = X          */
+#define TFA_OP_T 1 /* op(X) = X^T        */
+#define TFA_OP_C 2 /* op(X) = conj(X)^T  */
+#define TFA_OP_R 3 /* op(X) = conj(X)    */
+
+/*
+ * General complex GEMM on split planes: C = alpha * op(A) @ op(B) + bias, op(A) (m, k), op(B)
+ * (k, n).  A is stored (m, k), or (k, m) for TFA_OP_T/TFA_OP_C, with row stride lda; B is stored
+ * (k, n), or (n, k) for TFA_OP_T/TFA_OP_C, with row stride ldb.  These are the adjoint products
+ * of trnfft/nki/autograd.py:92-155 (_ComplexGEMMFn.backward dA = dC B^H, dB = A^H dC;
+ * _ComplexLinearFn.backward dX = dY conj(W), dW = dY^T conj(X)), which the reference runs as
+ * eight real torch matmuls; here each is one launch.
+ */
+int tfa_complex_gemm_ex(int64_t m, int64_t n, int64_t k, const float* a_re, const float* a_im, int64_t lda,
+                        int32_t a_op, const float* b_re, const float* b_im, int64_t ldb, int32_t b_op, float alpha,
+                        const float* bias_re, const float* bias_im, float* c_re, float* c_im, int64_t ldc,
+                        tfa_stream stream);
+
 /* Thread-local message describing the last failure on this thread ("" if none). */
 const char* tfa_last_error(void);
 

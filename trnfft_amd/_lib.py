@@ -24,6 +24,9 @@ KIND_STFT = 3
 KIND_FFT2 = 4
 KIND_REAL = 5
 
+# operand ops of tfa_complex_gemm_ex
+OP_N, OP_T, OP_C, OP_R = 0, 1, 2, 3
+
 STFT_CENTER = 1
 STFT_NORMALIZED = 2
 STFT_ONESIDED = 4
@@ -39,6 +42,7 @@ EXPORTS = (
     "tfa_stft_frames",
     "tfa_stft_execute",
     "tfa_complex_gemm",
+    "tfa_complex_gemm_ex",
     "tfa_last_error",
     "tfa_abi_version",
 )
@@ -82,6 +86,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tfa_stft_execute.restype = ctypes.c_int
     lib.tfa_complex_gemm.argtypes = [_i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _vp]
     lib.tfa_complex_gemm.restype = ctypes.c_int
+    lib.tfa_complex_gemm_ex.argtypes = [_i64, _i64, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i32, ctypes.c_float,
+                                        _vp, _vp, _vp, _vp, _i64, _vp]
+    lib.tfa_complex_gemm_ex.restype = ctypes.c_int
     lib.tfa_last_error.argtypes = []
     lib.tfa_last_error.restype = ctypes.c_char_p
     lib.tfa_abi_version.argtypes = []

@@ -13,18 +13,9 @@ import torch
 
 from . import _lib
 from .complex import ComplexTensor
-from .dispatch import _require_hip, ptr, stream_handle, target_device, to_device_f32
-from .fft_core import (
-    execute_1d,
-    execute_c2r,
-    execute_fft2,
-    execute_r2c,
-    execute_strided,
-    fft2_ok,
-    fft_core,
-    real_ok,
-    strided_ok,
-)
+from .dispatch import _require_hip, target_device, to_device_f32
+from . import autograd as _ag
+from .fft_core import fft2_ok, fft_core, real_ok, strided_ok
 from .plan import native_plan
 from .precision import _resolve
 
@@ -61,7 +52,7 @@ def _real_1d(x: torch.Tensor, inverse: bool) -> ComplexTensor:
     if x.shape[-1] == 1:
         return ComplexTensor(x.clone())
     _require_hip("fft")
-    return execute_1d(x.contiguous(), None, inverse)
+    return _ag.c2c(x, None, inverse)
 
 
 def rfft(input: torch.Tensor, n: int | None = None) -> ComplexTensor:
@@ -72,7 +63,7 @@ def rfft(input: torch.Tensor, n: int | None = None) -> ComplexTensor:
     if real_ok(n):
         _resolve(None)
         _require_hip("rfft")
-        return execute_r2c(input)
+        return _ag.r2c(input)
     result = _real_1d(input, inverse=False)
     half = n // 2 + 1
     return ComplexTensor(result.real[..., :half], result.imag[..., :half])
@@ -85,7 +76,7 @@ def irfft(input: ComplexTensor, n: int | None = None) -> torch.Tensor:
     if n == 2 * (input.shape[-1] - 1) and real_ok(n):
         _resolve(None)
         _require_hip("irfft")
-        return execute_c2r(input.real, input.imag, n)
+        return _ag.c2r(input.real, input.imag, n)
     dev = input.real.device
     full_re = torch.zeros(*input.shape[:-1], n, dtype=input.dtype, device=dev)
     full_im = torch.zeros(*input.shape[:-1], n, dtype=input.dtype, device=dev)
@@ -161,8 +152,8 @@ def _fftn(input, s, dim, inverse: bool) -> ComplexTensor:
         _resolve(None)
         _require_hip("fft2")
         if real_in:
-            return execute_fft2(x.contiguous(), None, inverse)
-        return execute_fft2(x.real, x.imag, inverse)
+            return _ag.fft2(x, None, inverse)
+        return _ag.fft2(x.real, x.imag, inverse)
     order = list(dim)
     if real_in and (ndim - 1) in order:
         # real input: transform the contiguous last axis first (it reads only the real plane);
@@ -289,7 +280,6 @@ def stft(
     out_dev = input.device
     x = to_device_f32(input, dev)
     win = to_device_f32(win, dev)
-    lead = x.shape[:-1]
     length = x.shape[-1]
     if center and pad_mode != "reflect":
         raise NotImplementedError(f"stft pad_mode={pad_mode!r}: only 'reflect' is implemented")
@@ -298,20 +288,8 @@ def stft(
     num_frames = stft_num_frames(length, n_fft, hop_length, center)
     if num_frames < 1:
         raise ValueError(f"signal of {length} samples is shorter than n_fft={n_fft}")
-    flags = (_lib.STFT_CENTER if center else 0) | (_lib.STFT_NORMALIZED if normalized else 0)
-    flags |= _lib.STFT_ONESIDED if onesided else 0
-    plan = native_plan(_lib.KIND_STFT, n_fft, False, dev.index, hop=hop_length, flags=flags)
-    bins = n_fft // 2 + 1 if onesided else n_fft
-    batch = 1
-    for d in lead:
-        batch *= d
-    out_re = torch.empty(*lead, bins, num_frames, dtype=torch.float32, device=dev)
-    out_im = torch.empty_like(out_re)
-    with torch.cuda.device(dev):
-        rc = _lib.lib().tfa_stft_execute(
-            plan.handle, batch, length, ptr(x), ptr(win), ptr(out_re), ptr(out_im), stream_handle(dev)
-        )
-    _lib.check(rc, "tfa_stft_execute")
+    out = _ag.stft(x, win, n_fft, hop_length, center, normalized, onesided, num_frames)
+    out_re, out_im = out.real, out.imag
     if center and x.dim() == 2 and x.shape[0] == 1:
         # the reference squeezes a (1, L) signal to 1-D after padding (trnfft/api.py:313-315),
         # so its result has no batch axis; keep that shape for drop-in compatibility
@@ -453,8 +431,8 @@ def _fft_along_dim(x, dim: int, inverse: bool) -> ComplexTensor:
         _resolve(None)
         _require_hip("fftn")
         if real_in:
-            return execute_strided(x.contiguous(), None, dim, inverse)
-        return execute_strided(x.real, x.imag, dim, inverse)
+            return _ag.c2c_strided(x, None, dim, inverse)
+        return _ag.c2c_strided(x.real, x.imag, dim, inverse)
     if real_in:
         moved = x.transpose(dim, -1).contiguous()
         res = _real_1d(moved, inverse)

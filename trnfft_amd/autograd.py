@@ -1,0 +1,304 @@
+"""Autograd for the HIP path (the role of trnfft/nki/autograd.py:1-205).
+
+The reference's pytorch path is differentiable because it is made of torch ops; its NKI kernels
+are wrapped in ``torch.autograd.Function`` classes whose backward emits the analytic adjoint
+(trnfft/nki/autograd.py:125-155 complex linear, :92-112 complex GEMM, :167-205 FFT).  Here every
+native launch that can sit on a training path is wrapped the same way, and the backward runs on
+the same native kernels:
+
+* c2c, any length, last axis / strided axis / both trailing axes (forward F, unnormalised):
+      dx = n * F^-1(dy);   inverse (F^-1, scaled 1/n):  dx = F(dy) / n
+  (trnfft/nki/autograd.py:190-203); for real input the gradient is the real part.
+* r2c (rfft, bins 0..n/2):  dx_j = Re sum_k dy_k e^{+2 pi i j k / n} = n * c2r(dy'), where dy'
+  halves bins 1..n/2-1 (c2r doubles them back and drops Im of bins 0 and n/2, whose real parts
+  are the only ones that reach a real signal).
+* c2r (irfft):  dX = r2c(dy) / n with bins 1..n/2-1 doubled (they appear twice in the
+  Hermitian-completed spectrum); bins 0 and n/2 get no imaginary gradient.
+* STFT: per-frame adjoint of the onesided (c2r as above) or two-sided (c2c) transform, times
+  the window, overlap-added back onto the padded signal (torch fold), then the reflect-pad
+  adjoint folds the padded edges back into the signal.  The window gradient, when asked for,
+  is the frame-by-frame correlation of the padded signal with the unwindowed frame gradient.
+* complex GEMM C = A B:            dA = dC B^H,  dB = A^H dC
+  complex linear Y = X W^T + b:    dX = dY conj(W),  dW = dY^T conj(X),  db = sum over rows of dY
+  each product one tfa_complex_gemm_ex launch (the reference runs eight real matmuls).
+
+Second derivatives are not provided (the backward passes are themselves not differentiable).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+from torch.autograd.function import once_differentiable
+
+from . import _lib
+from . import fft_core as _fc
+from .complex import ComplexTensor
+
+
+def _grad_on(*ts) -> bool:
+    return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in ts)
+
+
+def _c(t: torch.Tensor) -> torch.Tensor:
+    return t.contiguous()
+
+
+# ---------------------------------------------------------------------------------------------
+# c2c: last axis, strided axis, both trailing axes
+# ---------------------------------------------------------------------------------------------
+
+
+class _C2CFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, re, im, inverse: bool, mode: str, dim: int):
+        ctx.inverse, ctx.mode, ctx.dim, ctx.real_in = inverse, mode, dim, im is None
+        if mode == "last":
+            ctx.size = re.shape[-1]
+            y = _fc.execute_1d(re, im, inverse)
+        elif mode == "strided":
+            ctx.size = re.shape[dim]
+            y = _fc.execute_strided(re, im, dim, inverse)
+        else:  # "fft2"
+            ctx.size = re.shape[-1] * re.shape[-2]
+            y = _fc.execute_fft2(re, im, inverse)
+        return y.real, y.imag
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, g_re, g_im):
+        adj = not ctx.inverse
+        g_re, g_im = _c(g_re), _c(g_im)
+        if ctx.mode == "last":
+            g = _fc.execute_1d(g_re, g_im, adj)
+        elif ctx.mode == "strided":
+            g = _fc.execute_strided(g_re, g_im, ctx.dim, adj)
+        else:
+            g = _fc.execute_fft2(g_re, g_im, adj)
+        s = 1.0 / ctx.size if ctx.inverse else float(ctx.size)
+        d_re = g.real.mul_(s)
+        d_im = None if ctx.real_in else g.imag.mul_(s)
+        return d_re, d_im, None, None, None
+
+
+def _c2c(re, im, inverse, mode, dim=-1) -> ComplexTensor:
+    if _grad_on(re, im):
+        y_re, y_im = _C2CFn.apply(re, im, inverse, mode, dim)
+        return ComplexTensor._wrap(y_re, y_im)
+    if mode == "last":
+        return _fc.execute_1d(re, im, inverse)
+    if mode == "strided":
+        return _fc.execute_strided(re, im, dim, inverse)
+    return _fc.execute_fft2(re, im, inverse)
+
+
+def c2c(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> ComplexTensor:
+    """Last-axis transform (im None: real input), differentiable."""
+    return _c2c(re, im, inverse, "last")
+
+
+def c2c_strided(re: torch.Tensor, im: torch.Tensor | None, dim: int, inverse: bool) -> ComplexTensor:
+    """Transform along axis `dim` in place of a transpose round trip, differentiable."""
+    return _c2c(re, im, inverse, "strided", dim)
+
+
+def fft2(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> ComplexTensor:
+    """Transform over the two trailing axes, differentiable."""
+    return _c2c(re, im, inverse, "fft2")
+
+
+# ---------------------------------------------------------------------------------------------
+# real rows: r2c / c2r
+# ---------------------------------------------------------------------------------------------
+
+
+def _r2c_adjoint(g_re: torch.Tensor, g_im: torch.Tensor, n: int) -> torch.Tensor:
+    h = n // 2
+    g_re, g_im = g_re.clone(), g_im.clone()
+    g_re[..., 1:h] *= 0.5
+    g_im[..., 1:h] *= 0.5
+    return _fc.execute_c2r(g_re, g_im, n).mul_(float(n))
+
+
+def _c2r_adjoint(g: torch.Tensor, n: int):
+    h = n // 2
+    y = _fc.execute_r2c(_c(g))
+    d_re, d_im = y.real.mul_(1.0 / n), y.imag.mul_(1.0 / n)
+    d_re[..., 1:h] *= 2.0
+    d_im[..., 1:h] *= 2.0
+    d_im[..., 0] = 0.0
+    d_im[..., h] = 0.0
+    return d_re, d_im
+
+
+class _R2CFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        ctx.n = x.shape[-1]
+        y = _fc.execute_r2c(x)
+        return y.real, y.imag
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, g_re, g_im):
+        return _r2c_adjoint(g_re, g_im, ctx.n)
+
+
+class _C2RFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, re, im, n: int):
+        ctx.n = n
+        return _fc.execute_c2r(re, im, n)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, g):
+        d_re, d_im = _c2r_adjoint(g, ctx.n)
+        return d_re, d_im, None
+
+
+def r2c(x: torch.Tensor) -> ComplexTensor:
+    if _grad_on(x):
+        y_re, y_im = _R2CFn.apply(x)
+        return ComplexTensor._wrap(y_re, y_im)
+    return _fc.execute_r2c(x)
+
+
+def c2r(re: torch.Tensor, im: torch.Tensor, n: int) -> torch.Tensor:
+    if _grad_on(re, im):
+        return _C2RFn.apply(re, im, n)
+    return _fc.execute_c2r(re, im, n)
+
+
+# ---------------------------------------------------------------------------------------------
+# STFT
+# ---------------------------------------------------------------------------------------------
+
+
+class _StftFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, win, n_fft, hop, center, normalized, onesided, num_frames):
+        ctx.save_for_backward(x, win)
+        ctx.cfg = (n_fft, hop, center, normalized, onesided, num_frames)
+        return _fc.execute_stft(x, win, n_fft, hop, center, normalized, onesided, num_frames)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, g_re, g_im):
+        x, win = ctx.saved_tensors
+        n_fft, hop, center, normalized, onesided, frames = ctx.cfg
+        length = x.shape[-1]
+        lead = x.shape[:-1]
+        b = x.numel() // length
+        bins = g_re.shape[-2]
+        # (..., bins, frames) -> (b, frames, bins): one spectrum per row
+        gr = g_re.reshape(b, bins, frames).transpose(1, 2).contiguous()
+        gi = g_im.reshape(b, bins, frames).transpose(1, 2).contiguous()
+        if onesided:
+            fg = _r2c_adjoint(gr, gi, n_fft)  # (b, frames, n_fft)
+        else:
+            fg = _fc.execute_1d(gr, gi, True).real.mul_(float(n_fft))
+        if normalized:
+            fg.mul_(1.0 / math.sqrt(n_fft))
+        pad = n_fft // 2 if center else 0
+        if center:
+            xp = F.pad(x.reshape(b, 1, length), (pad, pad), mode="reflect").reshape(b, -1)
+        else:
+            xp = x.reshape(b, length)
+        lp = xp.shape[-1]
+        d_win = None
+        if ctx.needs_input_grad[1]:
+            fr = xp.unfold(-1, n_fft, hop)[:, :frames]  # (b, frames, n_fft)
+            d_win = (fr * fg).sum(dim=(0, 1))
+        d_x = None
+        if ctx.needs_input_grad[0]:
+            fg.mul_(win)
+            d_xp = F.fold(fg.transpose(1, 2), output_size=(1, lp), kernel_size=(1, n_fft), stride=(1, hop))
+            d_xp = d_xp.reshape(b, lp)
+            if center:
+                # x_pad[i] = x[pad - i] (i < pad), x_pad[pad + j] = x[j], x_pad[pad + L + i] = x[L - 2 - i]
+                d_x = d_xp[:, pad : pad + length].clone()
+                d_x[:, 1 : pad + 1] += d_xp[:, :pad].flip(-1)
+                d_x[:, length - 1 - pad : length - 1] += d_xp[:, pad + length :].flip(-1)
+            else:
+                d_x = d_xp[:, :length].contiguous()
+            d_x = d_x.reshape(*lead, length)
+        return d_x, d_win, None, None, None, None, None, None
+
+
+def stft(x, win, n_fft, hop, center, normalized, onesided, num_frames) -> ComplexTensor:
+    """Fused STFT kernel on device fp32 x (..., L), window (n_fft); differentiable in x and window."""
+    if _grad_on(x, win):
+        y_re, y_im = _StftFn.apply(x, win, n_fft, hop, center, normalized, onesided, num_frames)
+    else:
+        y_re, y_im = _fc.execute_stft(x, win, n_fft, hop, center, normalized, onesided, num_frames)
+    return ComplexTensor._wrap(y_re, y_im)
+
+
+# ---------------------------------------------------------------------------------------------
+# complex GEMM / linear
+# ---------------------------------------------------------------------------------------------
+
+
+class _ComplexGEMMFn(torch.autograd.Function):
+    """C = A @ op(B) (+ bias), op(B) = B or B^T; A (m, k) 2-D."""
+
+    @staticmethod
+    def forward(ctx, a_re, a_im, b_re, b_im, bias_re, bias_im, b_trans: bool, what: str):
+        from .dispatch import gemm_ex
+
+        ctx.save_for_backward(a_re, a_im, b_re, b_im)
+        ctx.b_trans, ctx.has_bias = b_trans, bias_re is not None
+        return gemm_ex(a_re, a_im, _lib.OP_N, b_re, b_im, _lib.OP_T if b_trans else _lib.OP_N, 1.0,
+                       bias_re, bias_im, what=what)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, g_re, g_im):
+        from .dispatch import gemm_ex
+
+        a_re, a_im, b_re, b_im = ctx.saved_tensors
+        g_re, g_im = _c(g_re), _c(g_im)
+        need = ctx.needs_input_grad
+        da_re = da_im = db_re = db_im = dbias_re = dbias_im = None
+        if need[0] or need[1]:
+            # dA = dC op(B)^H: op(B) = B -> B^H (OP_C of B); op(B) = B^T (linear) -> conj(B) (OP_R)
+            da_re, da_im = gemm_ex(g_re, g_im, _lib.OP_N, b_re, b_im, _lib.OP_R if ctx.b_trans else _lib.OP_C,
+                                   what="complex_gemm backward dA")
+        if need[2] or need[3]:
+            if ctx.b_trans:
+                # B^T = A^H dC  ->  B = dC^T conj(A)
+                db_re, db_im = gemm_ex(g_re, g_im, _lib.OP_T, a_re, a_im, _lib.OP_R, what="complex_gemm backward dB")
+            else:
+                db_re, db_im = gemm_ex(a_re, a_im, _lib.OP_C, g_re, g_im, _lib.OP_N, what="complex_gemm backward dB")
+        if ctx.has_bias and (need[4] or need[5]):
+            dbias_re, dbias_im = g_re.sum(0), g_im.sum(0)
+        return da_re, da_im, db_re, db_im, dbias_re, dbias_im, None, None
+
+
+def gemm(a_re, a_im, b_re, b_im, b_trans: bool, bias_re=None, bias_im=None, what="complex_gemm"):
+    """(c_re, c_im) = A @ op(B) (+ bias) for 2-D device fp32 planes; differentiable."""
+    if _grad_on(a_re, a_im, b_re, b_im, bias_re, bias_im):
+        return _ComplexGEMMFn.apply(a_re, a_im, b_re, b_im, bias_re, bias_im, b_trans, what)
+    from .dispatch import gemm_ex
+
+    return gemm_ex(a_re, a_im, _lib.OP_N, b_re, b_im, _lib.OP_T if b_trans else _lib.OP_N, 1.0, bias_re, bias_im,
+                   what=what)
+
+
+def fft_autograd(x_real: torch.Tensor, x_imag: torch.Tensor, inverse: bool, precision: str = "fast"):
+    """(y_re, y_im) of the last-axis transform, differentiable (trnfft/nki/autograd.py:204-205)."""
+    y = c2c(x_real, x_imag, inverse)
+    return y.real, y.imag
+
+
+def complex_gemm_autograd(a_real, a_imag, b_real, b_imag):
+    """C = A @ B, differentiable (trnfft/nki/autograd.py:115-116)."""
+    return gemm(a_real, a_imag, b_real, b_imag, False)
+
+
+def complex_linear_autograd(x_real, x_imag, w_real, w_imag):
+    """Y = X @ W^T, differentiable (trnfft/nki/autograd.py:158-159)."""
+    return gemm(x_real, x_imag, w_real, w_imag, True, what="complex_linear")

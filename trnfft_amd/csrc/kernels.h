@@ -153,15 +153,17 @@ struct Fft2Args {
 };
 hipError_t launch_fft2(const Fft2Args& a);
 
+// Operand ops of the complex GEMM: 0 = X, 1 = X^T, 2 = conj(X)^T, 3 = conj(X)
 struct GemmArgs {
   long long m, n, k;
   const float* a_re;
   const float* a_im;
   long long lda;
+  int a_op;
   const float* b_re;
   const float* b_im;
   long long ldb;
-  int b_trans;
+  int b_op;
   const float* bias_re;  // nullable
   const float* bias_im;
   float* c_re;

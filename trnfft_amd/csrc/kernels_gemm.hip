@@ -1,7 +1,9 @@
 // Complex GEMM on the fp32 matrix cores (v_mfma_f32_32x32x2f32), split re/im planes.
 //
-//   C = alpha * (A @ op(B)) + bias,  op(B) = B (B is k x n) or B^T (B is n x k, B_TRANS)
-//   C_re = A_re B_re - A_im B_im,  C_im = A_re B_im + A_im B_re
+//   C = alpha * (op(A) @ op(B)) + bias,  op(X) = X, X^T, conj(X)^T or conj(X)
+//   C_re = A_re B_re - A_im B_im,  C_im = A_re B_im + A_im B_re   (on the op'ed operands)
+// A transposed operand is staged through LDS in the same [k][i] layout as a plain one (only the
+// global load pattern differs); conjugation negates the imaginary plane as it is staged.
 //
 // One kernel computes all four real products: each k-step loads the A_re/A_im and B_re/B_im
 // fragments once from LDS and issues four MFMAs into two accumulator sets (the NKI kernel's
@@ -72,29 +74,50 @@ __device__ __forceinline__ void load_nmajor_tile(const float* __restrict__ P_re,
 }
 
 // LDS layout: S[plane][k][i] (i contiguous) so an MFMA operand fragment is 32 consecutive floats.
-__device__ __forceinline__ void store_kmajor(float (*S)[GBK][GLD], int t, const ATile& o) {
+// `sim` (+1 or -1) multiplies the imaginary plane (conjugation).
+__device__ __forceinline__ void store_kmajor(float (*S)[GBK][GLD], int t, const ATile& o, float sim) {
   const int r = t / 2, kq = (t % 2) * 8;
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     S[0][kq + c][r] = o.re[c];
-    S[1][kq + c][r] = o.im[c];
+    S[1][kq + c][r] = o.im[c] * sim;
   }
 }
 
-__device__ __forceinline__ void store_nmajor(float (*S)[GBK][GLD], int t, const ATile& o) {
+__device__ __forceinline__ void store_nmajor(float (*S)[GBK][GLD], int t, const ATile& o, float sim) {
   const int k = t / 16, j = (t % 16) * 8;
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     S[0][k][j + c] = o.re[c];
-    S[1][k][j + c] = o.im[c];
+    S[1][k][j + c] = o.im[c] * sim;
   }
 }
 
-template <bool B_TRANS>
+// Operand staging: A_T = op(A) is a transpose (A stored k x m); B_T = op(B) is a transpose
+// (B stored n x k).  A plain A and a transposed B are k-contiguous; the other two m/n-contiguous.
+template <bool A_T>
+__device__ __forceinline__ void load_a(const float* A_re, const float* A_im, long long lda, int M, int K, int row0,
+                                       int k0, int t, bool vec, ATile& o) {
+  if constexpr (A_T) load_nmajor_tile(A_re, A_im, lda, M, K, row0, k0, t, vec, o);
+  else load_kmajor_tile(A_re, A_im, lda, M, K, row0, k0, t, vec, o);
+}
+template <bool B_T>
+__device__ __forceinline__ void load_b(const float* B_re, const float* B_im, long long ldb, int N, int K, int col0,
+                                       int k0, int t, bool vec, ATile& o) {
+  if constexpr (B_T) load_kmajor_tile(B_re, B_im, ldb, N, K, col0, k0, t, vec, o);
+  else load_nmajor_tile(B_re, B_im, ldb, N, K, col0, k0, t, vec, o);
+}
+template <bool KMAJOR>
+__device__ __forceinline__ void stage(float (*S)[GBK][GLD], int t, const ATile& o, float sim) {
+  if constexpr (KMAJOR) store_kmajor(S, t, o, sim);
+  else store_nmajor(S, t, o, sim);
+}
+
+template <bool A_T, bool B_T>
 __global__ __launch_bounds__(256, 2) void cgemm_kernel(int M, int N, int K, const float* __restrict__ A_re,
-                                                    const float* __restrict__ A_im, long long lda,
+                                                    const float* __restrict__ A_im, long long lda, float a_sim,
                                                     const float* __restrict__ B_re, const float* __restrict__ B_im,
-                                                    long long ldb, const float* __restrict__ bias_re,
+                                                    long long ldb, float b_sim, const float* __restrict__ bias_re,
                                                     const float* __restrict__ bias_im, float* __restrict__ C_re,
                                                     float* __restrict__ C_im, long long ldc, float alpha) {
   __shared__ float As[2][GBK][GLD];
@@ -123,21 +146,18 @@ __global__ __launch_bounds__(256, 2) void cgemm_kernel(int M, int N, int K, cons
       }
 
   ATile pa, pb;
-  load_kmajor_tile(A_re, A_im, lda, M, K, row0, 0, t, a_vec, pa);
-  if constexpr (B_TRANS) load_kmajor_tile(B_re, B_im, ldb, N, K, col0, 0, t, b_vec, pb);
-  else load_nmajor_tile(B_re, B_im, ldb, N, K, col0, 0, t, b_vec, pb);
+  load_a<A_T>(A_re, A_im, lda, M, K, row0, 0, t, a_vec, pa);
+  load_b<B_T>(B_re, B_im, ldb, N, K, col0, 0, t, b_vec, pb);
 
   const int li = lane & 31;
   const int lk = lane >> 5;
   for (int k0 = 0; k0 < K; k0 += GBK) {
-    store_kmajor(As, t, pa);
-    if constexpr (B_TRANS) store_kmajor(Bs, t, pb);
-    else store_nmajor(Bs, t, pb);
+    stage<!A_T>(As, t, pa, a_sim);
+    stage<B_T>(Bs, t, pb, b_sim);
     __syncthreads();
     if (k0 + GBK < K) {
-      load_kmajor_tile(A_re, A_im, lda, M, K, row0, k0 + GBK, t, a_vec, pa);
-      if constexpr (B_TRANS) load_kmajor_tile(B_re, B_im, ldb, N, K, col0, k0 + GBK, t, b_vec, pb);
-      else load_nmajor_tile(B_re, B_im, ldb, N, K, col0, k0 + GBK, t, b_vec, pb);
+      load_a<A_T>(A_re, A_im, lda, M, K, row0, k0 + GBK, t, a_vec, pa);
+      load_b<B_T>(B_re, B_im, ldb, N, K, col0, k0 + GBK, t, b_vec, pb);
     }
 #pragma unroll
     for (int kk = 0; kk < GBK; kk += 2) {
@@ -186,16 +206,25 @@ __global__ __launch_bounds__(256, 2) void cgemm_kernel(int M, int N, int K, cons
     }
 }
 
+template <bool A_T, bool B_T>
+static void launch_cgemm_t(const GemmArgs& a, long long tiles) {
+  const float a_sim = (a.a_op == 2 || a.a_op == 3) ? -1.0f : 1.0f;
+  const float b_sim = (a.b_op == 2 || a.b_op == 3) ? -1.0f : 1.0f;
+  hipLaunchKernelGGL((cgemm_kernel<A_T, B_T>), dim3((unsigned)tiles), dim3(256), 0, a.stream, (int)a.m, (int)a.n,
+                     (int)a.k, a.a_re, a.a_im, a.lda, a_sim, a.b_re, a.b_im, a.ldb, b_sim, a.bias_re, a.bias_im,
+                     a.c_re, a.c_im, a.ldc, a.alpha);
+}
+
 hipError_t launch_cgemm(const GemmArgs& a) {
   const long long tiles = ((a.m + GBM - 1) / GBM) * ((a.n + GBN - 1) / GBN);
-  if (a.b_trans)
-    hipLaunchKernelGGL((cgemm_kernel<true>), dim3((unsigned)tiles), dim3(256), 0, a.stream, (int)a.m, (int)a.n,
-                       (int)a.k, a.a_re, a.a_im, a.lda, a.b_re, a.b_im, a.ldb, a.bias_re, a.bias_im, a.c_re,
-                       a.c_im, a.ldc, a.alpha);
-  else
-    hipLaunchKernelGGL((cgemm_kernel<false>), dim3((unsigned)tiles), dim3(256), 0, a.stream, (int)a.m, (int)a.n,
-                       (int)a.k, a.a_re, a.a_im, a.lda, a.b_re, a.b_im, a.ldb, a.bias_re, a.bias_im, a.c_re,
-                       a.c_im, a.ldc, a.alpha);
+  const bool at = a.a_op == 1 || a.a_op == 2, bt = a.b_op == 1 || a.b_op == 2;
+  if (at) {
+    if (bt) launch_cgemm_t<true, true>(a, tiles);
+    else launch_cgemm_t<true, false>(a, tiles);
+  } else {
+    if (bt) launch_cgemm_t<false, true>(a, tiles);
+    else launch_cgemm_t<false, false>(a, tiles);
+  }
   return hipGetLastError();
 }
 

@@ -402,8 +402,8 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
     case TFA_KIND_DFT_GEMM: {
       if (!in_im) return fail(TFA_ERR_INVALID, "DFT-GEMM needs both input planes");
       // X = x @ W (W symmetric, so x @ W^T), scaled 1/n when inverse
-      tfa::GemmArgs g{batch, n, n, in_re, in_im, n, plan->w_re, plan->w_im, n, 1, nullptr, nullptr,
-                      out_re, out_im, n, scale, s};
+      tfa::GemmArgs g{batch, n, n, in_re, in_im, n, TFA_OP_N, plan->w_re, plan->w_im, n, TFA_OP_T,
+                      nullptr, nullptr, out_re, out_im, n, scale, s};
       hipError_t e = tfa::launch_cgemm(g);
       return e == hipSuccess ? TFA_OK : hip_fail(e, "dft-gemm launch");
     }
@@ -465,20 +465,32 @@ int tfa_stft_execute(const tfa_plan* plan, int64_t batch, int64_t num_samples, c
   return e == hipSuccess ? TFA_OK : hip_fail(e, "stft launch");
 }
 
+int tfa_complex_gemm_ex(int64_t m, int64_t n, int64_t k, const float* a_re, const float* a_im, int64_t lda,
+                        int32_t a_op, const float* b_re, const float* b_im, int64_t ldb, int32_t b_op, float alpha,
+                        const float* bias_re, const float* bias_im, float* c_re, float* c_im, int64_t ldc,
+                        tfa_stream stream) {
+  if (m < 0 || n < 0 || k < 0) return fail(TFA_ERR_INVALID, "negative dimension");
+  if (a_op < TFA_OP_N || a_op > TFA_OP_R || b_op < TFA_OP_N || b_op > TFA_OP_R)
+    return fail(TFA_ERR_INVALID, "operand op must be TFA_OP_N, _T, _C or _R");
+  if (m == 0 || n == 0) return TFA_OK;
+  if (!a_re || !a_im || !b_re || !b_im || !c_re || !c_im) return fail(TFA_ERR_INVALID, "null data pointer");
+  if ((bias_re == nullptr) != (bias_im == nullptr)) return fail(TFA_ERR_INVALID, "bias needs both planes or neither");
+  const bool at = a_op == TFA_OP_T || a_op == TFA_OP_C, bt = b_op == TFA_OP_T || b_op == TFA_OP_C;
+  // stored shapes: A is (m, k) or (k, m) when transposed; B is (k, n) or (n, k) when transposed
+  if (lda < (at ? m : k) || ldb < (bt ? k : n) || ldc < n) return fail(TFA_ERR_INVALID, "leading dimension too small");
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return fail(TFA_ERR_UNSUPPORTED, "dimension above 2^31");
+  tfa::GemmArgs g{m, n, k, a_re, a_im, lda, a_op, b_re, b_im, ldb, b_op, bias_re, bias_im,
+                  c_re, c_im, ldc, alpha, static_cast<hipStream_t>(stream)};
+  hipError_t e = tfa::launch_cgemm(g);
+  return e == hipSuccess ? TFA_OK : hip_fail(e, "complex gemm launch");
+}
+
 int tfa_complex_gemm(int64_t m, int64_t n, int64_t k, const float* a_re, const float* a_im,
                      int64_t lda, const float* b_re, const float* b_im, int64_t ldb, int32_t b_trans,
                      const float* bias_re, const float* bias_im, float* c_re, float* c_im,
                      int64_t ldc, tfa_stream stream) {
-  if (m < 0 || n < 0 || k < 0) return fail(TFA_ERR_INVALID, "negative dimension");
-  if (m == 0 || n == 0) return TFA_OK;
-  if (!a_re || !a_im || !b_re || !b_im || !c_re || !c_im) return fail(TFA_ERR_INVALID, "null data pointer");
-  if ((bias_re == nullptr) != (bias_im == nullptr)) return fail(TFA_ERR_INVALID, "bias needs both planes or neither");
-  if (lda < k || ldc < n || ldb < (b_trans ? k : n)) return fail(TFA_ERR_INVALID, "leading dimension too small");
-  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return fail(TFA_ERR_UNSUPPORTED, "dimension above 2^31");
-  tfa::GemmArgs g{m, n, k, a_re, a_im, lda, b_re, b_im, ldb, b_trans ? 1 : 0, bias_re, bias_im,
-                  c_re, c_im, ldc, 1.0f, static_cast<hipStream_t>(stream)};
-  hipError_t e = tfa::launch_cgemm(g);
-  return e == hipSuccess ? TFA_OK : hip_fail(e, "complex gemm launch");
+  return tfa_complex_gemm_ex(m, n, k, a_re, a_im, lda, TFA_OP_N, b_re, b_im, ldb, b_trans ? TFA_OP_T : TFA_OP_N,
+                             1.0f, bias_re, bias_im, c_re, c_im, ldc, stream);
 }
 
 }  // extern "C"

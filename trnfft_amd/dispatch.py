@@ -106,33 +106,46 @@ def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
 
 
+def gemm_ex(a_re, a_im, a_op: int, b_re, b_im, b_op: int, alpha: float = 1.0, bias_re=None, bias_im=None,
+            what: str = "complex_gemm"):
+    """C = alpha * op(A) @ op(B) (+ bias) on the MFMA kernel for 2-D device fp32 planes; returns
+    (c_re, c_im).  op: _lib.OP_N (X), OP_T (X^T), OP_C (conj(X)^T), OP_R (conj(X))."""
+    dev = a_re.device
+    a_re, a_im, b_re, b_im = (t.contiguous() for t in (a_re, a_im, b_re, b_im))
+    at = a_op in (_lib.OP_T, _lib.OP_C)
+    bt = b_op in (_lib.OP_T, _lib.OP_C)
+    m, k = (a_re.shape[1], a_re.shape[0]) if at else a_re.shape
+    kb, n = (b_re.shape[1], b_re.shape[0]) if bt else b_re.shape
+    if kb != k:
+        raise ValueError(f"{what}: inner dimensions differ ({k} vs {kb})")
+    c_re = torch.empty(m, n, device=dev, dtype=torch.float32)
+    c_im = torch.empty(m, n, device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_complex_gemm_ex(
+            m, n, k, ptr(a_re), ptr(a_im), a_re.shape[1], a_op, ptr(b_re), ptr(b_im), b_re.shape[1], b_op,
+            float(alpha), ptr(bias_re), ptr(bias_im), ptr(c_re), ptr(c_im), n, stream_handle(dev),
+        )
+    _lib.check(rc, what)
+    return c_re, c_im
+
+
 def _gemm(a_re, a_im, b_re, b_im, b_trans: bool, bias_re=None, bias_im=None, what="complex_gemm"):
+    """op(B) = B or B^T; A's leading dimensions are batch rows.  Differentiable (the adjoint
+    products run on the same kernel)."""
+    from . import autograd as _ag
+
     _require_hip(what)
     dev = target_device(a_re, b_re)
     out_dev = a_re.device
     a_re, a_im = to_device_f32(a_re, dev), to_device_f32(a_im, dev)
     b_re, b_im = to_device_f32(b_re, dev), to_device_f32(b_im, dev)
     bias_re, bias_im = to_device_f32(bias_re, dev), to_device_f32(bias_im, dev)
+    if b_re.dim() != 2:
+        raise ValueError(f"{what}: expects a 2-D right operand")
     lead = a_re.shape[:-1]
     k = a_re.shape[-1]
-    m = 1
-    for s in lead:
-        m *= s
-    if b_trans:
-        n, kb = b_re.shape
-    else:
-        kb, n = b_re.shape
-    if kb != k:
-        raise ValueError(f"{what}: inner dimensions differ ({k} vs {kb})")
-    c_re = torch.empty(*lead, n, device=dev, dtype=torch.float32)
-    c_im = torch.empty(*lead, n, device=dev, dtype=torch.float32)
-    with torch.cuda.device(dev):
-        rc = _lib.lib().tfa_complex_gemm(
-            m, n, k, ptr(a_re), ptr(a_im), k, ptr(b_re), ptr(b_im), b_re.shape[1], int(b_trans),
-            ptr(bias_re), ptr(bias_im), ptr(c_re), ptr(c_im), n, stream_handle(dev),
-        )
-    _lib.check(rc, what)
-    out = ComplexTensor._wrap(c_re, c_im)
+    c_re, c_im = _ag.gemm(a_re.reshape(-1, k), a_im.reshape(-1, k), b_re, b_im, b_trans, bias_re, bias_im, what)
+    out = ComplexTensor._wrap(c_re.reshape(*lead, c_re.shape[-1]), c_im.reshape(*lead, c_im.shape[-1]))
     return out if out_dev == dev else out.to(out_dev)
 
 

@@ -45,9 +45,12 @@ def fft_core(
     if plan is None:
         plan = create_plan(n, inverse=inverse)
     _require_hip("fft_core")
-    if plan.algorithm == FFTAlgorithm.COOLEY_TUKEY and n <= _DFT_GEMM_THRESHOLD:
+    from . import autograd as _ag
+
+    if plan.algorithm == FFTAlgorithm.COOLEY_TUKEY and n <= _DFT_GEMM_THRESHOLD and not _ag._grad_on(x.real, x.imag):
         return _fft_via_gemm(x, inverse)
-    return execute_1d(x.real, x.imag, inverse)
+    # differentiable when the planes require grad (adjoint on the same kernels)
+    return _ag.c2c(x.real, x.imag, inverse)
 
 
 def execute_1d(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> ComplexTensor:
@@ -187,6 +190,31 @@ def execute_fft2(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> Co
     _lib.check(rc, "tfa_execute(fft2)")
     out = ComplexTensor._wrap(out_re, out_im)
     return out if out_dev == dev else out.to(out_dev)
+
+
+def execute_stft(x: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int, center: bool, normalized: bool,
+                 onesided: bool, num_frames: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Fused STFT kernel on device-resident fp32 x (..., L) and window (n_fft): (re, im) planes of
+    shape (..., bins, frames) (replaces trnfft/api.py:291-365 after its argument handling)."""
+    flags = (_lib.STFT_CENTER if center else 0) | (_lib.STFT_NORMALIZED if normalized else 0)
+    flags |= _lib.STFT_ONESIDED if onesided else 0
+    dev = x.device
+    x = x.contiguous()
+    win = win.contiguous()
+    plan = native_plan(_lib.KIND_STFT, n_fft, False, dev.index, hop=hop, flags=flags)
+    bins = n_fft // 2 + 1 if onesided else n_fft
+    lead = x.shape[:-1]
+    batch = 1
+    for d in lead:
+        batch *= d
+    out_re = torch.empty(*lead, bins, num_frames, dtype=torch.float32, device=dev)
+    out_im = torch.empty_like(out_re)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_stft_execute(
+            plan.handle, batch, x.shape[-1], ptr(x), ptr(win), ptr(out_re), ptr(out_im), stream_handle(dev)
+        )
+    _lib.check(rc, "tfa_stft_execute")
+    return out_re, out_im
 
 
 def strided_ok(n: int, stride: int) -> bool:

@@ -34,6 +34,5 @@ class ComplexLinear(nn.Module):
         nn.init.kaiming_uniform_(self.W_im.weight, a=math.sqrt(5))
 
     def forward(self, x: ComplexTensor) -> ComplexTensor:
-        return complex_linear(x, self.W_re.weight.detach(), self.W_im.weight.detach(),
-                              None if self.bias_re is None else self.bias_re.detach(),
-                              None if self.bias_im is None else self.bias_im.detach())
+        # differentiable in x, both weights and the bias (adjoint GEMMs on the same kernel)
+        return complex_linear(x, self.W_re.weight, self.W_im.weight, self.bias_re, self.bias_im)
