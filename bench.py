@@ -311,7 +311,14 @@ def bench_secondary():
     t = _time_rot(lambda k, st: chk(L.tfa_stft_execute(pl.handle, 64, 160000, P(xs[k]), P(win), P(os_[k][0]),
                                                    P(os_[k][1]), st)), S)
     rec("c2_stft_64x160000_nfft512", t, 40064 * 5 * 512 * 9, nbytes, sets=S)
-    del xs, os_
+    # inverse of C2 (fused istft: completion, inverse transform, window, overlap-add, envelope, trim)
+    ipl = native_plan(_lib.KIND_STFT, 512, True, dev.index, hop=256, flags=_lib.STFT_CENTER | _lib.STFT_ONESIDED)
+    ys = [torch.empty(64, 160000, device=dev) for _ in range(S)]
+    t = _time_rot(lambda k, st: chk(L.tfa_istft_execute(ipl.handle, 64, 626, P(os_[k][0]), P(os_[k][1]), P(win),
+                                                        P(ys[k]), 160000, st)), S)
+    rec("c2_istft_64x257x626_nfft512", t, 40064 * 5 * 512 * 9, nbytes, sets=S,
+        note="inverse of c2: spectra in, 64 x 160000 samples out")
+    del xs, os_, ys
     # C3: Bluestein (fused, one launch)
     for n, b in [(1000, 1024), (4099, 256)]:
         nbytes = 4 * b * n * 4

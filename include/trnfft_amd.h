@@ -124,6 +124,19 @@ int tfa_complex_gemm(int64_t m, int64_t n, int64_t k, const float* a_re, const f
                      const float* bias_re, const float* bias_im, float* c_re, float* c_im,
                      int64_t ldc, tfa_stream stream);
 
+/*
+ * Inverse STFT of onesided spectra (TFA_KIND_STFT plan created with inverse = 1; n = n_fft,
+ * hop, flags CENTER / NORMALIZED, ONESIDED required): spec_re/spec_im (batch, n/2+1, n_frames)
+ * -> out (batch, out_len), out_len from tfa_istft_length (length < 0: the default length).
+ * Hermitian completion, inverse transform, window, overlap-add, division by the window-square
+ * envelope where it exceeds 1e-8 (the raw overlap-add elsewhere), centre trim and zero fill to
+ * `length` in one kernel.  Replaces trnfft/api.py:368-470 (istft), whose per-frame loops
+ * (:438-452) and window-sum masking (:450-452) it fuses.
+ */
+int tfa_istft_length(const tfa_plan* plan, int64_t n_frames, int64_t length, int64_t* out_len);
+int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, const float* spec_re,
+                      const float* spec_im, const float* window, float* out, int64_t length, tfa_stream stream);
+
 /* Operand ops of tfa_complex_gemm_ex (BLAS-style, plus conjugation without transpose). */
 #define TFA_OP_N 0 /* op(X) = X          */
 #define TFA_OP_T 1 /* op(X) = X^T        */

@@ -1,0 +1,99 @@
+"""GPU parity of the fused inverse STFT against the oracle's restatement of trnfft/api.py:368-470
+(Hermitian completion, inverse c2c, real part, overlap-add with window-square envelope division
+and raw fallback, centre trim, length handling)."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import oracle
+import trnfft_amd
+from trnfft_amd import ComplexTensor
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm())
+
+
+def _spec(lead, n_fft, frames, seed):
+    g = torch.Generator().manual_seed(seed)
+    f = n_fft // 2 + 1
+    # arbitrary bins, imaginary parts at bins 0 and n/2 included (the real part drops them)
+    return torch.randn(*lead, f, frames, generator=g), torch.randn(*lead, f, frames, generator=g)
+
+
+CASES = [
+    # n_fft, hop, frames, center, normalized, length
+    (512, 128, 100, True, False, None),
+    (512, 256, 626, True, False, None),
+    (256, 64, 37, True, True, None),
+    (1024, 256, 9, True, False, 1500),       # shorter than the signal: truncation
+    (256, 64, 12, True, False, 2000),        # longer: zero fill
+    (128, 96, 20, False, False, None),       # hop not dividing n_fft
+    (64, 80, 15, False, False, None),        # hop > n_fft: gaps (raw overlap-add of nothing = 0)
+    (16, 4, 50, True, False, None),
+    (4096, 1024, 7, True, False, None),
+    (2048, 512, 5, False, True, None),
+    (512, 40, 30, True, False, None),        # long halo (12 frames)
+]
+
+
+@pytest.mark.parametrize("n_fft,hop,frames,center,normalized,length", CASES)
+def test_istft_matches_reference(n_fft, hop, frames, center, normalized, length):
+    re, im = _spec((3,), n_fft, frames, seed=n_fft + hop)
+    got = trnfft_amd.istft(ComplexTensor(re.cuda(), im.cuda()), n_fft, hop_length=hop, center=center,
+                           normalized=normalized, length=length)
+    ref = oracle.istft((re, im), n_fft, hop_length=hop, center=center, normalized=normalized, length=length)
+    assert got.shape == ref.shape
+    assert _rel(got, ref) <= 1e-6 * math.log2(n_fft) * 4
+    # these shapes run on the fused kernel (not the composed fallback)
+    assert trnfft_amd.api._istft_fused(ComplexTensor(re.cuda(), im.cuda()), n_fft, hop, n_fft, None, center,
+                                       normalized, True, length) is not None
+
+
+def test_istft_window_with_zeros_uses_raw_sum():
+    # a symmetric Hann (zero at both ends) without centring: the envelope is zero at the first
+    # sample, where the reference returns the raw (unwindowed) overlap-add
+    n_fft, hop, frames = 256, 64, 20
+    re, im = _spec((2,), n_fft, frames, seed=3)
+    w = torch.hann_window(n_fft, periodic=False)
+    got = trnfft_amd.istft(ComplexTensor(re.cuda(), im.cuda()), n_fft, hop_length=hop, window=w.cuda(), center=False)
+    ref = oracle.istft((re, im), n_fft, hop_length=hop, window=w, center=False)
+    assert _rel(got, ref) <= 1e-5
+    torch.testing.assert_close(got[:, 0].cpu(), ref[:, 0], rtol=1e-5, atol=1e-6)
+
+
+def test_istft_leading_dims_and_win_length():
+    n_fft, hop, frames = 512, 128, 33
+    re, im = _spec((2, 3), n_fft, frames, seed=4)
+    w = torch.hann_window(400)
+    got = trnfft_amd.istft(ComplexTensor(re.cuda(), im.cuda()), n_fft, hop_length=hop, win_length=400, window=w.cuda())
+    ref = oracle.istft((re, im), n_fft, hop_length=hop, win_length=400, window=w)
+    assert got.shape == ref.shape == (2, 3, (frames - 1) * hop)
+    assert _rel(got, ref) <= 1e-5
+
+
+def test_stft_istft_roundtrip_full_size():
+    # BASELINE config 2 shape: 64 waveforms x 160000 samples, n_fft 512, hop 256
+    from bench import make_stft_input
+
+    x = make_stft_input(64, 160000).cuda()
+    spec = trnfft_amd.stft(x, n_fft=512, hop_length=256)
+    y = trnfft_amd.istft(spec, n_fft=512, hop_length=256, length=160000)
+    assert y.shape == x.shape
+    assert _rel(y, x) <= 1e-5
+
+
+def test_istft_small_hop_falls_back_to_composition():
+    # halo too long for the fused tile: the composed path runs instead, same result
+    n_fft, hop, frames = 4096, 16, 300
+    re, im = _spec((1,), n_fft, frames, seed=5)
+    got = trnfft_amd.istft(ComplexTensor(re.cuda(), im.cuda()), n_fft, hop_length=hop)
+    ref = oracle.istft((re, im), n_fft, hop_length=hop)
+    assert _rel(got, ref) <= 1e-4

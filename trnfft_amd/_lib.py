@@ -41,6 +41,8 @@ EXPORTS = (
     "tfa_execute_strided",
     "tfa_stft_frames",
     "tfa_stft_execute",
+    "tfa_istft_length",
+    "tfa_istft_execute",
     "tfa_complex_gemm",
     "tfa_complex_gemm_ex",
     "tfa_last_error",
@@ -84,6 +86,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tfa_stft_frames.restype = ctypes.c_int
     lib.tfa_stft_execute.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp]
     lib.tfa_stft_execute.restype = ctypes.c_int
+    lib.tfa_istft_length.argtypes = [_vp, _i64, _i64, ctypes.POINTER(_i64)]
+    lib.tfa_istft_length.restype = ctypes.c_int
+    lib.tfa_istft_execute.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp]
+    lib.tfa_istft_execute.restype = ctypes.c_int
     lib.tfa_complex_gemm.argtypes = [_i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _vp]
     lib.tfa_complex_gemm.restype = ctypes.c_int
     lib.tfa_complex_gemm_ex.argtypes = [_i64, _i64, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i32, ctypes.c_float,

@@ -7,6 +7,7 @@ device (the reference's helpers allocate on the CPU, trnfft/api.py:55-56,487-488
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -309,11 +310,19 @@ def istft(
     onesided: bool = True,
     length: int | None = None,
 ) -> torch.Tensor:
-    """Inverse STFT by overlap-add with window-sum normalisation (trnfft/api.py:368-470)."""
+    """Inverse STFT by overlap-add with window-sum normalisation (trnfft/api.py:368-470).
+
+    Onesided spectra of power-of-two n_fft run as one fused kernel (completion, inverse
+    transform, window, overlap-add, envelope division, trim); when gradients are needed, or for
+    two-sided input, the same steps run as a composition of the differentiable kernels.
+    """
     if hop_length is None:
         hop_length = n_fft // 4
     if win_length is None:
         win_length = n_fft
+    fused = _istft_fused(input, n_fft, hop_length, win_length, window, center, normalized, onesided, length)
+    if fused is not None:
+        return fused
     dev = input.real.device
     win = _effective_window(
         window.to(dev) if window is not None else None, n_fft, win_length, input.dtype
@@ -362,6 +371,44 @@ def istft(
             pad = torch.zeros(*batch_shape, length - cur, dtype=output.dtype, device=dev)
             output = torch.cat([output, pad], dim=-1)
     return output.contiguous()
+
+
+def _istft_fused(spec, n_fft, hop, win_length, window, center, normalized, onesided, length):
+    """The fused inverse-STFT kernel, or None when its preconditions do not hold."""
+    from . import _lib
+    from .dispatch import ptr, stream_handle
+    from .plan import native_plan
+
+    re, im = spec.real, spec.imag
+    if (not onesided or n_fft < 16 or n_fft > 4096 or n_fft & (n_fft - 1) or re.dim() < 2
+            or re.shape[-2] != n_fft // 2 + 1 or re.shape[-1] < 1 or _ag._grad_on(re, im, window)):
+        return None
+    _resolve(None)
+    _require_hip("istft")
+    dev = target_device(re, im)
+    out_dev = re.device
+    flags = _lib.STFT_ONESIDED | (_lib.STFT_CENTER if center else 0) | (_lib.STFT_NORMALIZED if normalized else 0)
+    try:
+        plan = native_plan(_lib.KIND_STFT, n_fft, True, dev.index, hop=hop, flags=flags)
+    except NotImplementedError:
+        return None  # hop too small for the kernel's frame tile
+    win = _effective_window(window.to(dev) if window is not None else None, n_fft, win_length, torch.float32, dev)
+    win = to_device_f32(win, dev)
+    re = to_device_f32(re, dev)
+    im = to_device_f32(im, dev)
+    frames = re.shape[-1]
+    lead = re.shape[:-2]
+    batch = re.numel() // (re.shape[-2] * frames)
+    out_len = ctypes.c_int64()
+    lib = _lib.lib()
+    req = -1 if length is None else int(length)
+    _lib.check(lib.tfa_istft_length(plan.handle, frames, req, ctypes.byref(out_len)), "tfa_istft_length")
+    out = torch.empty(*lead, out_len.value, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.tfa_istft_execute(plan.handle, batch, frames, ptr(re), ptr(im), ptr(win), ptr(out), req,
+                                   stream_handle(dev))
+    _lib.check(rc, "tfa_istft_execute")
+    return out if out_dev == dev else out.to(out_dev)
 
 
 # --- Helpers ---------------------------------------------------------------------------------

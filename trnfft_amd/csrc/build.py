@@ -22,6 +22,7 @@ SOURCES = [
     "kernels_gemm.hip",
     "kernels_fft2.hip",
     "kernels_real.hip",
+    "kernels_istft.hip",
 ]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -30,6 +30,12 @@ __host__ __device__ constexpr int real_epth(int h, bool inverse) {
   return h <= 2 ? h : h >= 8192 ? 32 : (h <= (inverse ? 64 : 256)) ? 4 : 8;
 }
 
+// Elements per thread of the inverse-STFT pair transforms: one wavefront per transform up to
+// n = 1024 (wave-local exchanges), E = 32 at 4096.
+__host__ __device__ constexpr int istft_epth(int n) {
+  return n <= 16 ? n : n <= 64 ? 8 : n <= 256 ? 16 : n <= 512 ? 8 : n <= 2048 ? 16 : 32;
+}
+
 struct LdsShape {
   int n, e, t, npass;
   int radix[kMaxPasses];

@@ -138,6 +138,24 @@ struct RealArgs {
 };
 hipError_t launch_real(int n, const RealArgs& a);
 
+struct IstftArgs {
+  const float* spec_re;  // (batch, n_fft/2+1, n_frames)
+  const float* spec_im;
+  const float* window;   // n_fft
+  float* out;            // (batch, out_pitch)
+  const float2* tw;      // inverse LDS-FFT table for n_fft (istft_epth layout)
+  int n_frames, hop, halo;  // halo = floor((n_fft-1)/hop) frames recomputed before each tile
+  long long batch;
+  long long expected_len;  // n_fft + (n_frames-1)*hop samples before the centre trim
+  long long start;         // first kept sample (n_fft/2 when centred)
+  long long write_len;     // samples written per row; [write_len, out_pitch) is zero-filled
+  long long out_pitch;
+  float scale;  // 1/n_fft (x sqrt(n_fft) when normalized)
+  hipStream_t stream;
+};
+hipError_t launch_istft(int n_fft, const IstftArgs& a);
+int istft_frames_per_tile(int n_fft);
+
 struct Fft2Args {
   const float* in_re;
   const float* in_im;  // nullptr: real input

@@ -1,0 +1,164 @@
+// Fused inverse STFT of onesided spectra: Hermitian completion, inverse transform, window,
+// overlap-add, window-envelope normalisation and the centre trim in one kernel.
+//
+// The reference (trnfft/api.py:368-470) materialises the completed two-sided spectrum, runs a
+// complex inverse per frame, keeps the real part, and then overlap-adds with index_add into an
+// output, a raw (unwindowed) sum and a window-square envelope before dividing where the envelope
+// exceeds 1e-8 (raw sum elsewhere).  Here one workgroup owns a run of output samples:
+//   1. the onesided bins of FR consecutive frames are staged into LDS (lanes over frames: each
+//      load instruction reads consecutive frames of one bin row of the (batch, bins, frames)
+//      input, the layout the forward STFT writes);
+//   2. two real frames share one complex inverse transform: Z = X_a + i X_b with X_a, X_b the
+//      Hermitian completions (imaginary parts of bins 0 and n/2 dropped, as the reference's real
+//      part drops them), so IFFT(Z) = x_a + i x_b;
+//   3. every output sample the workgroup owns gathers its covering frames from LDS: the windowed
+//      sum, the raw sum and the envelope, then the normalised sample is written once.
+// A sample is covered by frames t with t*hop <= s < t*hop + n, so a workgroup that owns the
+// samples of frames [t0, t0 + FR') also transforms the H = floor((n-1)/hop) frames before t0
+// (recomputed halo, no atomics and no second pass).
+#include "kernels.h"
+
+namespace tfa {
+
+template <int NFFT>
+struct IstftCfg {
+  static constexpr int E = istft_epth(NFFT);
+  static constexpr int T = NFFT / E;
+  static constexpr int F = NFFT / 2 + 1;                    // onesided bins
+  static constexpr int RP = 2 * lds_pad(NFFT) + 4;          // floats per pair region (>= 4F, >= 2n)
+  static constexpr int PAIRS_T = 1024 / T < 32 ? 1024 / T : 32;
+  static constexpr int PAIRS_L = (kLdsBytes - NFFT * 4) / (RP * 4);
+  static constexpr int PAIRS = PAIRS_T < PAIRS_L ? PAIRS_T : PAIRS_L;
+  static constexpr int FR = 2 * PAIRS;  // frames per workgroup (owned + halo)
+  static constexpr int THREADS = PAIRS * T;
+  static_assert(PAIRS >= 1 && RP >= 4 * F && RP >= 2 * NFFT, "istft tile");
+};
+
+template <int NFFT>
+__global__ __launch_bounds__(IstftCfg<NFFT>::THREADS) void istft_kernel(
+    const float* __restrict__ sre, const float* __restrict__ sim, const float* __restrict__ win,
+    float* __restrict__ out, const float2* __restrict__ tw, int n_frames, int hop, int halo, int owned,
+    int tiles_per_signal, long long expected_len, long long start, long long write_len, long long out_pitch,
+    float scale) {
+  using C = IstftCfg<NFFT>;
+  constexpr int E = C::E, T = C::T, F = C::F, RP = C::RP, FR = C::FR, THREADS = C::THREADS;
+  constexpr bool WL = T <= 64;
+  __shared__ float lds[C::PAIRS * RP];
+  __shared__ float wl[NFFT];
+  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
+  const long long b = tile / tiles_per_signal;
+  const int t0 = (int)(tile % tiles_per_signal) * owned;  // first owned frame
+  const int ta = t0 - halo > 0 ? t0 - halo : 0;          // first frame of the tile
+  const int nf = (t0 + owned < n_frames ? t0 + owned : n_frames) - ta;  // frames in the tile (<= FR)
+
+  for (int i = threadIdx.x; i < NFFT; i += THREADS) wl[i] = win[i];
+  // 1. stage bins: region of pair p = [re_a | im_a | re_b | im_b], F floats each
+  const size_t sbase = (size_t)b * F * n_frames + ta;
+  for (int i = threadIdx.x; i < F * FR; i += THREADS) {
+    const int f = i % FR, k = i / FR;
+    float re = 0.0f, im = 0.0f;
+    if (f < nf) {
+      re = ld_stream(sre + sbase + (size_t)k * n_frames + f);
+      im = ld_stream(sim + sbase + (size_t)k * n_frames + f);
+    }
+    float* reg = lds + (f >> 1) * RP + (f & 1) * 2 * F;
+    reg[k] = re;
+    reg[F + k] = (k == 0 || k == NFFT / 2) ? 0.0f : im;
+  }
+  __syncthreads();
+  // 2. one complex inverse transform per frame pair
+  const int pl = threadIdx.x / T, tid = threadIdx.x % T;
+  float* reg = lds + pl * RP;
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int k = tid + T * e;
+    if (k <= NFFT / 2) {  // Z = X_a + i X_b
+      v[e] = make_float2((reg[k] - reg[3 * F + k]) * scale, (reg[F + k] + reg[2 * F + k]) * scale);
+    } else {              // X[k] = conj X[n-k]:  Z = (ra + ib) + i (rb - ia) at n-k
+      const int q = NFFT - k;
+      v[e] = make_float2((reg[q] + reg[3 * F + q]) * scale, (reg[2 * F + q] - reg[F + q]) * scale);
+    }
+  }
+  exchange_sync<WL>();  // the transform reuses this pair's region
+  LdsFft<NFFT, E, 1, WL>::run(v, reg, reg + lds_pad(NFFT), tw, tid);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    reg[tid + T * e] = v[e].x;         // frame 2p
+    reg[NFFT + tid + T * e] = v[e].y;  // frame 2p + 1
+  }
+  __syncthreads();
+  // 3. owned samples: [t0*hop, (t0+owned)*hop), the last tile up to the end of the signal
+  const long long s_lo = (long long)t0 * hop;
+  long long s_hi = (long long)(t0 + owned) * hop;
+  if (t0 + owned >= n_frames || s_hi > expected_len) s_hi = expected_len;
+  float* dst = out + (size_t)b * out_pitch;
+  for (long long s = s_lo + threadIdx.x; s < s_hi; s += THREADS) {
+    const long long o = s - start;
+    if (o < 0 || o >= write_len) continue;
+    long long tf = s - NFFT + 1;
+    int t_first = tf <= 0 ? 0 : (int)((tf + hop - 1) / hop);
+    if (t_first < ta) t_first = ta;
+    int t_last = (int)(s / hop);
+    if (t_last > ta + nf - 1) t_last = ta + nf - 1;
+    float acc = 0.0f, raw = 0.0f, env = 0.0f;
+    for (int t = t_first; t <= t_last; ++t) {
+      const int j = (int)(s - (long long)t * hop);
+      const int f = t - ta;
+      const float x = lds[(f >> 1) * RP + (f & 1) * NFFT + j];
+      const float w = wl[j];
+      acc += x * w;
+      raw += x;
+      env += w * w;
+    }
+    dst[o] = env > 1e-8f ? acc / env : raw;
+  }
+  // samples past the end of the signal up to the requested length are zero
+  if (t0 + owned >= n_frames)
+    for (long long o = write_len + threadIdx.x; o < out_pitch; o += THREADS) dst[o] = 0.0f;
+}
+
+template <int NFFT>
+static hipError_t launch_istft_n(const IstftArgs& a) {
+  using C = IstftCfg<NFFT>;
+  const int owned = C::FR - a.halo;
+  if (owned < 1) return hipErrorInvalidValue;
+  const int tiles = (a.n_frames + owned - 1) / owned;
+  const long long blocks = a.batch * (long long)tiles;
+  hipLaunchKernelGGL((istft_kernel<NFFT>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream, a.spec_re,
+                     a.spec_im, a.window, a.out, a.tw, a.n_frames, a.hop, a.halo, owned, tiles, a.expected_len,
+                     a.start, a.write_len, a.out_pitch, a.scale);
+  return hipGetLastError();
+}
+
+int istft_frames_per_tile(int n_fft) {
+  switch (n_fft) {
+    case 16: return IstftCfg<16>::FR;
+    case 32: return IstftCfg<32>::FR;
+    case 64: return IstftCfg<64>::FR;
+    case 128: return IstftCfg<128>::FR;
+    case 256: return IstftCfg<256>::FR;
+    case 512: return IstftCfg<512>::FR;
+    case 1024: return IstftCfg<1024>::FR;
+    case 2048: return IstftCfg<2048>::FR;
+    case 4096: return IstftCfg<4096>::FR;
+    default: return 0;
+  }
+}
+
+hipError_t launch_istft(int n_fft, const IstftArgs& a) {
+  switch (n_fft) {
+    case 16: return launch_istft_n<16>(a);
+    case 32: return launch_istft_n<32>(a);
+    case 64: return launch_istft_n<64>(a);
+    case 128: return launch_istft_n<128>(a);
+    case 256: return launch_istft_n<256>(a);
+    case 512: return launch_istft_n<512>(a);
+    case 1024: return launch_istft_n<1024>(a);
+    case 2048: return launch_istft_n<2048>(a);
+    case 4096: return launch_istft_n<4096>(a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace tfa

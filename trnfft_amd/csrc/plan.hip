@@ -261,6 +261,21 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         rc = fail(TFA_ERR_INVALID, "hop_length must be >= 1");
         break;
       }
+      if (desc->inverse) {
+        // inverse STFT: inverse table in the pair-transform layout of the istft kernel
+        if (!(desc->flags & TFA_STFT_ONESIDED)) {
+          rc = fail(TFA_ERR_UNSUPPORTED, "fused inverse STFT takes onesided spectra");
+          break;
+        }
+        if ((n - 1) / desc->hop >= tfa::istft_frames_per_tile((int)n)) {
+          rc = fail(TFA_ERR_UNSUPPORTED, "hop_length too small for the fused inverse STFT tile");
+          break;
+        }
+        p->inv.n = n;
+        p->inv.dir = 1;
+        rc = p->upload(lds_table((int)n, 1, tfa::istft_epth((int)n)), &p->inv.tw);
+        break;
+      }
       rc = p->build_c2c(n, -1, &p->fwd);
       break;
     case TFA_KIND_FFT2: {
@@ -463,6 +478,44 @@ int tfa_stft_execute(const tfa_plan* plan, int64_t batch, int64_t num_samples, c
                   (int)pad, (int)frames, n_bins, batch, scale, static_cast<hipStream_t>(stream)};
   hipError_t e = tfa::launch_stft((int)n_fft, a);
   return e == hipSuccess ? TFA_OK : hip_fail(e, "stft launch");
+}
+
+int tfa_istft_length(const tfa_plan* plan, int64_t n_frames, int64_t length, int64_t* out_len) {
+  if (!plan || !out_len || plan->d.kind != TFA_KIND_STFT || !plan->d.inverse)
+    return fail(TFA_ERR_INVALID, "not an inverse STFT plan");
+  if (n_frames < 1) return fail(TFA_ERR_INVALID, "need at least one frame");
+  const int64_t n_fft = plan->d.n;
+  const int64_t pad = (plan->d.flags & TFA_STFT_CENTER) ? n_fft / 2 : 0;
+  int64_t cur = n_fft + (n_frames - 1) * plan->d.hop - pad;
+  if (pad && cur > pad && length < 0) cur -= pad;
+  *out_len = length >= 0 ? length : cur;
+  return TFA_OK;
+}
+
+int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, const float* spec_re,
+                      const float* spec_im, const float* window, float* out, int64_t length, tfa_stream stream) {
+  if (!plan || plan->d.kind != TFA_KIND_STFT || !plan->d.inverse) return fail(TFA_ERR_INVALID, "not an inverse STFT plan");
+  if (batch < 0) return fail(TFA_ERR_INVALID, "negative batch");
+  if (batch == 0) return TFA_OK;
+  if (!spec_re || !spec_im || !window || !out) return fail(TFA_ERR_INVALID, "null data pointer");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
+    return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  int64_t out_len = 0;
+  int rc = tfa_istft_length(plan, n_frames, length, &out_len);
+  if (rc) return rc;
+  const int64_t n_fft = plan->d.n, hop = plan->d.hop;
+  const int64_t expected = n_fft + (n_frames - 1) * hop;
+  if (expected > INT32_MAX / 2 || n_frames > INT32_MAX / 2) return fail(TFA_ERR_UNSUPPORTED, "signal too long");
+  const int64_t start = (plan->d.flags & TFA_STFT_CENTER) ? n_fft / 2 : 0;
+  int64_t cur = expected - start;
+  if (start && cur > start && length < 0) cur -= start;
+  const double sc = (plan->d.flags & TFA_STFT_NORMALIZED) ? std::sqrt((double)n_fft) / (double)n_fft : 1.0 / (double)n_fft;
+  tfa::IstftArgs a{spec_re, spec_im, window, out, plan->inv.tw, (int)n_frames, (int)hop, (int)((n_fft - 1) / hop),
+                   batch, expected, start, cur < out_len ? cur : out_len, out_len, (float)sc,
+                   static_cast<hipStream_t>(stream)};
+  hipError_t e = tfa::launch_istft((int)n_fft, a);
+  return e == hipSuccess ? TFA_OK : hip_fail(e, "istft launch");
 }
 
 int tfa_complex_gemm_ex(int64_t m, int64_t n, int64_t k, const float* a_re, const float* a_im, int64_t lda,
