@@ -30,6 +30,10 @@ __host__ __device__ constexpr int real_epth(int h, bool inverse) {
   return h <= 2 ? h : h >= 8192 ? 32 : (h <= (inverse ? 64 : 256)) ? 4 : 8;
 }
 
+// Elements per thread of the forward STFT's pair transforms (many lanes per transform measured
+// fastest at every n_fft).
+__host__ __device__ constexpr int stft_epth(int n) { return n < 8 ? n : 8; }
+
 // Elements per thread of the inverse-STFT pair transforms: one wavefront per transform up to
 // n = 1024 (wave-local exchanges), E = 32 at 4096.
 __host__ __device__ constexpr int istft_epth(int n) {

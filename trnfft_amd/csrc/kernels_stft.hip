@@ -15,20 +15,18 @@
 
 namespace tfa {
 
-// Frame pairs per workgroup: 512 threads (n_fft = 512: 32 pairs = 64 frames = 256 B per row
-// segment) within the LDS budget.  A sweep on MI355X showed time falling almost linearly with
-// frames per workgroup: short output row segments are what cost.
+// Launch shape from a sweep on MI355X (64 waveforms x 160000 samples, hop n_fft/2, buffers
+// rotated past the Infinity Cache, n_fft 64..4096): E = 8 elements per thread (many lanes per
+// transform) is fastest at every length, with 8192/n_fft frame pairs per workgroup (~70 KB of LDS,
+// two workgroups per CU, 256..1024 threads); stft_epth (fft_shape.h) gives E.
 template <int NFFT>
 constexpr int stft_default_pairs() {
-  constexpr int t = NFFT / lds_epth(NFFT);
-  int p = t >= 512 ? 1 : 512 / t;
-  while (p > 1 && (long long)p * (lds_pad(NFFT) + 1) * 8 + NFFT * 4 > kLdsBytes) p /= 2;
-  return p;
+  constexpr int p = 8192 / NFFT;
+  return p < 2 ? 2 : p > 32 ? 32 : p;
 }
-
-template <int NFFT, int PAIRS_ = stft_default_pairs<NFFT>()>
+template <int NFFT, int PAIRS_ = stft_default_pairs<NFFT>(), int E_ = stft_epth(NFFT)>
 struct StftCfg {
-  static constexpr int E = lds_epth(NFFT);
+  static constexpr int E = E_;
   static constexpr int T = NFFT / E;
   static constexpr int PADN = lds_pad(NFFT) + 1;  // odd pitch: pair regions start on different banks
   static constexpr int PAIRS = PAIRS_;             // complex transforms per workgroup
@@ -42,12 +40,12 @@ struct StftCfg {
 // staging-area word of sample i of the tile span (one pad word per 32 spreads frame starts over banks)
 __device__ __forceinline__ int stage_pad(int i) { return i + (i >> 5); }
 
-template <int NFFT, int PAIRS = stft_default_pairs<NFFT>()>
-__global__ __launch_bounds__((StftCfg<NFFT, PAIRS>::THREADS)) void stft_kernel(
+template <int NFFT, int PAIRS = stft_default_pairs<NFFT>(), int E_ = stft_epth(NFFT)>
+__global__ __launch_bounds__((StftCfg<NFFT, PAIRS, E_>::THREADS)) void stft_kernel(
     const float* __restrict__ sig, const float* __restrict__ win, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ tw, int length, int hop, int pad,
     int n_frames, int n_bins, int tiles_per_signal, float scale) {
-  using C = StftCfg<NFFT, PAIRS>;
+  using C = StftCfg<NFFT, PAIRS, E_>;
   constexpr int E = C::E, T = C::T, FR = C::FR, PADN = C::PADN, THREADS = C::THREADS;
   __shared__ float lds[C::LDSF];
   __shared__ float wl[NFFT];
@@ -117,7 +115,7 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS>::THREADS)) void stft_kernel(
   }
   float* my_re = lds + pl * PADN;
   float* my_im = lds + (PAIRS + pl) * PADN;
-  LdsFft<NFFT, E, -1, false>::run(v, my_re, my_im, tw, tid);
+  LdsFft<NFFT, E, -1, (T <= 64)>::run(v, my_re, my_im, tw, tid);
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     my_re[lds_pad(tid + T * e)] = v[e].x;
@@ -142,8 +140,10 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS>::THREADS)) void stft_kernel(
     const float re = odd ? (zi + yi) : (zr + yr);
     const float im = odd ? (yr - zr) : (zi - yi);
     const size_t o = ob + (size_t)k * n_frames + fr;
-    st_stream(out_re + o, re * hs);
-    st_stream(out_im + o, im * hs);
+    // plain (not streaming) stores: a workgroup's row segments rarely start on a cache line,
+    // and L2 merges the partial lines the neighbouring workgroups write (measured 1.4x faster)
+    out_re[o] = re * hs;
+    out_im[o] = im * hs;
   }
 }
 

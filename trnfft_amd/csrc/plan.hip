@@ -276,7 +276,9 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         rc = p->upload(lds_table((int)n, 1, tfa::istft_epth((int)n)), &p->inv.tw);
         break;
       }
-      rc = p->build_c2c(n, -1, &p->fwd);
+      p->fwd.n = n;
+      p->fwd.dir = -1;
+      rc = p->upload(lds_table((int)n, -1, tfa::stft_epth((int)n)), &p->fwd.tw);
       break;
     case TFA_KIND_FFT2: {
       const int64_t h = desc->n2;
