@@ -34,6 +34,11 @@ __host__ __device__ constexpr int real_epth(int h, bool inverse) {
 // fastest at every n_fft).
 __host__ __device__ constexpr int stft_epth(int n) { return n < 8 ? n : 8; }
 
+// Elements per thread of the 2-D transform's paired real-row pass 1 and column pass 2 (the
+// many-lanes-per-transform shape that also won for the STFT).
+__host__ __device__ constexpr int fft2_pair_epth(int w) { return w < 8 ? w : 8; }
+__host__ __device__ constexpr int fft2_col_epth(int hr) { return hr < 8 ? hr : 8; }
+
 // Elements per thread of the inverse-STFT pair transforms: one wavefront per transform up to
 // n = 1024 (wave-local exchanges), E = 32 at 4096.
 __host__ __device__ constexpr int istft_epth(int n) {

@@ -161,8 +161,9 @@ struct Fft2Args {
   const float* in_im;  // nullptr: real input
   float* out_re;       // must not alias the input
   float* out_im;
-  const float2* tw_w;   // LDS-FFT table for length w
-  const float2* tw_hr;  // LDS-FFT table for length h/8
+  const float2* tw_w;       // LDS-FFT table for length w (complex rows)
+  const float2* tw_w_pair;  // LDS-FFT table for length w in the paired-real-row layout
+  const float2* tw_hr;      // LDS-FFT table for length h/8 (column pass layout)
   const float2* tw_h;   // W_h^i, i < h
   long long batch, h, w;
   float scale;  // applied in pass 2 (1/(h*w) for the inverse)

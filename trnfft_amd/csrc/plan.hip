@@ -78,6 +78,7 @@ struct tfa_plan {
   float2* hs = nullptr;
   C2cTables col;          // FFT2: LDS table for n2/8 (pass 2)
   float2* tw_h = nullptr;  // FFT2: W_{n2}^i, i < n2
+  float2* tw_w_pair = nullptr;  // FFT2: row table in the paired-real-row layout
   float2* twr = nullptr;  // REAL: W_n^k, k < n/2
   float* w_re = nullptr;  // DFT-GEMM matrix
   float* w_im = nullptr;
@@ -287,7 +288,10 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         break;
       }
       if ((rc = p->build_c2c(n, dir, &p->fwd))) break;
-      if ((rc = p->build_c2c(h / 8, dir, &p->col))) break;
+      if ((rc = p->upload(lds_table((int)n, dir, tfa::fft2_pair_epth((int)n)), &p->tw_w_pair))) break;
+      p->col.n = h / 8;
+      p->col.dir = dir;
+      if ((rc = p->upload(lds_table((int)(h / 8), dir, tfa::fft2_col_epth((int)(h / 8))), &p->col.tw))) break;
       std::vector<float2> th((size_t)h);
       for (int64_t i = 0; i < h; ++i) th[(size_t)i] = unit_root(i, h, dir);
       rc = p->upload(th, &p->tw_h);
@@ -400,7 +404,8 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
       if (in_re == out_re || (in_im && in_im == out_im)) return fail(TFA_ERR_INVALID, "FFT2 output must not alias the input");
       const int64_t h = plan->d.n2;
       const float s2 = plan->d.inverse ? (float)(1.0 / ((double)n * (double)h)) : 1.0f;
-      tfa::Fft2Args f{in_re, in_im, out_re, out_im, plan->fwd.tw, plan->col.tw, plan->tw_h, batch, h, n, s2, plan->fwd.dir, s};
+      tfa::Fft2Args f{in_re, in_im, out_re, out_im, plan->fwd.tw, plan->tw_w_pair, plan->col.tw, plan->tw_h,
+                      batch, h, n, s2, plan->fwd.dir, s};
       hipError_t e = tfa::launch_fft2(f);
       return e == hipSuccess ? TFA_OK : hip_fail(e, "fft2 launch");
     }
@@ -508,7 +513,8 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
   if (rc) return rc;
   const int64_t n_fft = plan->d.n, hop = plan->d.hop;
   const int64_t expected = n_fft + (n_frames - 1) * hop;
-  if (expected > INT32_MAX / 2 || n_frames > INT32_MAX / 2) return fail(TFA_ERR_UNSUPPORTED, "signal too long");
+  if (expected > INT32_MAX / 2 || n_frames > INT32_MAX / 2 || out_len > INT32_MAX / 2)
+    return fail(TFA_ERR_UNSUPPORTED, "signal too long");
   const int64_t start = (plan->d.flags & TFA_STFT_CENTER) ? n_fft / 2 : 0;
   int64_t cur = expected - start;
   if (start && cur > start && length < 0) cur -= start;
