@@ -12,13 +12,23 @@
 
 namespace tfa {
 
-template <int M, bool REAL_IN>
-__global__ __launch_bounds__(C2cThreads<M>::THREADS) void bluestein_fused_kernel(
+// Launch shape of the fused kernel: E elements per thread, THR threads per workgroup.
+template <int M, int E_, int THR>
+struct BlueCfg {
+  static constexpr int E = E_;
+  static constexpr int T = M / E;
+  static constexpr int XF = T >= THR ? 1 : THR / T;
+  static constexpr int THREADS = XF * T;
+  static constexpr int PADN = lds_pad(M) > 1 ? lds_pad(M) : 1;
+};
+
+template <int M, bool REAL_IN, int E_ = blue_epth(M), int THR = blue_threads(M)>
+__global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fused_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re,
     float* out_im, const float2* __restrict__ chirp, const float2* __restrict__ hs,
     const float2* __restrict__ tw_f, const float2* __restrict__ tw_i, int n, long long batch,
     float scale) {
-  using C = C2cThreads<M>;
+  using C = BlueCfg<M, E_, THR>;
   constexpr int E = C::E, T = C::T;
   __shared__ float lre[C::XF * C::PADN];
   __shared__ float lim[C::XF * C::PADN];
@@ -60,7 +70,7 @@ __global__ __launch_bounds__(C2cThreads<M>::THREADS) void bluestein_fused_kernel
 
 template <int M>
 static hipError_t launch_blue_m(const BluesteinArgs& a) {
-  using C = C2cThreads<M>;
+  using C = BlueCfg<M, blue_epth(M), blue_threads(M)>;
   const long long blocks = (a.batch + C::XF - 1) / C::XF;
   if (a.in_im == nullptr)
     hipLaunchKernelGGL((bluestein_fused_kernel<M, true>), dim3((unsigned)blocks), dim3(C::THREADS), 0,

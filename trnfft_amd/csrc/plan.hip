@@ -235,8 +235,17 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         break;
       }
       p->blue_fused = m <= kMaxLdsN;
-      if ((rc = p->build_c2c(m, -1, &p->fwd))) break;
-      if ((rc = p->build_c2c(m, 1, &p->inv))) break;
+      if (p->blue_fused) {
+        // the fused kernel's own launch shape (tfa::blue_epth) fixes its table layout
+        p->fwd.n = p->inv.n = m;
+        p->fwd.dir = -1;
+        p->inv.dir = 1;
+        if ((rc = p->upload(lds_table((int)m, -1, tfa::blue_epth((int)m)), &p->fwd.tw))) break;
+        if ((rc = p->upload(lds_table((int)m, 1, tfa::blue_epth((int)m)), &p->inv.tw))) break;
+      } else {
+        if ((rc = p->build_c2c(m, -1, &p->fwd))) break;
+        if ((rc = p->build_c2c(m, 1, &p->inv))) break;
+      }
       const std::vector<float2> chirp = reference_chirp(n, dir);
       // h = conj(chirp) circularly wrapped (trnfft/fft_core.py:1337-1345); H = FFT_m(h) / m
       std::vector<std::complex<double>> h((size_t)m, {0.0, 0.0});
