@@ -166,7 +166,8 @@ def bench_headline(steps: int, warmup: int):
             for k in range(steps):
                 step(k, strm)
     torch.cuda.current_stream().wait_stream(cap)
-    graph.replay()  # warm-up replay
+    for _ in range(2):  # warm-up replays (the first replay after capture runs measurably slower)
+        graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record()

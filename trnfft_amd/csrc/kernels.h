@@ -29,13 +29,13 @@ __device__ __forceinline__ float4 ld_stream4(const float4* p) {
 }
 
 // Thread layout of the batched LDS kernels for transform length N: T threads per transform,
-// XF transforms per workgroup (at least 256 threads per workgroup), PADN LDS floats per plane
+// XF transforms per workgroup (c2c_threads(N) threads per workgroup), PADN LDS floats per plane
 // per transform (1 when the transform needs no exchange).
-template <int N>
+template <int N, int E_ = c2c_epth(N), int THR = c2c_threads(N)>
 struct C2cThreads {
-  static constexpr int E = lds_epth(N);
+  static constexpr int E = E_;
   static constexpr int T = N / E;
-  static constexpr int XF = T >= 256 ? 1 : 256 / T;
+  static constexpr int XF = T >= THR ? 1 : THR / T;
   static constexpr int THREADS = XF * T;
   static constexpr LdsShape S = make_shape(N, E);
   static constexpr int PADN = S.npass > 1 ? lds_pad(N) : 1;

@@ -20,11 +20,11 @@ namespace tfa {
 // TAIL = false: every transform slot of the grid is inside the batch (no guards at all; the
 // guard-free instruction stream measured fastest).  TAIL = true: one workgroup for the ragged
 // remainder, slots past the batch end neither load nor store.
-template <int N, int DIR, bool REAL_IN, bool TAIL>
-__global__ __launch_bounds__(C2cThreads<N>::THREADS) void c2c_lds_kernel(
+template <int N, int DIR, bool REAL_IN, bool TAIL, int E_ = c2c_epth(N), int THR = c2c_threads(N)>
+__global__ __launch_bounds__((C2cThreads<N, E_, THR>::THREADS)) void c2c_lds_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re,
     float* out_im, const float2* __restrict__ tw, long long first, long long batch, float scale) {
-  using C = C2cThreads<N>;
+  using C = C2cThreads<N, E_, THR>;
   constexpr int E = C::E, T = C::T;
   __shared__ float lre[C::XF * C::PADN];
   __shared__ float lim[C::XF * C::PADN];

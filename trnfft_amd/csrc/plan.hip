@@ -61,7 +61,8 @@ struct C2cTables {
   int64_t n = 0;
   int dir = -1;
   bool fourstep = false;
-  float2* tw = nullptr;  // LDS path
+  float2* tw = nullptr;      // LDS path, batched kernel layout
+  float2* tw_lds = nullptr;  // LDS path, strided / 2-D row kernel layout
   int n1 = 0, n2 = 0, lo_bits = 0;
   float2 *tw1 = nullptr, *tw2 = nullptr, *tw_lo = nullptr, *tw_hi = nullptr;
 };
@@ -105,7 +106,14 @@ struct tfa_plan {
     t->dir = dir;
     if (n <= kMaxLdsN) {
       t->fourstep = false;
-      return upload(lds_table((int)n, dir), &t->tw);
+      // the batched kernel's layout (tfa::c2c_epth); the strided and 2-D row kernels use the
+      // tfa::lds_epth layout, a second table only where the two differ
+      int rc = upload(lds_table((int)n, dir, tfa::c2c_epth((int)n)), &t->tw);
+      if (rc || tfa::c2c_epth((int)n) == tfa::lds_epth((int)n)) {
+        t->tw_lds = t->tw;
+        return rc;
+      }
+      return upload(lds_table((int)n, dir), &t->tw_lds);
     }
     if (n > kMaxFourStepN) return fail(TFA_ERR_UNSUPPORTED, "power-of-two length above 2^24 not supported");
     t->fourstep = true;
@@ -413,7 +421,7 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
       if (in_re == out_re || (in_im && in_im == out_im)) return fail(TFA_ERR_INVALID, "FFT2 output must not alias the input");
       const int64_t h = plan->d.n2;
       const float s2 = plan->d.inverse ? (float)(1.0 / ((double)n * (double)h)) : 1.0f;
-      tfa::Fft2Args f{in_re, in_im, out_re, out_im, plan->fwd.tw, plan->tw_w_pair, plan->col.tw, plan->tw_h,
+      tfa::Fft2Args f{in_re, in_im, out_re, out_im, plan->fwd.tw_lds, plan->tw_w_pair, plan->col.tw, plan->tw_h,
                       batch, h, n, s2, plan->fwd.dir, s};
       hipError_t e = tfa::launch_fft2(f);
       return e == hipSuccess ? TFA_OK : hip_fail(e, "fft2 launch");
@@ -456,7 +464,7 @@ int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, con
     return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
   const C2cTables& t = plan->d.inverse ? plan->inv : plan->fwd;
   const float scale = plan->d.inverse ? (float)(1.0 / (double)plan->d.n) : 1.0f;
-  tfa::StridedArgs a{in_re, in_im, out_re, out_im, t.tw, nullptr, nullptr, outer, stride, 0, 0u, scale,
+  tfa::StridedArgs a{in_re, in_im, out_re, out_im, t.tw_lds, nullptr, nullptr, outer, stride, 0, 0u, scale,
                      t.dir, false, static_cast<hipStream_t>(stream)};
   hipError_t e = tfa::launch_strided((int)plan->d.n, a);
   return e == hipSuccess ? TFA_OK : hip_fail(e, "strided launch");
