@@ -22,12 +22,19 @@ __host__ __device__ constexpr int lds_epth(int n) {
   return n <= 16 ? n : (n == 32 || n == 64) ? 8 : (n == 512 || n == 4096) ? 32 : 16;
 }
 
-// Batched c2c kernel launch shape: N = 1024 (the headline shape) runs 8 elements per thread in
-// 512-thread workgroups (4 transforms of 128 threads), measured 13.12 us against 13.64 us for
-// E = 16 / 256 threads (4096 rows, in-run sweep over E 4..32 and 64..1024 threads); the other
-// lengths keep lds_epth with 256-thread workgroups.
-__host__ __device__ constexpr int c2c_epth(int n) { return n == 1024 ? 8 : lds_epth(n); }
-__host__ __device__ constexpr int c2c_threads(int n) { return n == 1024 ? 512 : 256; }
+// Batched c2c kernel launch shape (elements per thread, threads per workgroup), from an in-run
+// sweep on MI355X over E in {4, 8, 16, 32} and 256..1024 threads at 4M complex elements per
+// launch, buffers rotated past the Infinity Cache.  Headline N = 1024: E = 8 / 512 threads,
+// 13.12 us against 13.64 us for the former E = 16 / 256.  Other lengths (us, new vs former):
+// 64 15.3 vs 20.7, 128 14.8 vs ~16, 256 14.2 vs ~15, 4096 14.2 vs 16.5, 8192 16.2 vs 19.0,
+// 16384 22.3 vs 24.6; 512 and 2048 unchanged within 1 %.
+__host__ __device__ constexpr int c2c_epth(int n) {
+  return n == 64 || n == 128 ? 4 : (n == 256 || n == 1024 || n == 2048 || n == 4096) ? 8
+         : (n == 8192 || n == 16384) ? 32 : lds_epth(n);
+}
+__host__ __device__ constexpr int c2c_threads(int n) {
+  return n == 64 || n == 256 ? 1024 : (n == 128 || n == 1024 || n == 2048 || n == 4096 || n == 16384) ? 512 : 256;
+}
 
 // Elements per thread of the real-row kernels (r2c / c2r over a half-length h complex transform),
 // from a launch-shape sweep on MI355X (4M real samples per launch, buffers rotated past the
