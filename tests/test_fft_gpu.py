@@ -123,3 +123,29 @@ def test_bluestein_vs_oracle(n, batch, inverse):
     got = _gpu_fft(re, im, inverse)
     ref = oracle.fft_core(re, im, inverse)
     assert rel_l2(*got, *ref) <= tol_bluestein(n), (n, inverse)
+
+
+@pytest.mark.parametrize("inverse", [False, True])
+def test_bluestein_fused_and_split_paths_agree(inverse):
+    # m = 16384 (n = 4099) runs the fused one-row-per-workgroup kernel for large batches and the
+    # split three-pass path for small ones; rows must agree across the two paths, and the fused
+    # batch is checked against the oracle on a few rows
+    re, im = seeded_complex(2048, 4099, seed=11)
+    fused = _gpu_fft(re, im, inverse)  # 2048 rows: fused kernel
+    split = _gpu_fft(re[:5], im[:5], inverse)  # 5 rows: split path
+    assert rel_l2(fused[0][:5], fused[1][:5], *split) <= tol_bluestein(4099)
+    ref = oracle.fft_core(re[:5], im[:5], inverse)
+    assert rel_l2(fused[0][:5], fused[1][:5], *ref) <= tol_bluestein(4099)
+    assert rel_l2(*split, *ref) <= tol_bluestein(4099)
+
+
+@pytest.mark.parametrize("n,batch", [(70000, 1), ((1 << 20) + 1, 1)])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_bluestein_split_large_vs_oracle(n, batch, inverse):
+    # split path at m = 262144 (512 x 512) and m = 2^22 (2048 x 2048).  The reference's fp32
+    # chirp angle makes its operator drift from the exact DFT as n grows, so parity is against
+    # the oracle's restatement of that operator, not a round trip
+    re, im = seeded_complex(batch, n, seed=n % 997)
+    got = _gpu_fft(re, im, inverse)
+    ref = oracle.fft_core(re, im, inverse)
+    assert rel_l2(*got, *ref) <= tol_bluestein(n), (n, inverse)

@@ -41,6 +41,14 @@ struct C2cThreads {
   static constexpr int PADN = S.npass > 1 ? lds_pad(N) : 1;
 };
 
+// Columns per workgroup for a strided (column) pass over transforms of length L: as wide as the
+// LDS and the 1024-thread limit allow (wider tiles = longer contiguous HBM segments), at most 64.
+__host__ __device__ constexpr int fourstep_tile(int l) {
+  int c = 64;
+  while (c > 1 && ((long long)c * (lds_pad(l) + 1) * 8 > kLdsBytes || c * (l / lds_epth(l)) > 1024)) c /= 2;
+  return c;
+}
+
 struct C2cArgs {
   const float* in_re;
   const float* in_im;  // nullptr: real input (imaginary part zero)
@@ -107,9 +115,29 @@ struct BluesteinArgs {
   hipStream_t stream;
 };
 hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a);
-hipError_t launch_bluestein_pre(const BluesteinArgs& a, float* y_re, float* y_im);
-hipError_t launch_bluestein_mul(const BluesteinArgs& a, float* y_re, float* y_im);
-hipError_t launch_bluestein_post(const BluesteinArgs& a, const float* y_re, const float* y_im);
+
+// Split (transposed-domain four-step) Bluestein, m = m1 * m2 >= 16384.
+struct BlueSplitArgs {
+  const float* in_re;
+  const float* in_im;  // nullptr: real input
+  float* out_re;
+  float* out_im;
+  float* ws_re;  // workspace, batch * m floats per plane
+  float* ws_im;
+  const float2* chirp;  // n entries
+  const float2* hp;     // m entries: H/m in transposed order, hp[k1*m2 + k2] = H[k1 + m1*k2] / m
+  const float2* tw1f;   // LDS-FFT tables for m1 (lds_epth layout), forward / inverse
+  const float2* tw1i;
+  const float2* tw2f;   // LDS-FFT tables for m2 (c2c_epth layout), forward / inverse
+  const float2* tw2i;
+  const float2* lo;  // W_m^j, j < 2^lo_bits
+  const float2* hi;  // W_m^(j << lo_bits)
+  int lo_bits, n;
+  long long batch;
+  float scale;
+  hipStream_t stream;
+};
+hipError_t launch_bluestein_split(int m1, int m2, const BlueSplitArgs& a);
 
 struct StftArgs {
   const float* signal;  // (batch, length)

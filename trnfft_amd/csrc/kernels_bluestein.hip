@@ -6,8 +6,18 @@
 // stored (first n entries only): one HBM read and one HBM write per element, against the
 // reference's three separate m-point FFTs and five full-size temporaries.
 //
-// Staged path (m > 16384): chirp/pad kernel -> four-step FFT_m -> pointwise * H/m -> four-step
-// IFFT_m -> chirp/slice kernel, with the intermediate rows in the caller's workspace.
+// Split path (m > 16384, and m = 16384 when there are too few rows to fill the GPU): each row is
+// spread over many workgroups with a transposed-domain four-step, m = M1 * M2, y[n1*M2 + n2],
+// spectrum index k = k1 + M1*k2:
+//   K1 (columns): y = x * chirp (zero past n), M1-point transform down each column n2, times
+//      W_m^(n2*k1)  ->  Z[k1][n2] in the workspace;
+//   K2 (rows): per row k1, M2-point forward transform (the spectrum Y[k1 + M1*k2] lands in row
+//      k1), times H/m in the same permuted order, M2-point inverse transform, times W_m^-(n2*k1);
+//   K3 (columns): M1-point inverse transform down each column gives p[n1*M2 + n2], times chirp
+//      and the output scale, first n entries stored.
+// The spectrum is never brought back to natural order: the filter multiply happens in the
+// transposed domain, so the chain is three passes (the intermediate, batch*m*8 bytes, stays in
+// the Infinity Cache at the BASELINE sizes) instead of two full four-step transforms.
 #include "kernels.h"
 
 namespace tfa {
@@ -102,72 +112,166 @@ hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a) {
   }
 }
 
-// ---- staged path helpers ----------------------------------------------------------------------
-// y[b, i] = x[b, i] * chirp[i] for i < n, 0 for n <= i < m.
-__global__ void bluestein_pre_kernel(const float* __restrict__ in_re, const float* __restrict__ in_im,
-                                     float* __restrict__ y_re, float* __restrict__ y_im,
-                                     const float2* __restrict__ chirp, int n, int m, long long total) {
-  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= total) return;
-  const long long b = g / m;
-  const int i = (int)(g - b * m);
-  float2 y = make_float2(0.0f, 0.0f);
-  if (i < n) {
-    const size_t s = (size_t)b * n + i;
-    y = cmul(make_float2(in_re[s], in_im ? in_im[s] : 0.0f), chirp[i]);
+// ---- split path ---------------------------------------------------------------------------------
+
+// W_m^j from the two-level table (j < m); conjugated when CONJ.
+template <bool CONJ>
+__device__ __forceinline__ float2 root_m(const float2* __restrict__ lo, const float2* __restrict__ hi, unsigned j,
+                                         int lo_bits) {
+  const float2 w = cmul(lo[j & ((1u << lo_bits) - 1)], hi[j >> lo_bits]);
+  return CONJ ? make_float2(w.x, -w.y) : w;
+}
+
+// Column passes: C adjacent columns of one row's M1 x M2 view per workgroup (coalesced across
+// columns), LDS Stockham down the column.
+template <int M1>
+struct BlueColCfg {
+  static constexpr int E = lds_epth(M1);
+  static constexpr int T = M1 / E;
+  static constexpr int C = fourstep_tile(M1);
+  static constexpr int PADN = lds_pad(M1) + 1;
+};
+
+template <int M1, bool REAL_IN>
+__global__ __launch_bounds__((BlueColCfg<M1>::C * BlueColCfg<M1>::T)) void blue_col_fwd_kernel(
+    const float* __restrict__ in_re, const float* __restrict__ in_im, float* __restrict__ ws_re,
+    float* __restrict__ ws_im, const float2* __restrict__ chirp, const float2* __restrict__ tw,
+    const float2* __restrict__ lo, const float2* __restrict__ hi, int lo_bits, int n, int m2, int tiles) {
+  using G = BlueColCfg<M1>;
+  constexpr int E = G::E, T = G::T, C = G::C, PADN = G::PADN;
+  __shared__ float lre[C * PADN];
+  __shared__ float lim[C * PADN];
+  const int c = threadIdx.x % C, t = threadIdx.x / C;
+  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
+  const long long b = tile / tiles;
+  const int col = (int)(tile % tiles) * C + c;
+  const unsigned m = (unsigned)M1 * (unsigned)m2;
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = (t + T * e) * m2 + col;
+    float2 y = make_float2(0.0f, 0.0f);
+    if (i < n) {
+      const size_t s = (size_t)b * n + i;
+      y = cmul(make_float2(in_re[s], REAL_IN ? 0.0f : in_im[s]), chirp[i]);
+    }
+    v[e] = y;
   }
-  y_re[g] = y.x;
-  y_im[g] = y.y;
+  LdsFft<M1, E, -1, false>::run(v, lre + c * PADN, lim + c * PADN, tw, t);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int k1 = t + T * e;
+    const float2 y = cmul(v[e], root_m<false>(lo, hi, ((unsigned)col * (unsigned)k1) & (m - 1), lo_bits));
+    const size_t o = (size_t)b * m + (size_t)k1 * m2 + col;
+    st_stream(ws_re + o, y.x);
+    st_stream(ws_im + o, y.y);
+  }
 }
 
-// y[b, i] *= hs[i]
-__global__ void bluestein_mul_kernel(float* __restrict__ y_re, float* __restrict__ y_im,
-                                     const float2* __restrict__ hs, int m, long long total) {
-  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= total) return;
-  const int i = (int)(g % m);
-  const float2 y = cmul(make_float2(y_re[g], y_im[g]), hs[i]);
-  y_re[g] = y.x;
-  y_im[g] = y.y;
+template <int M1>
+__global__ __launch_bounds__((BlueColCfg<M1>::C * BlueColCfg<M1>::T)) void blue_col_inv_kernel(
+    const float* __restrict__ ws_re, const float* __restrict__ ws_im, float* __restrict__ out_re,
+    float* __restrict__ out_im, const float2* __restrict__ chirp, const float2* __restrict__ tw, int n, int m2,
+    int tiles, float scale) {
+  using G = BlueColCfg<M1>;
+  constexpr int E = G::E, T = G::T, C = G::C, PADN = G::PADN;
+  __shared__ float lre[C * PADN];
+  __shared__ float lim[C * PADN];
+  const int c = threadIdx.x % C, t = threadIdx.x / C;
+  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
+  const long long b = tile / tiles;
+  const int col = (int)(tile % tiles) * C + c;
+  const size_t m = (size_t)M1 * m2;
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const size_t s = (size_t)b * m + (size_t)(t + T * e) * m2 + col;
+    v[e] = make_float2(ld_stream(ws_re + s), ld_stream(ws_im + s));
+  }
+  LdsFft<M1, E, 1, false>::run(v, lre + c * PADN, lim + c * PADN, tw, t);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = (t + T * e) * m2 + col;
+    if (i < n) {
+      const float2 y = cmul(v[e], chirp[i]);
+      const size_t o = (size_t)b * n + i;
+      out_re[o] = y.x * scale;
+      out_im[o] = y.y * scale;
+    }
+  }
 }
 
-// out[b, i] = y[b, i] * chirp[i] * scale for i < n
-__global__ void bluestein_post_kernel(const float* __restrict__ y_re, const float* __restrict__ y_im,
-                                      float* out_re, float* out_im, const float2* __restrict__ chirp,
-                                      int n, int m, long long total, float scale) {
-  const long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= total) return;
-  const long long b = g / n;
-  const int i = (int)(g - b * n);
-  const size_t s = (size_t)b * m + i;
-  const float2 y = cmul(make_float2(y_re[s], y_im[s]), chirp[i]);
-  out_re[g] = y.x * scale;
-  out_im[g] = y.y * scale;
+// Row pass: forward M2-point transform, filter, inverse M2-point transform, inverse twiddle, in
+// place in the workspace (rows of M2 contiguous elements; batched-c2c launch shape).
+template <int M2>
+__global__ __launch_bounds__(C2cThreads<M2>::THREADS) void blue_row_kernel(
+    float* __restrict__ ws_re, float* __restrict__ ws_im, const float2* __restrict__ hp,
+    const float2* __restrict__ tw_f, const float2* __restrict__ tw_i, const float2* __restrict__ lo,
+    const float2* __restrict__ hi, int lo_bits, int m1) {
+  using C = C2cThreads<M2>;
+  constexpr int E = C::E, T = C::T;
+  constexpr bool WL = T <= 64;
+  __shared__ float lre[C::XF * C::PADN];
+  __shared__ float lim[C::XF * C::PADN];
+  const int tid = threadIdx.x % T, xf = threadIdx.x / T;
+  const long long row = (long long)blockIdx.x * C::XF + xf;  // (batch, k1)
+  const int k1 = (int)(row % m1);
+  const unsigned m = (unsigned)m1 * (unsigned)M2;
+  float* pr = ws_re + (size_t)row * M2 + tid;
+  float* pi = ws_im + (size_t)row * M2 + tid;
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = make_float2(pr[T * e], pi[T * e]);
+  LdsFft<M2, E, -1, WL>::run(v, lre + xf * C::PADN, lim + xf * C::PADN, tw_f, tid);
+  const float2* h = hp + (size_t)k1 * M2 + tid;
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], h[T * e]);
+  LdsFft<M2, E, 1, WL>::run(v, lre + xf * C::PADN, lim + xf * C::PADN, tw_i, tid);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const unsigned n2 = (unsigned)(tid + T * e);
+    const float2 y = cmul(v[e], root_m<true>(lo, hi, (n2 * (unsigned)k1) & (m - 1), lo_bits));
+    pr[T * e] = y.x;
+    pi[T * e] = y.y;
+  }
 }
 
-static unsigned blocks_for(long long total, int threads) {
-  return (unsigned)((total + threads - 1) / threads);
-}
-
-hipError_t launch_bluestein_pre(const BluesteinArgs& a, float* y_re, float* y_im) {
-  const long long total = a.batch * (long long)a.m;
-  hipLaunchKernelGGL(bluestein_pre_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, a.stream,
-                     a.in_re, a.in_im, y_re, y_im, a.chirp, a.n, a.m, total);
+template <int M1, int M2>
+static hipError_t launch_blue_split_t(const BlueSplitArgs& a) {
+  using G = BlueColCfg<M1>;
+  using R = C2cThreads<M2>;
+  static_assert(M2 % G::C == 0 && M1 % R::XF == 0, "split tiles");
+  const int tiles = M2 / G::C;
+  const unsigned cblocks = (unsigned)(a.batch * tiles);
+  if (a.in_im == nullptr)
+    hipLaunchKernelGGL((blue_col_fwd_kernel<M1, true>), dim3(cblocks), dim3(G::C * G::T), 0, a.stream, a.in_re,
+                       a.in_im, a.ws_re, a.ws_im, a.chirp, a.tw1f, a.lo, a.hi, a.lo_bits, a.n, M2, tiles);
+  else
+    hipLaunchKernelGGL((blue_col_fwd_kernel<M1, false>), dim3(cblocks), dim3(G::C * G::T), 0, a.stream, a.in_re,
+                       a.in_im, a.ws_re, a.ws_im, a.chirp, a.tw1f, a.lo, a.hi, a.lo_bits, a.n, M2, tiles);
+  hipLaunchKernelGGL((blue_row_kernel<M2>), dim3((unsigned)(a.batch * M1 / R::XF)), dim3(R::THREADS), 0, a.stream,
+                     a.ws_re, a.ws_im, a.hp, a.tw2f, a.tw2i, a.lo, a.hi, a.lo_bits, M1);
+  hipLaunchKernelGGL((blue_col_inv_kernel<M1>), dim3(cblocks), dim3(G::C * G::T), 0, a.stream, a.ws_re, a.ws_im,
+                     a.out_re, a.out_im, a.chirp, a.tw1i, a.n, M2, tiles, a.scale);
   return hipGetLastError();
 }
 
-hipError_t launch_bluestein_mul(const BluesteinArgs& a, float* y_re, float* y_im) {
-  const long long total = a.batch * (long long)a.m;
-  hipLaunchKernelGGL(bluestein_mul_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, a.stream,
-                     y_re, y_im, a.hs, a.m, total);
-  return hipGetLastError();
-}
-
-hipError_t launch_bluestein_post(const BluesteinArgs& a, const float* y_re, const float* y_im) {
-  const long long total = a.batch * (long long)a.n;
-  hipLaunchKernelGGL(bluestein_post_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, a.stream,
-                     y_re, y_im, a.out_re, a.out_im, a.chirp, a.n, a.m, total, a.scale);
-  return hipGetLastError();
+hipError_t launch_bluestein_split(int m1, int m2, const BlueSplitArgs& a) {
+  const long long key = (long long)m1 * 65536 + m2;
+  switch (key) {
+    case 128LL * 65536 + 128: return launch_blue_split_t<128, 128>(a);
+    case 128LL * 65536 + 256: return launch_blue_split_t<128, 256>(a);
+    case 256LL * 65536 + 256: return launch_blue_split_t<256, 256>(a);
+    case 256LL * 65536 + 512: return launch_blue_split_t<256, 512>(a);
+    case 512LL * 65536 + 512: return launch_blue_split_t<512, 512>(a);
+    case 512LL * 65536 + 1024: return launch_blue_split_t<512, 1024>(a);
+    case 1024LL * 65536 + 1024: return launch_blue_split_t<1024, 1024>(a);
+    case 1024LL * 65536 + 2048: return launch_blue_split_t<1024, 2048>(a);
+    case 2048LL * 65536 + 2048: return launch_blue_split_t<2048, 2048>(a);
+    case 2048LL * 65536 + 4096: return launch_blue_split_t<2048, 4096>(a);
+    case 4096LL * 65536 + 4096: return launch_blue_split_t<4096, 4096>(a);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace tfa

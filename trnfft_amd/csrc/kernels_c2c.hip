@@ -108,14 +108,6 @@ hipError_t launch_c2c_lds(int n, const C2cArgs& a) {
 // ---------------------------------------------------------------------------------------------
 // Four-step: x viewed as (N1 rows) x (N2 columns), n = N2*n1 + n2, k = k1 + N1*k2.
 // ---------------------------------------------------------------------------------------------
-// Columns per workgroup for a strided pass over transforms of length L: as wide as the LDS and
-// the 1024-thread limit allow (wider tiles = longer contiguous HBM segments), at most 64.
-__host__ __device__ constexpr int fourstep_tile(int l) {
-  int c = 64;
-  while (c > 1 && ((long long)c * (lds_pad(l) + 1) * 8 > kLdsBytes || c * (l / lds_epth(l)) > 1024)) c /= 2;
-  return c;
-}
-
 // Strided-axis transform: x viewed as (outer, N1, S) row-major; transform along the N1 axis
 // (element stride S) for every (outer, column) pair.  One workgroup = C adjacent columns of one
 // outer block, so each load/store instruction covers C consecutive floats.  With TWIDDLE the

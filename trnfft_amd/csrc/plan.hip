@@ -31,6 +31,11 @@ bool is_pow2(int64_t n) { return n > 0 && (n & (n - 1)) == 0; }
 constexpr int64_t kMaxLdsN = 16384;
 // Largest power-of-two transform of the two-pass four-step path (4096 x 4096).
 constexpr int64_t kMaxFourStepN = int64_t(1) << 24;
+// Smallest padded Bluestein length with the split three-pass path (m1 = m2 = 128), and the row
+// count below which it replaces the fused kernel at m = 16384 (measured at 256 rows: fused 35.6
+// us, split 57.3 us, so only a handful of rows, which leave most CUs idle, go split).
+constexpr int64_t kMinBlueSplitM = 16384;
+constexpr int64_t kBlueSplitRows = 64;
 
 // exp(dir * 2*pi*i * num / den), num reduced mod den first; computed in fp64, rounded to fp32.
 float2 unit_root(int64_t num, int64_t den, int dir) {
@@ -74,7 +79,11 @@ struct tfa_plan {
   int device = 0;
   int64_t m = 0;  // padded length (Bluestein), else n
   C2cTables fwd, inv;  // C2C uses the one for its direction; Bluestein uses both (length m)
-  bool blue_fused = false;
+  bool blue_fused = false;  // Bluestein: fused one-launch kernel available (m <= 16384)
+  bool blue_split = false;  // Bluestein: split three-pass path available (m >= 16384)
+  int blue_m1 = 0, blue_m2 = 0, blue_lo_bits = 0;
+  float2 *b_tw1f = nullptr, *b_tw1i = nullptr, *b_tw2f = nullptr, *b_tw2i = nullptr;
+  float2 *b_lo = nullptr, *b_hi = nullptr, *b_hp = nullptr;
   float2* chirp = nullptr;
   float2* hs = nullptr;
   C2cTables col;          // FFT2: LDS table for n2/8 (pass 2)
@@ -133,6 +142,14 @@ struct tfa_plan {
 };
 
 namespace {
+
+// Bluestein path choice: the fused kernel holds one row per workgroup, so with fewer than
+// kBlueSplitRows rows it leaves most of the GPU idle and the split three-pass path (each row
+// spread over many workgroups per pass) takes over; above 16384 only the split path exists.
+bool blue_use_split(const tfa_plan* p, int64_t batch) {
+  if (!p->blue_fused) return true;
+  return p->blue_split && batch < kBlueSplitRows;
+}
 
 size_t c2c_workspace(const C2cTables& t, int64_t batch) {
   return t.fourstep ? (size_t)2 * sizeof(float) * (size_t)batch * (size_t)t.n : 0;
@@ -243,6 +260,7 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         break;
       }
       p->blue_fused = m <= kMaxLdsN;
+      p->blue_split = m >= kMinBlueSplitM;
       if (p->blue_fused) {
         // the fused kernel's own launch shape (tfa::blue_epth) fixes its table layout
         p->fwd.n = p->inv.n = m;
@@ -250,9 +268,6 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         p->inv.dir = 1;
         if ((rc = p->upload(lds_table((int)m, -1, tfa::blue_epth((int)m)), &p->fwd.tw))) break;
         if ((rc = p->upload(lds_table((int)m, 1, tfa::blue_epth((int)m)), &p->inv.tw))) break;
-      } else {
-        if ((rc = p->build_c2c(m, -1, &p->fwd))) break;
-        if ((rc = p->build_c2c(m, 1, &p->inv))) break;
       }
       const std::vector<float2> chirp = reference_chirp(n, dir);
       // h = conj(chirp) circularly wrapped (trnfft/fft_core.py:1337-1345); H = FFT_m(h) / m
@@ -267,7 +282,29 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       for (int64_t i = 0; i < m; ++i)
         hs[(size_t)i] = make_float2((float)(h[(size_t)i].real() / (double)m), (float)(h[(size_t)i].imag() / (double)m));
       if ((rc = p->upload(chirp, &p->chirp))) break;
-      rc = p->upload(hs, &p->hs);
+      if ((rc = p->upload(hs, &p->hs))) break;
+      if (p->blue_split) {
+        // m = m1 * m2 (m1 = 2^floor(log2 m / 2)); tables of the three passes, H/m permuted to
+        // the transposed spectrum order hp[k1*m2 + k2] = H[k1 + m1*k2] / m
+        const int lg = tfa::ilog2((int)m);
+        p->blue_m1 = 1 << (lg / 2);
+        p->blue_m2 = (int)(m / p->blue_m1);
+        p->blue_lo_bits = (lg + 1) / 2;
+        const int m1 = p->blue_m1, m2 = p->blue_m2;
+        if ((rc = p->upload(lds_table(m1, -1), &p->b_tw1f))) break;
+        if ((rc = p->upload(lds_table(m1, 1), &p->b_tw1i))) break;
+        if ((rc = p->upload(lds_table(m2, -1, tfa::c2c_epth(m2)), &p->b_tw2f))) break;
+        if ((rc = p->upload(lds_table(m2, 1, tfa::c2c_epth(m2)), &p->b_tw2i))) break;
+        std::vector<float2> lo((size_t)1 << p->blue_lo_bits), hi((size_t)(m >> p->blue_lo_bits));
+        for (size_t j = 0; j < lo.size(); ++j) lo[j] = unit_root((int64_t)j, m, -1);
+        for (size_t j = 0; j < hi.size(); ++j) hi[j] = unit_root((int64_t)j << p->blue_lo_bits, m, -1);
+        if ((rc = p->upload(lo, &p->b_lo))) break;
+        if ((rc = p->upload(hi, &p->b_hi))) break;
+        std::vector<float2> hp((size_t)m);
+        for (int k1 = 0; k1 < m1; ++k1)
+          for (int k2 = 0; k2 < m2; ++k2) hp[(size_t)k1 * m2 + k2] = hs[(size_t)k1 + (size_t)m1 * k2];
+        rc = p->upload(hp, &p->b_hp);
+      }
       break;
     }
     case TFA_KIND_STFT:
@@ -370,8 +407,7 @@ int tfa_plan_workspace_size(const tfa_plan* plan, int64_t batch, size_t* bytes) 
       *bytes = c2c_workspace(plan->d.inverse ? plan->inv : plan->fwd, batch);
       break;
     case TFA_KIND_BLUESTEIN:
-      if (!plan->blue_fused)
-        *bytes = (size_t)2 * sizeof(float) * (size_t)batch * (size_t)plan->m + c2c_workspace(plan->fwd, batch);
+      if (blue_use_split(plan, batch)) *bytes = (size_t)2 * sizeof(float) * (size_t)batch * (size_t)plan->m;
       break;
     default:
       break;
@@ -400,22 +436,18 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
       tfa::BluesteinArgs a{in_re, in_im, out_re, out_im, plan->chirp, plan->hs, plan->fwd.tw,
                            plan->inv.tw, (int)n, (int)plan->m, batch, scale, s};
       hipError_t e;
-      if (plan->blue_fused) {
+      if (!blue_use_split(plan, batch)) {
         e = tfa::launch_bluestein_fused((int)plan->m, a);
         return e == hipSuccess ? TFA_OK : hip_fail(e, "bluestein launch");
       }
-      if (!workspace) return fail(TFA_ERR_INVALID, "staged Bluestein needs a workspace");
+      if (!workspace) return fail(TFA_ERR_INVALID, "split Bluestein needs a workspace (tfa_plan_workspace_size)");
       float* y_re = static_cast<float*>(workspace);
       float* y_im = y_re + (size_t)batch * (size_t)plan->m;
-      void* inner_ws = y_im + (size_t)batch * (size_t)plan->m;
-      if ((e = tfa::launch_bluestein_pre(a, y_re, y_im)) != hipSuccess) return hip_fail(e, "bluestein pre");
-      int rc = run_c2c(plan->fwd, batch, y_re, y_im, y_re, y_im, inner_ws, 1.0f, s);
-      if (rc) return rc;
-      if ((e = tfa::launch_bluestein_mul(a, y_re, y_im)) != hipSuccess) return hip_fail(e, "bluestein mul");
-      rc = run_c2c(plan->inv, batch, y_re, y_im, y_re, y_im, inner_ws, 1.0f, s);
-      if (rc) return rc;
-      if ((e = tfa::launch_bluestein_post(a, y_re, y_im)) != hipSuccess) return hip_fail(e, "bluestein post");
-      return TFA_OK;
+      tfa::BlueSplitArgs sa{in_re, in_im, out_re, out_im, y_re, y_im, plan->chirp, plan->b_hp, plan->b_tw1f,
+                            plan->b_tw1i, plan->b_tw2f, plan->b_tw2i, plan->b_lo, plan->b_hi, plan->blue_lo_bits,
+                            (int)n, batch, scale, s};
+      e = tfa::launch_bluestein_split(plan->blue_m1, plan->blue_m2, sa);
+      return e == hipSuccess ? TFA_OK : hip_fail(e, "bluestein split launch");
     }
     case TFA_KIND_FFT2: {
       if (in_re == out_re || (in_im && in_im == out_im)) return fail(TFA_ERR_INVALID, "FFT2 output must not alias the input");
