@@ -37,6 +37,18 @@ __device__ __forceinline__ void st_stream2(float2* p, float2 v) {
   __builtin_nontemporal_store(r, reinterpret_cast<f2v*>(p));
 }
 
+// w[e] = base * W_{2E}^e (W = exp(DIR 2 pi i / 2E)): with base = W_N^tid this is W_N^(tid + T e)
+// for N = 2 T E, so one table load per thread replaces E of them.
+template <int E, int DIR, int I = 0>
+struct TwRow {
+  __device__ __forceinline__ static void fill(float2 (&w)[E], float2 base) {
+    if constexpr (I < E) {
+      w[I] = twiddle_const<I, 2 * E, DIR>(base);
+      TwRow<E, DIR, I + 1>::fill(w, base);
+    }
+  }
+};
+
 // x: (batch, 2H) real rows; out: (batch, H+1) bins.  twr[k] = W_N^k = exp(-2 pi i k / N), k < H.
 template <int H, bool TAIL, int E_ = real_epth(H, false), int THR = 256>
 __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
@@ -67,6 +79,8 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
   if (!valid) return;
   float* qr = out_re + (size_t)b * (H + 1) + tid;
   float* qi = out_im + (size_t)b * (H + 1) + tid;
+  float2 wk[E];
+  TwRow<E, -1>::fill(wk, twr[tid]);  // W_N^k, k = tid + T e (9.8 -> 9.1 us against E table loads)
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int k = tid + T * e;
@@ -75,7 +89,7 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
     const float2 c = make_float2(mre[r], -mim[r]);  // conj Z[H-k]
     const float2 ev = make_float2(0.5f * (a.x + c.x), 0.5f * (a.y + c.y));
     const float2 od = make_float2(0.5f * (a.y - c.y), -0.5f * (a.x - c.x));  // (a - c) / 2i
-    const float2 y = cadd(ev, cmul(twr[k], od));
+    const float2 y = cadd(ev, cmul(wk[e], od));
     st_stream(qr + T * e, y.x);
     st_stream(qi + T * e, y.y);
   }
@@ -116,6 +130,7 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
   }
   exchange_sync<WL>();
   float2 v[E];
+  // (the table loads measured faster here than TwRow's derived twiddles: 8.2 vs 9.0 us)
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int k = tid + T * e;
