@@ -168,3 +168,23 @@ def test_fft2_two_pass_complex_and_inverse(shape):
     ref_back = oracle.ifftn(ref, dim=(-2, -1))
     assert rel_l2(back.real, back.imag, *ref_back) <= tol_pow2(n)
     assert rel_l2(back.real, back.imag, re, im) <= 2 * tol_pow2(n)
+
+
+@pytest.mark.parametrize("shape", [(2, 16, 16), (1, 4096, 16), (3, 16, 2048), (2, 512, 1024), (1, 128, 64), (2, 64, 32)])
+def test_fft2_two_pass_real_half_spectrum(shape):
+    # real input: pass 1 writes columns 0..W/2, pass 2 completes W/2+1..W-1 from the 2-D
+    # Hermitian symmetry; forward and inverse (ifftn of a real array) against the oracle
+    rng = np.random.default_rng(13)
+    x = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
+    n = shape[-1] * shape[-2]
+    got = trnfft_amd.fft2(x.cuda())
+    ref = oracle.fft2(x)
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(n)
+    inv = trnfft_amd.ifftn(x.cuda(), dim=(-2, -1))
+    ref_inv = oracle.ifftn(x, dim=(-2, -1))
+    assert rel_l2(inv.real, inv.imag, *ref_inv) <= tol_pow2(n)
+    # the completed half is the conjugate reflection of the computed one, exactly
+    g = torch.complex(got.real, got.imag).cpu()
+    mirrored = torch.conj(torch.roll(torch.flip(g, dims=(-2, -1)), shifts=(1, 1), dims=(-2, -1)))
+    w = shape[-1]
+    assert torch.equal(g[..., w // 2 + 1:], mirrored[..., w // 2 + 1:])

@@ -7,6 +7,9 @@
 //         (LDS Stockham), then applies the 8-point DFT across those rows and the twiddle
 //         W_H^(r1 q2), and writes the 8 results as the consecutive rows 8*r1 + q2: every HBM
 //         access is a whole contiguous row.
+// Real input: pass 1 pairs rows and writes columns 0..W/2 only; pass 2 transforms those and
+//         writes each column w < W/2 a second time as column W-w (2-D Hermitian symmetry), so
+//         the half-spectrum is read once and the full spectrum written once.
 // Pass 2 (in place on the output): for each group q2, the HR-point transform over r1 of the rows
 //         q2 + 8*r1 gives Y[q2 + 8*q1], which lands on row q2 + 8*q1 -- the same row set, so a
 //         workgroup (C adjacent columns of one group) reads and then overwrites only its own data.
@@ -122,7 +125,8 @@ __global__ __launch_bounds__((Fft2RowPair<W, E_>::THREADS)) void fft2_pass1_real
   float2 tq[8];
 #pragma unroll
   for (int q = 1; q < 8; ++q) tq[q] = tw_h[(r1 * q) & (H - 1)];
-  for (int k = threadIdx.x; k < W; k += THREADS) {
+  // columns 0..W/2 only: pass 2 completes the rest from the 2-D Hermitian symmetry
+  for (int k = threadIdx.x; k <= W / 2; k += THREADS) {
     const int ik = lds_pad(k), ir = lds_pad((W - k) & (W - 1));
     float2 z[8];
 #pragma unroll
@@ -152,7 +156,10 @@ __host__ __device__ constexpr int fft2_tile(int hr) {
   return c;
 }
 
-template <int HR, int DIR, int C = fft2_tile(HR), int E_ = fft2_col_epth(HR)>
+// HALF (real input): pass 1 wrote only columns 0..W/2; each transformed column w in 1..W/2-1 is
+// also written, conjugated and row-reflected, as column W-w (X[h][w] = conj X[-h][-w] for a real
+// image).  Columns above W/2 are never read, so these writes race with nothing.
+template <int HR, int DIR, bool HALF = false, int C = fft2_tile(HR), int E_ = fft2_col_epth(HR)>
 __global__ __launch_bounds__(C * (HR / E_)) void fft2_pass2_kernel(
     float* re, float* im, const float2* __restrict__ tw, int W, int tiles_per_group, float scale) {
   constexpr int E = E_, T = HR / E;
@@ -166,7 +173,7 @@ __global__ __launch_bounds__(C * (HR / E_)) void fft2_pass2_kernel(
   const long long b = grp / 8;
   const int q2 = (int)(grp % 8);
   const int col = (int)(tile % tiles_per_group) * C + c;
-  const bool valid = col < W;
+  const bool valid = col < (HALF ? W / 2 + 1 : W);
   // element r1 (input) and q1 (output) of column col in group q2 both live at row q2 + 8*index
   const size_t base = (size_t)b * (8 * HR) * W + (size_t)q2 * W + col;
   const size_t step = (size_t)8 * W;
@@ -187,6 +194,21 @@ __global__ __launch_bounds__(C * (HR / E_)) void fft2_pass2_kernel(
     st_stream(re + o, v[e].x);
     st_stream(im + o, v[e].y);
   }
+  if constexpr (HALF) {
+    if (col >= 1 && col < W / 2) {
+      constexpr int H = 8 * HR;
+      const size_t mb = (size_t)b * H * W + (size_t)(W - col);
+      // the mirror of an aligned column tile [w0, w0 + C) is [W - w0 - C + 1, W - w0]: one
+      // column off the line grid, so plain stores (L2 merges the neighbouring tile's halves)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int h = q2 + 8 * (t + T * e);
+        const size_t o = mb + (size_t)((H - h) & (H - 1)) * W;
+        re[o] = v[e].x;
+        im[o] = -v[e].y;
+      }
+    }
+  }
 }
 
 template <int W, int DIR>
@@ -204,10 +226,15 @@ static hipError_t launch_pass1_w(const Fft2Args& a) {
 template <int HR, int DIR>
 static hipError_t launch_pass2_h(const Fft2Args& a) {
   constexpr int C = fft2_tile(HR), T = HR / fft2_col_epth(HR);
-  const int tiles = (int)((a.w + C - 1) / C);
+  const bool half = a.in_im == nullptr;  // real input: pass 1 wrote columns 0..W/2
+  const int tiles = (int)(((half ? a.w / 2 + 1 : a.w) + C - 1) / C);
   const long long blocks = a.batch * 8 * (long long)tiles;
-  hipLaunchKernelGGL((fft2_pass2_kernel<HR, DIR>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream, a.out_re,
-                     a.out_im, a.tw_hr, (int)a.w, tiles, a.scale);
+  if (half)
+    hipLaunchKernelGGL((fft2_pass2_kernel<HR, DIR, true>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream,
+                       a.out_re, a.out_im, a.tw_hr, (int)a.w, tiles, a.scale);
+  else
+    hipLaunchKernelGGL((fft2_pass2_kernel<HR, DIR, false>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream,
+                       a.out_re, a.out_im, a.tw_hr, (int)a.w, tiles, a.scale);
   return hipGetLastError();
 }
 
