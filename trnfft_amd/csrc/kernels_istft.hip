@@ -60,8 +60,10 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
     const int f = i % FR, k = i / FR;
     float re = 0.0f, im = 0.0f;
     if (f < nf) {
-      re = ld_stream(sre + sbase + (size_t)k * n_frames + f);
-      im = ld_stream(sim + sbase + (size_t)k * n_frames + f);
+      // plain loads: a bin row segment is FR frames (64 bytes at n_fft 512), so a cache line is
+      // shared with the neighbouring tile, which then finds it in L2 (measured 4 % faster)
+      re = sre[sbase + (size_t)k * n_frames + f];
+      im = sim[sbase + (size_t)k * n_frames + f];
     }
     float* reg = lds + (f >> 1) * RP + (f & 1) * 2 * F;
     reg[k] = re;
