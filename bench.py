@@ -166,16 +166,23 @@ def bench_headline(steps: int, warmup: int):
             for k in range(steps):
                 step(k, strm)
     torch.cuda.current_stream().wait_stream(cap)
-    for _ in range(2):  # warm-up replays (the first replay after capture runs measurably slower)
+    for _ in range(3):  # warm-up replays (the first replays after capture run measurably slower)
         graph.replay()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record()
-    graph.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    t_region_launch = ev0.elapsed_time(ev1) * 1e-3 / (2 * steps)
+    # the K-step region is timed three times (each: synchronize, events around one replay of all
+    # K steps, synchronize); the median region is reported
+    regions = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record()
+        graph.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        regions.append((ev0.elapsed_time(ev1) * 1e-3, time.perf_counter() - t0))
+    regions.sort()
+    t_region, wall = regions[1]
+    t_region_launch = t_region / (2 * steps)
 
     # per-launch kernel durations (separate pass, event pairs around each launch)
     timer = EventTimer()
@@ -221,6 +228,7 @@ def bench_headline(steps: int, warmup: int):
         "wall_s": wall,
         "ms_per_step": wall / steps * 1e3,
         "value": flops_step * steps / wall / 1e9,
+        "regions_ms": [round(r[0] * 1e3, 4) for r in regions],
         "t_launch_s": t_launch,
         "t_launch_median_s": _median(d),
         "bytes_launch": bytes_launch,
@@ -478,9 +486,11 @@ def main(argv=None):
         "dtype": "f32",
         "data": "synthetic: N(0,1) re/im, seed 42, 4096x1024 (BASELINE config 1)",
         "value_eager": round(2 * flops_fft(1024, 4096) * args.steps / head["wall_eager_s"] / 1e9, 1),
+        "timed_regions_ms": head["regions_ms"],
         "config": {
             "workload": "batched c2c FFT, 4096 x N=1024 fp32 split re/im; step = forward fft of one batch + "
-            "inverse fft of another, buffers rotated over >1 GiB; K steps replayed as one HIP graph",
+            "inverse fft of another, buffers rotated over >1 GiB; K steps replayed as one HIP graph, the "
+            "K-step region timed 3 times after 3 warm-up replays, median reported",
             "n": 1024,
             "batch": 4096,
             "buffer_sets": head["buffer_sets"],
