@@ -48,14 +48,25 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   const bool valid = b < batch;
   const size_t base = (size_t)b * n;
 
-  float2 v[E];
+  // every workgroup of the launch runs the same phase at the same time, so nothing hides a
+  // table load issued where it is used: the chirp is loaded once (it multiplies both the input
+  // and the output) and the filter spectrum is requested before the forward transform
+  // (with 16 or more elements per thread the extra registers would spill: both tables are then
+  // read where they are used)
+  constexpr bool PRE = E <= 8;
+  float2 v[E], ch[PRE ? E : 1], hv[PRE ? E : 1];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int i = tid + T * e;
+    const float2 c = i < n ? chirp[i] : make_float2(0.0f, 0.0f);
+    if constexpr (PRE) {
+      ch[e] = c;
+      hv[e] = hs[i];
+    }
     float2 y = make_float2(0.0f, 0.0f);
     if (valid && i < n) {
       const float2 x = make_float2(in_re[base + i], REAL_IN ? 0.0f : in_im[base + i]);
-      y = cmul(x, chirp[i]);
+      y = cmul(x, c);
     }
     v[e] = y;
   }
@@ -63,14 +74,14 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   float* my_im = lim + xf * C::PADN;
   LdsFft<M, E, -1, (T <= 64)>::run(v, my_re, my_im, tw_f, tid);
 #pragma unroll
-  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], hs[tid + T * e]);
+  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], PRE ? hv[PRE ? e : 0] : hs[tid + T * e]);
   LdsFft<M, E, 1, (T <= 64)>::run(v, my_re, my_im, tw_i, tid);
   if (valid) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int i = tid + T * e;
       if (i < n) {
-        const float2 y = cmul(v[e], chirp[i]);
+        const float2 y = cmul(v[e], PRE ? ch[PRE ? e : 0] : chirp[i]);
         out_re[base + i] = y.x * scale;
         out_im[base + i] = y.y * scale;
       }
