@@ -463,7 +463,7 @@ def main(argv=None):
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU only (requested --gpus {args.gpus}): every config here is a batch "
-            "of independent transforms; see DESIGN.md for how the path shards across GPUs",
+            "of independent transforms, which would shard by batch rows with no communication",
             file=sys.stderr,
         )
         return 2
