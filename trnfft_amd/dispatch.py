@@ -6,7 +6,7 @@
 
 This package is the HIP dispatch target only: every compute entry point raises RuntimeError
 when ``_use_hip()`` is False.  There is no CPU fallback inside it; trnfft keeps its own pytorch
-path and consults ``_use_hip()`` before delegating here (see INTEGRATION.md at the repo root).
+path and consults ``_use_hip()`` before delegating here.
 
 CPU inputs are moved to the current GPU and results moved back, as the reference's NKI path
 does with its XLA device (trnfft/nki/dispatch.py:423-428, trnfft/nki/autograd.py:58-60).
