@@ -61,3 +61,29 @@ def test_graph_replay_stft_and_fft2():
         assert torch.equal(o2.real, e2.real) and torch.equal(o2.imag, e2.imag)
         trnfft_amd.fft(torch.randn(16, 64, device="cuda"))
         torch.cuda.synchronize()
+
+
+def test_graph_replay_real_istft_and_split_bluestein():
+    # r2c / c2r kernels, the fused inverse STFT, and the split Bluestein path (its workspace is a
+    # tensor allocated inside the captured region, so it comes from the graph's memory pool)
+    g0 = torch.Generator().manual_seed(10)
+    rows = torch.randn(64, 1024, generator=g0).cuda()
+    bins = ComplexTensor(torch.randn(64, 513, generator=g0).cuda(), torch.randn(64, 513, generator=g0).cuda())
+    spec = trnfft_amd.stft(torch.randn(3, 12000, generator=g0).cuda(), n_fft=512, hop_length=128)
+    few = ComplexTensor(torch.randn(3, 8193, generator=g0).cuda(), torch.randn(3, 8193, generator=g0).cuda())
+
+    def ops():
+        return (trnfft_amd.rfft(rows), trnfft_amd.irfft(bins), trnfft_amd.istft(spec, n_fft=512, hop_length=128),
+                trnfft_amd.fft(few))
+
+    e = ops()
+    g, o = _capture(ops)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o[0].real, e[0].real) and torch.equal(o[0].imag, e[0].imag)
+        assert torch.equal(o[1], e[1])
+        assert torch.equal(o[2], e[2])
+        assert torch.equal(o[3].real, e[3].real) and torch.equal(o[3].imag, e[3].imag)
+        trnfft_amd.fft(torch.randn(16, 64, device="cuda"))
+        torch.cuda.synchronize()
