@@ -1,0 +1,108 @@
+"""C ABI argument checking on a GPU (plans need a device): every rejected call returns its status
+code and leaves a message, as include/trnfft_amd.h documents, and launches nothing."""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from trnfft_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+VP = ctypes.c_void_p
+
+
+def _plan(kind, n, inverse=0, hop=0, flags=0, n2=0):
+    h = VP()
+    d = _lib.PlanDesc(kind=kind, inverse=inverse, n=n, hop=hop, flags=flags, reserved=0, n2=n2)
+    rc = _lib.lib().tfa_plan_create(ctypes.byref(h), ctypes.byref(d))
+    return rc, h
+
+
+def _err():
+    return _lib.lib().tfa_last_error().decode()
+
+
+def P(t):
+    return VP(t.data_ptr()) if t is not None else None
+
+
+def test_plan_kind_limits():
+    lib = _lib.lib()
+    for kind, n, extra in [(_lib.KIND_REAL, 3, {}), (_lib.KIND_REAL, 65536, {}), (_lib.KIND_C2C, 1000, {}),
+                           (_lib.KIND_STFT, 100, {"hop": 10}), (_lib.KIND_FFT2, 4096, {"n2": 64}),
+                           (_lib.KIND_STFT, 512, {"hop": 0}), (_lib.KIND_DFT_GEMM, 8192, {}), (99, 8, {})]:
+        rc, h = _plan(kind, n, **extra)
+        assert rc in (_lib.TFA_ERR_INVALID, _lib.TFA_ERR_UNSUPPORTED), (kind, n, rc)
+        assert not h.value and _err()
+    # inverse STFT: two-sided spectra and too-short hops are refused at plan time
+    rc, _ = _plan(_lib.KIND_STFT, 512, inverse=1, hop=128, flags=_lib.STFT_CENTER)
+    assert rc == _lib.TFA_ERR_UNSUPPORTED
+    rc, _ = _plan(_lib.KIND_STFT, 4096, inverse=1, hop=16, flags=_lib.STFT_ONESIDED)
+    assert rc == _lib.TFA_ERR_UNSUPPORTED and "hop" in _err()
+    assert lib.tfa_abi_version() >> 16 == 1
+
+
+def test_real_plan_argument_checks():
+    lib = _lib.lib()
+    st = VP(torch.cuda.current_stream().cuda_stream)
+    rc, fwd = _plan(_lib.KIND_REAL, 256)
+    assert rc == 0
+    rc, inv = _plan(_lib.KIND_REAL, 256, inverse=1)
+    assert rc == 0
+    x = torch.randn(4, 256, device="cuda")
+    re = torch.empty(4, 129, device="cuda")
+    im = torch.empty_like(re)
+    # r2c takes real input: an imaginary plane is refused
+    assert lib.tfa_execute(fwd, 4, P(x), P(x), P(re), P(im), None, st) == _lib.TFA_ERR_INVALID
+    # real rows must be 8-byte aligned
+    flat = torch.randn(1 + 4 * 256, device="cuda")
+    assert lib.tfa_execute(fwd, 4, VP(flat.data_ptr() + 4), None, P(re), P(im), None, st) == _lib.TFA_ERR_INVALID
+    # c2r: both input planes needed, no aliasing of the output with an input
+    y = torch.empty(4, 256, device="cuda")
+    assert lib.tfa_execute(inv, 4, P(re), None, P(y), None, None, st) == _lib.TFA_ERR_INVALID
+    assert lib.tfa_execute(inv, 4, P(re), P(im), P(re), None, None, st) == _lib.TFA_ERR_INVALID
+    # valid calls succeed
+    assert lib.tfa_execute(fwd, 4, P(x), None, P(re), P(im), None, st) == 0
+    assert lib.tfa_execute(inv, 4, P(re), P(im), P(y), None, None, st) == 0
+    torch.cuda.synchronize()
+    torch.testing.assert_close(y, x, rtol=1e-5, atol=1e-5)
+    lib.tfa_plan_destroy(fwd)
+    lib.tfa_plan_destroy(inv)
+
+
+def test_gemm_ex_argument_checks():
+    lib = _lib.lib()
+    st = VP(torch.cuda.current_stream().cuda_stream)
+    a = torch.randn(8, 4, device="cuda")
+    b = torch.randn(4, 6, device="cuda")
+    c = torch.empty(8, 6, device="cuda")
+    d = torch.empty_like(c)
+    ok = lib.tfa_complex_gemm_ex(8, 6, 4, P(a), P(a), 4, _lib.OP_N, P(b), P(b), 6, _lib.OP_N, 1.0, None, None,
+                                 P(c), P(d), 6, st)
+    assert ok == 0
+    assert lib.tfa_complex_gemm_ex(8, 6, 4, P(a), P(a), 4, 7, P(b), P(b), 6, _lib.OP_N, 1.0, None, None,
+                                   P(c), P(d), 6, st) == _lib.TFA_ERR_INVALID
+    # transposed A is stored (k, m): lda must cover m
+    assert lib.tfa_complex_gemm_ex(8, 6, 4, P(a), P(a), 4, _lib.OP_T, P(b), P(b), 6, _lib.OP_N, 1.0, None, None,
+                                   P(c), P(d), 6, st) == _lib.TFA_ERR_INVALID
+    assert lib.tfa_complex_gemm_ex(8, 6, 4, P(a), P(a), 4, _lib.OP_N, P(b), P(b), 6, _lib.OP_N, 1.0, P(b), None,
+                                   P(c), P(d), 6, st) == _lib.TFA_ERR_INVALID
+    torch.cuda.synchronize()
+
+
+def test_bluestein_split_needs_workspace():
+    lib = _lib.lib()
+    st = VP(torch.cuda.current_stream().cuda_stream)
+    rc, p = _plan(_lib.KIND_BLUESTEIN, 8193)  # m = 32768: split path only
+    assert rc == 0
+    size = ctypes.c_size_t()
+    assert lib.tfa_plan_workspace_size(p, 2, ctypes.byref(size)) == 0 and size.value == 2 * 4 * 2 * 32768
+    x = torch.randn(2, 8193, device="cuda")
+    y = torch.empty_like(x)
+    assert lib.tfa_execute(p, 2, P(x), P(x), P(y), P(y), None, st) == _lib.TFA_ERR_INVALID
+    assert "workspace" in _err()
+    lib.tfa_plan_destroy(p)
