@@ -38,13 +38,37 @@ def test_pow2_lds_vs_oracle(n, inverse):
     assert rel_l2(*got, *ref) <= tol_pow2(n), (n, inverse)
 
 
-@pytest.mark.parametrize("n", [1 << 15, 1 << 16, 1 << 17, 1 << 18, 1 << 20])
+@pytest.mark.parametrize("n", [1 << 15, 1 << 16, 1 << 17, 1 << 18, 1 << 19, 1 << 20, 1 << 21])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_pow2_fourstep_vs_oracle(n, inverse):
+    # every (n1, n2) split of the two-pass path up to 1024 x 2048 (column tile 32, row tile 32/16)
     re, im = seeded_complex(2, n, seed=n)
     got = _gpu_fft(re, im, inverse)
     ref = oracle.fft_core(re, im, inverse)
     assert rel_l2(*got, *ref) <= tol_pow2(n), (n, inverse)
+
+
+@pytest.mark.parametrize("lg", [22, 23, 24])
+def test_pow2_fourstep_largest_vs_numpy(lg):
+    # splits 2048 x 2048, 2048 x 4096 and 4096 x 4096 (16- and 8-transform tiles): one row
+    # against numpy's float64 FFT (the oracle's radix-2 loop is too slow at these sizes), forward
+    # and inverse
+    n = 1 << lg
+    re, im = seeded_complex(1, n, seed=lg)
+    x = re.double().numpy() + 1j * im.double().numpy()
+    for inverse in (False, True):
+        got = _gpu_fft(re, im, inverse)
+        ref = np.fft.ifft(x) if inverse else np.fft.fft(x)
+        assert rel_l2(*got, ref.real, ref.imag) <= tol_pow2(n), (n, inverse)
+
+
+@pytest.mark.parametrize("n", [1 << 15, 1 << 20])
+def test_pow2_fourstep_real_input(n):
+    # real rows take the column pass's real-input variant (imaginary plane never read)
+    re, _ = seeded_complex(3, n, seed=7)
+    X = trnfft_amd.fft(re.cuda())
+    ref = oracle.fft_core(re, torch.zeros_like(re), False)
+    assert rel_l2(X.real, X.imag, *ref) <= tol_pow2(n)
 
 
 def test_config1_batched_1024_roundtrip():

@@ -65,6 +65,10 @@ __host__ __device__ constexpr int istft_epth(int n) {
   return n <= 16 ? n : n <= 64 ? 8 : n <= 256 ? 16 : n <= 512 ? 8 : n <= 2048 ? 16 : 32;
 }
 
+// Elements per thread of the four-step passes over transforms of length l (128..4096): 32 threads
+// per transform up to l = 1024 (one 32-transform tile = 1024 threads), 32 elements above.
+__host__ __device__ constexpr int fourstep_epth(int l) { return l <= 1024 ? (l >= 128 ? l / 32 : 4) : 32; }
+
 struct LdsShape {
   int n, e, t, npass;
   int radix[kMaxPasses];

@@ -67,16 +67,11 @@ struct StridedArgs {
   const float* in_im;  // nullptr: real input
   float* out_re;       // may equal in_re (in place)
   float* out_im;
-  const float2* tw;     // LDS-FFT table for length n1
-  const float2* tw_lo;  // four-step twiddle tables (TWIDDLE only)
-  const float2* tw_hi;
+  const float2* tw;     // LDS-FFT table for length n1 (lds_epth layout)
   long long outer;   // independent (n1 x stride) blocks
   long long stride;  // element stride of the transformed axis = number of columns
-  int lo_bits;
-  unsigned nmask;  // (n1 * n2) - 1 for the four-step twiddle
-  float scale;     // applied when !twiddle
+  float scale;
   int dir;
-  bool twiddle;
   hipStream_t stream;
 };
 hipError_t launch_strided(int n1, const StridedArgs& a);
@@ -84,12 +79,12 @@ hipError_t launch_strided(int n1, const StridedArgs& a);
 struct FourStepArgs {
   const float* in_re;
   const float* in_im;  // nullptr: real input
-  float* t_re;         // workspace, batch * n1 * n2 floats each
+  float* t_re;         // workspace, batch * n1 * n2 floats each (blocked layout, see the kernels)
   float* t_im;
   float* out_re;
   float* out_im;
-  const float2* tw1;  // LDS-FFT table for length n1
-  const float2* tw2;  // LDS-FFT table for length n2
+  const float2* tw1;  // LDS-FFT table for length n1 (fourstep_epth layout)
+  const float2* tw2;  // LDS-FFT table for length n2 (fourstep_epth layout)
   const float2* tw_lo;  // W_N^j, j < 2^lo_bits
   const float2* tw_hi;  // W_N^(j << lo_bits)
   int n1, n2, lo_bits;

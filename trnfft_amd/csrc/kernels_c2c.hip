@@ -4,12 +4,12 @@
 //    registers + LDS for all its passes (replaces the reference's per-stage launches,
 //    trnfft/fft_core.py:53-117 on CPU and :1063-1238 on the NKI path).
 //  * strided_kernel: transform along a non-contiguous axis (element stride S), C adjacent
-//    columns per workgroup; replaces the transpose copies of trnfft/api.py:496-516 for fftn/fft2
-//    and is the column pass of the four-step path.
-//  * four-step (strided_kernel with twiddle + fourstep_row_kernel): N = N1*N2 > 16384 in two HBM
-//    passes (column FFTs with the W_N^{n2*k1} twiddle fused into their store, then row FFTs whose
-//    output is transposed through LDS so the strided store stays coalesced).  This is the
-//    single-GPU form of the reference's row-column decomposition, trnfft/nki/multicore.py:151-219.
+//    columns per workgroup; replaces the transpose copies of trnfft/api.py:496-516 for fftn/fft2.
+//  * four-step (fourstep_col_kernel + fourstep_row_kernel): N = N1*N2 > 16384 in two HBM passes
+//    (column FFTs with the W_N^{n2*k1} twiddle, written in a blocked layout that the row pass
+//    reads contiguously; row FFTs stored to the transposed output with whole-line segments).
+//    This is the single-GPU form of the reference's row-column decomposition,
+//    trnfft/nki/multicore.py:151-219.
 #include "kernels.h"
 
 namespace tfa {
@@ -106,17 +106,14 @@ hipError_t launch_c2c_lds(int n, const C2cArgs& a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Four-step: x viewed as (N1 rows) x (N2 columns), n = N2*n1 + n2, k = k1 + N1*k2.
-// ---------------------------------------------------------------------------------------------
 // Strided-axis transform: x viewed as (outer, N1, S) row-major; transform along the N1 axis
 // (element stride S) for every (outer, column) pair.  One workgroup = C adjacent columns of one
-// outer block, so each load/store instruction covers C consecutive floats.  With TWIDDLE the
-// result k1 of column c is multiplied by W_Ntot^(c*k1) (the four-step column pass, with S = N2).
-template <int N1, int DIR, bool REAL_IN, bool TWIDDLE, int C = fourstep_tile(N1)>
+// outer block, so each load/store instruction covers C consecutive floats.
+// ---------------------------------------------------------------------------------------------
+template <int N1, int DIR, bool REAL_IN, int C = fourstep_tile(N1)>
 __global__ __launch_bounds__(C * (N1 / lds_epth(N1))) void strided_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re, float* out_im,
-    const float2* __restrict__ tw, const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi,
-    long long stride, int tiles_per_block, int lo_bits, unsigned nmask, float scale) {
+    const float2* __restrict__ tw, long long stride, int tiles_per_block, float scale) {
   constexpr int E = lds_epth(N1), T = N1 / E;
   constexpr int PADN = lds_pad(N1) + 1;
   __shared__ float lre[C * PADN];
@@ -137,18 +134,10 @@ __global__ __launch_bounds__(C * (N1 / lds_epth(N1))) void strided_kernel(
   }
   LdsFft<N1, E, DIR, false>::run(v, lre + c * PADN, lim + c * PADN, tw, t);
   if (!valid) return;
-  const unsigned lomask = (1u << lo_bits) - 1;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int k1 = t + T * e;
-    float2 y = v[e];
-    if constexpr (TWIDDLE) {
-      const unsigned m = ((unsigned)col * (unsigned)k1) & nmask;
-      y = cmul(y, cmul(tw_lo[m & lomask], tw_hi[m >> lo_bits]));
-    } else {
-      y = cscale(y, scale);
-    }
-    const size_t i = base + (size_t)k1 * stride;
+    const float2 y = cscale(v[e], scale);
+    const size_t i = base + (size_t)(t + T * e) * stride;
     if constexpr (C * 4 < 128) {
       // row segments shorter than a cache line: plain stores, so L2 merges the partial lines
       // of neighbouring workgroups before they reach HBM (measured 1.1x faster at N1 = 1024)
@@ -161,127 +150,229 @@ __global__ __launch_bounds__(C * (N1 / lds_epth(N1))) void strided_kernel(
   }
 }
 
-// Row pass: FFT over n2 of each row k1 of tmp (contiguous), output X[k1 + N1*k2] for C
-// adjacent rows, transposed through LDS so each store covers C consecutive k1.
-template <int N2, int DIR, int C = fourstep_tile(N2)>
-__global__ __launch_bounds__(C * (N2 / lds_epth(N2))) void fourstep_row_kernel(
-    const float* __restrict__ t_re, const float* __restrict__ t_im, float* __restrict__ out_re,
-    float* __restrict__ out_im, const float2* __restrict__ tw, int n1_len, long long batch,
-    float scale) {
-  constexpr int E = lds_epth(N2), T = N2 / E;
-  constexpr int PADN = lds_pad(N2) + 1;
-  constexpr int THREADS = C * T;
-  __shared__ float lre[C * PADN];
-  __shared__ float lim[C * PADN];
-  const int t = threadIdx.x % T;  // position in row (fast across lanes: coalesced loads)
-  const int r = threadIdx.x / T;
-  const int tiles_per_b = n1_len / C;
-  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
-  const long long b = tile / tiles_per_b;
-  const int k1_0 = (int)(tile % tiles_per_b) * C;
-  const size_t N = (size_t)n1_len * N2;
-  const size_t row_base = (size_t)b * N + (size_t)(k1_0 + r) * N2;
+// ---------------------------------------------------------------------------------------------
+// Four-step: x viewed as (N1 rows) x (N2 columns), n = N2*n1 + n2, k = k1 + N1*k2.
+//   pass 1 (fourstep_col_kernel): DFT over n1 of TILE adjacent columns n2, times W_N^(n2*k1),
+//     written to the workspace in the blocked layout tmp[kb][n2][kk] with k1 = kb*CK + kk and CK
+//     the pass-2 tile, so the tile's output is N1/CK contiguous runs of TILE*CK floats;
+//   pass 2 (fourstep_row_kernel): DFT over n2 of the CK rows k1 = kb*CK + r, read as one
+//     contiguous CK*N2 run, stored to X[k1 + N1*k2] with CK consecutive k1 per store.
+// With 32-transform tiles (lengths up to 1024) every HBM side of both passes moves whole 128-byte
+// lines; 2048 and 4096 use 16 and 8 transforms per tile (the LDS holds no more).
+// ---------------------------------------------------------------------------------------------
+template <int L>
+struct FourStepCfg {
+  static constexpr int TILE = L <= 1024 ? 32 : 32768 / L;
+  static constexpr int E = fourstep_epth(L);
+  static constexpr int T = L / E;
+  static constexpr int THREADS = TILE * T;
+  static constexpr int PADN = lds_pad(L) + 1;
+  // both planes in LDS when they fit, else the real and imaginary planes take turns
+  static constexpr bool SPLIT = 2LL * TILE * PADN * 4 > kLdsBytes;
+  static_assert(THREADS == 1024 && (SPLIT ? 1LL : 2LL) * TILE * PADN * 4 <= kLdsBytes, "four-step tile");
+};
 
+template <int N1, int DIR, bool REAL_IN, int CK>
+__global__ __launch_bounds__(FourStepCfg<N1>::THREADS) void fourstep_col_kernel(
+    const float* __restrict__ in_re, const float* __restrict__ in_im, float* __restrict__ out_re,
+    float* __restrict__ out_im, const float2* __restrict__ tw, const float2* __restrict__ tw_lo,
+    const float2* __restrict__ tw_hi, long long stride, int tiles_per_block, int lo_bits, unsigned nmask) {
+  using Cfg = FourStepCfg<N1>;
+  constexpr int C = Cfg::TILE, E = Cfg::E, T = Cfg::T, THREADS = Cfg::THREADS, PADN = Cfg::PADN;
+  constexpr bool SPLIT = Cfg::SPLIT;
+  constexpr int TF = E < 4 ? E : 4;  // twiddle factor group
+  __shared__ float lre[C * PADN];
+  __shared__ float lim[SPLIT ? 1 : C * PADN];
+  const int c = threadIdx.x % C;  // column within the tile (fast across lanes: whole lines)
+  const int t = threadIdx.x / C;
+  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
+  const long long b = tile / tiles_per_block;
+  const long long col0 = (tile % tiles_per_block) * C;
+  const unsigned col = (unsigned)(col0 + c);
+  const size_t base = (size_t)b * N1 * stride + col;
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const size_t i = row_base + t + T * e;
-    v[e] = make_float2(t_re[i], t_im[i]);
+    const size_t i = base + (size_t)(t + T * e) * stride;
+    v[e] = make_float2(ld_stream(in_re + i), REAL_IN ? 0.0f : ld_stream(in_im + i));
   }
-  LdsFft<N2, E, DIR, false>::run(v, lre + r * PADN, lim + r * PADN, tw, t);
-  // transpose: element (row r, k2) -> LDS[r*PADN + k2], read back with the row index fast
+  LdsFft<N1, E, DIR, false, SPLIT>::run(v, lre + c * PADN, SPLIT ? lre : lim + c * PADN, tw, t);
+
+  // W_N^(col*k1) for k1 = t + T*(TF*a + q): W^(col*(t + T*TF*a)) * W^(col*T*q), each root read as
+  // W^lo * W^hi from the two small tables (TF-1 + E/TF table pairs per thread instead of E);
+  // the scheduling barrier keeps one group's loads in flight at a time (register pressure)
+  const unsigned lomask = (1u << lo_bits) - 1;
+  float2 q[TF];
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int idx = r * PADN + lds_pad(t + T * e);
-    lre[idx] = v[e].x;
-    lim[idx] = v[e].y;
+  for (int j = 1; j < TF; ++j) {
+    const unsigned m = (col * (unsigned)(T * j)) & nmask;
+    q[j] = cmul(tw_lo[m & lomask], tw_hi[m >> lo_bits]);
   }
-  __syncthreads();
-  const int rr = threadIdx.x % C;
-  const int q = threadIdx.x / C;
-  constexpr int QN = THREADS / C;  // == T
-  const size_t obase = (size_t)b * N + k1_0 + rr;
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int k2 = q + QN * e;
-    const int idx = rr * PADN + lds_pad(k2);
-    const size_t o = obase + (size_t)k2 * n1_len;
-    out_re[o] = lre[idx] * scale;
-    out_im[o] = lim[idx] * scale;
+  for (int a = 0; a < E / TF; ++a) {
+    const unsigned m = (col * (unsigned)(t + T * TF * a)) & nmask;
+    const float2 p = cmul(tw_lo[m & lomask], tw_hi[m >> lo_bits]);
+    v[TF * a] = cmul(v[TF * a], p);
+#pragma unroll
+    for (int j = 1; j < TF; ++j) v[TF * a + j] = cmul(v[TF * a + j], cmul(p, q[j]));
+    __builtin_amdgcn_sched_barrier(0);
   }
-  (void)batch;
+
+  // blocked store through LDS: linear position w of a run holds (column w / CK, kk = w % CK)
+  const size_t obase = (size_t)b * N1 * stride + (size_t)col0 * CK;
+  __syncthreads();  // every lane is past the transform's last LDS read
+#pragma unroll
+  for (int plane = 0; plane < (SPLIT ? 2 : 1); ++plane) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int idx = c * PADN + lds_pad(t + T * e);
+      if constexpr (SPLIT) {
+        lre[idx] = plane ? v[e].y : v[e].x;
+      } else {
+        lre[idx] = v[e].x;
+        lim[idx] = v[e].y;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      // thread x stores position w = x % RUN of run kb = x / RUN + RPI * i (RUN = C*CK floats)
+      constexpr int RUN = C * CK, RPI = THREADS / RUN;
+      const int w = threadIdx.x % RUN, kk = w % CK, kb = threadIdx.x / RUN + RPI * i;
+      const int idx = (w / CK) * PADN +
+                      (CK % 16 == 0 ? lds_pad(kk) + kb * (CK + CK / 16) : lds_pad(kb * CK + kk));
+      const size_t o = obase + (size_t)(threadIdx.x / RUN) * stride * CK + w + (size_t)(RPI * i) * stride * CK;
+      if constexpr (SPLIT) {
+        st_stream((plane ? out_im : out_re) + o, lre[idx]);
+      } else {
+        st_stream(out_re + o, lre[idx]);
+        st_stream(out_im + o, lim[idx]);
+      }
+    }
+    if (SPLIT && plane == 0) __syncthreads();
+  }
 }
 
-template <int N1, int DIR, bool TWIDDLE>
+template <int N2, int DIR>
+__global__ __launch_bounds__(FourStepCfg<N2>::THREADS) void fourstep_row_kernel(
+    const float* __restrict__ t_re, const float* __restrict__ t_im, float* __restrict__ out_re,
+    float* __restrict__ out_im, const float2* __restrict__ tw, int n1_len, float scale) {
+  using Cfg = FourStepCfg<N2>;
+  constexpr int CK = Cfg::TILE, E = Cfg::E, T = Cfg::T, PADN = Cfg::PADN;
+  constexpr bool SPLIT = Cfg::SPLIT;
+  __shared__ float lre[CK * PADN];
+  __shared__ float lim[SPLIT ? 1 : CK * PADN];
+  const int r = threadIdx.x % CK;  // row within the tile (fast across lanes)
+  const int t = threadIdx.x / CK;
+  const int tiles_per_b = n1_len / CK;
+  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
+  const long long b = tile / tiles_per_b;
+  const int kb = (int)(tile % tiles_per_b);
+  const size_t N = (size_t)n1_len * N2;
+  const size_t ibase = (size_t)b * N + (size_t)kb * N2 * CK + r;
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const size_t i = ibase + (size_t)(t + T * e) * CK;
+    v[e] = make_float2(ld_stream(t_re + i), ld_stream(t_im + i));
+  }
+  LdsFft<N2, E, DIR, false, SPLIT>::run(v, lre + r * PADN, SPLIT ? lre : lim + r * PADN, tw, t);
+  const size_t obase = (size_t)b * N + (size_t)kb * CK + r;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const size_t o = obase + (size_t)(t + T * e) * n1_len;
+    if constexpr (CK * 4 < 128) {  // sub-line segments: plain stores (L2 merges them)
+      out_re[o] = v[e].x * scale;
+      out_im[o] = v[e].y * scale;
+    } else {
+      st_stream(out_re + o, v[e].x * scale);
+      st_stream(out_im + o, v[e].y * scale);
+    }
+  }
+}
+
+template <int N1, int DIR>
 static hipError_t launch_strided_t(const StridedArgs& a) {
   constexpr int C = fourstep_tile(N1), T = N1 / lds_epth(N1);
   const long long tiles = (a.stride + C - 1) / C;
   const long long blocks = a.outer * tiles;
   if (a.in_im == nullptr)
-    hipLaunchKernelGGL((strided_kernel<N1, DIR, true, TWIDDLE>), dim3((unsigned)blocks), dim3(C * T), 0,
-                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.tw_lo, a.tw_hi, a.stride,
-                       (int)tiles, a.lo_bits, a.nmask, a.scale);
+    hipLaunchKernelGGL((strided_kernel<N1, DIR, true>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream, a.in_re,
+                       a.in_im, a.out_re, a.out_im, a.tw, a.stride, (int)tiles, a.scale);
   else
-    hipLaunchKernelGGL((strided_kernel<N1, DIR, false, TWIDDLE>), dim3((unsigned)blocks), dim3(C * T), 0,
-                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.tw_lo, a.tw_hi, a.stride,
-                       (int)tiles, a.lo_bits, a.nmask, a.scale);
+    hipLaunchKernelGGL((strided_kernel<N1, DIR, false>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream, a.in_re,
+                       a.in_im, a.out_re, a.out_im, a.tw, a.stride, (int)tiles, a.scale);
   return hipGetLastError();
 }
 
-template <int DIR, bool TWIDDLE>
+template <int DIR>
 static hipError_t launch_strided_dir(int n1, const StridedArgs& a) {
   switch (n1) {
-    case 2: return launch_strided_t<2, DIR, TWIDDLE>(a);
-    case 4: return launch_strided_t<4, DIR, TWIDDLE>(a);
-    case 8: return launch_strided_t<8, DIR, TWIDDLE>(a);
-    case 16: return launch_strided_t<16, DIR, TWIDDLE>(a);
-    case 32: return launch_strided_t<32, DIR, TWIDDLE>(a);
-    case 64: return launch_strided_t<64, DIR, TWIDDLE>(a);
-    case 128: return launch_strided_t<128, DIR, TWIDDLE>(a);
-    case 256: return launch_strided_t<256, DIR, TWIDDLE>(a);
-    case 512: return launch_strided_t<512, DIR, TWIDDLE>(a);
-    case 1024: return launch_strided_t<1024, DIR, TWIDDLE>(a);
-    case 2048: return launch_strided_t<2048, DIR, TWIDDLE>(a);
-    case 4096: return launch_strided_t<4096, DIR, TWIDDLE>(a);
+    case 2: return launch_strided_t<2, DIR>(a);
+    case 4: return launch_strided_t<4, DIR>(a);
+    case 8: return launch_strided_t<8, DIR>(a);
+    case 16: return launch_strided_t<16, DIR>(a);
+    case 32: return launch_strided_t<32, DIR>(a);
+    case 64: return launch_strided_t<64, DIR>(a);
+    case 128: return launch_strided_t<128, DIR>(a);
+    case 256: return launch_strided_t<256, DIR>(a);
+    case 512: return launch_strided_t<512, DIR>(a);
+    case 1024: return launch_strided_t<1024, DIR>(a);
+    case 2048: return launch_strided_t<2048, DIR>(a);
+    case 4096: return launch_strided_t<4096, DIR>(a);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_strided(int n1, const StridedArgs& a) {
-  if (a.dir < 0) return a.twiddle ? launch_strided_dir<-1, true>(n1, a) : launch_strided_dir<-1, false>(n1, a);
-  return a.twiddle ? launch_strided_dir<1, true>(n1, a) : launch_strided_dir<1, false>(n1, a);
+  return a.dir < 0 ? launch_strided_dir<-1>(n1, a) : launch_strided_dir<1>(n1, a);
 }
 
-template <int N2, int DIR>
-static hipError_t launch_row_t(const FourStepArgs& a) {
-  constexpr int C = fourstep_tile(N2), T = N2 / lds_epth(N2);
-  if (a.n1 % C) return hipErrorInvalidValue;
-  const long long blocks = a.batch * (a.n1 / C);
-  hipLaunchKernelGGL((fourstep_row_kernel<N2, DIR>), dim3((unsigned)blocks), dim3(C * T), 0,
-                     a.stream, a.t_re, a.t_im, a.out_re, a.out_im, a.tw2, a.n1, a.batch, a.scale);
+template <int N1, int N2, int DIR>
+static hipError_t launch_fourstep_t(const FourStepArgs& a) {
+  using C1 = FourStepCfg<N1>;
+  using C2 = FourStepCfg<N2>;
+  constexpr int CK = C2::TILE;
+  static_assert(N2 % C1::TILE == 0 && N1 % CK == 0, "four-step tiles");
+  const unsigned nmask = (unsigned)((long long)N1 * N2 - 1);
+  const long long cols = a.batch * (N2 / C1::TILE);
+  if (a.in_im == nullptr)
+    hipLaunchKernelGGL((fourstep_col_kernel<N1, DIR, true, CK>), dim3((unsigned)cols), dim3(C1::THREADS), 0,
+                       a.stream, a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, (long long)N2,
+                       N2 / C1::TILE, a.lo_bits, nmask);
+  else
+    hipLaunchKernelGGL((fourstep_col_kernel<N1, DIR, false, CK>), dim3((unsigned)cols), dim3(C1::THREADS), 0,
+                       a.stream, a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, (long long)N2,
+                       N2 / C1::TILE, a.lo_bits, nmask);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const long long rows = a.batch * (N1 / CK);
+  hipLaunchKernelGGL((fourstep_row_kernel<N2, DIR>), dim3((unsigned)rows), dim3(C2::THREADS), 0, a.stream, a.t_re,
+                     a.t_im, a.out_re, a.out_im, a.tw2, N1, a.scale);
   return hipGetLastError();
 }
 
+// n = n1 * n2 with n1 = 2^floor(lg/2) <= n2 (the plan's split)
 template <int DIR>
-static hipError_t launch_row_dir(const FourStepArgs& a) {
-  switch (a.n2) {
-    case 64: return launch_row_t<64, DIR>(a);
-    case 128: return launch_row_t<128, DIR>(a);
-    case 256: return launch_row_t<256, DIR>(a);
-    case 512: return launch_row_t<512, DIR>(a);
-    case 1024: return launch_row_t<1024, DIR>(a);
-    case 2048: return launch_row_t<2048, DIR>(a);
-    case 4096: return launch_row_t<4096, DIR>(a);
+static hipError_t launch_fourstep_dir(const FourStepArgs& a) {
+  const long long key = (long long)a.n1 * 8192 + a.n2;
+  switch (key) {
+    case 128LL * 8192 + 256: return launch_fourstep_t<128, 256, DIR>(a);
+    case 256LL * 8192 + 256: return launch_fourstep_t<256, 256, DIR>(a);
+    case 256LL * 8192 + 512: return launch_fourstep_t<256, 512, DIR>(a);
+    case 512LL * 8192 + 512: return launch_fourstep_t<512, 512, DIR>(a);
+    case 512LL * 8192 + 1024: return launch_fourstep_t<512, 1024, DIR>(a);
+    case 1024LL * 8192 + 1024: return launch_fourstep_t<1024, 1024, DIR>(a);
+    case 1024LL * 8192 + 2048: return launch_fourstep_t<1024, 2048, DIR>(a);
+    case 2048LL * 8192 + 2048: return launch_fourstep_t<2048, 2048, DIR>(a);
+    case 2048LL * 8192 + 4096: return launch_fourstep_t<2048, 4096, DIR>(a);
+    case 4096LL * 8192 + 4096: return launch_fourstep_t<4096, 4096, DIR>(a);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_fourstep(const FourStepArgs& a) {
-  StridedArgs col{a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, a.batch, a.n2,
-                  a.lo_bits, (unsigned)((long long)a.n1 * a.n2 - 1), 1.0f, a.dir, true, a.stream};
-  hipError_t e = launch_strided(a.n1, col);
-  if (e != hipSuccess) return e;
-  return a.dir < 0 ? launch_row_dir<-1>(a) : launch_row_dir<1>(a);
+  return a.dir < 0 ? launch_fourstep_dir<-1>(a) : launch_fourstep_dir<1>(a);
 }
 
 }  // namespace tfa

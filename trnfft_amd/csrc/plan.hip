@@ -131,8 +131,8 @@ struct tfa_plan {
     t->n2 = (int)(n / t->n1);   // row transform length (contiguous), n2 >= n1
     t->lo_bits = (lg + 1) / 2;
     int rc;
-    if ((rc = upload(lds_table(t->n1, dir), &t->tw1))) return rc;
-    if ((rc = upload(lds_table(t->n2, dir), &t->tw2))) return rc;
+    if ((rc = upload(lds_table(t->n1, dir, tfa::fourstep_epth(t->n1)), &t->tw1))) return rc;
+    if ((rc = upload(lds_table(t->n2, dir, tfa::fourstep_epth(t->n2)), &t->tw2))) return rc;
     std::vector<float2> lo((size_t)1 << t->lo_bits), hi((size_t)(n >> t->lo_bits));
     for (size_t j = 0; j < lo.size(); ++j) lo[j] = unit_root((int64_t)j, n, dir);
     for (size_t j = 0; j < hi.size(); ++j) hi[j] = unit_root((int64_t)j << t->lo_bits, n, dir);
@@ -496,8 +496,8 @@ int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, con
     return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
   const C2cTables& t = plan->d.inverse ? plan->inv : plan->fwd;
   const float scale = plan->d.inverse ? (float)(1.0 / (double)plan->d.n) : 1.0f;
-  tfa::StridedArgs a{in_re, in_im, out_re, out_im, t.tw_lds, nullptr, nullptr, outer, stride, 0, 0u, scale,
-                     t.dir, false, static_cast<hipStream_t>(stream)};
+  tfa::StridedArgs a{in_re, in_im, out_re, out_im, t.tw_lds, outer, stride, scale, t.dir,
+                     static_cast<hipStream_t>(stream)};
   hipError_t e = tfa::launch_strided((int)plan->d.n, a);
   return e == hipSuccess ? TFA_OK : hip_fail(e, "strided launch");
 }
