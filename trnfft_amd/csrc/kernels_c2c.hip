@@ -189,11 +189,13 @@ __global__ __launch_bounds__(FourStepCfg<N1>::THREADS) void fourstep_col_kernel(
   const long long b = tile / tiles_per_block;
   const long long col0 = (tile % tiles_per_block) * C;
   const unsigned col = (unsigned)(col0 + c);
-  const size_t base = (size_t)b * N1 * stride + col;
+  // per-thread base plus a workgroup-uniform offset per element (no per-element index math)
+  const size_t base = (size_t)b * N1 * stride + col + (size_t)t * stride;
+  const size_t step = (size_t)T * stride;
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const size_t i = base + (size_t)(t + T * e) * stride;
+    const size_t i = base + e * step;
     v[e] = make_float2(ld_stream(in_re + i), REAL_IN ? 0.0f : ld_stream(in_im + i));
   }
   LdsFft<N1, E, DIR, false, SPLIT>::run(v, lre + c * PADN, SPLIT ? lre : lim + c * PADN, tw, t);
@@ -225,7 +227,7 @@ __global__ __launch_bounds__(FourStepCfg<N1>::THREADS) void fourstep_col_kernel(
   for (int plane = 0; plane < (SPLIT ? 2 : 1); ++plane) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const int idx = c * PADN + lds_pad(t + T * e);
+      const int idx = c * PADN + (T % 16 == 0 ? lds_pad(t) + e * (T + T / 16) : lds_pad(t + T * e));
       if constexpr (SPLIT) {
         lre[idx] = plane ? v[e].y : v[e].x;
       } else {
@@ -269,18 +271,19 @@ __global__ __launch_bounds__(FourStepCfg<N2>::THREADS) void fourstep_row_kernel(
   const long long b = tile / tiles_per_b;
   const int kb = (int)(tile % tiles_per_b);
   const size_t N = (size_t)n1_len * N2;
-  const size_t ibase = (size_t)b * N + (size_t)kb * N2 * CK + r;
+  const size_t ibase = (size_t)b * N + (size_t)kb * N2 * CK + r + (size_t)t * CK;
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const size_t i = ibase + (size_t)(t + T * e) * CK;
+    const size_t i = ibase + (size_t)e * (T * CK);
     v[e] = make_float2(ld_stream(t_re + i), ld_stream(t_im + i));
   }
   LdsFft<N2, E, DIR, false, SPLIT>::run(v, lre + r * PADN, SPLIT ? lre : lim + r * PADN, tw, t);
-  const size_t obase = (size_t)b * N + (size_t)kb * CK + r;
+  const size_t obase = (size_t)b * N + (size_t)kb * CK + r + (size_t)t * n1_len;
+  const size_t ostep = (size_t)T * n1_len;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const size_t o = obase + (size_t)(t + T * e) * n1_len;
+    const size_t o = obase + e * ostep;
     if constexpr (CK * 4 < 128) {  // sub-line segments: plain stores (L2 merges them)
       out_re[o] = v[e].x * scale;
       out_im[o] = v[e].y * scale;
