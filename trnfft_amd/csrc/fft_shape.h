@@ -32,6 +32,9 @@ __host__ __device__ constexpr int c2c_epth(int n) {
   return n == 64 || n == 128 ? 4 : (n == 256 || n == 1024 || n == 2048 || n == 4096) ? 8
          : (n == 8192 || n == 16384) ? 32 : lds_epth(n);
 }
+// Interleaved (re, im) LDS exchange (one 64-bit access per element) in the batched c2c kernel:
+// measured 1-4 % faster at most lengths (identical results), 2-4 % slower at 512 and 8192.
+__host__ __device__ constexpr bool c2c_il(int n) { return n != 512 && n != 8192; }
 __host__ __device__ constexpr int c2c_threads(int n) {
   return n == 64 || n == 256 ? 1024 : (n == 128 || n == 1024 || n == 2048 || n == 4096 || n == 16384) ? 512 : 256;
 }

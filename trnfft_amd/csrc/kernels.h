@@ -29,8 +29,9 @@ __device__ __forceinline__ float4 ld_stream4(const float4* p) {
 }
 
 // Thread layout of the batched LDS kernels for transform length N: T threads per transform,
-// XF transforms per workgroup (c2c_threads(N) threads per workgroup), PADN LDS floats per plane
-// per transform (1 when the transform needs no exchange).
+// XF transforms per workgroup (c2c_threads(N) threads per workgroup), PADN LDS entries per
+// transform (float2 when the exchange is interleaved, floats per plane otherwise; 1 when the
+// transform needs no exchange).
 template <int N, int E_ = c2c_epth(N), int THR = c2c_threads(N)>
 struct C2cThreads {
   static constexpr int E = E_;

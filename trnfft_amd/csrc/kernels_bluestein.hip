@@ -40,8 +40,7 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
     float scale) {
   using C = BlueCfg<M, E_, THR>;
   constexpr int E = C::E, T = C::T;
-  __shared__ float lre[C::XF * C::PADN];
-  __shared__ float lim[C::XF * C::PADN];
+  __shared__ float2 lds[C::XF * C::PADN];  // interleaved (re, im) exchange
   const int tid = threadIdx.x & (T - 1);
   const int xf = threadIdx.x / T;
   const long long b = (long long)blockIdx.x * C::XF + xf;
@@ -70,12 +69,11 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
     }
     v[e] = y;
   }
-  float* my_re = lre + xf * C::PADN;
-  float* my_im = lim + xf * C::PADN;
-  LdsFft<M, E, -1, (T <= 64)>::run(v, my_re, my_im, tw_f, tid);
+  float* my = reinterpret_cast<float*>(lds + xf * C::PADN);
+  LdsFft<M, E, -1, (T <= 64), false, true>::run(v, my, my, tw_f, tid);
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = cmul(v[e], PRE ? hv[PRE ? e : 0] : hs[tid + T * e]);
-  LdsFft<M, E, 1, (T <= 64)>::run(v, my_re, my_im, tw_i, tid);
+  LdsFft<M, E, 1, (T <= 64), false, true>::run(v, my, my, tw_i, tid);
   if (valid) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
@@ -150,8 +148,7 @@ __global__ __launch_bounds__((BlueColCfg<M1>::C * BlueColCfg<M1>::T)) void blue_
     const float2* __restrict__ lo, const float2* __restrict__ hi, int lo_bits, int n, int m2, int tiles) {
   using G = BlueColCfg<M1>;
   constexpr int E = G::E, T = G::T, C = G::C, PADN = G::PADN;
-  __shared__ float lre[C * PADN];
-  __shared__ float lim[C * PADN];
+  __shared__ float2 lds[C * PADN];  // interleaved (re, im) exchange
   const int c = threadIdx.x % C, t = threadIdx.x / C;
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
   const long long b = tile / tiles;
@@ -168,7 +165,7 @@ __global__ __launch_bounds__((BlueColCfg<M1>::C * BlueColCfg<M1>::T)) void blue_
     }
     v[e] = y;
   }
-  LdsFft<M1, E, -1, false>::run(v, lre + c * PADN, lim + c * PADN, tw, t);
+  LdsFft<M1, E, -1, false, false, true>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int k1 = t + T * e;
@@ -186,8 +183,7 @@ __global__ __launch_bounds__((BlueColCfg<M1>::C * BlueColCfg<M1>::T)) void blue_
     int tiles, float scale) {
   using G = BlueColCfg<M1>;
   constexpr int E = G::E, T = G::T, C = G::C, PADN = G::PADN;
-  __shared__ float lre[C * PADN];
-  __shared__ float lim[C * PADN];
+  __shared__ float2 lds[C * PADN];  // interleaved (re, im) exchange
   const int c = threadIdx.x % C, t = threadIdx.x / C;
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
   const long long b = tile / tiles;
@@ -199,7 +195,7 @@ __global__ __launch_bounds__((BlueColCfg<M1>::C * BlueColCfg<M1>::T)) void blue_
     const size_t s = (size_t)b * m + (size_t)(t + T * e) * m2 + col;
     v[e] = make_float2(ld_stream(ws_re + s), ld_stream(ws_im + s));
   }
-  LdsFft<M1, E, 1, false>::run(v, lre + c * PADN, lim + c * PADN, tw, t);
+  LdsFft<M1, E, 1, false, false, true>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int i = (t + T * e) * m2 + col;
@@ -222,8 +218,7 @@ __global__ __launch_bounds__(C2cThreads<M2>::THREADS) void blue_row_kernel(
   using C = C2cThreads<M2>;
   constexpr int E = C::E, T = C::T;
   constexpr bool WL = T <= 64;
-  __shared__ float lre[C::XF * C::PADN];
-  __shared__ float lim[C::XF * C::PADN];
+  __shared__ float2 lds[C::XF * C::PADN];  // interleaved (re, im) exchange
   const int tid = threadIdx.x % T, xf = threadIdx.x / T;
   const long long row = (long long)blockIdx.x * C::XF + xf;  // (batch, k1)
   const int k1 = (int)(row % m1);
@@ -233,11 +228,12 @@ __global__ __launch_bounds__(C2cThreads<M2>::THREADS) void blue_row_kernel(
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = make_float2(pr[T * e], pi[T * e]);
-  LdsFft<M2, E, -1, WL>::run(v, lre + xf * C::PADN, lim + xf * C::PADN, tw_f, tid);
+  float* my = reinterpret_cast<float*>(lds + xf * C::PADN);
+  LdsFft<M2, E, -1, WL, false, true>::run(v, my, nullptr, tw_f, tid);
   const float2* h = hp + (size_t)k1 * M2 + tid;
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = cmul(v[e], h[T * e]);
-  LdsFft<M2, E, 1, WL>::run(v, lre + xf * C::PADN, lim + xf * C::PADN, tw_i, tid);
+  LdsFft<M2, E, 1, WL, false, true>::run(v, my, nullptr, tw_i, tid);
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const unsigned n2 = (unsigned)(tid + T * e);

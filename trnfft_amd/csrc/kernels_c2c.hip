@@ -26,8 +26,9 @@ __global__ __launch_bounds__((C2cThreads<N, E_, THR>::THREADS)) void c2c_lds_ker
     float* out_im, const float2* __restrict__ tw, long long first, long long batch, float scale) {
   using C = C2cThreads<N, E_, THR>;
   constexpr int E = C::E, T = C::T;
-  __shared__ float lre[C::XF * C::PADN];
-  __shared__ float lim[C::XF * C::PADN];
+  // interleaved (re, im) exchange, or two planes, in the same LDS bytes
+  constexpr bool IL = c2c_il(N);
+  __shared__ float2 lds[C::XF * C::PADN];
   const int tid = threadIdx.x & (T - 1);
   const int xf = threadIdx.x / T;
   const long long b = first + (long long)blockIdx.x * C::XF + xf;
@@ -51,7 +52,12 @@ __global__ __launch_bounds__((C2cThreads<N, E_, THR>::THREADS)) void c2c_lds_ker
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = make_float2(0.0f, 0.0f);
   }
-  LdsFft<N, E, DIR, (T <= 64)>::run(v, lre + xf * C::PADN, lim + xf * C::PADN, tw, tid);
+  if constexpr (IL) {
+    LdsFft<N, E, DIR, (T <= 64), false, true>::run(v, reinterpret_cast<float*>(lds + xf * C::PADN), nullptr, tw, tid);
+  } else {
+    float* planes = reinterpret_cast<float*>(lds);
+    LdsFft<N, E, DIR, (T <= 64)>::run(v, planes + xf * C::PADN, planes + (C::XF + xf) * C::PADN, tw, tid);
+  }
   if (valid) {
     float* qr = out_re + base + tid;
     float* qi = out_im + base + tid;
@@ -63,17 +69,71 @@ __global__ __launch_bounds__((C2cThreads<N, E_, THR>::THREADS)) void c2c_lds_ker
   }
 }
 
+// Short transforms (2 <= N <= 32): one thread per row, the whole transform in registers (the
+// in-register DFT with compile-time twiddles).  A thread per row would touch one cache line per
+// lane, so the workgroup's XS rows move between HBM and LDS as one contiguous run per plane:
+// every global access instruction covers 64 consecutive floats (N = 16, 4M elements: 169 us with
+// the row-per-thread loads of the LDS kernel, copy speed with this one).
+constexpr int kSmallRows = 256;
+
+template <int N, int DIR, bool REAL_IN, bool TAIL>
+__global__ __launch_bounds__(kSmallRows) void c2c_small_kernel(
+    const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re, float* out_im,
+    long long first, long long batch, float scale) {
+  constexpr int XS = kSmallRows, P = N + 1;  // odd row pitch: a column read hits distinct banks
+  __shared__ float2 lds[XS * P];
+  const long long r0 = first + (long long)blockIdx.x * XS;
+  const int count = TAIL ? (int)(batch - r0 < XS ? batch - r0 : XS) * N : XS * N;  // floats per plane
+  const size_t g0 = (size_t)r0 * N;
+  const float sc = DIR < 0 ? 1.0f : scale;  // inverse: 1/n applied on input (exact for powers of two)
+  for (int i = threadIdx.x; i < count; i += XS) {
+    const float xr = ld_stream(in_re + g0 + i);
+    const float xi = REAL_IN ? 0.0f : ld_stream(in_im + g0 + i);
+    lds[(i / N) * P + i % N] = make_float2(xr * sc, xi * sc);
+  }
+  __syncthreads();
+  float2 v[N];
+  float2* row = lds + threadIdx.x * P;  // rows past a ragged tail hold stale data, never stored
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = row[k];
+  Dft<N, DIR>::run(v);
+#pragma unroll
+  for (int k = 0; k < N; ++k) row[k] = v[k];
+  __syncthreads();
+  for (int i = threadIdx.x; i < count; i += XS) {
+    const float2 y = lds[(i / N) * P + i % N];
+    st_stream(out_re + g0 + i, y.x);
+    st_stream(out_im + g0 + i, y.y);
+  }
+}
+
+template <int N, int DIR, bool REAL_IN>
+static hipError_t launch_c2c_small_t(const C2cArgs& a) {
+  const long long full = a.batch / kSmallRows;
+  if (full > 0)
+    hipLaunchKernelGGL((c2c_small_kernel<N, DIR, REAL_IN, false>), dim3((unsigned)full), dim3(kSmallRows), 0,
+                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, 0LL, a.batch, a.scale);
+  if (full * kSmallRows < a.batch)
+    hipLaunchKernelGGL((c2c_small_kernel<N, DIR, REAL_IN, true>), dim3(1), dim3(kSmallRows), 0, a.stream,
+                       a.in_re, a.in_im, a.out_re, a.out_im, full * kSmallRows, a.batch, a.scale);
+  return hipGetLastError();
+}
+
 template <int N, int DIR, bool REAL_IN>
 static hipError_t launch_c2c_lds_t(const C2cArgs& a) {
-  using C = C2cThreads<N>;
-  const long long full = a.batch / C::XF;
-  if (full > 0)
-    hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN, false>), dim3((unsigned)full), dim3(C::THREADS), 0,
-                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, 0LL, a.batch, a.scale);
-  if (full * C::XF < a.batch)
-    hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN, true>), dim3(1), dim3(C::THREADS), 0, a.stream, a.in_re,
-                       a.in_im, a.out_re, a.out_im, a.tw, full * C::XF, a.batch, a.scale);
-  return hipGetLastError();
+  if constexpr (N >= 2 && N <= 32) {
+    return launch_c2c_small_t<N, DIR, REAL_IN>(a);
+  } else {
+    using C = C2cThreads<N>;
+    const long long full = a.batch / C::XF;
+    if (full > 0)
+      hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN, false>), dim3((unsigned)full), dim3(C::THREADS), 0,
+                         a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, 0LL, a.batch, a.scale);
+    if (full * C::XF < a.batch)
+      hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN, true>), dim3(1), dim3(C::THREADS), 0, a.stream,
+                         a.in_re, a.in_im, a.out_re, a.out_im, a.tw, full * C::XF, a.batch, a.scale);
+    return hipGetLastError();
+  }
 }
 
 template <int N>
@@ -116,8 +176,9 @@ __global__ __launch_bounds__(C * (N1 / lds_epth(N1))) void strided_kernel(
     const float2* __restrict__ tw, long long stride, int tiles_per_block, float scale) {
   constexpr int E = lds_epth(N1), T = N1 / E;
   constexpr int PADN = lds_pad(N1) + 1;
-  __shared__ float lre[C * PADN];
-  __shared__ float lim[C * PADN];
+  // interleaved (re, im) exchange except at 4096 (two planes measured 3.5 % faster there)
+  constexpr bool IL = N1 != 4096;
+  __shared__ float2 lds[C * PADN];
   const int c = threadIdx.x % C;  // column within tile (fast across lanes: coalesced)
   const int t = threadIdx.x / C;
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
@@ -132,7 +193,12 @@ __global__ __launch_bounds__(C * (N1 / lds_epth(N1))) void strided_kernel(
     const size_t i = base + (size_t)(t + T * e) * stride;
     v[e] = valid ? make_float2(ld_stream(in_re + i), REAL_IN ? 0.0f : ld_stream(in_im + i)) : make_float2(0.0f, 0.0f);
   }
-  LdsFft<N1, E, DIR, false>::run(v, lre + c * PADN, lim + c * PADN, tw, t);
+  if constexpr (IL) {
+    LdsFft<N1, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);
+  } else {
+    float* planes = reinterpret_cast<float*>(lds);
+    LdsFft<N1, E, DIR, false>::run(v, planes + c * PADN, planes + (C + c) * PADN, tw, t);
+  }
   if (!valid) return;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -167,7 +233,7 @@ struct FourStepCfg {
   static constexpr int T = L / E;
   static constexpr int THREADS = TILE * T;
   static constexpr int PADN = lds_pad(L) + 1;
-  // both planes in LDS when they fit, else the real and imaginary planes take turns
+  // both planes (interleaved) in LDS when they fit, else the real and imaginary planes take turns
   static constexpr bool SPLIT = 2LL * TILE * PADN * 4 > kLdsBytes;
   static_assert(THREADS == 1024 && (SPLIT ? 1LL : 2LL) * TILE * PADN * 4 <= kLdsBytes, "four-step tile");
 };
@@ -181,8 +247,9 @@ __global__ __launch_bounds__(FourStepCfg<N1>::THREADS) void fourstep_col_kernel(
   constexpr int C = Cfg::TILE, E = Cfg::E, T = Cfg::T, THREADS = Cfg::THREADS, PADN = Cfg::PADN;
   constexpr bool SPLIT = Cfg::SPLIT;
   constexpr int TF = E < 4 ? E : 4;  // twiddle factor group
-  __shared__ float lre[C * PADN];
-  __shared__ float lim[SPLIT ? 1 : C * PADN];
+  // split planes take turns through one float plane; otherwise interleaved (re, im) entries
+  __shared__ float2 lds[SPLIT ? (C * PADN + 1) / 2 : C * PADN];
+  float* lre = reinterpret_cast<float*>(lds);
   const int c = threadIdx.x % C;  // column within the tile (fast across lanes: whole lines)
   const int t = threadIdx.x / C;
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
@@ -198,7 +265,10 @@ __global__ __launch_bounds__(FourStepCfg<N1>::THREADS) void fourstep_col_kernel(
     const size_t i = base + e * step;
     v[e] = make_float2(ld_stream(in_re + i), REAL_IN ? 0.0f : ld_stream(in_im + i));
   }
-  LdsFft<N1, E, DIR, false, SPLIT>::run(v, lre + c * PADN, SPLIT ? lre : lim + c * PADN, tw, t);
+  if constexpr (SPLIT)
+    LdsFft<N1, E, DIR, false, true>::run(v, lre + c * PADN, nullptr, tw, t);
+  else
+    LdsFft<N1, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);
 
   // W_N^(col*k1) for k1 = t + T*(TF*a + q): W^(col*(t + T*TF*a)) * W^(col*T*q), each root read as
   // W^lo * W^hi from the two small tables (TF-1 + E/TF table pairs per thread instead of E);
@@ -231,8 +301,7 @@ __global__ __launch_bounds__(FourStepCfg<N1>::THREADS) void fourstep_col_kernel(
       if constexpr (SPLIT) {
         lre[idx] = plane ? v[e].y : v[e].x;
       } else {
-        lre[idx] = v[e].x;
-        lim[idx] = v[e].y;
+        lds[idx] = v[e];
       }
     }
     __syncthreads();
@@ -247,8 +316,9 @@ __global__ __launch_bounds__(FourStepCfg<N1>::THREADS) void fourstep_col_kernel(
       if constexpr (SPLIT) {
         st_stream((plane ? out_im : out_re) + o, lre[idx]);
       } else {
-        st_stream(out_re + o, lre[idx]);
-        st_stream(out_im + o, lim[idx]);
+        const float2 y = lds[idx];
+        st_stream(out_re + o, y.x);
+        st_stream(out_im + o, y.y);
       }
     }
     if (SPLIT && plane == 0) __syncthreads();
@@ -262,8 +332,8 @@ __global__ __launch_bounds__(FourStepCfg<N2>::THREADS) void fourstep_row_kernel(
   using Cfg = FourStepCfg<N2>;
   constexpr int CK = Cfg::TILE, E = Cfg::E, T = Cfg::T, PADN = Cfg::PADN;
   constexpr bool SPLIT = Cfg::SPLIT;
-  __shared__ float lre[CK * PADN];
-  __shared__ float lim[SPLIT ? 1 : CK * PADN];
+  __shared__ float2 lds[SPLIT ? (CK * PADN + 1) / 2 : CK * PADN];
+  float* lre = reinterpret_cast<float*>(lds);
   const int r = threadIdx.x % CK;  // row within the tile (fast across lanes)
   const int t = threadIdx.x / CK;
   const int tiles_per_b = n1_len / CK;
@@ -278,7 +348,10 @@ __global__ __launch_bounds__(FourStepCfg<N2>::THREADS) void fourstep_row_kernel(
     const size_t i = ibase + (size_t)e * (T * CK);
     v[e] = make_float2(ld_stream(t_re + i), ld_stream(t_im + i));
   }
-  LdsFft<N2, E, DIR, false, SPLIT>::run(v, lre + r * PADN, SPLIT ? lre : lim + r * PADN, tw, t);
+  if constexpr (SPLIT)
+    LdsFft<N2, E, DIR, false, true>::run(v, lre + r * PADN, nullptr, tw, t);
+  else
+    LdsFft<N2, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + r * PADN), nullptr, tw, t);
   const size_t obase = (size_t)b * N + (size_t)kb * CK + r + (size_t)t * n1_len;
   const size_t ostep = (size_t)T * n1_len;
 #pragma unroll

@@ -32,8 +32,7 @@ __global__ __launch_bounds__(Fft2Row<W>::THREADS) void fft2_pass1_kernel(
   using C = Fft2Row<W>;
   constexpr int E = C::E, T = C::T, PADW = C::PADW;
   static_assert(8 * E >= 16 && (W * 8) % C::THREADS == 0, "layout");
-  __shared__ float lre[8 * PADW];
-  __shared__ float lim[8 * PADW];
+  __shared__ float2 lds[8 * PADW];  // interleaved (re, im)
   const long long g = blockIdx.x;
   const long long b = g / HR;
   const int r1 = (int)(g % HR);
@@ -49,13 +48,9 @@ __global__ __launch_bounds__(Fft2Row<W>::THREADS) void fft2_pass1_kernel(
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = make_float2(ld_stream(pr + T * e), REAL_IN ? 0.0f : ld_stream(pi + T * e));
   }
-  LdsFft<W, E, DIR, false>::run(v, lre + j * PADW, lim + j * PADW, tw_w, tid);
+  LdsFft<W, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + j * PADW), nullptr, tw_w, tid);
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int idx = j * PADW + lds_pad(tid + T * e);
-    lre[idx] = v[e].x;
-    lim[idx] = v[e].y;
-  }
+  for (int e = 0; e < E; ++e) lds[j * PADW + lds_pad(tid + T * e)] = v[e];
   __syncthreads();
   // cross-row 8-point DFT: thread t handles columns k = t + THREADS*m, m < W*8/THREADS/8
   constexpr int KPT = W / C::THREADS;  // columns per thread (>= 1 since W >= THREADS/8 * 8)
@@ -67,10 +62,7 @@ __global__ __launch_bounds__(Fft2Row<W>::THREADS) void fft2_pass1_kernel(
     const int k = threadIdx.x + C::THREADS * m;
     float2 z[8];
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      const int idx = jj * PADW + lds_pad(k);
-      z[jj] = make_float2(lre[idx], lim[idx]);
-    }
+    for (int jj = 0; jj < 8; ++jj) z[jj] = lds[jj * PADW + lds_pad(k)];
     Dft<8, DIR>::run(z);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -100,8 +92,7 @@ __global__ __launch_bounds__((Fft2RowPair<W, E_>::THREADS)) void fft2_pass1_real
     const float2* __restrict__ tw_h, int H, int HR) {
   using C = Fft2RowPair<W, E_>;
   constexpr int E = C::E, T = C::T, PADW = C::PADW, THREADS = C::THREADS;
-  __shared__ float lre[4 * PADW];
-  __shared__ float lim[4 * PADW];
+  __shared__ float2 lds[4 * PADW];  // interleaved (re, im)
   const long long g = blockIdx.x;
   const long long b = g / HR;
   const int r1 = (int)(g % HR);
@@ -114,13 +105,9 @@ __global__ __launch_bounds__((Fft2RowPair<W, E_>::THREADS)) void fft2_pass1_real
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = make_float2(ld_stream(pa + T * e), ld_stream(pb + T * e));
-  LdsFft<W, E, DIR, (T <= 64)>::run(v, lre + p * PADW, lim + p * PADW, tw_w, tid);
+  LdsFft<W, E, DIR, (T <= 64), false, true>::run(v, reinterpret_cast<float*>(lds + p * PADW), nullptr, tw_w, tid);
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int idx = p * PADW + lds_pad(tid + T * e);
-    lre[idx] = v[e].x;
-    lim[idx] = v[e].y;
-  }
+  for (int e = 0; e < E; ++e) lds[p * PADW + lds_pad(tid + T * e)] = v[e];
   __syncthreads();
   float2 tq[8];
 #pragma unroll
@@ -131,8 +118,9 @@ __global__ __launch_bounds__((Fft2RowPair<W, E_>::THREADS)) void fft2_pass1_real
     float2 z[8];
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
-      const float ar = lre[pp * PADW + ik], ai = lim[pp * PADW + ik];
-      const float cr = lre[pp * PADW + ir], ci = -lim[pp * PADW + ir];  // conj Z[W-k]
+      const float2 za = lds[pp * PADW + ik], zc = lds[pp * PADW + ir];
+      const float ar = za.x, ai = za.y;
+      const float cr = zc.x, ci = -zc.y;  // conj Z[W-k]
       z[2 * pp] = make_float2(0.5f * (ar + cr), 0.5f * (ai + ci));
       z[2 * pp + 1] = make_float2(0.5f * (ai - ci), -0.5f * (ar - cr));
     }
@@ -164,8 +152,7 @@ __global__ __launch_bounds__(C * (HR / E_)) void fft2_pass2_kernel(
     float* re, float* im, const float2* __restrict__ tw, int W, int tiles_per_group, float scale) {
   constexpr int E = E_, T = HR / E;
   constexpr int PADN = lds_pad(HR) + 1;
-  __shared__ float lre[C * PADN];
-  __shared__ float lim[C * PADN];
+  __shared__ float2 lds[C * PADN];  // interleaved (re, im) exchange
   const int c = threadIdx.x % C;
   const int t = threadIdx.x / C;
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
@@ -186,7 +173,7 @@ __global__ __launch_bounds__(C * (HR / E_)) void fft2_pass2_kernel(
   }
   // every value this workgroup loads is consumed by the transform (whose first exchange is a
   // workgroup barrier) before any thread stores; no other workgroup touches these elements
-  LdsFft<HR, E, DIR, false>::run(v, lre + c * PADN, lim + c * PADN, tw, t);
+  LdsFft<HR, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);
   if (!valid) return;
 #pragma unroll
   for (int e = 0; e < E; ++e) {

@@ -27,7 +27,7 @@ struct IstftCfg {
   static constexpr int E = E_;
   static constexpr int T = NFFT / E;
   static constexpr int F = NFFT / 2 + 1;                    // onesided bins
-  static constexpr int RP = 2 * lds_pad(NFFT) + 4;          // floats per pair region (>= 4F, >= 2n)
+  static constexpr int RP = 2 * lds_pad(NFFT) + 4;          // floats per pair region (>= 4F, >= 2n, even)
   static constexpr int PAIRS_T = 1024 / T < MAXP ? 1024 / T : MAXP;
   static constexpr int PAIRS_L = (kLdsBytes - NFFT * 4) / (RP * 4);
   static constexpr int PAIRS = PAIRS_T < PAIRS_L ? PAIRS_T : PAIRS_L;
@@ -45,8 +45,9 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
   using C = IstftCfg<NFFT, E_, MAXP>;
   constexpr int E = C::E, T = C::T, F = C::F, RP = C::RP, FR = C::FR, THREADS = C::THREADS;
   constexpr bool WL = T <= 64;
-  __shared__ float lds[C::PAIRS * RP];
+  __shared__ float2 lds2[C::PAIRS * RP / 2];  // RP is even: every pair region is 8-byte aligned
   __shared__ float wl[NFFT];
+  float* lds = reinterpret_cast<float*>(lds2);
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
   const long long b = tile / tiles_per_signal;
   const int t0 = (int)(tile % tiles_per_signal) * owned;  // first owned frame
@@ -85,7 +86,7 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
     }
   }
   exchange_sync<WL>();  // the transform reuses this pair's region
-  LdsFft<NFFT, E, 1, WL>::run(v, reg, reg + lds_pad(NFFT), tw, tid);
+  LdsFft<NFFT, E, 1, WL, false, true>::run(v, reg, nullptr, tw, tid);  // interleaved exchange
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     reg[tid + T * e] = v[e].x;         // frame 2p

@@ -57,24 +57,19 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
   using C = RealCfg<H, E_, THR>;
   constexpr int E = C::E, T = C::T;
   constexpr bool WL = T <= 64;
-  __shared__ float lre[C::XF * C::PADR];
-  __shared__ float lim[C::XF * C::PADR];
+  __shared__ float2 lds[C::XF * C::PADR];  // interleaved (re, im)
   const int tid = threadIdx.x % T;
   const int xf = threadIdx.x / T;
   const long long b = first + (long long)blockIdx.x * C::XF + xf;
   const bool valid = !TAIL || b < batch;
-  float* mre = lre + xf * C::PADR;
-  float* mim = lim + xf * C::PADR;
+  float2* m = lds + xf * C::PADR;
   const float2* src = reinterpret_cast<const float2*>(x + (size_t)b * (2 * H)) + tid;
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = valid ? ld_stream2(src + T * e) : make_float2(0.0f, 0.0f);
-  LdsFft<H, E, -1, WL>::run(v, mre, mim, tw, tid);
+  LdsFft<H, E, -1, WL, false, true>::run(v, reinterpret_cast<float*>(m), nullptr, tw, tid);
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    mre[lds_pad(tid + T * e)] = v[e].x;
-    mim[lds_pad(tid + T * e)] = v[e].y;
-  }
+  for (int e = 0; e < E; ++e) m[lds_pad(tid + T * e)] = v[e];
   exchange_sync<WL>();
   if (!valid) return;
   float* qr = out_re + (size_t)b * (H + 1) + tid;
@@ -84,9 +79,9 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int k = tid + T * e;
-    const int r = lds_pad((H - k) & (H - 1));
+    const float2 z = m[lds_pad((H - k) & (H - 1))];
     const float2 a = v[e];
-    const float2 c = make_float2(mre[r], -mim[r]);  // conj Z[H-k]
+    const float2 c = make_float2(z.x, -z.y);  // conj Z[H-k]
     const float2 ev = make_float2(0.5f * (a.x + c.x), 0.5f * (a.y + c.y));
     const float2 od = make_float2(0.5f * (a.y - c.y), -0.5f * (a.x - c.x));  // (a - c) / 2i
     const float2 y = cadd(ev, cmul(wk[e], od));
@@ -107,26 +102,23 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
   using C = RealCfg<H, E_, THR>;
   constexpr int E = C::E, T = C::T;
   constexpr bool WL = T <= 64;
-  __shared__ float lre[C::XF * C::PADR];
-  __shared__ float lim[C::XF * C::PADR];
+  __shared__ float2 lds[C::XF * C::PADR];  // interleaved (re, im)
   const int tid = threadIdx.x % T;
   const int xf = threadIdx.x / T;
   const long long b = first + (long long)blockIdx.x * C::XF + xf;
   const bool valid = !TAIL || b < batch;
-  float* mre = lre + xf * C::PADR;
-  float* mim = lim + xf * C::PADR;
+  float2* m = lds + xf * C::PADR;
   const float* pr = in_re + (size_t)b * (H + 1) + tid;
   const float* pi = in_im + (size_t)b * (H + 1) + tid;
   float2 a[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     a[e] = valid ? make_float2(ld_stream(pr + T * e), ld_stream(pi + T * e)) : make_float2(0.0f, 0.0f);
-    mre[lds_pad(tid + T * e)] = a[e].x;
-    mim[lds_pad(tid + T * e)] = a[e].y;
+    m[lds_pad(tid + T * e)] = a[e];
   }
   if (tid == 0) {
-    mre[lds_pad(H)] = valid ? ld_stream(pr + H) : 0.0f;  // Im X[H] is never read
-    a[0].y = 0.0f;                                       // Im X[0] drops out
+    m[lds_pad(H)] = make_float2(valid ? ld_stream(pr + H) : 0.0f, 0.0f);  // Im X[H] is never read
+    a[0].y = 0.0f;                                                        // Im X[0] drops out
   }
   exchange_sync<WL>();
   float2 v[E];
@@ -134,14 +126,14 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int k = tid + T * e;
-    const int r = lds_pad(H - k);
-    const float2 c = make_float2(mre[r], k == 0 ? 0.0f : -mim[r]);  // conj X[H-k]
+    const float2 z = m[lds_pad(H - k)];
+    const float2 c = make_float2(z.x, k == 0 ? 0.0f : -z.y);  // conj X[H-k]
     const float2 sum = cadd(a[e], c);
     const float2 dif = cmul(csub(a[e], c), make_float2(twr[k].x, -twr[k].y));  // x W_N^-k
     v[e] = make_float2((sum.x - dif.y) * scale, (sum.y + dif.x) * scale);         // sum + i dif
   }
   exchange_sync<WL>();  // the transform below reuses this transform's LDS
-  LdsFft<H, E, 1, WL>::run(v, mre, mim, tw, tid);
+  LdsFft<H, E, 1, WL, false, true>::run(v, reinterpret_cast<float*>(m), nullptr, tw, tid);
   if (!valid) return;
   float2* dst = reinterpret_cast<float2*>(x + (size_t)b * (2 * H)) + tid;
 #pragma unroll

@@ -33,6 +33,7 @@ struct StftCfg {
   static constexpr int FR = 2 * PAIRS;             // frames per workgroup
   static constexpr int THREADS = PAIRS * T;
   static constexpr int LDSF = 2 * PAIRS * PADN;  // floats of the spectra area (also the staging area)
+  // the spectra are interleaved (re, im) float2 entries: PADN per pair
   static_assert((long long)LDSF * 4 + NFFT * 4 <= kLdsBytes, "STFT tile exceeds LDS");
   static_assert(THREADS > 0 && (FR & (FR - 1)) == 0, "frame tile must be a power of two");
 };
@@ -47,8 +48,9 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS, E_>::THREADS)) void stft_kern
     int n_frames, int n_bins, int tiles_per_signal, float scale) {
   using C = StftCfg<NFFT, PAIRS, E_>;
   constexpr int E = C::E, T = C::T, FR = C::FR, PADN = C::PADN, THREADS = C::THREADS;
-  __shared__ float lds[C::LDSF];
+  __shared__ float2 lds2[C::LDSF / 2];
   __shared__ float wl[NFFT];
+  float* lds = reinterpret_cast<float*>(lds2);
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
   const long long b = tile / tiles_per_signal;
   const int f0 = (int)(tile % tiles_per_signal) * FR;
@@ -113,14 +115,10 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS, E_>::THREADS)) void stft_kern
       v[e] = make_float2(s[0], s[1]);
     }
   }
-  float* my_re = lds + pl * PADN;
-  float* my_im = lds + (PAIRS + pl) * PADN;
-  LdsFft<NFFT, E, -1, (T <= 64)>::run(v, my_re, my_im, tw, tid);
+  float2* my = lds2 + pl * PADN;
+  LdsFft<NFFT, E, -1, (T <= 64), false, true>::run(v, reinterpret_cast<float*>(my), nullptr, tw, tid);
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    my_re[lds_pad(tid + T * e)] = v[e].x;
-    my_im[lds_pad(tid + T * e)] = v[e].y;
-  }
+  for (int e = 0; e < E; ++e) my[lds_pad(tid + T * e)] = v[e];
   __syncthreads();
   // 3. lanes over consecutive frames fr: frame fr = 2p (+1) is the real (imaginary) part of pair p.
   //    Flat loop over (bin, frame) so any FR / THREADS ratio is covered; every iteration advances.
@@ -131,11 +129,9 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS, E_>::THREADS)) void stft_kern
     const int fr = i % FR;
     const int k = i / FR;
     if (f0 + fr >= n_frames) continue;
-    const float* zr_p = lds + (fr >> 1) * PADN;
-    const float* zi_p = lds + (PAIRS + (fr >> 1)) * PADN;
-    const int ik = lds_pad(k);
-    const int inr = lds_pad((NFFT - k) & (NFFT - 1));
-    const float zr = zr_p[ik], zi = zi_p[ik], yr = zr_p[inr], yi = zi_p[inr];
+    const float2* zp = lds2 + (fr >> 1) * PADN;
+    const float2 z = zp[lds_pad(k)], y = zp[lds_pad((NFFT - k) & (NFFT - 1))];
+    const float zr = z.x, zi = z.y, yr = y.x, yi = y.y;
     const bool odd = fr & 1;
     const float re = odd ? (zi + yi) : (zr + yr);
     const float im = odd ? (yr - zr) : (zi - yi);
