@@ -12,6 +12,7 @@ import oracle
 import trnfft_amd
 from conftest import rel_l2, tol_pow2
 from trnfft_amd import ComplexTensor
+from trnfft_amd.fft_core import fft2_small_ok
 
 pytestmark = pytest.mark.gpu
 
@@ -156,7 +157,8 @@ def test_stft_edge_shapes(n_fft, hop, length, batch_shape):
 
 
 @pytest.mark.parametrize("shape", [(2, 16, 16), (1, 4096, 16), (3, 16, 2048), (2, 512, 1024), (1, 128, 64)])
-def test_fft2_two_pass_complex_and_inverse(shape):
+def test_fft2_complex_and_inverse(shape):
+    # (16, 16) and (128, 64) take the single-pass small-image kernel, the others the two passes
     rng = np.random.default_rng(11)
     re = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
     im = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
@@ -171,9 +173,10 @@ def test_fft2_two_pass_complex_and_inverse(shape):
 
 
 @pytest.mark.parametrize("shape", [(2, 16, 16), (1, 4096, 16), (3, 16, 2048), (2, 512, 1024), (1, 128, 64), (2, 64, 32)])
-def test_fft2_two_pass_real_half_spectrum(shape):
-    # real input: pass 1 writes columns 0..W/2, pass 2 completes W/2+1..W-1 from the 2-D
-    # Hermitian symmetry; forward and inverse (ifftn of a real array) against the oracle
+def test_fft2_real_input(shape):
+    # real input.  Two-pass shapes: pass 1 writes columns 0..W/2, pass 2 completes W/2+1..W-1
+    # from the 2-D Hermitian symmetry; small images are transformed whole.  Forward and inverse
+    # (ifftn of a real array) against the oracle
     rng = np.random.default_rng(13)
     x = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
     n = shape[-1] * shape[-2]
@@ -183,8 +186,54 @@ def test_fft2_two_pass_real_half_spectrum(shape):
     inv = trnfft_amd.ifftn(x.cuda(), dim=(-2, -1))
     ref_inv = oracle.ifftn(x, dim=(-2, -1))
     assert rel_l2(inv.real, inv.imag, *ref_inv) <= tol_pow2(n)
-    # the completed half is the conjugate reflection of the computed one, exactly
     g = torch.complex(got.real, got.imag).cpu()
-    mirrored = torch.conj(torch.roll(torch.flip(g, dims=(-2, -1)), shifts=(1, 1), dims=(-2, -1)))
+    mirrored = torch.conj(torch.roll(torch.flip(g, dims=(-2, -1)), shifts=(1, 1), dims=(-2, -1))).resolve_conj()
     w = shape[-1]
-    assert torch.equal(g[..., w // 2 + 1:], mirrored[..., w // 2 + 1:])
+    if fft2_small_ok(shape[-2], shape[-1]):
+        # computed whole: Hermitian to rounding
+        assert rel_l2(g.real, g.imag, mirrored.real, mirrored.imag) <= tol_pow2(n)
+    else:
+        # the completed half is the conjugate reflection of the computed one, exactly
+        assert torch.equal(g[..., w // 2 + 1:], mirrored[..., w // 2 + 1:])
+
+
+# every image shape of the single-pass kernel's families (4096 elements per workgroup below
+# 4096, one image at 4096..16384), ragged batches that leave a partial workgroup, complex and
+# real input, forward and inverse
+@pytest.mark.parametrize("shape", [(37, 4, 4), (5, 4, 64), (3, 64, 4), (19, 16, 16), (7, 8, 32), (3, 32, 64),
+                                   (2, 64, 64), (3, 8, 1024), (2, 1024, 8), (3, 128, 128), (2, 16, 1024),
+                                   (2, 1024, 16), (1, 256, 64)])
+def test_fft2_small_images(shape):
+    assert fft2_small_ok(shape[-2], shape[-1])
+    rng = np.random.default_rng(21)
+    re = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
+    im = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
+    n = shape[-1] * shape[-2]
+    got = trnfft_amd.fft2(ComplexTensor(re.cuda(), im.cuda()))
+    ref = oracle.fft2((re, im))
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(n), shape
+    back = trnfft_amd.ifftn(got, dim=(-2, -1))
+    assert rel_l2(back.real, back.imag, re, im) <= 2 * tol_pow2(n), shape
+    x = np.fft.fft2(re.double().numpy())
+    gr = trnfft_amd.fft2(re.cuda())
+    assert rel_l2(gr.real, gr.imag, x.real, x.imag) <= tol_pow2(n), shape
+
+
+def test_fft2_small_image_known_answers():
+    # impulse -> all ones; constant -> n at DC; a pure 2-D tone -> one bin
+    h, w = 16, 32
+    x = torch.zeros(h, w)
+    x[0, 0] = 1.0
+    y = trnfft_amd.fft2(x.cuda())
+    assert torch.allclose(y.real.cpu(), torch.ones(h, w)) and torch.allclose(y.imag.cpu(), torch.zeros(h, w))
+    y = trnfft_amd.fft2(torch.ones(h, w).cuda())
+    ref = torch.zeros(h, w)
+    ref[0, 0] = h * w
+    assert torch.allclose(y.real.cpu(), ref, atol=1e-4) and torch.allclose(y.imag.cpu(), torch.zeros(h, w), atol=1e-4)
+    r = torch.arange(h).double()[:, None]
+    c = torch.arange(w).double()[None, :]
+    ang = 2 * math.pi * (3 * r / h + 5 * c / w)
+    z = trnfft_amd.fft2(ComplexTensor(torch.cos(ang).float().cuda(), torch.sin(ang).float().cuda()))
+    ref = torch.zeros(h, w)
+    ref[3, 5] = h * w
+    assert torch.allclose(z.real.cpu(), ref, atol=1e-3) and torch.allclose(z.imag.cpu(), torch.zeros(h, w), atol=1e-3)

@@ -56,6 +56,18 @@ def test_create_plan_matches_reference_choice():
     assert trnfft_amd.create_plan(1000, True) is trnfft_amd.create_plan(1000, True)
 
 
+def test_fft2_shape_gates():
+    # the single-pass small-image kernel: powers of two, h*w <= 16384, both axes >= 4 and >= its
+    # elements per thread (4 up to 4096 elements, 8 at 8192, 16 at 16384); two passes otherwise
+    from trnfft_amd.fft_core import fft2_ok, fft2_small_ok
+
+    for h, w in [(4, 4), (4, 64), (64, 4), (16, 16), (128, 128), (8, 1024), (1024, 8), (16, 1024), (1024, 16)]:
+        assert fft2_small_ok(h, w), (h, w)
+    for h, w in [(2, 64), (64, 2), (4, 2048), (8, 2048), (256, 128), (12, 16), (3, 3)]:
+        assert not fft2_small_ok(h, w), (h, w)
+    assert fft2_ok(4, 4) and fft2_ok(16, 2048) and fft2_ok(4096, 16) and not fft2_ok(4, 2048)
+
+
 def test_backend_selection_semantics():
     assert trnfft_amd.get_backend() == "auto"
     with pytest.raises(AssertionError):

@@ -56,6 +56,16 @@ __host__ __device__ constexpr int stft_epth(int n) { return n < 8 ? n : 8; }
 __host__ __device__ constexpr int fft2_pair_epth(int w) { return w < 8 ? w : 8; }
 __host__ __device__ constexpr int fft2_col_epth(int hr) { return hr < 8 ? hr : 8; }
 
+// Single-pass 2-D transform of small images (h*w <= 16384 complex: whole images in LDS).  A
+// workgroup of 1024 threads takes IMG images (4096 elements when images are smaller) and keeps
+// E = IMG*h*w/1024 elements per thread in both the row and the column phase.
+__host__ __device__ constexpr int fft2_small_img(int h, int w) { return h * w >= 4096 ? 1 : 4096 / (h * w); }
+__host__ __device__ constexpr int fft2_small_epth(int h, int w) { return fft2_small_img(h, w) * h * w / 1024; }
+__host__ __device__ constexpr bool fft2_small_ok(long long h, long long w) {
+  return h >= 4 && w >= 4 && (h & (h - 1)) == 0 && (w & (w - 1)) == 0 && h * w <= 16384 &&
+         h >= fft2_small_epth((int)h, (int)w) && w >= fft2_small_epth((int)h, (int)w);
+}
+
 // Fused Bluestein launch shape.  m = 2048 (n = 1000): E = 8 with 512-thread workgroups measured
 // 16.2 -> 14.7 us against the batched-c2c shape (E = 16, 256 threads); other lengths keep the
 // latter (m = 16384: E = 16 and E = 32 within 2 %).

@@ -189,6 +189,8 @@ struct Fft2Args {
   const float2* tw_w_pair;  // LDS-FFT table for length w in the paired-real-row layout
   const float2* tw_hr;      // LDS-FFT table for length h/8 (column pass layout)
   const float2* tw_h;   // W_h^i, i < h
+  const float2* tw_sw;  // single-pass small-image kernel: LDS-FFT tables for w and h
+  const float2* tw_sh;  //   (fft2_small_epth layout); used when fft2_small_ok(h, w)
   long long batch, h, w;
   float scale;  // applied in pass 2 (1/(h*w) for the inverse)
   int dir;

@@ -225,8 +225,142 @@ static hipError_t launch_pass2_h(const Fft2Args& a) {
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------------
+// Single-pass small images (h*w <= 16384): one HBM read and one HBM write per element.  The
+// workgroup's IMG images are staged row-major into LDS (row r of image i at (i*H + r)*RW, entry c
+// at lds_pad(c)); every row is transformed with its own LDS row as the exchange area, written
+// back transposed (column k at (i*W + k)*CH, entry r at lds_pad(r)); every column is transformed
+// in place the same way; the store phase reads the columns back in row order.
+// ---------------------------------------------------------------------------------------------
+template <int H, int W>
+struct Fft2SmallCfg {
+  static constexpr int IMG = fft2_small_img(H, W);
+  static constexpr int E = fft2_small_epth(H, W);
+  static constexpr int TW = W / E, TH = H / E;   // threads per row / per column
+  static constexpr int THREADS = 1024;
+  static constexpr int RW = lds_pad(W) + 1, CH = lds_pad(H) + 1;  // odd pitches
+  static constexpr int PER = H * RW > W * CH ? H * RW : W * CH;    // float2 entries per image
+  static constexpr int P = H * W;
+  static_assert(IMG * H * TW == THREADS && IMG * W * TH == THREADS, "one row / column per thread group");
+  static_assert((long long)IMG * PER * 8 <= kLdsBytes, "small-image tile exceeds LDS");
+};
+
+template <int H, int W, int DIR, bool REAL_IN, bool TAIL>
+__global__ __launch_bounds__(1024) void fft2_small_kernel(
+    const float* __restrict__ in_re, const float* __restrict__ in_im, float* __restrict__ out_re,
+    float* __restrict__ out_im, const float2* __restrict__ tw_w, const float2* __restrict__ tw_h,
+    long long first, long long batch, float scale) {
+  using C = Fft2SmallCfg<H, W>;
+  constexpr int E = C::E, TW = C::TW, TH = C::TH, RW = C::RW, CH = C::CH, P = C::P, IMG = C::IMG;
+  __shared__ float2 lds[IMG * C::PER];
+  const long long i0 = first + (long long)blockIdx.x * IMG;  // first image of the tile
+  const int count = TAIL ? (int)((batch - i0 < IMG ? batch - i0 : IMG) * P) : IMG * P;
+  const size_t g0 = (size_t)i0 * P;
+  const float sc = DIR < 0 ? 1.0f : scale;  // inverse: 1/(h*w) on the input (exact, powers of two)
+  for (int i = threadIdx.x; i < count; i += 1024) {
+    const int img = i / P, r = (i % P) / W, c = i % W;
+    const float xr = ld_stream(in_re + g0 + i);
+    const float xi = REAL_IN ? 0.0f : ld_stream(in_im + g0 + i);
+    lds[(img * H + r) * RW + lds_pad(c)] = make_float2(xr * sc, xi * sc);
+  }
+  __syncthreads();
+  float2 v[E];
+  {  // rows (images past a ragged tail hold stale LDS data: transformed, never stored)
+    const int row = threadIdx.x / TW, tid = threadIdx.x % TW;  // row = img*H + r
+    float2* base = lds + row * RW;
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = base[lds_pad(tid + TW * e)];
+    __syncthreads();  // the row area becomes the transform's exchange area
+    LdsFft<W, E, DIR, (TW <= 64), false, true>::run(v, reinterpret_cast<float*>(base), nullptr, tw_w, tid);
+    __syncthreads();
+    const int img = row / H, r = row % H;
+#pragma unroll
+    for (int e = 0; e < E; ++e) lds[(img * W + tid + TW * e) * CH + lds_pad(r)] = v[e];
+    __syncthreads();
+  }
+  {  // columns
+    const int col = threadIdx.x / TH, tid = threadIdx.x % TH;  // col = img*W + k
+    float2* base = lds + col * CH;
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = base[lds_pad(tid + TH * e)];
+    __syncthreads();
+    LdsFft<H, E, DIR, (TH <= 64), false, true>::run(v, reinterpret_cast<float*>(base), nullptr, tw_h, tid);
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e) base[lds_pad(tid + TH * e)] = v[e];
+    __syncthreads();
+  }
+  for (int i = threadIdx.x; i < count; i += 1024) {
+    const int img = i / P, q = (i % P) / W, k = i % W;
+    const float2 y = lds[(img * W + k) * CH + lds_pad(q)];
+    st_stream(out_re + g0 + i, y.x);
+    st_stream(out_im + g0 + i, y.y);
+  }
+}
+
+template <int H, int W, int DIR>
+static hipError_t launch_fft2_small_hw(const Fft2Args& a) {
+  if constexpr (fft2_small_ok(H, W)) {
+    using C = Fft2SmallCfg<H, W>;
+    const long long full = a.batch / C::IMG;
+    const bool real_in = a.in_im == nullptr;
+    if (full > 0) {
+      if (real_in)
+        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, true, false>), dim3((unsigned)full), dim3(1024), 0, a.stream,
+                           a.in_re, a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, 0LL, a.batch, a.scale);
+      else
+        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, false, false>), dim3((unsigned)full), dim3(1024), 0,
+                           a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, 0LL, a.batch, a.scale);
+    }
+    if (full * C::IMG < a.batch) {  // ragged tail: one workgroup
+      if (real_in)
+        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, true, true>), dim3(1), dim3(1024), 0, a.stream, a.in_re,
+                           a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, full * C::IMG, a.batch, a.scale);
+      else
+        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, false, true>), dim3(1), dim3(1024), 0, a.stream, a.in_re,
+                           a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, full * C::IMG, a.batch, a.scale);
+    }
+    return hipGetLastError();
+  } else {
+    return hipErrorInvalidValue;
+  }
+}
+
+template <int H, int DIR>
+static hipError_t launch_fft2_small_h(const Fft2Args& a) {
+  switch (a.w) {
+    case 4: return launch_fft2_small_hw<H, 4, DIR>(a);
+    case 8: return launch_fft2_small_hw<H, 8, DIR>(a);
+    case 16: return launch_fft2_small_hw<H, 16, DIR>(a);
+    case 32: return launch_fft2_small_hw<H, 32, DIR>(a);
+    case 64: return launch_fft2_small_hw<H, 64, DIR>(a);
+    case 128: return launch_fft2_small_hw<H, 128, DIR>(a);
+    case 256: return launch_fft2_small_hw<H, 256, DIR>(a);
+    case 512: return launch_fft2_small_hw<H, 512, DIR>(a);
+    case 1024: return launch_fft2_small_hw<H, 1024, DIR>(a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int DIR>
+static hipError_t launch_fft2_small(const Fft2Args& a) {
+  switch (a.h) {
+    case 4: return launch_fft2_small_h<4, DIR>(a);
+    case 8: return launch_fft2_small_h<8, DIR>(a);
+    case 16: return launch_fft2_small_h<16, DIR>(a);
+    case 32: return launch_fft2_small_h<32, DIR>(a);
+    case 64: return launch_fft2_small_h<64, DIR>(a);
+    case 128: return launch_fft2_small_h<128, DIR>(a);
+    case 256: return launch_fft2_small_h<256, DIR>(a);
+    case 512: return launch_fft2_small_h<512, DIR>(a);
+    case 1024: return launch_fft2_small_h<1024, DIR>(a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <int DIR>
 static hipError_t launch_fft2_dir(const Fft2Args& a) {
+  if (fft2_small_ok(a.h, a.w)) return launch_fft2_small<DIR>(a);
   hipError_t e;
   switch (a.w) {  // 8 rows x W/E threads must fit one 1024-thread workgroup: W <= 2048
     case 16: e = launch_pass1_w<16, DIR>(a); break;

@@ -89,6 +89,7 @@ struct tfa_plan {
   C2cTables col;          // FFT2: LDS table for n2/8 (pass 2)
   float2* tw_h = nullptr;  // FFT2: W_{n2}^i, i < n2
   float2* tw_w_pair = nullptr;  // FFT2: row table in the paired-real-row layout
+  float2 *tw_sw = nullptr, *tw_sh = nullptr;  // FFT2 small images: row / column tables
   float2* twr = nullptr;  // REAL: W_n^k, k < n/2
   float* w_re = nullptr;  // DFT-GEMM matrix
   float* w_im = nullptr;
@@ -337,8 +338,18 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       break;
     case TFA_KIND_FFT2: {
       const int64_t h = desc->n2;
+      if (tfa::fft2_small_ok(h, n)) {  // whole images in LDS: single pass
+        const int e = tfa::fft2_small_epth((int)h, (int)n);
+        p->fwd.n = n;
+        p->fwd.dir = dir;
+        if ((rc = p->upload(lds_table((int)n, dir, e), &p->tw_sw))) break;
+        rc = p->upload(lds_table((int)h, dir, e), &p->tw_sh);
+        break;
+      }
       if (!is_pow2(n) || n < 16 || n > 2048 || !is_pow2(h) || h < 16 || h > 4096) {
-        rc = fail(TFA_ERR_UNSUPPORTED, "FFT2 plans need power-of-two 16 <= n <= 2048 and 16 <= n2 <= 4096");
+        rc = fail(TFA_ERR_UNSUPPORTED,
+                  "FFT2 plans need power-of-two 16 <= n <= 2048 and 16 <= n2 <= 4096, or n * n2 <= 16384 "
+                  "with both axes >= 4 (and >= 8 / 16 at n * n2 = 8192 / 16384)");
         break;
       }
       if ((rc = p->build_c2c(n, dir, &p->fwd))) break;
@@ -454,7 +465,7 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
       const int64_t h = plan->d.n2;
       const float s2 = plan->d.inverse ? (float)(1.0 / ((double)n * (double)h)) : 1.0f;
       tfa::Fft2Args f{in_re, in_im, out_re, out_im, plan->fwd.tw_lds, plan->tw_w_pair, plan->col.tw, plan->tw_h,
-                      batch, h, n, s2, plan->fwd.dir, s};
+                      plan->tw_sw, plan->tw_sh, batch, h, n, s2, plan->fwd.dir, s};
       hipError_t e = tfa::launch_fft2(f);
       return e == hipSuccess ? TFA_OK : hip_fail(e, "fft2 launch");
     }

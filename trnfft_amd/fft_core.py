@@ -164,12 +164,26 @@ def execute_strided(re: torch.Tensor, im: torch.Tensor | None, dim: int, inverse
     return out if out_dev == dev else out.to(out_dev)
 
 
-def fft2_ok(h: int, w: int) -> bool:
-    """Shapes the two-pass 2-D kernels take: power-of-two 16 <= w <= 2048, 16 <= h <= 4096."""
+def fft2_small_ok(h: int, w: int) -> bool:
+    """Images the single-pass 2-D kernel holds in LDS (mirror of tfa::fft2_small_ok): powers of
+    two, h*w <= 16384, both axes >= 4 and >= the kernel's elements per thread."""
     def p2(v):
         return v > 0 and (v & (v - 1)) == 0
 
-    return p2(h) and p2(w) and 16 <= w <= 2048 and 16 <= h <= 4096
+    if not (p2(h) and p2(w) and h >= 4 and w >= 4 and h * w <= 16384):
+        return False
+    img = 1 if h * w >= 4096 else 4096 // (h * w)
+    e = img * h * w // 1024
+    return h >= e and w >= e
+
+
+def fft2_ok(h: int, w: int) -> bool:
+    """Shapes the 2-D kernels take: the single-pass small-image kernel, or the two-pass kernels
+    (power-of-two 16 <= w <= 2048, 16 <= h <= 4096)."""
+    def p2(v):
+        return v > 0 and (v & (v - 1)) == 0
+
+    return fft2_small_ok(h, w) or (p2(h) and p2(w) and 16 <= w <= 2048 and 16 <= h <= 4096)
 
 
 def execute_fft2(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> ComplexTensor:
