@@ -77,6 +77,25 @@ def test_fftn_ifftn_vs_numpy(shape, dim, s):
         assert rel_l2(got.real, got.imag, *ref_o) <= 3 * tol_bluestein(max(shape))
 
 
+# transforms along axis -2 with few trailing columns: whole (n x s) blocks staged through LDS
+# (s <= half the strided kernel's column tile), ragged block counts, complex and real input
+@pytest.mark.parametrize("shape", [(37, 2, 3), (9, 16, 1), (11, 64, 5), (5, 128, 3), (7, 512, 7), (3, 1024, 8),
+                                   (5, 1024, 2), (3, 4096, 2), (2, 4096, 1), (65, 32, 31)])
+def test_fft_along_axis_with_few_trailing_columns(shape):
+    rng = np.random.default_rng(5)
+    re = rng.standard_normal(shape).astype(np.float32)
+    im = rng.standard_normal(shape).astype(np.float32)
+    x = ComplexTensor(torch.from_numpy(re).cuda(), torch.from_numpy(im).cuda())
+    n = shape[1]
+    for inverse in (False, True):
+        got = trnfft_amd.fftn(x, dim=(1,)) if not inverse else trnfft_amd.ifftn(x, dim=(1,))
+        z = re.astype(np.float64) + 1j * im
+        ref = np.fft.ifft(z, axis=1) if inverse else np.fft.fft(z, axis=1)
+        assert _np_rel(got, ref) <= tol_pow2(n), (shape, inverse)
+    got = trnfft_amd.fftn(torch.from_numpy(re).cuda(), dim=(1,))
+    assert _np_rel(got, np.fft.fft(re.astype(np.float64), axis=1)) <= tol_pow2(n), shape
+
+
 @pytest.mark.parametrize("n_in,n", [(100, 128), (300, 256), (1000, 1000), (64, 100), (4096, 4000)])
 def test_fft_ifft_n_param(n_in, n):
     rng = np.random.default_rng(5)

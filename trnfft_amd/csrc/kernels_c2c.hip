@@ -367,9 +367,84 @@ __global__ __launch_bounds__(FourStepCfg<N2>::THREADS) void fourstep_row_kernel(
   }
 }
 
+// floor(n / d) and n % d for 0 <= n < 2^24 (float reciprocal, one correction step: exact there)
+__device__ __forceinline__ int divmod_small(int n, int d, float rd, int& r) {
+  int q = (int)((float)n * rd);
+  r = n - q * d;
+  if (r < 0) {
+    --q;
+    r += d;
+  } else if (r >= d) {
+    ++q;
+    r -= d;
+  }
+  return q;
+}
+
+// Strided transform with few columns (stride <= C/2): the column tile of strided_kernel would be
+// mostly idle and its row segments a few floats long.  Here a workgroup takes G = C / stride
+// whole (N1 x stride) blocks, contiguous in memory: they are read and written as one run per
+// plane and transposed through LDS (column g*stride + col of the tile at region c*PADN, the
+// transform's own exchange area, entry j at lds_pad(j)).
+template <int N1, int DIR, bool REAL_IN, int C = fourstep_tile(N1)>
+__global__ __launch_bounds__(C * (N1 / lds_epth(N1))) void strided_small_kernel(
+    const float* __restrict__ in_re, const float* __restrict__ in_im, float* __restrict__ out_re,
+    float* __restrict__ out_im, const float2* __restrict__ tw, long long outer, int stride, int groups,
+    float scale) {
+  constexpr int E = lds_epth(N1), T = N1 / E, THREADS = C * T;
+  constexpr int PADN = lds_pad(N1) + 1;
+  __shared__ float2 lds[C * PADN];
+  const long long o0 = (long long)blockIdx.x * groups;  // first block of the tile
+  const int ng = (int)(outer - o0 < groups ? outer - o0 : groups);
+  const int blk = N1 * stride;    // floats per block
+  const int count = ng * blk;     // floats per plane in the tile (< 2^24: C * N1 <= 2^18)
+  const size_t g0 = (size_t)o0 * blk;
+  const float rs = 1.0f / (float)stride;
+  const float rb = 1.0f / (float)blk;
+  for (int i = threadIdx.x; i < count; i += THREADS) {
+    int rem, col;
+    const int g = divmod_small(i, blk, rb, rem);
+    const int j = divmod_small(rem, stride, rs, col);
+    const float xr = ld_stream(in_re + g0 + i);
+    const float xi = REAL_IN ? 0.0f : ld_stream(in_im + g0 + i);
+    lds[(g * stride + col) * PADN + lds_pad(j)] = make_float2(xr, xi);
+  }
+  __syncthreads();
+  const int c = threadIdx.x % C, t = threadIdx.x / C;  // columns past the tile's ng*stride: stale, never stored
+  float2* base = lds + c * PADN;
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = base[lds_pad(t + T * e)];
+  __syncthreads();  // the column area becomes the transform's exchange area
+  LdsFft<N1, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(base), nullptr, tw, t);
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < E; ++e) base[lds_pad(t + T * e)] = cscale(v[e], scale);
+  __syncthreads();
+  for (int i = threadIdx.x; i < count; i += THREADS) {
+    int rem, col;
+    const int g = divmod_small(i, blk, rb, rem);
+    const int j = divmod_small(rem, stride, rs, col);
+    const float2 y = lds[(g * stride + col) * PADN + lds_pad(j)];
+    st_stream(out_re + g0 + i, y.x);
+    st_stream(out_im + g0 + i, y.y);
+  }
+}
+
 template <int N1, int DIR>
 static hipError_t launch_strided_t(const StridedArgs& a) {
   constexpr int C = fourstep_tile(N1), T = N1 / lds_epth(N1);
+  if (2 * a.stride <= C) {
+    const int groups = (int)(C / a.stride);
+    const long long blocks = (a.outer + groups - 1) / groups;
+    if (a.in_im == nullptr)
+      hipLaunchKernelGGL((strided_small_kernel<N1, DIR, true>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream,
+                         a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.outer, (int)a.stride, groups, a.scale);
+    else
+      hipLaunchKernelGGL((strided_small_kernel<N1, DIR, false>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream,
+                         a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.outer, (int)a.stride, groups, a.scale);
+    return hipGetLastError();
+  }
   const long long tiles = (a.stride + C - 1) / C;
   const long long blocks = a.outer * tiles;
   if (a.in_im == nullptr)
