@@ -40,7 +40,9 @@ CASES = [
     (16, 4, 50, True, False, None),
     (4096, 1024, 7, True, False, None),
     (2048, 512, 5, False, True, None),
-    (512, 40, 30, True, False, None),        # long halo (12 frames)
+    (512, 40, 30, True, False, None),        # long halo (12 frames): the widest tile
+    (1024, 128, 40, True, False, None),      # halo 7 > half the measured 8-frame tile: widest tile
+    (32, 16, 300, True, False, None),
 ]
 
 

@@ -72,11 +72,12 @@ __host__ __device__ constexpr bool fft2_small_ok(long long h, long long w) {
 __host__ __device__ constexpr int blue_epth(int m) { return m == 2048 ? 8 : lds_epth(m); }
 __host__ __device__ constexpr int blue_threads(int m) { return m == 2048 ? 512 : 256; }
 
-// Elements per thread of the inverse-STFT pair transforms: one wavefront per transform up to
-// n = 1024 (wave-local exchanges), E = 32 at 4096.
-__host__ __device__ constexpr int istft_epth(int n) {
-  return n <= 16 ? n : n <= 64 ? 8 : n <= 256 ? 16 : n <= 512 ? 8 : n <= 2048 ? 16 : 32;
-}
+// Inverse-STFT launch shape from a sweep on MI355X (64 x 160000 samples, hop n/2, n_fft 16..4096,
+// E in {4, 8, 16} x 128..1024 threads): E = 8 elements per thread up to n = 2048, 16 at 4096;
+// 256 threads per workgroup up to n = 64, 512 up to 1024, 1024 above (n = 16: 64 -> 45 us,
+// 256: 65 -> 48, 1024: 73 -> 63, 4096: 122 -> 100 against the former shapes).
+__host__ __device__ constexpr int istft_epth(int n) { return n <= 2048 ? 8 : 16; }
+__host__ __device__ constexpr int istft_threads(int n) { return n <= 64 ? 256 : n <= 1024 ? 512 : 1024; }
 
 // Elements per thread of the four-step passes over transforms of length l (128..4096): 32 threads
 // per transform up to l = 1024 (one 32-transform tile = 1024 threads), 32 elements above.

@@ -20,9 +20,9 @@
 
 namespace tfa {
 
-// Frame pairs per workgroup: 512 threads (n_fft 512: 8 pairs, 16 frames) measured fastest; more
-// frames per workgroup cost LDS (fewer resident workgroups) without shortening the gather.
-template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = 512 / (NFFT / E_) < 1 ? 1 : 512 / (NFFT / E_)>
+// MAXP caps the frame pairs per workgroup (istft_threads(NFFT) / T in the measured shape; more
+// frames per workgroup cost LDS and resident workgroups without shortening the gather).
+template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = istft_threads(NFFT) / (NFFT / E_)>
 struct IstftCfg {
   static constexpr int E = E_;
   static constexpr int T = NFFT / E;
@@ -36,7 +36,7 @@ struct IstftCfg {
   static_assert(PAIRS >= 1 && RP >= 4 * F && RP >= 2 * NFFT, "istft tile");
 };
 
-template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = 512 / (NFFT / E_) < 1 ? 1 : 512 / (NFFT / E_)>
+template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = istft_threads(NFFT) / (NFFT / E_)>
 __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_kernel(
     const float* __restrict__ sre, const float* __restrict__ sim, const float* __restrict__ win,
     float* __restrict__ out, const float2* __restrict__ tw, int n_frames, int hop, int halo, int owned,
@@ -122,30 +122,46 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
     for (int o = write_len + (int)threadIdx.x; o < out_pitch; o += THREADS) dst[o] = 0.0f;
 }
 
-template <int NFFT>
-static hipError_t launch_istft_n(const IstftArgs& a) {
-  using C = IstftCfg<NFFT>;
+template <int NFFT, int MAXP>
+static hipError_t launch_istft_cfg(const IstftArgs& a) {
+  using C = IstftCfg<NFFT, istft_epth(NFFT), MAXP>;
   const int owned = C::FR - a.halo;
   if (owned < 1) return hipErrorInvalidValue;
   const int tiles = (a.n_frames + owned - 1) / owned;
   const long long blocks = a.batch * (long long)tiles;
-  hipLaunchKernelGGL((istft_kernel<NFFT>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream, a.spec_re,
-                     a.spec_im, a.window, a.out, a.tw, a.n_frames, a.hop, a.halo, owned, tiles, (int)a.expected_len,
-                     (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale);
+  hipLaunchKernelGGL((istft_kernel<NFFT, istft_epth(NFFT), MAXP>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
+                     a.stream, a.spec_re, a.spec_im, a.window, a.out, a.tw, a.n_frames, a.hop, a.halo, owned, tiles,
+                     (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale);
   return hipGetLastError();
+}
+
+// The measured shape, unless the hop is so short that the recomputed halo frames would be half
+// its tile or more: then the widest tile (1024 threads, as LDS allows), same elements per thread.
+template <int NFFT>
+static hipError_t launch_istft_n(const IstftArgs& a) {
+  constexpr int T = NFFT / istft_epth(NFFT);
+  constexpr int FAST = istft_threads(NFFT) / T, WIDE = 1024 / T;
+  if (2 * a.halo <= IstftCfg<NFFT, istft_epth(NFFT), FAST>::FR) return launch_istft_cfg<NFFT, FAST>(a);
+  return launch_istft_cfg<NFFT, WIDE>(a);
+}
+
+// frames per tile of the widest shape: the hop bound the plan checks
+template <int NFFT>
+constexpr int istft_wide_fr() {
+  return IstftCfg<NFFT, istft_epth(NFFT), 1024 / (NFFT / istft_epth(NFFT))>::FR;
 }
 
 int istft_frames_per_tile(int n_fft) {
   switch (n_fft) {
-    case 16: return IstftCfg<16>::FR;
-    case 32: return IstftCfg<32>::FR;
-    case 64: return IstftCfg<64>::FR;
-    case 128: return IstftCfg<128>::FR;
-    case 256: return IstftCfg<256>::FR;
-    case 512: return IstftCfg<512>::FR;
-    case 1024: return IstftCfg<1024>::FR;
-    case 2048: return IstftCfg<2048>::FR;
-    case 4096: return IstftCfg<4096>::FR;
+    case 16: return istft_wide_fr<16>();
+    case 32: return istft_wide_fr<32>();
+    case 64: return istft_wide_fr<64>();
+    case 128: return istft_wide_fr<128>();
+    case 256: return istft_wide_fr<256>();
+    case 512: return istft_wide_fr<512>();
+    case 1024: return istft_wide_fr<1024>();
+    case 2048: return istft_wide_fr<2048>();
+    case 4096: return istft_wide_fr<4096>();
     default: return 0;
   }
 }
