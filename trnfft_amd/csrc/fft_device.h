@@ -195,14 +195,17 @@ __device__ __forceinline__ void exchange_sync() {
 // IL: `lre` holds lds_pad(N) interleaved float2 (re, im) entries (lim unused): one 64-bit LDS
 // access per element instead of two 32-bit ones (gfx950 serves a 64-lane ds_read_b64 of
 // consecutive float2 in the cycles of a ds_read_b32, so this halves LDS time as well).
-template <int N, int E, int DIR, bool WAVE_LOCAL, bool SPLIT = false, bool IL = false>
+// PF: each pass requests the next pass's twiddles before its exchange barriers, so their table
+// latency overlaps the exchange instead of following it (E/2 float4 more registers live there).
+template <int N, int E, int DIR, bool WAVE_LOCAL, bool SPLIT = false, bool IL = false, bool PF = false>
 struct LdsFft {
   static constexpr LdsShape S = make_shape(N, E);
   static constexpr int T = N / E;
+  static constexpr int TQ = PF ? (E / 2 > 0 ? E / 2 : 1) : 1;  // float4 twiddles per thread per pass
 
   template <int P>
   __device__ __forceinline__ static void pass(float2 (&v)[E], float* lre, float* lim,
-                                              const float2* __restrict__ tw, int tid) {
+                                              const float2* __restrict__ tw, int tid, const float4 (&tc)[TQ]) {
     if constexpr (P < S.npass) {
       constexpr int R = S.radix[P];
       constexpr int NB = E / R;
@@ -222,7 +225,7 @@ struct LdsFft {
           const float4* t4 = reinterpret_cast<const float4*>(tw + S.twoff[P] + k * R);
 #pragma unroll
           for (int r2 = 0; r2 < R / 2; ++r2) {
-            float4 q = t4[r2];
+            float4 q = PF ? tc[PF ? b * (R / 2) + r2 : 0] : t4[r2];
             if (r2 > 0) w[b][2 * r2] = cmul(w[b][2 * r2], make_float2(q.x, q.y));
             w[b][2 * r2 + 1] = cmul(w[b][2 * r2 + 1], make_float2(q.z, q.w));
           }
@@ -236,6 +239,17 @@ struct LdsFft {
         }
       }
       if constexpr (!LAST) {
+        float4 tn[TQ];
+        if constexpr (PF) {
+          constexpr int R1 = S.radix[P + 1], NB1 = E / R1, LS1 = S.ls[P + 1];
+#pragma unroll
+          for (int b = 0; b < NB1; ++b) {
+            const int k1 = (tid + b * T) & (LS1 - 1);
+            const float4* t4 = reinterpret_cast<const float4*>(tw + S.twoff[P + 1] + k1 * R1);
+#pragma unroll
+            for (int r2 = 0; r2 < R1 / 2; ++r2) tn[b * (R1 / 2) + r2] = t4[r2];
+          }
+        }
         if constexpr (!SPLIT) {
           exchange_sync<WAVE_LOCAL>();
           load_pass(v, lre, lim, tid, IL ? 3 : 2);
@@ -253,7 +267,7 @@ struct LdsFft {
             exchange_sync<WAVE_LOCAL>();
           }
         }
-        pass<P + 1>(v, lre, lim, tw, tid);
+        pass<P + 1>(v, lre, lim, tw, tid, tn);
       }
     }
   }
@@ -321,7 +335,8 @@ struct LdsFft {
 
   __device__ __forceinline__ static void run(float2 (&v)[E], float* lre, float* lim,
                                              const float2* __restrict__ tw, int tid) {
-    pass<0>(v, lre, lim, tw, tid);
+    const float4 none[TQ] = {};
+    pass<0>(v, lre, lim, tw, tid, none);
   }
 };
 

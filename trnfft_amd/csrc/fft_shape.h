@@ -35,6 +35,10 @@ __host__ __device__ constexpr int c2c_epth(int n) {
 // Interleaved (re, im) LDS exchange (one 64-bit access per element) in the batched c2c kernel:
 // measured 1-4 % faster at most lengths (identical results), 2-4 % slower at 512 and 8192.
 __host__ __device__ constexpr bool c2c_il(int n) { return n != 512 && n != 8192; }
+// Next-pass twiddle prefetch (LdsFft PF) where one or two transforms fill a workgroup and the
+// table latency after each exchange is exposed: N = 16384 21.2 -> 18.8 us; at high occupancy it
+// costs registers and time (N = 1024: 12.7 -> 15.3 us), so it is off below 8192.
+__host__ __device__ constexpr bool c2c_pf(int n) { return n >= 8192; }
 __host__ __device__ constexpr int c2c_threads(int n) {
   return n == 64 || n == 256 ? 1024 : (n == 128 || n == 1024 || n == 2048 || n == 4096 || n == 16384) ? 512 : 256;
 }
@@ -67,10 +71,12 @@ __host__ __device__ constexpr bool fft2_small_ok(long long h, long long w) {
 }
 
 // Fused Bluestein launch shape.  m = 2048 (n = 1000): E = 8 with 512-thread workgroups measured
-// 16.2 -> 14.7 us against the batched-c2c shape (E = 16, 256 threads); other lengths keep the
-// latter (m = 16384: E = 16 and E = 32 within 2 %).
-__host__ __device__ constexpr int blue_epth(int m) { return m == 2048 ? 8 : lds_epth(m); }
-__host__ __device__ constexpr int blue_threads(int m) { return m == 2048 ? 512 : 256; }
+// 16.2 -> 14.7 us against the batched-c2c shape (E = 16, 256 threads).  m >= 8192 (one row per
+// workgroup, latency-bound): E = 32 / 512 threads with the next-pass twiddle prefetch, m = 16384
+// 30.5 -> 26.9 us against E = 16 without it.  Other lengths keep the batched-c2c shape.
+__host__ __device__ constexpr int blue_epth(int m) { return m == 2048 ? 8 : m >= 8192 ? 32 : lds_epth(m); }
+__host__ __device__ constexpr int blue_threads(int m) { return m == 2048 || m >= 8192 ? 512 : 256; }
+__host__ __device__ constexpr bool blue_pf(int m) { return m >= 8192; }
 
 // Inverse-STFT launch shape from a sweep on MI355X (64 x 160000 samples, hop n/2, n_fft 16..4096,
 // E in {4, 8, 16} x 128..1024 threads): E = 8 elements per thread up to n = 2048, 16 at 4096;

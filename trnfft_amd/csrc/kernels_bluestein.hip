@@ -70,10 +70,11 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
     v[e] = y;
   }
   float* my = reinterpret_cast<float*>(lds + xf * C::PADN);
-  LdsFft<M, E, -1, (T <= 64), false, true>::run(v, my, my, tw_f, tid);
+  constexpr bool PF = blue_pf(M);
+  LdsFft<M, E, -1, (T <= 64), false, true, PF>::run(v, my, nullptr, tw_f, tid);
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = cmul(v[e], PRE ? hv[PRE ? e : 0] : hs[tid + T * e]);
-  LdsFft<M, E, 1, (T <= 64), false, true>::run(v, my, my, tw_i, tid);
+  LdsFft<M, E, 1, (T <= 64), false, true, PF>::run(v, my, nullptr, tw_i, tid);
   if (valid) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {

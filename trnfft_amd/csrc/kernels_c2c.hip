@@ -52,11 +52,14 @@ __global__ __launch_bounds__((C2cThreads<N, E_, THR>::THREADS)) void c2c_lds_ker
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = make_float2(0.0f, 0.0f);
   }
+  constexpr bool PF = c2c_pf(N);
   if constexpr (IL) {
-    LdsFft<N, E, DIR, (T <= 64), false, true>::run(v, reinterpret_cast<float*>(lds + xf * C::PADN), nullptr, tw, tid);
+    LdsFft<N, E, DIR, (T <= 64), false, true, PF>::run(v, reinterpret_cast<float*>(lds + xf * C::PADN), nullptr, tw,
+                                                      tid);
   } else {
     float* planes = reinterpret_cast<float*>(lds);
-    LdsFft<N, E, DIR, (T <= 64)>::run(v, planes + xf * C::PADN, planes + (C::XF + xf) * C::PADN, tw, tid);
+    LdsFft<N, E, DIR, (T <= 64), false, false, PF>::run(v, planes + xf * C::PADN, planes + (C::XF + xf) * C::PADN, tw,
+                                                       tid);
   }
   if (valid) {
     float* qr = out_re + base + tid;
