@@ -15,8 +15,10 @@ from trnfft_amd import ComplexTensor
 pytestmark = pytest.mark.gpu
 
 # (n, batch): batches not a multiple of the transforms per workgroup exercise the tail launch
-CASES = [(4, 300), (8, 257), (16, 33), (32, 65), (64, 7), (128, 5), (256, 3), (512, 3), (1024, 5),
-         (2048, 3), (4096, 2), (8192, 2), (16384, 1), (32768, 2)]
+# (n <= 64 run one row per thread with 256-row staging tiles: 300, 257, 1000 and 513 rows leave
+# a partial tile after full ones)
+CASES = [(4, 300), (8, 257), (16, 33), (16, 1000), (32, 65), (64, 7), (64, 513), (128, 5), (256, 3), (512, 3),
+         (1024, 5), (2048, 3), (4096, 2), (8192, 2), (16384, 1), (32768, 2)]
 
 
 @pytest.mark.parametrize("n,batch", CASES)

@@ -50,6 +50,8 @@ __host__ __device__ constexpr int c2c_threads(int n) {
 __host__ __device__ constexpr int real_epth(int h, bool inverse) {
   return h <= 2 ? h : h >= 8192 ? 32 : (h <= (inverse ? 64 : 256)) ? 4 : 8;
 }
+// next-pass twiddle prefetch for the real-row kernels where a workgroup holds one row (h >= 8192)
+__host__ __device__ constexpr bool real_pf(int h) { return h >= 8192; }
 
 // Elements per thread of the forward STFT's pair transforms (many lanes per transform measured
 // fastest at every n_fft).
