@@ -95,6 +95,20 @@ def test_dft_gemm_vs_oracle(n, inverse):
     assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(n), (n, inverse)
 
 
+def test_config5b_full_size_both_formulations():
+    # BASELINE config 5b at full size (65536 x 256, forward): the DFT-as-GEMM on the matrix cores
+    # and the Stockham kernel, each against the oracle on all rows
+    from trnfft_amd import fft_core as fc
+
+    re, im = seeded_complex(65536, 256)
+    x = ComplexTensor(re.cuda(), im.cuda())
+    ref = oracle.fft_core(re, im, False)
+    gemm = fc._fft_via_gemm(x, False)
+    assert rel_l2(gemm.real, gemm.imag, *ref) <= tol_pow2(256)
+    stockham = trnfft_amd.fft(x)
+    assert rel_l2(stockham.real, stockham.imag, *ref) <= tol_pow2(256)
+
+
 def test_dft_gemm_threshold_routing():
     from trnfft_amd import fft_core as fc
 
