@@ -96,8 +96,9 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
 /*
  * Batched 1-D transform along a strided axis, in place allowed: data viewed as (outer, n, stride)
  * row-major, each of the outer*stride columns transformed along its n elements (element stride
- * `stride`).  TFA_KIND_C2C plans with n <= 4096 only.  Replaces the transpose-copy + contiguous
- * FFT + transpose-back of trnfft/api.py:496-516 (_fft_along_dim) used by fft2/fftn/ifftn.
+ * `stride`).  TFA_KIND_C2C plans with n <= 4096, or TFA_KIND_BLUESTEIN plans with n <= 2048
+ * (padded length m <= 4096).  Replaces the transpose-copy + contiguous FFT + transpose-back of
+ * trnfft/api.py:496-516 (_fft_along_dim) used by fft2/fftn/ifftn.
  */
 int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, const float* in_re,
                         const float* in_im, float* out_re, float* out_im, tfa_stream stream);

@@ -96,6 +96,42 @@ def test_fft_along_axis_with_few_trailing_columns(shape):
     assert _np_rel(got, np.fft.fft(re.astype(np.float64), axis=1)) <= tol_pow2(n), shape
 
 
+# non-power-of-two axes along a strided dimension (Bluestein in place down the columns, padded
+# length m <= 4096): against numpy float64 and against the last-axis Bluestein path on the moved
+# axis (same chirp and filter, so the two agree far inside the parity tolerance)
+@pytest.mark.parametrize("shape", [(3, 3, 70), (2, 5, 3), (4, 12, 16), (3, 17, 33), (2, 100, 64), (2, 480, 40),
+                                   (2, 1000, 8), (1, 2047, 5), (2, 2000, 100)])
+def test_non_pow2_axis_strided_bluestein(shape):
+    from trnfft_amd.fft_core import strided_ok
+
+    rng = np.random.default_rng(17)
+    re = rng.standard_normal(shape).astype(np.float32)
+    im = rng.standard_normal(shape).astype(np.float32)
+    n, stride = shape[1], shape[2]
+    assert strided_ok(n, stride)
+    x = ComplexTensor(torch.from_numpy(re).cuda(), torch.from_numpy(im).cuda())
+    z = re.astype(np.float64) + 1j * im
+    for inverse in (False, True):
+        got = trnfft_amd.ifftn(x, dim=(1,)) if inverse else trnfft_amd.fftn(x, dim=(1,))
+        ref = np.fft.ifft(z, axis=1) if inverse else np.fft.fft(z, axis=1)
+        assert _np_rel(got, ref) <= 3 * tol_bluestein(n), (shape, inverse)
+        moved = ComplexTensor(x.real.transpose(1, 2).contiguous(), x.imag.transpose(1, 2).contiguous())
+        last = trnfft_amd.ifft(moved) if inverse else trnfft_amd.fft(moved)
+        assert rel_l2(got.real, got.imag, last.real.transpose(1, 2), last.imag.transpose(1, 2)) <= 1e-5, shape
+    got = trnfft_amd.fftn(torch.from_numpy(re).cuda(), dim=(1,))
+    assert _np_rel(got, np.fft.fft(re.astype(np.float64), axis=1)) <= 3 * tol_bluestein(n), shape
+
+
+def test_fft2_non_pow2_image():
+    # 480 x 640: the 640 axis runs the contiguous Bluestein kernel, the 480 axis the strided one
+    rng = np.random.default_rng(19)
+    x = rng.standard_normal((2, 480, 640)).astype(np.float32)
+    got = trnfft_amd.fft2(torch.from_numpy(x).cuda())
+    assert _np_rel(got, np.fft.fft2(x.astype(np.float64))) <= 3 * tol_bluestein(640)
+    back = trnfft_amd.ifftn(got, dim=(-2, -1))
+    assert rel_l2(back.real, back.imag, torch.from_numpy(x), torch.zeros(2, 480, 640)) <= 6 * tol_bluestein(640)
+
+
 @pytest.mark.parametrize("n_in,n", [(100, 128), (300, 256), (1000, 1000), (64, 100), (4096, 4000)])
 def test_fft_ifft_n_param(n_in, n):
     rng = np.random.default_rng(5)

@@ -112,6 +112,24 @@ struct BluesteinArgs {
 };
 hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a);
 
+// Bluestein down a strided axis (x viewed as (outer, n, stride)), m <= kMaxStridedBlueM.
+constexpr int kMaxStridedBlueM = 4096;
+struct StridedBlueArgs {
+  const float* in_re;
+  const float* in_im;  // nullptr: real input
+  float* out_re;       // may equal in_re (in place)
+  float* out_im;
+  const float2* chirp;  // n entries
+  const float2* hs;     // FFT_m(h) / m, m entries
+  const float2* tw_f;   // LDS-FFT tables for length m in the lds_epth(m) layout
+  const float2* tw_i;
+  long long outer, stride;
+  int n;
+  float scale;
+  hipStream_t stream;
+};
+hipError_t launch_strided_bluestein(int m, const StridedBlueArgs& a);
+
 // Split (transposed-domain four-step) Bluestein, m = m1 * m2 >= 16384.
 struct BlueSplitArgs {
   const float* in_re;

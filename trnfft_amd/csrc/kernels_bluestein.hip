@@ -103,6 +103,87 @@ static hipError_t launch_blue_m(const BluesteinArgs& a) {
   return hipGetLastError();
 }
 
+// Bluestein down a strided axis: x viewed as (outer, n, S); every column of n elements at stride
+// S runs the fused kernel's steps (chirp, zero padding to M, FFT_M, times H/M, IFFT_M, chirp,
+// scale) in LDS, C adjacent columns per workgroup so each access instruction covers C consecutive
+// floats.  Replaces the transpose round trip of trnfft/api.py:496-516 for non-power-of-two axes.
+template <int M, bool REAL_IN, int C = fourstep_tile(M)>
+__global__ __launch_bounds__(C * (M / lds_epth(M))) void strided_blue_kernel(
+    const float* in_re, const float* in_im, float* out_re, float* out_im, const float2* __restrict__ chirp,
+    const float2* __restrict__ hs, const float2* __restrict__ tw_f, const float2* __restrict__ tw_i, long long stride,
+    int tiles_per_block, int n, float scale) {
+  // in place is allowed: a workgroup reads all of its columns before its first barrier and no
+  // other workgroup touches them
+  constexpr int E = lds_epth(M), T = M / E;
+  constexpr int PADN = lds_pad(M) + 1;
+  __shared__ float2 lds[C * PADN];  // interleaved (re, im) exchange, one column per region
+  const int c = threadIdx.x % C;  // column within the tile (fast across lanes)
+  const int t = threadIdx.x / C;
+  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
+  const long long b = tile / tiles_per_block;
+  const long long col = (tile % tiles_per_block) * C + c;
+  const bool valid = col < stride;
+  const size_t base = (size_t)b * n * stride + col;
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = t + T * e;
+    float2 y = make_float2(0.0f, 0.0f);
+    if (valid && i < n) {
+      const size_t s = base + (size_t)i * stride;
+      y = cmul(make_float2(in_re[s], REAL_IN ? 0.0f : in_im[s]), chirp[i]);
+    }
+    v[e] = y;
+  }
+  float* my = reinterpret_cast<float*>(lds + c * PADN);
+  LdsFft<M, E, -1, false, false, true>::run(v, my, nullptr, tw_f, t);
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], hs[t + T * e]);
+  LdsFft<M, E, 1, false, false, true>::run(v, my, nullptr, tw_i, t);
+  if (!valid) return;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = t + T * e;
+    if (i < n) {
+      const float2 y = cmul(v[e], chirp[i]);
+      const size_t o = base + (size_t)i * stride;
+      out_re[o] = y.x * scale;  // plain stores: row segments of C floats (L2 merges partial lines)
+      out_im[o] = y.y * scale;
+    }
+  }
+}
+
+template <int M>
+static hipError_t launch_strided_blue_m(const StridedBlueArgs& a) {
+  constexpr int C = fourstep_tile(M), T = M / lds_epth(M);
+  const long long tiles = (a.stride + C - 1) / C;
+  const long long blocks = a.outer * tiles;
+  if (a.in_im == nullptr)
+    hipLaunchKernelGGL((strided_blue_kernel<M, true>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream, a.in_re,
+                       a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i, a.stride, (int)tiles, a.n, a.scale);
+  else
+    hipLaunchKernelGGL((strided_blue_kernel<M, false>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream, a.in_re,
+                       a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i, a.stride, (int)tiles, a.n, a.scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_strided_bluestein(int m, const StridedBlueArgs& a) {
+  switch (m) {
+    case 4: return launch_strided_blue_m<4>(a);
+    case 8: return launch_strided_blue_m<8>(a);
+    case 16: return launch_strided_blue_m<16>(a);
+    case 32: return launch_strided_blue_m<32>(a);
+    case 64: return launch_strided_blue_m<64>(a);
+    case 128: return launch_strided_blue_m<128>(a);
+    case 256: return launch_strided_blue_m<256>(a);
+    case 512: return launch_strided_blue_m<512>(a);
+    case 1024: return launch_strided_blue_m<1024>(a);
+    case 2048: return launch_strided_blue_m<2048>(a);
+    case 4096: return launch_strided_blue_m<4096>(a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a) {
   switch (m) {
     case 4: return launch_blue_m<4>(a);

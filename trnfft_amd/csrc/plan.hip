@@ -86,6 +86,7 @@ struct tfa_plan {
   float2 *b_lo = nullptr, *b_hi = nullptr, *b_hp = nullptr;
   float2* chirp = nullptr;
   float2* hs = nullptr;
+  float2 *b_tw_sf = nullptr, *b_tw_si = nullptr;  // Bluestein m <= 4096: strided-axis kernel tables
   C2cTables col;          // FFT2: LDS table for n2/8 (pass 2)
   float2* tw_h = nullptr;  // FFT2: W_{n2}^i, i < n2
   float2* tw_w_pair = nullptr;  // FFT2: row table in the paired-real-row layout
@@ -269,6 +270,15 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         p->inv.dir = 1;
         if ((rc = p->upload(lds_table((int)m, -1, tfa::blue_epth((int)m)), &p->fwd.tw))) break;
         if ((rc = p->upload(lds_table((int)m, 1, tfa::blue_epth((int)m)), &p->inv.tw))) break;
+        if (m <= tfa::kMaxStridedBlueM) {  // the strided-axis kernel's layout (tfa::lds_epth)
+          if (tfa::blue_epth((int)m) == tfa::lds_epth((int)m)) {
+            p->b_tw_sf = p->fwd.tw;
+            p->b_tw_si = p->inv.tw;
+          } else {
+            if ((rc = p->upload(lds_table((int)m, -1), &p->b_tw_sf))) break;
+            if ((rc = p->upload(lds_table((int)m, 1), &p->b_tw_si))) break;
+          }
+        }
       }
       const std::vector<float2> chirp = reference_chirp(n, dir);
       // h = conj(chirp) circularly wrapped (trnfft/fft_core.py:1337-1345); H = FFT_m(h) / m
@@ -498,13 +508,22 @@ int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, con
                         const float* in_im, float* out_re, float* out_im, tfa_stream stream) {
   if (!plan) return fail(TFA_ERR_INVALID, "null plan");
   if (outer < 0 || stride < 1) return fail(TFA_ERR_INVALID, "bad outer/stride");
-  if (plan->d.kind != TFA_KIND_C2C || plan->d.n > 4096 || plan->d.n < 2)
-    return fail(TFA_ERR_UNSUPPORTED, "strided transforms need a power-of-two C2C plan with 2 <= n <= 4096");
+  const bool blue = plan->d.kind == TFA_KIND_BLUESTEIN && plan->m <= tfa::kMaxStridedBlueM;
+  if (!blue && (plan->d.kind != TFA_KIND_C2C || plan->d.n > 4096 || plan->d.n < 2))
+    return fail(TFA_ERR_UNSUPPORTED,
+                "strided transforms need a power-of-two C2C plan with 2 <= n <= 4096 or a Bluestein plan with n <= 2048");
   if (outer == 0) return TFA_OK;
   if (!in_re || !out_re || !out_im) return fail(TFA_ERR_INVALID, "null data pointer");
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
     return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  if (blue) {
+    const float bscale = plan->d.inverse ? (float)(1.0 / (double)plan->d.n) : 1.0f;
+    tfa::StridedBlueArgs ba{in_re, in_im, out_re, out_im, plan->chirp, plan->hs, plan->b_tw_sf, plan->b_tw_si,
+                            outer, stride, (int)plan->d.n, bscale, static_cast<hipStream_t>(stream)};
+    hipError_t be = tfa::launch_strided_bluestein((int)plan->m, ba);
+    return be == hipSuccess ? TFA_OK : hip_fail(be, "strided Bluestein launch");
+  }
   const C2cTables& t = plan->d.inverse ? plan->inv : plan->fwd;
   const float scale = plan->d.inverse ? (float)(1.0 / (double)plan->d.n) : 1.0f;
   tfa::StridedArgs a{in_re, in_im, out_re, out_im, t.tw_lds, outer, stride, scale, t.dir,

@@ -130,12 +130,15 @@ def execute_c2r(re: torch.Tensor, im: torch.Tensor, n: int) -> torch.Tensor:
     return out if out_dev == dev else out.to(out_dev)
 
 
-# longest power-of-two axis the strided kernel transforms in place of a transpose round trip
+# longest power-of-two axis the strided kernel transforms in place of a transpose round trip, and
+# longest other axis (Bluestein padded length m <= 4096)
 _STRIDED_MAX_N = 4096
+_STRIDED_BLUE_MAX_N = 2048
 
 
 def execute_strided(re: torch.Tensor, im: torch.Tensor | None, dim: int, inverse: bool) -> ComplexTensor:
-    """Transform along a non-last axis `dim` without moving it (power-of-two n <= 4096).
+    """Transform along a non-last axis `dim` without moving it (power-of-two n <= 4096, other
+    n <= 2048 through the strided Bluestein kernel).
 
     The contiguous tensor is viewed as (outer, n, stride); every column is transformed along
     its n elements by the strided kernel (replaces trnfft/api.py:496-516's transposes).
@@ -152,7 +155,8 @@ def execute_strided(re: torch.Tensor, im: torch.Tensor | None, dim: int, inverse
     stride = 1
     for s_ in shape[dim + 1 :]:
         stride *= s_
-    plan = native_plan(_lib.KIND_C2C, n, inverse, dev.index)
+    kind = _lib.KIND_C2C if (n & (n - 1)) == 0 else _lib.KIND_BLUESTEIN
+    plan = native_plan(kind, n, inverse, dev.index)
     out_re = torch.empty_like(re)
     out_im = torch.empty_like(re)
     with torch.cuda.device(dev):
@@ -232,7 +236,11 @@ def execute_stft(x: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int, cente
 
 
 def strided_ok(n: int, stride: int) -> bool:
-    return 2 <= n <= _STRIDED_MAX_N and (n & (n - 1)) == 0 and stride >= 1
+    if stride < 1 or n < 2:
+        return False
+    if (n & (n - 1)) == 0:
+        return n <= _STRIDED_MAX_N
+    return n <= _STRIDED_BLUE_MAX_N
 
 
 def _fft_via_gemm(x: ComplexTensor, inverse: bool) -> ComplexTensor:
