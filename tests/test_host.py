@@ -97,6 +97,11 @@ def test_precision_modes():
     assert _resolve(None) == "fast"
     with pytest.raises(NotImplementedError):
         _resolve("double")
+    # the reference's Ozaki toggle exists (trnfft/__init__.py:66); the modes stay unsupported
+    trnfft_amd.set_ozaki_product_precision_verified(True)
+    with pytest.raises(NotImplementedError):
+        _resolve("ozaki")
+    trnfft_amd.set_ozaki_product_precision_verified(False)
 
 
 class TestComplexTensor:

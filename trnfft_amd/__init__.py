@@ -28,7 +28,7 @@ from .api import (
 from .complex import ComplexTensor, complex_matmul
 from .dispatch import HAS_HIP, complex_gemm, complex_linear, get_backend, set_backend
 from .plan import FFTAlgorithm, FFTPlan, clear_plan_cache, create_plan
-from .precision import get_precision, set_precision
+from .precision import get_precision, set_ozaki_product_precision_verified, set_precision
 
 __all__ = [
     "fft",
@@ -58,5 +58,6 @@ __all__ = [
     "set_backend",
     "get_backend",
     "set_precision",
+    "set_ozaki_product_precision_verified",
     "get_precision",
 ]

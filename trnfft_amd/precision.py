@@ -26,6 +26,18 @@ def get_precision() -> str:
     return _precision
 
 
+_ozaki_product_precision_verified = False
+
+
+def set_ozaki_product_precision_verified(verified: bool = True) -> None:
+    """Interface of trnfft/fft_core.py:186-197 (declares that the matrix units multiply bf16
+    pairs at fp32 precision, enabling the reference's "ozaki" modes).  Recorded for callers that
+    set it; the Ozaki modes themselves are Trainium experiments that this backend does not run
+    (``_resolve`` raises NotImplementedError for them either way)."""
+    global _ozaki_product_precision_verified
+    _ozaki_product_precision_verified = bool(verified)
+
+
 def _resolve(precision) -> str:
     """Per-call override against the global (trnfft/precision.py:88-94), restricted to "fast"."""
     if precision is None:
