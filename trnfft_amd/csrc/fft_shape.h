@@ -26,10 +26,11 @@ __host__ __device__ constexpr int lds_epth(int n) {
 // sweep on MI355X over E in {4, 8, 16, 32} and 256..1024 threads at 4M complex elements per
 // launch, buffers rotated past the Infinity Cache.  Headline N = 1024: E = 8 / 512 threads,
 // 13.12 us against 13.64 us for the former E = 16 / 256.  Other lengths (us, new vs former):
-// 64 15.3 vs 20.7, 128 14.8 vs ~16, 256 14.2 vs ~15, 4096 14.2 vs 16.5, 8192 16.2 vs 19.0,
-// 16384 22.3 vs 24.6; 512 and 2048 unchanged within 1 %.
+// 128 14.8 vs ~16, 256 14.2 vs ~15, 4096 14.2 vs 16.5, 8192 16.2 vs 19.0, 16384 22.3 vs 24.6;
+// 512 and 2048 unchanged within 1 %.  n <= 64 run the staged short-row kernel with n / c2c_epth
+// threads per row: E = 8 there (n = 16: 14.9 -> 12.6 us, 64: 15.6 -> 12.6 us against E = 16 / 4).
 __host__ __device__ constexpr int c2c_epth(int n) {
-  return n == 64 || n == 128 ? 4 : (n == 256 || n == 1024 || n == 2048 || n == 4096) ? 8
+  return n == 16 || n == 64 ? 8 : n == 128 ? 4 : (n == 256 || n == 1024 || n == 2048 || n == 4096) ? 8
          : (n == 8192 || n == 16384) ? 32 : lds_epth(n);
 }
 // Interleaved (re, im) LDS exchange (one 64-bit access per element) in the batched c2c kernel:

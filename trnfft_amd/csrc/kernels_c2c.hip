@@ -72,39 +72,57 @@ __global__ __launch_bounds__((C2cThreads<N, E_, THR>::THREADS)) void c2c_lds_ker
   }
 }
 
-// Short transforms (2 <= N <= 32): one thread per row, the whole transform in registers (the
-// in-register DFT with compile-time twiddles).  A thread per row would touch one cache line per
-// lane, so the workgroup's XS rows move between HBM and LDS as one contiguous run per plane:
-// every global access instruction covers 64 consecutive floats (N = 16, 4M elements: 169 us with
-// the row-per-thread loads of the LDS kernel, copy speed with this one).
-constexpr int kSmallRows = 256;
+// Short transforms (2 <= N <= 64): a few threads per row (one up to N = 16, the whole transform
+// an in-register DFT; N / c2c_epth(N) above, exchanging through the row's own LDS area inside a
+// wavefront).  Threads that each load their own row segment would touch one cache line per
+// lane (N <= 16) or half a line (N = 32, 64), so the workgroup's XS rows move between HBM and
+// LDS as one contiguous run per plane: every global access instruction covers 64 consecutive
+// floats (4M elements: N = 16 169 -> 15 us, N = 32 33 -> 12 us).
+template <int N>
+struct C2cSmallCfg {
+  static constexpr int TPR = N <= 8 ? 1 : N / c2c_epth(N);  // threads per row
+  static constexpr int XS = TPR <= 4 ? 256 : 1024 / TPR;     // rows per workgroup
+  static constexpr int E = N / TPR;
+  static constexpr int THREADS = XS * TPR;
+  // row pitch in float2: odd, and room for the exchange's padded indexing when TPR > 1
+  static constexpr int P = TPR == 1 ? N + 1 : lds_pad(N) + 1;
+  __device__ static constexpr int idx(int j) { return TPR == 1 ? j : lds_pad(j); }
+};
 
 template <int N, int DIR, bool REAL_IN, bool TAIL>
-__global__ __launch_bounds__(kSmallRows) void c2c_small_kernel(
+__global__ __launch_bounds__(C2cSmallCfg<N>::THREADS) void c2c_small_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re, float* out_im,
-    long long first, long long batch, float scale) {
-  constexpr int XS = kSmallRows, P = N + 1;  // odd row pitch: a column read hits distinct banks
+    const float2* __restrict__ tw, long long first, long long batch, float scale) {
+  using C = C2cSmallCfg<N>;
+  constexpr int XS = C::XS, P = C::P, TPR = C::TPR, E = C::E, THREADS = C::THREADS;
   __shared__ float2 lds[XS * P];
   const long long r0 = first + (long long)blockIdx.x * XS;
   const int count = TAIL ? (int)(batch - r0 < XS ? batch - r0 : XS) * N : XS * N;  // floats per plane
   const size_t g0 = (size_t)r0 * N;
   const float sc = DIR < 0 ? 1.0f : scale;  // inverse: 1/n applied on input (exact for powers of two)
-  for (int i = threadIdx.x; i < count; i += XS) {
+  for (int i = threadIdx.x; i < count; i += THREADS) {
     const float xr = ld_stream(in_re + g0 + i);
     const float xi = REAL_IN ? 0.0f : ld_stream(in_im + g0 + i);
-    lds[(i / N) * P + i % N] = make_float2(xr * sc, xi * sc);
+    lds[(i / N) * P + C::idx(i % N)] = make_float2(xr * sc, xi * sc);
   }
   __syncthreads();
-  float2 v[N];
-  float2* row = lds + threadIdx.x * P;  // rows past a ragged tail hold stale data, never stored
+  const int tid = threadIdx.x % TPR;
+  float2* row = lds + (threadIdx.x / TPR) * P;  // rows past a ragged tail hold stale data, never stored
+  float2 v[E];
 #pragma unroll
-  for (int k = 0; k < N; ++k) v[k] = row[k];
-  Dft<N, DIR>::run(v);
+  for (int e = 0; e < E; ++e) v[e] = row[C::idx(tid + TPR * e)];
+  if constexpr (TPR == 1) {
+    Dft<N, DIR>::run(v);
+  } else {
+    exchange_sync<true>();  // the row's area becomes its exchange area (one wavefront per row group)
+    LdsFft<N, E, DIR, true, false, true>::run(v, reinterpret_cast<float*>(row), nullptr, tw, tid);
+    exchange_sync<true>();
+  }
 #pragma unroll
-  for (int k = 0; k < N; ++k) row[k] = v[k];
+  for (int e = 0; e < E; ++e) row[C::idx(tid + TPR * e)] = v[e];
   __syncthreads();
-  for (int i = threadIdx.x; i < count; i += XS) {
-    const float2 y = lds[(i / N) * P + i % N];
+  for (int i = threadIdx.x; i < count; i += THREADS) {
+    const float2 y = lds[(i / N) * P + C::idx(i % N)];
     st_stream(out_re + g0 + i, y.x);
     st_stream(out_im + g0 + i, y.y);
   }
@@ -112,19 +130,20 @@ __global__ __launch_bounds__(kSmallRows) void c2c_small_kernel(
 
 template <int N, int DIR, bool REAL_IN>
 static hipError_t launch_c2c_small_t(const C2cArgs& a) {
-  const long long full = a.batch / kSmallRows;
+  constexpr int THREADS = C2cSmallCfg<N>::THREADS, XS = C2cSmallCfg<N>::XS;
+  const long long full = a.batch / XS;
   if (full > 0)
-    hipLaunchKernelGGL((c2c_small_kernel<N, DIR, REAL_IN, false>), dim3((unsigned)full), dim3(kSmallRows), 0,
-                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, 0LL, a.batch, a.scale);
-  if (full * kSmallRows < a.batch)
-    hipLaunchKernelGGL((c2c_small_kernel<N, DIR, REAL_IN, true>), dim3(1), dim3(kSmallRows), 0, a.stream,
-                       a.in_re, a.in_im, a.out_re, a.out_im, full * kSmallRows, a.batch, a.scale);
+    hipLaunchKernelGGL((c2c_small_kernel<N, DIR, REAL_IN, false>), dim3((unsigned)full), dim3(THREADS), 0,
+                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, 0LL, a.batch, a.scale);
+  if (full * XS < a.batch)
+    hipLaunchKernelGGL((c2c_small_kernel<N, DIR, REAL_IN, true>), dim3(1), dim3(THREADS), 0, a.stream,
+                       a.in_re, a.in_im, a.out_re, a.out_im, a.tw, full * XS, a.batch, a.scale);
   return hipGetLastError();
 }
 
 template <int N, int DIR, bool REAL_IN>
 static hipError_t launch_c2c_lds_t(const C2cArgs& a) {
-  if constexpr (N >= 2 && N <= 32) {
+  if constexpr (N >= 2 && N <= 64) {
     return launch_c2c_small_t<N, DIR, REAL_IN>(a);
   } else {
     using C = C2cThreads<N>;
