@@ -140,13 +140,25 @@ def test_bluestein_vs_reference_golden(direction):
         assert err <= tol_bluestein(int(n)), (int(n), direction, err)
 
 
-@pytest.mark.parametrize("n,batch", [(1000, 1024), (4099, 256), (3, 5), (17, 33), (8193, 4), (20000, 2)])
+@pytest.mark.parametrize("n,batch", [(1000, 1024), (4099, 256), (3, 5), (17, 33), (8193, 4), (20000, 2),
+                                     # short rows (m <= 256, staged per workgroup): full tiles plus a
+                                     # ragged one, every padded length 4..256 and real input below
+                                     (2, 600), (5, 1000), (7, 257), (12, 300), (31, 513), (33, 129),
+                                     (60, 200), (100, 130), (127, 65), (129, 3)])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_bluestein_vs_oracle(n, batch, inverse):
     re, im = seeded_complex(batch, n, seed=n)
     got = _gpu_fft(re, im, inverse)
     ref = oracle.fft_core(re, im, inverse)
     assert rel_l2(*got, *ref) <= tol_bluestein(n), (n, inverse)
+
+
+@pytest.mark.parametrize("n", [3, 12, 100])
+def test_bluestein_short_rows_real_input(n):
+    re, _ = seeded_complex(301, n, seed=n + 1)
+    X = trnfft_amd.fft(re.cuda())
+    ref = oracle.fft_core(re, torch.zeros_like(re), False)
+    assert rel_l2(X.real, X.imag, *ref) <= tol_bluestein(n)
 
 
 @pytest.mark.parametrize("inverse", [False, True])

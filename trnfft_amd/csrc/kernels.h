@@ -28,6 +28,21 @@ __device__ __forceinline__ float4 ld_stream4(const float4* p) {
   return make_float4(r.x, r.y, r.z, r.w);
 }
 
+// floor(n / d) and n % d for 0 <= n < 2^24 and rd = 1.0f / d (float reciprocal, one correction
+// step: exact in that range)
+__device__ __forceinline__ int divmod_small(int n, int d, float rd, int& r) {
+  int q = (int)((float)n * rd);
+  r = n - q * d;
+  if (r < 0) {
+    --q;
+    r += d;
+  } else if (r >= d) {
+    ++q;
+    r -= d;
+  }
+  return q;
+}
+
 // Thread layout of the batched LDS kernels for transform length N: T threads per transform,
 // XF transforms per workgroup (c2c_threads(N) threads per workgroup), PADN LDS entries per
 // transform (float2 when the exchange is interleaved, floats per plane otherwise; 1 when the

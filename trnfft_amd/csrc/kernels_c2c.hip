@@ -389,20 +389,6 @@ __global__ __launch_bounds__(FourStepCfg<N2>::THREADS) void fourstep_row_kernel(
   }
 }
 
-// floor(n / d) and n % d for 0 <= n < 2^24 (float reciprocal, one correction step: exact there)
-__device__ __forceinline__ int divmod_small(int n, int d, float rd, int& r) {
-  int q = (int)((float)n * rd);
-  r = n - q * d;
-  if (r < 0) {
-    --q;
-    r += d;
-  } else if (r >= d) {
-    ++q;
-    r -= d;
-  }
-  return q;
-}
-
 // Strided transform with few columns (stride <= C/2): the column tile of strided_kernel would be
 // mostly idle and its row segments a few floats long.  Here a workgroup takes G = C / stride
 // whole (N1 x stride) blocks, contiguous in memory: they are read and written as one run per
