@@ -87,3 +87,30 @@ def test_graph_replay_real_istft_and_split_bluestein():
         assert torch.equal(o[3].real, e[3].real) and torch.equal(o[3].imag, e[3].imag)
         trnfft_amd.fft(torch.randn(16, 64, device="cuda"))
         torch.cuda.synchronize()
+
+
+def test_graph_replay_short_rows_small_images_and_strided_axes():
+    # the staged kernels: short c2c rows (N = 16, 32, 64), short real rows, single-pass small
+    # images, strided axes with few trailing columns and Bluestein down a strided axis
+    g0 = torch.Generator().manual_seed(21)
+    a = ComplexTensor(torch.randn(300, 32, generator=g0).cuda(), torch.randn(300, 32, generator=g0).cuda())
+    b = ComplexTensor(torch.randn(700, 16, generator=g0).cuda(), torch.randn(700, 16, generator=g0).cuda())
+    c = ComplexTensor(torch.randn(130, 64, generator=g0).cuda(), torch.randn(130, 64, generator=g0).cuda())
+    r = torch.randn(513, 16, generator=g0).cuda()
+    img = ComplexTensor(torch.randn(19, 16, 16, generator=g0).cuda(), torch.randn(19, 16, 16, generator=g0).cuda())
+    few = ComplexTensor(torch.randn(9, 128, 3, generator=g0).cuda(), torch.randn(9, 128, 3, generator=g0).cuda())
+    blue = ComplexTensor(torch.randn(3, 100, 40, generator=g0).cuda(), torch.randn(3, 100, 40, generator=g0).cuda())
+
+    def run():
+        return (trnfft_amd.fft(a), trnfft_amd.ifft(b), trnfft_amd.fft(c), trnfft_amd.rfft(r), trnfft_amd.fft2(img),
+                trnfft_amd.fftn(few, dim=(1,)), trnfft_amd.ifftn(blue, dim=(1,)))
+
+    eager = run()
+    g, outs = _capture(run)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o.real, e.real) and torch.equal(o.imag, e.imag)
+        trnfft_amd.fft(a)  # unrelated eager work between replays
+        torch.cuda.synchronize()
