@@ -254,3 +254,38 @@ def test_istft_gradient_flows():
                     length=3000)
     (z * c).sum().backward()
     assert rel_l2(sr.grad, si.grad, r_r.grad, r_i.grad) <= 1e-4
+
+
+def test_reference_named_autograd_entry_points():
+    # the names trnfft's NKI autograd module exposes (trnfft/nki/autograd.py:115-116, 158-159,
+    # 204-205), here on the HIP kernels: values and gradients against fp64 torch
+    from trnfft_amd import autograd as ag
+
+    g = torch.Generator().manual_seed(31)
+    xr, xi = torch.randn(6, 64, generator=g), torch.randn(6, 64, generator=g)
+    a_r, a_i = _leaf(xr), _leaf(xi)
+    y_re, y_im = ag.fft_autograd(a_r, a_i, False)
+    (y_re.square().sum() + y_im.sum()).backward()
+    r_r, r_i = xr.double().requires_grad_(True), xi.double().requires_grad_(True)
+    z = torch.fft.fft(torch.complex(r_r, r_i))
+    (z.real.square().sum() + z.imag.sum()).backward()
+    assert rel_l2(y_re, y_im, z.real.detach(), z.imag.detach()) <= TOL
+    assert rel_l2(a_r.grad, a_i.grad, r_r.grad, r_i.grad) <= TOL
+
+    ar, ai = torch.randn(8, 16, generator=g), torch.randn(8, 16, generator=g)
+    br, bi = torch.randn(16, 5, generator=g), torch.randn(16, 5, generator=g)
+    la_r, la_i, lb_r, lb_i = _leaf(ar), _leaf(ai), _leaf(br), _leaf(bi)
+    c_re, c_im = ag.complex_gemm_autograd(la_r, la_i, lb_r, lb_i)
+    (c_re.sum() + 2 * c_im.sum()).backward()
+    rar, rai = ar.double().requires_grad_(True), ai.double().requires_grad_(True)
+    rbr, rbi = br.double().requires_grad_(True), bi.double().requires_grad_(True)
+    C = torch.complex(rar, rai) @ torch.complex(rbr, rbi)
+    (C.real.sum() + 2 * C.imag.sum()).backward()
+    assert rel_l2(c_re, c_im, C.real.detach(), C.imag.detach()) <= TOL
+    assert rel_l2(la_r.grad, la_i.grad, rar.grad, rai.grad) <= TOL
+    assert rel_l2(lb_r.grad, lb_i.grad, rbr.grad, rbi.grad) <= TOL
+
+    wr, wi = torch.randn(5, 16, generator=g), torch.randn(5, 16, generator=g)
+    y_re, y_im = ag.complex_linear_autograd(_leaf(ar), _leaf(ai), _leaf(wr), _leaf(wi))
+    Y = torch.complex(ar.double(), ai.double()) @ torch.complex(wr.double(), wi.double()).T
+    assert rel_l2(y_re, y_im, Y.real, Y.imag) <= TOL
