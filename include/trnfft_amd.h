@@ -104,6 +104,18 @@ int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, con
                         const float* in_im, float* out_re, float* out_im, tfa_stream stream);
 
 /*
+ * tfa_execute_strided extended to power-of-two TFA_KIND_C2C axes 4096 < n <= 2^24 with
+ * stride >= 16: two strided passes (n = n1 * n2) through `workspace`, whose size
+ * tfa_strided_workspace_size reports (2 * 4 * outer * n * stride bytes for such axes, else 0).
+ * In place allowed (out_* == in_*); the workspace must not overlap the data.  Every other
+ * plan/stride goes to tfa_execute_strided (workspace unused).  Replaces the same transposes of
+ * trnfft/api.py:496-516 for long axes.
+ */
+int tfa_strided_workspace_size(const tfa_plan* plan, int64_t outer, int64_t stride, size_t* bytes);
+int tfa_execute_strided_ws(const tfa_plan* plan, int64_t outer, int64_t stride, const float* in_re,
+                           const float* in_im, float* out_re, float* out_im, void* workspace, tfa_stream stream);
+
+/*
  * Short-time Fourier transform of `batch` real signals of `num_samples` samples each.  Frames
  * of n_fft samples every hop, after reflect padding when TFA_STFT_CENTER; each frame is
  * multiplied by window (device pointer, n_fft floats, already centre-padded to n_fft) and

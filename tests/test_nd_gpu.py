@@ -122,6 +122,88 @@ def test_non_pow2_axis_strided_bluestein(shape):
     assert _np_rel(got, np.fft.fft(re.astype(np.float64), axis=1)) <= 3 * tol_bluestein(n), shape
 
 
+# power-of-two axes longer than 4096 along a strided dimension (stride >= 16): the two-pass
+# strided four-step (n = n1 * n2, every split from 64 x 128 up), against numpy float64 at sizes
+# numpy finishes quickly, with ragged strides and real input
+@pytest.mark.parametrize("shape", [(3, 8192, 16), (2, 16384, 17), (1, 32768, 48), (2, 65536, 16), (1, 131072, 24),
+                                   (1, 262144, 16)])
+def test_long_pow2_axis_strided_fourstep_vs_numpy(shape):
+    from trnfft_amd.fft_core import strided_ok
+
+    n, stride = shape[1], shape[2]
+    assert strided_ok(n, stride)
+    rng = np.random.default_rng(23)
+    re = rng.standard_normal(shape).astype(np.float32)
+    im = rng.standard_normal(shape).astype(np.float32)
+    x = ComplexTensor(torch.from_numpy(re).cuda(), torch.from_numpy(im).cuda())
+    z = re.astype(np.float64) + 1j * im
+    for inverse in (False, True):
+        got = trnfft_amd.ifftn(x, dim=(1,)) if inverse else trnfft_amd.fftn(x, dim=(1,))
+        ref = np.fft.ifft(z, axis=1) if inverse else np.fft.fft(z, axis=1)
+        assert _np_rel(got, ref) <= tol_pow2(n), (shape, inverse)
+    got = trnfft_amd.fftn(torch.from_numpy(re).cuda(), dim=(1,))
+    assert _np_rel(got, np.fft.fft(re.astype(np.float64), axis=1)) <= tol_pow2(n), shape
+
+
+# the largest splits (2^19 .. 2^24 along the axis, 16 trailing columns: up to 2^28 elements), where
+# numpy float64 is too slow: against the contiguous four-step on the moved axis (a different
+# kernel pair over the same split) and through the inverse round trip
+@pytest.mark.parametrize("lg", [19, 20, 21, 22, 23, 24])
+def test_long_pow2_axis_strided_fourstep_large(lg):
+    n, stride = 1 << lg, 16
+    g = torch.Generator(device="cuda").manual_seed(lg)
+    re = torch.randn((1, n, stride), generator=g, device="cuda")
+    im = torch.randn((1, n, stride), generator=g, device="cuda")
+    x = ComplexTensor(re, im)
+
+    def rel(a_re, a_im, b_re, b_im):  # relative L2 on the GPU, float64 accumulation
+        num = ((a_re.double() - b_re.double()) ** 2).sum() + ((a_im.double() - b_im.double()) ** 2).sum()
+        return float(torch.sqrt(num / ((b_re.double() ** 2).sum() + (b_im.double() ** 2).sum())))
+
+    got = trnfft_amd.fftn(x, dim=(1,))
+    moved = ComplexTensor(re.transpose(1, 2).contiguous(), im.transpose(1, 2).contiguous())
+    last = trnfft_amd.fft(moved)
+    assert rel(got.real, got.imag, last.real.transpose(1, 2), last.imag.transpose(1, 2)) <= 2 * tol_pow2(n), lg
+    del last, moved
+    back = trnfft_amd.ifftn(got, dim=(1,))
+    assert rel(back.real, back.imag, re, im) <= 2 * tol_pow2(n), lg
+
+
+def test_strided_fourstep_abi_in_place_and_workspace():
+    # tfa_execute_strided_ws through the C ABI: workspace size, in place (out == in), and the
+    # missing-workspace error
+    import ctypes
+
+    from trnfft_amd import _lib
+    from trnfft_amd.dispatch import ptr, stream_handle
+    from trnfft_amd.plan import native_plan
+
+    outer, n, stride = 2, 16384, 20
+    rng = np.random.default_rng(29)
+    re = rng.standard_normal((outer, n, stride)).astype(np.float32)
+    im = rng.standard_normal((outer, n, stride)).astype(np.float32)
+    d_re, d_im = torch.from_numpy(re).cuda(), torch.from_numpy(im).cuda()
+    lib = _lib.lib()
+    plan = native_plan(_lib.KIND_C2C, n, False, 0)
+    nbytes = ctypes.c_size_t(0)
+    assert lib.tfa_strided_workspace_size(plan.handle, outer, stride, ctypes.byref(nbytes)) == 0
+    assert nbytes.value == 2 * 4 * outer * n * stride
+    ws = torch.empty(nbytes.value // 4, device="cuda")
+    dev = torch.device("cuda", 0)
+    assert lib.tfa_execute_strided_ws(plan.handle, outer, stride, ptr(d_re), ptr(d_im), ptr(d_re), ptr(d_im),
+                                      None, stream_handle(dev)) != 0
+    rc = lib.tfa_execute_strided_ws(plan.handle, outer, stride, ptr(d_re), ptr(d_im), ptr(d_re), ptr(d_im), ptr(ws),
+                                    stream_handle(dev))
+    assert rc == 0
+    torch.cuda.synchronize()
+    ref = np.fft.fft(re.astype(np.float64) + 1j * im, axis=1)
+    assert rel_l2(d_re, d_im, ref.real, ref.imag) <= tol_pow2(n)
+    # short axes and small strides need no workspace
+    small = native_plan(_lib.KIND_C2C, 4096, False, 0)
+    assert lib.tfa_strided_workspace_size(small.handle, outer, stride, ctypes.byref(nbytes)) == 0 and nbytes.value == 0
+    assert lib.tfa_strided_workspace_size(plan.handle, outer, 15, ctypes.byref(nbytes)) == 0 and nbytes.value == 0
+
+
 def test_fft2_non_pow2_image():
     # 480 x 640: the 640 axis runs the contiguous Bluestein kernel, the 480 axis the strided one
     rng = np.random.default_rng(19)

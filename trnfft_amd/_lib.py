@@ -39,6 +39,8 @@ EXPORTS = (
     "tfa_plan_padded_n",
     "tfa_execute",
     "tfa_execute_strided",
+    "tfa_strided_workspace_size",
+    "tfa_execute_strided_ws",
     "tfa_stft_frames",
     "tfa_stft_execute",
     "tfa_istft_length",
@@ -82,6 +84,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tfa_execute.restype = ctypes.c_int
     lib.tfa_execute_strided.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp]
     lib.tfa_execute_strided.restype = ctypes.c_int
+    lib.tfa_strided_workspace_size.argtypes = [_vp, _i64, _i64, ctypes.POINTER(ctypes.c_size_t)]
+    lib.tfa_strided_workspace_size.restype = ctypes.c_int
+    lib.tfa_execute_strided_ws.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.tfa_execute_strided_ws.restype = ctypes.c_int
     lib.tfa_stft_frames.argtypes = [_vp, _i64, ctypes.POINTER(_i64)]
     lib.tfa_stft_frames.restype = ctypes.c_int
     lib.tfa_stft_execute.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp]

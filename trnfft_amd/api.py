@@ -458,9 +458,10 @@ def _resize_dim_real(x: torch.Tensor, dim: int, n: int) -> torch.Tensor:
 def _fft_along_dim(x, dim: int, inverse: bool) -> ComplexTensor:
     """1-D FFT along `dim` of a ComplexTensor or real tensor (trnfft/api.py:496-516).
 
-    The last axis runs the contiguous kernels; another power-of-two axis (n <= 4096) runs the
-    strided kernel in place of the reference's transpose / FFT / transpose-back copies; other
-    lengths along a non-last axis keep the transpose round trip.
+    The last axis runs the contiguous kernels; another axis runs the strided kernels in place of
+    the reference's transpose / FFT / transpose-back copies (power-of-two n <= 4096, other
+    n <= 2048, and power-of-two n <= 2^24 over at least 16 trailing columns); the remaining
+    shapes keep the transpose round trip.
     """
     real_in = _is_real_tensor(x)
     shape = tuple(x.shape)

@@ -17,6 +17,7 @@ LIB = os.path.join(PKG, "libtrnfft_amd.so")
 SOURCES = [
     "plan.hip",
     "kernels_c2c.hip",
+    "kernels_strided.hip",
     "kernels_bluestein.hip",
     "kernels_stft.hip",
     "kernels_gemm.hip",

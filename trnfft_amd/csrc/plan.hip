@@ -70,6 +70,7 @@ struct C2cTables {
   float2* tw_lds = nullptr;  // LDS path, strided / 2-D row kernel layout
   int n1 = 0, n2 = 0, lo_bits = 0;
   float2 *tw1 = nullptr, *tw2 = nullptr, *tw_lo = nullptr, *tw_hi = nullptr;
+  float2 *tws1 = nullptr, *tws2 = nullptr;  // n1 / n2 tables in the strided kernels' lds_epth layout
 };
 
 }  // namespace
@@ -120,14 +121,21 @@ struct tfa_plan {
       // the batched kernel's layout (tfa::c2c_epth); the strided and 2-D row kernels use the
       // tfa::lds_epth layout, a second table only where the two differ
       int rc = upload(lds_table((int)n, dir, tfa::c2c_epth((int)n)), &t->tw);
-      if (rc || tfa::c2c_epth((int)n) == tfa::lds_epth((int)n)) {
-        t->tw_lds = t->tw;
-        return rc;
-      }
-      return upload(lds_table((int)n, dir), &t->tw_lds);
+      if (!rc && tfa::c2c_epth((int)n) != tfa::lds_epth((int)n)) rc = upload(lds_table((int)n, dir), &t->tw_lds);
+      else t->tw_lds = t->tw;
+      // lengths beyond the strided kernel's reach (n > 4096) also carry the four-step split
+      // tables: a strided axis of that length runs as two strided passes
+      if (rc || n <= tfa::kMaxStridedN) return rc;
+      return build_split(n, dir, t);
     }
     if (n > kMaxFourStepN) return fail(TFA_ERR_UNSUPPORTED, "power-of-two length above 2^24 not supported");
     t->fourstep = true;
+    return build_split(n, dir, t);
+  }
+
+  // n = n1 * n2 (n1 = 2^floor(lg/2) <= n2): LDS-FFT tables of both lengths (tfa::fourstep_epth
+  // layout) and the two-level W_n^j tables of the twiddle between the passes
+  int build_split(int64_t n, int dir, C2cTables* t) {
     const int lg = tfa::ilog2(n);
     t->n1 = 1 << (lg / 2);      // column transform length (strided)
     t->n2 = (int)(n / t->n1);   // row transform length (contiguous), n2 >= n1
@@ -135,6 +143,10 @@ struct tfa_plan {
     int rc;
     if ((rc = upload(lds_table(t->n1, dir, tfa::fourstep_epth(t->n1)), &t->tw1))) return rc;
     if ((rc = upload(lds_table(t->n2, dir, tfa::fourstep_epth(t->n2)), &t->tw2))) return rc;
+    t->tws1 = t->tw1;
+    t->tws2 = t->tw2;
+    if (tfa::lds_epth(t->n1) != tfa::fourstep_epth(t->n1) && (rc = upload(lds_table(t->n1, dir), &t->tws1))) return rc;
+    if (tfa::lds_epth(t->n2) != tfa::fourstep_epth(t->n2) && (rc = upload(lds_table(t->n2, dir), &t->tws2))) return rc;
     std::vector<float2> lo((size_t)1 << t->lo_bits), hi((size_t)(n >> t->lo_bits));
     for (size_t j = 0; j < lo.size(); ++j) lo[j] = unit_root((int64_t)j, n, dir);
     for (size_t j = 0; j < hi.size(); ++j) hi[j] = unit_root((int64_t)j << t->lo_bits, n, dir);
@@ -219,7 +231,7 @@ std::vector<float2> reference_chirp(int64_t n, int sign) {
 
 extern "C" {
 
-int32_t tfa_abi_version(void) { return (1 << 16) | 0; }
+int32_t tfa_abi_version(void) { return (1 << 16) | 1; }
 
 const char* tfa_last_error(void) { return g_last_error.c_str(); }
 
@@ -504,14 +516,54 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
   }
 }
 
+namespace {
+
+// power-of-two C2C axis longer than the single-pass strided kernel: two strided passes
+bool strided_fourstep(const tfa_plan* plan, int64_t stride) {
+  return plan->d.kind == TFA_KIND_C2C && plan->d.n > tfa::kMaxStridedN && stride >= tfa::kMinStridedFourStepStride;
+}
+
+}  // namespace
+
+int tfa_strided_workspace_size(const tfa_plan* plan, int64_t outer, int64_t stride, size_t* bytes) {
+  if (!plan || !bytes) return fail(TFA_ERR_INVALID, "null argument");
+  if (outer < 0 || stride < 1) return fail(TFA_ERR_INVALID, "bad outer/stride");
+  *bytes = strided_fourstep(plan, stride) ? (size_t)2 * sizeof(float) * (size_t)outer * (size_t)plan->d.n * (size_t)stride : 0;
+  return TFA_OK;
+}
+
+int tfa_execute_strided_ws(const tfa_plan* plan, int64_t outer, int64_t stride, const float* in_re,
+                           const float* in_im, float* out_re, float* out_im, void* workspace, tfa_stream stream) {
+  if (!plan) return fail(TFA_ERR_INVALID, "null plan");
+  if (!strided_fourstep(plan, stride))
+    return tfa_execute_strided(plan, outer, stride, in_re, in_im, out_re, out_im, stream);
+  if (outer < 0) return fail(TFA_ERR_INVALID, "bad outer/stride");
+  if (outer == 0) return TFA_OK;
+  if (!in_re || !out_re || !out_im) return fail(TFA_ERR_INVALID, "null data pointer");
+  if (!workspace) return fail(TFA_ERR_INVALID, "strided four-step transform needs a workspace");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
+    return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  const C2cTables& t = plan->d.inverse ? plan->inv : plan->fwd;
+  const size_t plane = (size_t)outer * (size_t)plan->d.n * (size_t)stride;
+  float* t_re = static_cast<float*>(workspace);
+  const float scale = plan->d.inverse ? (float)(1.0 / (double)plan->d.n) : 1.0f;
+  tfa::StridedFourStepArgs a{in_re, in_im, t_re, t_re + plane, out_re, out_im, t.tws1, t.tws2, t.tw_lo, t.tw_hi,
+                             t.n1, t.n2, t.lo_bits, outer, stride, scale, t.dir, static_cast<hipStream_t>(stream)};
+  hipError_t e = tfa::launch_strided_fourstep(a);
+  if (e == hipErrorInvalidValue) return fail(TFA_ERR_UNSUPPORTED, "strided four-step: shape beyond the launch grid");
+  return e == hipSuccess ? TFA_OK : hip_fail(e, "strided four-step launch");
+}
+
 int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, const float* in_re,
                         const float* in_im, float* out_re, float* out_im, tfa_stream stream) {
   if (!plan) return fail(TFA_ERR_INVALID, "null plan");
   if (outer < 0 || stride < 1) return fail(TFA_ERR_INVALID, "bad outer/stride");
   const bool blue = plan->d.kind == TFA_KIND_BLUESTEIN && plan->m <= tfa::kMaxStridedBlueM;
-  if (!blue && (plan->d.kind != TFA_KIND_C2C || plan->d.n > 4096 || plan->d.n < 2))
+  if (!blue && (plan->d.kind != TFA_KIND_C2C || plan->d.n > tfa::kMaxStridedN || plan->d.n < 2))
     return fail(TFA_ERR_UNSUPPORTED,
-                "strided transforms need a power-of-two C2C plan with 2 <= n <= 4096 or a Bluestein plan with n <= 2048");
+                "strided transforms need a power-of-two C2C plan with 2 <= n <= 4096 or a Bluestein plan with n <= 2048 "
+                "(longer power-of-two axes with stride >= 16: tfa_execute_strided_ws)");
   if (outer == 0) return TFA_OK;
   if (!in_re || !out_re || !out_im) return fail(TFA_ERR_INVALID, "null data pointer");
   int dev = -1;

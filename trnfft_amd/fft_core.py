@@ -18,6 +18,8 @@ Inverse transforms are scaled by 1/n inside the kernels, as the reference scales
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -130,18 +132,22 @@ def execute_c2r(re: torch.Tensor, im: torch.Tensor, n: int) -> torch.Tensor:
     return out if out_dev == dev else out.to(out_dev)
 
 
-# longest power-of-two axis the strided kernel transforms in place of a transpose round trip, and
-# longest other axis (Bluestein padded length m <= 4096)
+# longest power-of-two axis the single-pass strided kernel transforms in place of a transpose
+# round trip, longest other axis (Bluestein padded length m <= 4096), and the strided four-step's
+# reach (longer power-of-two axes with at least 16 trailing columns, two passes + workspace)
 _STRIDED_MAX_N = 4096
 _STRIDED_BLUE_MAX_N = 2048
+_STRIDED_FS_MAX_N = 1 << 24
+_STRIDED_FS_MIN_STRIDE = 16
 
 
 def execute_strided(re: torch.Tensor, im: torch.Tensor | None, dim: int, inverse: bool) -> ComplexTensor:
-    """Transform along a non-last axis `dim` without moving it (power-of-two n <= 4096, other
-    n <= 2048 through the strided Bluestein kernel).
+    """Transform along a non-last axis `dim` without moving it: power-of-two n <= 4096 and
+    other n <= 2048 in one strided pass, power-of-two 4096 < n <= 2^24 (stride >= 16) as a
+    two-pass strided four-step through a workspace.
 
     The contiguous tensor is viewed as (outer, n, stride); every column is transformed along
-    its n elements by the strided kernel (replaces trnfft/api.py:496-516's transposes).
+    its n elements (replaces trnfft/api.py:496-516's transposes).
     """
     shape = re.shape
     n = shape[dim]
@@ -159,11 +165,20 @@ def execute_strided(re: torch.Tensor, im: torch.Tensor | None, dim: int, inverse
     plan = native_plan(kind, n, inverse, dev.index)
     out_re = torch.empty_like(re)
     out_im = torch.empty_like(re)
+    lib = _lib.lib()
     with torch.cuda.device(dev):
-        rc = _lib.lib().tfa_execute_strided(
-            plan.handle, outer, stride, ptr(re), ptr(im), ptr(out_re), ptr(out_im), stream_handle(dev)
-        )
-    _lib.check(rc, "tfa_execute_strided")
+        nbytes = ctypes.c_size_t(0)
+        _lib.check(lib.tfa_strided_workspace_size(plan.handle, outer, stride, ctypes.byref(nbytes)),
+                   "tfa_strided_workspace_size")
+        if nbytes.value:
+            ws = torch.empty(nbytes.value // 4, dtype=torch.float32, device=dev)
+            rc = lib.tfa_execute_strided_ws(plan.handle, outer, stride, ptr(re), ptr(im), ptr(out_re), ptr(out_im),
+                                            ptr(ws), stream_handle(dev))
+            _lib.check(rc, "tfa_execute_strided_ws")
+        else:
+            rc = lib.tfa_execute_strided(plan.handle, outer, stride, ptr(re), ptr(im), ptr(out_re), ptr(out_im),
+                                         stream_handle(dev))
+            _lib.check(rc, "tfa_execute_strided")
     out = ComplexTensor._wrap(out_re, out_im)
     return out if out_dev == dev else out.to(out_dev)
 
@@ -239,7 +254,7 @@ def strided_ok(n: int, stride: int) -> bool:
     if stride < 1 or n < 2:
         return False
     if (n & (n - 1)) == 0:
-        return n <= _STRIDED_MAX_N
+        return n <= _STRIDED_MAX_N or (n <= _STRIDED_FS_MAX_N and stride >= _STRIDED_FS_MIN_STRIDE)
     return n <= _STRIDED_BLUE_MAX_N
 
 
