@@ -93,22 +93,25 @@ struct StridedArgs {
 hipError_t launch_strided(int n1, const StridedArgs& a);
 
 // Longest axis the single-pass strided kernel takes; longer power-of-two axes (up to 2^24) run
-// as two strided passes (strided four-step) with a workspace.
+// as two or three strided passes (strided multi-pass four-step) through a workspace.
 constexpr int kMaxStridedN = 4096;
-// Smallest trailing stride of the strided four-step (column tiles of 16..32 floats).
+// Smallest trailing stride of the strided multi-pass path (column tiles of 16..64 floats).
 constexpr long long kMinStridedFourStepStride = 16;
+// Axes of 2^kStridedThreePassLg and more use three factors (each <= 256: 64-column tiles).
+constexpr int kStridedThreePassLg = 21;
 struct StridedFourStepArgs {
   const float* in_re;
   const float* in_im;  // nullptr: real input
   float* t_re;         // workspace, outer * n * stride floats each
   float* t_im;
-  float* out_re;       // may equal in_re (pass 1 reads all input before pass 2 writes); not the workspace
+  float* out_re;       // may equal in_re (the first pass reads all input before the last writes); not the workspace
   float* out_im;
-  const float2* tw1;    // LDS-FFT table for n1 (lds_epth layout)
-  const float2* tw2;    // LDS-FFT table for n2 (lds_epth layout)
+  int npass;            // 2 or 3 factors, n = len[0] * ... * len[npass-1], each 64..4096
+  int len[3];
+  const float2* tw[3];  // LDS-FFT table of each factor (lds_epth layout)
   const float2* tw_lo;  // W_n^j, j < 2^lo_bits
   const float2* tw_hi;  // W_n^(j << lo_bits)
-  int n1, n2, lo_bits;
+  int lo_bits;
   long long outer, stride;
   float scale;
   int dir;

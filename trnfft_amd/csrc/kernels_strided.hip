@@ -1,28 +1,46 @@
-// Strided four-step: a power-of-two axis of length N = N1*N2 > 4096 transformed where it lies,
-// data viewed as (outer, N, S) row-major.  Position n = N2*n1 + n2, output k = k1 + N1*k2 (the
-// split of the contiguous four-step), column s < S.  Two strided passes through a workspace, no
-// transposes:
-//   pass 1 (L = N1): columns col = n2*S + s of each outer block, element stride N2*S; DFT over n1,
-//     times W_N^(n2*k1), written to tmp[o][k1][n2][s] (the input's own layout);
-//   pass 2 (L = N2): columns col = k1*S + s; DFT over n2 read from tmp[o][k1][.][s] (element
-//     stride S, base k1*N2*S + s), written to X[o][k1 + N1*k2][s] (element stride N1*S, base col).
+// Strided multi-pass FFT: a power-of-two axis of length N = L1*...*LP > 4096 (P = 2 or 3 factors)
+// transformed where it lies, data viewed as (outer, N, S) row-major, S columns.  The recursive
+// four-step with the factors as passes, each a strided pass through a workspace, no transposes:
+//   pass p < P: for every block (o, k1..k_{p-1}) of M_{p-1} = Lp*M_p positions (M_p = L_{p+1}..LP),
+//     columns col = m*S + s (m < M_p): DFT over the Lp positions n_p*M_p + m (element stride
+//     M_p*S), times W_{M_{p-1}}^(m*k_p), written back in the same layout (output k_p where n_p
+//     was), so the block splits into Lp blocks (o, k1..k_p) of M_p positions;
+//   pass P: for every (o, k1..k_{P-1}, s), the DFT over the LP positions of block (o, k1..k_{P-1})
+//     (element stride S), written to X[o][k1 + L1*k2 + ... + L1..L_{P-1}*kP][s].
 // Replaces, for such axes, the transpose-copy + contiguous FFT + transpose-back of
 // trnfft/api.py:496-516 (_fft_along_dim).
 #include "kernels.h"
 
 namespace tfa {
 
-// One kernel serves both passes: column col = q*S + r (q = col / S) is read from
-// o*blk + q*in_hi + r + j*in_step (j < L) and written to o*blk + q*out_hi + r + k*out_step.  A
-// workgroup takes C adjacent columns of one outer block (the strided kernel's shape); with
-// N1, N2 >= 64 >= C every tile is whole.  TWIDDLE (pass 1): output k1 of column col is
-// multiplied by W_N^(q*k1), read as W^lo * W^hi from the two small tables.
+namespace {
+
+// Addressing of one pass.  Column col = q*S + r (q = col / S); with qa = q & (2^qa_bits - 1) and
+// qb = q >> qa_bits, element j of the column is read from o*blk + qa*in_a + qb*in_b + r + j*in_step
+// and output k written to o*blk + qa*out_a + qb*out_b + r + k*out_step.  Twiddled passes
+// multiply output k by W_N^((q*tw_mult*k) mod N) (tables W^lo, W^hi of the whole length N).
+struct SfsPass {
+  long long S, blk, tiles_per_block;
+  long long in_a, in_b, in_step, out_a, out_b, out_step;
+  int qa_bits;
+  unsigned tw_mult;
+  int lo_bits;
+  unsigned nmask;
+  float scale;
+};
+
+// bits of the column-index split that leave qb = 0 for any column index in range
+constexpr int kNoSplit = 40;
+
+}  // namespace
+
+// A workgroup takes C adjacent columns of one block (the single-pass strided kernel's shape);
+// every pass has at least 64 >= C columns per block, so every tile is whole.  The data pointers
+// are not restrict: a middle pass runs in place (in == out).
 template <int L, int DIR, bool REAL_IN, bool TWIDDLE, int C = fourstep_tile(L)>
 __global__ __launch_bounds__(C * (L / lds_epth(L))) void strided_fs_kernel(
-    const float* __restrict__ in_re, const float* __restrict__ in_im, float* __restrict__ out_re,
-    float* __restrict__ out_im, const float2* __restrict__ tw, const float2* __restrict__ tw_lo,
-    const float2* __restrict__ tw_hi, long long S, long long blk, long long in_hi, long long in_step,
-    long long out_hi, long long out_step, long long tiles_per_block, int lo_bits, unsigned nmask, float scale) {
+    const float* in_re, const float* in_im, float* out_re, float* out_im, const float2* __restrict__ tw,
+    const float2* __restrict__ tw_lo, const float2* __restrict__ tw_hi, SfsPass p) {
   constexpr int E = lds_epth(L), T = L / E;
   constexpr int PADN = lds_pad(L) + 1;
   // interleaved (re, im) exchange except at 4096 (as the single-pass strided kernel)
@@ -31,11 +49,12 @@ __global__ __launch_bounds__(C * (L / lds_epth(L))) void strided_fs_kernel(
   const int c = threadIdx.x % C;  // column within the tile (fast across lanes)
   const int t = threadIdx.x / C;
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
-  const long long o = tile / tiles_per_block;
-  const long long col = (tile % tiles_per_block) * C + c;
-  const long long q = col / S, r = col - q * S;
-  const size_t ib = (size_t)(o * blk + q * in_hi + r) + (size_t)t * (size_t)in_step;
-  const size_t istep = (size_t)T * (size_t)in_step;
+  const long long o = tile / p.tiles_per_block;
+  const long long col = (tile % p.tiles_per_block) * C + c;
+  const long long q = col / p.S, r = col - q * p.S;
+  const long long qa = q & ((1LL << p.qa_bits) - 1), qb = q >> p.qa_bits;
+  const size_t ib = (size_t)(o * p.blk + qa * p.in_a + qb * p.in_b + r) + (size_t)t * (size_t)p.in_step;
+  const size_t istep = (size_t)T * (size_t)p.in_step;
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -49,31 +68,32 @@ __global__ __launch_bounds__(C * (L / lds_epth(L))) void strided_fs_kernel(
     LdsFft<L, E, DIR, false>::run(v, planes + c * PADN, planes + (C + c) * PADN, tw, t);
   }
   if constexpr (TWIDDLE) {
-    // k1 = t + T*(TF*a + j): W^(q*(t + T*TF*a)) * W^(q*T*j), TF-1 + E/TF table pairs per thread
+    // output k = t + T*(TF*a + j): W^(g*(t + T*TF*a)) * W^(g*T*j) with g = q*tw_mult, TF-1 + E/TF
+    // table pairs per thread; products mod 2^32 keep the exponent exact mod N (N | 2^32)
     constexpr int TF = E < 4 ? E : 4;
-    const unsigned qq = (unsigned)q;
-    const unsigned lomask = (1u << lo_bits) - 1;
+    const unsigned g = (unsigned)q * p.tw_mult;
+    const unsigned lomask = (1u << p.lo_bits) - 1;
     float2 w[TF];
 #pragma unroll
     for (int j = 1; j < TF; ++j) {
-      const unsigned m = (qq * (unsigned)(T * j)) & nmask;
-      w[j] = cmul(tw_lo[m & lomask], tw_hi[m >> lo_bits]);
+      const unsigned m = (g * (unsigned)(T * j)) & p.nmask;
+      w[j] = cmul(tw_lo[m & lomask], tw_hi[m >> p.lo_bits]);
     }
 #pragma unroll
     for (int a = 0; a < E / TF; ++a) {
-      const unsigned m = (qq * (unsigned)(t + T * TF * a)) & nmask;
-      const float2 p = cmul(tw_lo[m & lomask], tw_hi[m >> lo_bits]);
-      v[TF * a] = cmul(v[TF * a], p);
+      const unsigned m = (g * (unsigned)(t + T * TF * a)) & p.nmask;
+      const float2 f = cmul(tw_lo[m & lomask], tw_hi[m >> p.lo_bits]);
+      v[TF * a] = cmul(v[TF * a], f);
 #pragma unroll
-      for (int j = 1; j < TF; ++j) v[TF * a + j] = cmul(v[TF * a + j], cmul(p, w[j]));
+      for (int j = 1; j < TF; ++j) v[TF * a + j] = cmul(v[TF * a + j], cmul(f, w[j]));
     }
   }
-  const size_t ob = (size_t)(o * blk + q * out_hi + r) + (size_t)t * (size_t)out_step;
-  const size_t ostep = (size_t)T * (size_t)out_step;
+  const size_t ob = (size_t)(o * p.blk + qa * p.out_a + qb * p.out_b + r) + (size_t)t * (size_t)p.out_step;
+  const size_t ostep = (size_t)T * (size_t)p.out_step;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const size_t i = ob + e * ostep;
-    const float2 y = TWIDDLE ? v[e] : cscale(v[e], scale);
+    const float2 y = TWIDDLE ? v[e] : cscale(v[e], p.scale);
     if constexpr (C * 4 < 128) {
       // row segments shorter than a cache line: plain stores (L2 merges neighbouring partial lines)
       out_re[i] = y.x;
@@ -85,56 +105,114 @@ __global__ __launch_bounds__(C * (L / lds_epth(L))) void strided_fs_kernel(
   }
 }
 
-template <int N1, int N2, int DIR>
-static hipError_t launch_strided_fs_t(const StridedFourStepArgs& a) {
-  constexpr int C1 = fourstep_tile(N1), C2 = fourstep_tile(N2);
-  constexpr int TH1 = C1 * (N1 / lds_epth(N1)), TH2 = C2 * (N2 / lds_epth(N2));
-  static_assert(N2 % C1 == 0 && N1 % C2 == 0, "strided four-step tiles must be whole");
-  const long long S = a.stride, N = (long long)N1 * N2, blk = N * S;
-  const unsigned nmask = (unsigned)(N - 1);
-  const long long tiles1 = (long long)N2 * S / C1, tiles2 = (long long)N1 * S / C2;
-  if (a.outer * tiles1 > 0xffffffffLL || a.outer * tiles2 > 0xffffffffLL) return hipErrorInvalidValue;
-  // pass 1: columns n2*S + s, element stride N2*S, same layout in and out, twiddled
-  if (a.in_im == nullptr)
-    hipLaunchKernelGGL((strided_fs_kernel<N1, DIR, true, true>), dim3((unsigned)(a.outer * tiles1)), dim3(TH1), 0,
-                       a.stream, a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, S, blk, S,
-                       (long long)N2 * S, S, (long long)N2 * S, tiles1, a.lo_bits, nmask, 1.0f);
+template <int L, int DIR>
+static hipError_t launch_sfs_pass_t(const float* in_re, const float* in_im, float* out_re, float* out_im,
+                                    const float2* tw, const StridedFourStepArgs& a, long long blocks, bool twiddle,
+                                    const SfsPass& p, hipStream_t s) {
+  constexpr int C = fourstep_tile(L), TH = C * (L / lds_epth(L));
+  const long long grid = blocks * p.tiles_per_block;
+  if (grid > 0xffffffffLL) return hipErrorInvalidValue;
+  if (twiddle && in_im == nullptr)
+    hipLaunchKernelGGL((strided_fs_kernel<L, DIR, true, true>), dim3((unsigned)grid), dim3(TH), 0, s, in_re, in_im,
+                       out_re, out_im, tw, a.tw_lo, a.tw_hi, p);
+  else if (twiddle)
+    hipLaunchKernelGGL((strided_fs_kernel<L, DIR, false, true>), dim3((unsigned)grid), dim3(TH), 0, s, in_re, in_im,
+                       out_re, out_im, tw, a.tw_lo, a.tw_hi, p);
   else
-    hipLaunchKernelGGL((strided_fs_kernel<N1, DIR, false, true>), dim3((unsigned)(a.outer * tiles1)), dim3(TH1), 0,
-                       a.stream, a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, S, blk, S,
-                       (long long)N2 * S, S, (long long)N2 * S, tiles1, a.lo_bits, nmask, 1.0f);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  // pass 2: columns k1*S + s, read at k1*N2*S + s + n2*S, written at k1*S + s + k2*N1*S
-  hipLaunchKernelGGL((strided_fs_kernel<N2, DIR, false, false>), dim3((unsigned)(a.outer * tiles2)), dim3(TH2), 0,
-                     a.stream, a.t_re, a.t_im, a.out_re, a.out_im, a.tw2, a.tw_lo, a.tw_hi, S, blk, (long long)N2 * S,
-                     S, S, (long long)N1 * S, tiles2, a.lo_bits, nmask, a.scale);
+    hipLaunchKernelGGL((strided_fs_kernel<L, DIR, false, false>), dim3((unsigned)grid), dim3(TH), 0, s, in_re, in_im,
+                       out_re, out_im, tw, a.tw_lo, a.tw_hi, p);
   return hipGetLastError();
 }
 
-// n = n1 * n2 with n1 = 2^floor(lg/2) <= n2 (the plan's split)
+// Column tile of the pass over length l (the host mirror of the template default).
+static int sfs_tile(int l) { return fourstep_tile(l); }
+
 template <int DIR>
-static hipError_t launch_strided_fs_dir(const StridedFourStepArgs& a) {
-  const long long key = (long long)a.n1 * 8192 + a.n2;
-  switch (key) {
-    case 64LL * 8192 + 128: return launch_strided_fs_t<64, 128, DIR>(a);
-    case 128LL * 8192 + 128: return launch_strided_fs_t<128, 128, DIR>(a);
-    case 128LL * 8192 + 256: return launch_strided_fs_t<128, 256, DIR>(a);
-    case 256LL * 8192 + 256: return launch_strided_fs_t<256, 256, DIR>(a);
-    case 256LL * 8192 + 512: return launch_strided_fs_t<256, 512, DIR>(a);
-    case 512LL * 8192 + 512: return launch_strided_fs_t<512, 512, DIR>(a);
-    case 512LL * 8192 + 1024: return launch_strided_fs_t<512, 1024, DIR>(a);
-    case 1024LL * 8192 + 1024: return launch_strided_fs_t<1024, 1024, DIR>(a);
-    case 1024LL * 8192 + 2048: return launch_strided_fs_t<1024, 2048, DIR>(a);
-    case 2048LL * 8192 + 2048: return launch_strided_fs_t<2048, 2048, DIR>(a);
-    case 2048LL * 8192 + 4096: return launch_strided_fs_t<2048, 4096, DIR>(a);
-    case 4096LL * 8192 + 4096: return launch_strided_fs_t<4096, 4096, DIR>(a);
+static hipError_t launch_sfs_pass(int l, const float* in_re, const float* in_im, float* out_re, float* out_im,
+                                  const float2* tw, const StridedFourStepArgs& a, long long blocks, bool twiddle,
+                                  const SfsPass& p) {
+  switch (l) {
+#define TFA_SFS_CASE(LEN) \
+  case LEN: return launch_sfs_pass_t<LEN, DIR>(in_re, in_im, out_re, out_im, tw, a, blocks, twiddle, p, a.stream);
+    TFA_SFS_CASE(64)
+    TFA_SFS_CASE(128)
+    TFA_SFS_CASE(256)
+    TFA_SFS_CASE(512)
+    TFA_SFS_CASE(1024)
+    TFA_SFS_CASE(2048)
+    TFA_SFS_CASE(4096)
+#undef TFA_SFS_CASE
     default: return hipErrorInvalidValue;
   }
 }
 
+template <int DIR>
+static hipError_t launch_strided_fs_dir(const StridedFourStepArgs& a) {
+  const int P = a.npass;
+  long long N = 1;
+  for (int i = 0; i < P; ++i) N *= a.len[i];
+  const long long S = a.stride;
+  const unsigned nmask = (unsigned)(N - 1);
+  // pass 1 reads the input and writes the workspace; later non-final passes transform the
+  // workspace in place (a workgroup writes exactly the addresses it read, after reading all of
+  // them); the final pass reads the workspace and writes the output
+  long long M_prev = N, K = 1;  // block length before this pass, product of earlier factors
+  for (int i = 0; i < P; ++i) {
+    const int L = a.len[i];
+    const long long M = M_prev / L;
+    const bool last = i == P - 1;
+    SfsPass p{};
+    p.S = S;
+    p.lo_bits = a.lo_bits;
+    p.nmask = nmask;
+    p.scale = a.scale;
+    hipError_t e;
+    if (!last) {
+      // blocks (o, k1..k_{i-1}) of M_prev*S floats; columns m*S + s over M*S
+      p.blk = M_prev * S;
+      p.tiles_per_block = M * S / sfs_tile(L);
+      p.in_a = p.out_a = S;
+      p.in_b = p.out_b = 0;
+      p.qa_bits = kNoSplit;
+      p.in_step = p.out_step = M * S;
+      p.tw_mult = (unsigned)K;  // W_{M_prev}^x = W_N^(x*K)
+      const float* src_re = i == 0 ? a.in_re : a.t_re;
+      const float* src_im = i == 0 ? a.in_im : a.t_im;
+      e = launch_sfs_pass<DIR>(L, src_re, src_im, a.t_re, a.t_im, a.tw[i], a, a.outer * K, true, p);
+    } else {
+      // columns col = (k1 + L1*k2 + ...)*S + s over K*S; block (o, k1..k_{P-1}) at row-major
+      // index k1*(L2..L_{P-1}) + ... + k_{P-1} of LP*S floats each
+      p.blk = N * S;
+      p.tiles_per_block = K * S / sfs_tile(L);
+      p.in_step = S;
+      p.out_a = S;
+      p.out_b = 0;
+      p.out_step = K * S;
+      if (P == 2) {
+        p.qa_bits = kNoSplit;
+        p.in_a = (long long)L * S;  // q = k1
+        p.in_b = 0;
+      } else {
+        // q = k1 + L1*k2: block index k1*L2 + k2
+        p.qa_bits = ilog2(a.len[0]);
+        p.in_a = (long long)a.len[1] * L * S;
+        p.in_b = (long long)L * S;
+        p.out_b = (long long)a.len[0] * S;
+      }
+      p.tw_mult = 0;
+      e = launch_sfs_pass<DIR>(L, a.t_re, a.t_im, a.out_re, a.out_im, a.tw[i], a, a.outer, false, p);
+    }
+    if (e != hipSuccess) return e;
+    K *= L;
+    M_prev = M;
+  }
+  return hipSuccess;
+}
+
 hipError_t launch_strided_fourstep(const StridedFourStepArgs& a) {
-  if (a.stride < kMinStridedFourStepStride || a.outer < 1) return hipErrorInvalidValue;
+  if (a.stride < kMinStridedFourStepStride || a.outer < 1 || a.npass < 2 || a.npass > 3) return hipErrorInvalidValue;
+  for (int i = 0; i < a.npass; ++i)
+    if (a.len[i] < 64 || a.len[i] > 4096) return hipErrorInvalidValue;
   return a.dir < 0 ? launch_strided_fs_dir<-1>(a) : launch_strided_fs_dir<1>(a);
 }
 

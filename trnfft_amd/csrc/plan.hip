@@ -70,7 +70,8 @@ struct C2cTables {
   float2* tw_lds = nullptr;  // LDS path, strided / 2-D row kernel layout
   int n1 = 0, n2 = 0, lo_bits = 0;
   float2 *tw1 = nullptr, *tw2 = nullptr, *tw_lo = nullptr, *tw_hi = nullptr;
-  float2 *tws1 = nullptr, *tws2 = nullptr;  // n1 / n2 tables in the strided kernels' lds_epth layout
+  int s_np = 0, s_len[3] = {0, 0, 0};  // strided multi-pass split of n > 4096 (2 or 3 factors)
+  float2* s_tw[3] = {nullptr, nullptr, nullptr};  // its per-factor tables (lds_epth layout)
 };
 
 }  // namespace
@@ -123,14 +124,53 @@ struct tfa_plan {
       int rc = upload(lds_table((int)n, dir, tfa::c2c_epth((int)n)), &t->tw);
       if (!rc && tfa::c2c_epth((int)n) != tfa::lds_epth((int)n)) rc = upload(lds_table((int)n, dir), &t->tw_lds);
       else t->tw_lds = t->tw;
-      // lengths beyond the strided kernel's reach (n > 4096) also carry the four-step split
-      // tables: a strided axis of that length runs as two strided passes
       if (rc || n <= tfa::kMaxStridedN) return rc;
-      return build_split(n, dir, t);
+      if ((rc = build_roots(n, dir, t))) return rc;
+      return build_strided_split(n, dir, t);
     }
     if (n > kMaxFourStepN) return fail(TFA_ERR_UNSUPPORTED, "power-of-two length above 2^24 not supported");
     t->fourstep = true;
-    return build_split(n, dir, t);
+    int rc = build_split(n, dir, t);
+    if (!rc) rc = build_strided_split(n, dir, t);
+    return rc;
+  }
+
+  // W_n^j = W^lo * W^hi tables (j = hi << lo_bits | lo)
+  int build_roots(int64_t n, int dir, C2cTables* t) {
+    const int lg = tfa::ilog2(n);
+    t->lo_bits = (lg + 1) / 2;
+    std::vector<float2> lo((size_t)1 << t->lo_bits), hi((size_t)(n >> t->lo_bits));
+    for (size_t j = 0; j < lo.size(); ++j) lo[j] = unit_root((int64_t)j, n, dir);
+    for (size_t j = 0; j < hi.size(); ++j) hi[j] = unit_root((int64_t)j << t->lo_bits, n, dir);
+    int rc = upload(lo, &t->tw_lo);
+    return rc ? rc : upload(hi, &t->tw_hi);
+  }
+
+  // factors of a strided axis n > 4096 (multi-pass strided path): two, n1 = 2^floor(lg/2) <= n2,
+  // below 2^21; three of 128..256 from 2^21 (every pass with 64-column tiles)
+  int build_strided_split(int64_t n, int dir, C2cTables* t) {
+    const int lg = tfa::ilog2(n);
+    int bits[3];
+    if (lg >= tfa::kStridedThreePassLg) {
+      t->s_np = 3;
+      bits[0] = lg / 3;
+      bits[1] = (lg - bits[0]) / 2;
+      bits[2] = lg - bits[0] - bits[1];
+    } else {
+      t->s_np = 2;
+      bits[0] = lg / 2;
+      bits[1] = lg - bits[0];
+    }
+    for (int i = 0; i < t->s_np; ++i) {
+      t->s_len[i] = 1 << bits[i];
+      if (i > 0 && t->s_len[i] == t->s_len[i - 1]) {
+        t->s_tw[i] = t->s_tw[i - 1];
+        continue;
+      }
+      int rc = upload(lds_table(t->s_len[i], dir), &t->s_tw[i]);
+      if (rc) return rc;
+    }
+    return TFA_OK;
   }
 
   // n = n1 * n2 (n1 = 2^floor(lg/2) <= n2): LDS-FFT tables of both lengths (tfa::fourstep_epth
@@ -143,15 +183,7 @@ struct tfa_plan {
     int rc;
     if ((rc = upload(lds_table(t->n1, dir, tfa::fourstep_epth(t->n1)), &t->tw1))) return rc;
     if ((rc = upload(lds_table(t->n2, dir, tfa::fourstep_epth(t->n2)), &t->tw2))) return rc;
-    t->tws1 = t->tw1;
-    t->tws2 = t->tw2;
-    if (tfa::lds_epth(t->n1) != tfa::fourstep_epth(t->n1) && (rc = upload(lds_table(t->n1, dir), &t->tws1))) return rc;
-    if (tfa::lds_epth(t->n2) != tfa::fourstep_epth(t->n2) && (rc = upload(lds_table(t->n2, dir), &t->tws2))) return rc;
-    std::vector<float2> lo((size_t)1 << t->lo_bits), hi((size_t)(n >> t->lo_bits));
-    for (size_t j = 0; j < lo.size(); ++j) lo[j] = unit_root((int64_t)j, n, dir);
-    for (size_t j = 0; j < hi.size(); ++j) hi[j] = unit_root((int64_t)j << t->lo_bits, n, dir);
-    if ((rc = upload(lo, &t->tw_lo))) return rc;
-    return upload(hi, &t->tw_hi);
+    return build_roots(n, dir, t);
   }
 };
 
@@ -548,8 +580,9 @@ int tfa_execute_strided_ws(const tfa_plan* plan, int64_t outer, int64_t stride, 
   const size_t plane = (size_t)outer * (size_t)plan->d.n * (size_t)stride;
   float* t_re = static_cast<float*>(workspace);
   const float scale = plan->d.inverse ? (float)(1.0 / (double)plan->d.n) : 1.0f;
-  tfa::StridedFourStepArgs a{in_re, in_im, t_re, t_re + plane, out_re, out_im, t.tws1, t.tws2, t.tw_lo, t.tw_hi,
-                             t.n1, t.n2, t.lo_bits, outer, stride, scale, t.dir, static_cast<hipStream_t>(stream)};
+  tfa::StridedFourStepArgs a{in_re, in_im, t_re, t_re + plane, out_re, out_im, t.s_np, {t.s_len[0], t.s_len[1], t.s_len[2]},
+                             {t.s_tw[0], t.s_tw[1], t.s_tw[2]}, t.tw_lo, t.tw_hi, t.lo_bits, outer, stride, scale, t.dir,
+                             static_cast<hipStream_t>(stream)};
   hipError_t e = tfa::launch_strided_fourstep(a);
   if (e == hipErrorInvalidValue) return fail(TFA_ERR_UNSUPPORTED, "strided four-step: shape beyond the launch grid");
   return e == hipSuccess ? TFA_OK : hip_fail(e, "strided four-step launch");
