@@ -68,6 +68,19 @@ def test_fft2_shape_gates():
     assert fft2_ok(4, 4) and fft2_ok(16, 2048) and fft2_ok(4096, 16) and not fft2_ok(4, 2048)
 
 
+def test_strided_axis_gates():
+    # strided-axis kernels in place of transposes: power-of-two n <= 4096 and other n <= 2048 at
+    # any stride; power-of-two n up to 2^24 with >= 4 trailing columns (>= 8 from 2^21)
+    from trnfft_amd.fft_core import strided_ok
+
+    for n, s in [(2, 1), (4096, 1), (3, 7), (2047, 1), (2048, 1), (8192, 4), (1 << 20, 4), (1 << 21, 8),
+                 (1 << 24, 8), (1 << 24, 1000)]:
+        assert strided_ok(n, s), (n, s)
+    for n, s in [(8192, 3), (1 << 20, 1), (1 << 21, 7), (1 << 24, 4), (1 << 25, 64), (2049, 16), (4099, 64),
+                 (1, 4), (16, 0)]:
+        assert not strided_ok(n, s), (n, s)
+
+
 def test_backend_selection_semantics():
     assert trnfft_amd.get_backend() == "auto"
     with pytest.raises(AssertionError):

@@ -122,11 +122,11 @@ def test_non_pow2_axis_strided_bluestein(shape):
     assert _np_rel(got, np.fft.fft(re.astype(np.float64), axis=1)) <= 3 * tol_bluestein(n), shape
 
 
-# power-of-two axes longer than 4096 along a strided dimension (stride >= 16): the two-pass
+# power-of-two axes longer than 4096 along a strided dimension (stride >= 4): the two-pass
 # strided four-step (n = n1 * n2, every split from 64 x 128 up), against numpy float64 at sizes
-# numpy finishes quickly, with ragged strides and real input
+# numpy finishes quickly, with ragged strides (down to the minimum of 4) and real input
 @pytest.mark.parametrize("shape", [(3, 8192, 16), (2, 16384, 17), (1, 32768, 48), (2, 65536, 16), (1, 131072, 24),
-                                   (1, 262144, 16)])
+                                   (1, 262144, 16), (5, 8192, 4), (3, 65536, 5), (1, 262144, 7)])
 def test_long_pow2_axis_strided_fourstep_vs_numpy(shape):
     from trnfft_amd.fft_core import strided_ok
 
@@ -145,12 +145,16 @@ def test_long_pow2_axis_strided_fourstep_vs_numpy(shape):
     assert _np_rel(got, np.fft.fft(re.astype(np.float64), axis=1)) <= tol_pow2(n), shape
 
 
-# the largest splits (2^19 .. 2^24 along the axis, 16 trailing columns: up to 2^28 elements), where
-# numpy float64 is too slow: against the contiguous four-step on the moved axis (a different
-# kernel pair over the same split) and through the inverse round trip
-@pytest.mark.parametrize("lg", [19, 20, 21, 22, 23, 24])
-def test_long_pow2_axis_strided_fourstep_large(lg):
-    n, stride = 1 << lg, 16
+# the largest splits (2^19 .. 2^24 along the axis, up to 2^28 elements; three factors from 2^21,
+# with the minimum 8 columns there), where numpy float64 is too slow: against the contiguous
+# four-step on the moved axis (different kernels over another split) and through the inverse
+# round trip
+@pytest.mark.parametrize("lg,stride", [(19, 16), (20, 16), (21, 16), (21, 8), (22, 16), (22, 9), (23, 16), (24, 16)])
+def test_long_pow2_axis_strided_fourstep_large(lg, stride):
+    from trnfft_amd.fft_core import strided_ok
+
+    n = 1 << lg
+    assert strided_ok(n, stride)
     g = torch.Generator(device="cuda").manual_seed(lg)
     re = torch.randn((1, n, stride), generator=g, device="cuda")
     im = torch.randn((1, n, stride), generator=g, device="cuda")
@@ -201,7 +205,7 @@ def test_strided_fourstep_abi_in_place_and_workspace():
     # short axes and small strides need no workspace
     small = native_plan(_lib.KIND_C2C, 4096, False, 0)
     assert lib.tfa_strided_workspace_size(small.handle, outer, stride, ctypes.byref(nbytes)) == 0 and nbytes.value == 0
-    assert lib.tfa_strided_workspace_size(plan.handle, outer, 15, ctypes.byref(nbytes)) == 0 and nbytes.value == 0
+    assert lib.tfa_strided_workspace_size(plan.handle, outer, 3, ctypes.byref(nbytes)) == 0 and nbytes.value == 0
 
 
 def test_fft2_non_pow2_image():

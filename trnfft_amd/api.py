@@ -460,7 +460,7 @@ def _fft_along_dim(x, dim: int, inverse: bool) -> ComplexTensor:
 
     The last axis runs the contiguous kernels; another axis runs the strided kernels in place of
     the reference's transpose / FFT / transpose-back copies (power-of-two n <= 4096, other
-    n <= 2048, and power-of-two n <= 2^24 over at least 16 trailing columns); the remaining
+    n <= 2048, and power-of-two n <= 2^24 over at least 4 or 8 trailing columns); the remaining
     shapes keep the transpose round trip.
     """
     real_in = _is_real_tensor(x)

@@ -95,10 +95,12 @@ hipError_t launch_strided(int n1, const StridedArgs& a);
 // Longest axis the single-pass strided kernel takes; longer power-of-two axes (up to 2^24) run
 // as two or three strided passes (strided multi-pass four-step) through a workspace.
 constexpr int kMaxStridedN = 4096;
-// Smallest trailing stride of the strided multi-pass path (column tiles of 16..64 floats).
-constexpr long long kMinStridedFourStepStride = 16;
 // Axes of 2^kStridedThreePassLg and more use three factors (each <= 256: 64-column tiles).
 constexpr int kStridedThreePassLg = 21;
+// Smallest trailing stride of the strided multi-pass path: the last pass reads runs of `stride`
+// floats, and below these strides the transpose round trip measured faster (2^22 x 2: 112 vs
+// 167 us; 2^20 x 1: 35 vs 37 us; from 4 / 8 columns the strided passes win 1.3-1.8x).
+__host__ __device__ constexpr long long strided_fs_min_stride(int npass) { return npass >= 3 ? 8 : 4; }
 struct StridedFourStepArgs {
   const float* in_re;
   const float* in_im;  // nullptr: real input

@@ -210,7 +210,7 @@ static hipError_t launch_strided_fs_dir(const StridedFourStepArgs& a) {
 }
 
 hipError_t launch_strided_fourstep(const StridedFourStepArgs& a) {
-  if (a.stride < kMinStridedFourStepStride || a.outer < 1 || a.npass < 2 || a.npass > 3) return hipErrorInvalidValue;
+  if (a.npass < 2 || a.npass > 3 || a.stride < strided_fs_min_stride(a.npass) || a.outer < 1) return hipErrorInvalidValue;
   for (int i = 0; i < a.npass; ++i)
     if (a.len[i] < 64 || a.len[i] > 4096) return hipErrorInvalidValue;
   return a.dir < 0 ? launch_strided_fs_dir<-1>(a) : launch_strided_fs_dir<1>(a);

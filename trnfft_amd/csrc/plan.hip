@@ -552,7 +552,9 @@ namespace {
 
 // power-of-two C2C axis longer than the single-pass strided kernel: two strided passes
 bool strided_fourstep(const tfa_plan* plan, int64_t stride) {
-  return plan->d.kind == TFA_KIND_C2C && plan->d.n > tfa::kMaxStridedN && stride >= tfa::kMinStridedFourStepStride;
+  if (plan->d.kind != TFA_KIND_C2C || plan->d.n <= tfa::kMaxStridedN) return false;
+  const C2cTables& t = plan->d.inverse ? plan->inv : plan->fwd;
+  return stride >= tfa::strided_fs_min_stride(t.s_np);
 }
 
 }  // namespace
@@ -596,7 +598,7 @@ int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, con
   if (!blue && (plan->d.kind != TFA_KIND_C2C || plan->d.n > tfa::kMaxStridedN || plan->d.n < 2))
     return fail(TFA_ERR_UNSUPPORTED,
                 "strided transforms need a power-of-two C2C plan with 2 <= n <= 4096 or a Bluestein plan with n <= 2048 "
-                "(longer power-of-two axes with stride >= 16: tfa_execute_strided_ws)");
+                "(longer power-of-two axes with stride >= 4, >= 8 from 2^21: tfa_execute_strided_ws)");
   if (outer == 0) return TFA_OK;
   if (!in_re || !out_re || !out_im) return fail(TFA_ERR_INVALID, "null data pointer");
   int dev = -1;

@@ -133,18 +133,23 @@ def execute_c2r(re: torch.Tensor, im: torch.Tensor, n: int) -> torch.Tensor:
 
 
 # longest power-of-two axis the single-pass strided kernel transforms in place of a transpose
-# round trip, longest other axis (Bluestein padded length m <= 4096), and the strided four-step's
-# reach (longer power-of-two axes with at least 16 trailing columns, two passes + workspace)
+# round trip, longest other axis (Bluestein padded length m <= 4096), and the strided multi-pass
+# path's reach (longer power-of-two axes: two passes with >= 4 trailing columns, three passes from
+# 2^21 with >= 8; mirror of tfa::strided_fs_min_stride)
 _STRIDED_MAX_N = 4096
 _STRIDED_BLUE_MAX_N = 2048
 _STRIDED_FS_MAX_N = 1 << 24
-_STRIDED_FS_MIN_STRIDE = 16
+_STRIDED_FS_THREE_PASS_N = 1 << 21
+
+
+def _strided_fs_min_stride(n: int) -> int:
+    return 8 if n >= _STRIDED_FS_THREE_PASS_N else 4
 
 
 def execute_strided(re: torch.Tensor, im: torch.Tensor | None, dim: int, inverse: bool) -> ComplexTensor:
     """Transform along a non-last axis `dim` without moving it: power-of-two n <= 4096 and
-    other n <= 2048 in one strided pass, power-of-two 4096 < n <= 2^24 (stride >= 16) as a
-    two-pass strided four-step through a workspace.
+    other n <= 2048 in one strided pass, power-of-two 4096 < n <= 2^24 (stride >= 4, >= 8 from
+    2^21) as a two- or three-pass strided four-step through a workspace.
 
     The contiguous tensor is viewed as (outer, n, stride); every column is transformed along
     its n elements (replaces trnfft/api.py:496-516's transposes).
@@ -254,7 +259,7 @@ def strided_ok(n: int, stride: int) -> bool:
     if stride < 1 or n < 2:
         return False
     if (n & (n - 1)) == 0:
-        return n <= _STRIDED_MAX_N or (n <= _STRIDED_FS_MAX_N and stride >= _STRIDED_FS_MIN_STRIDE)
+        return n <= _STRIDED_MAX_N or (n <= _STRIDED_FS_MAX_N and stride >= _strided_fs_min_stride(n))
     return n <= _STRIDED_BLUE_MAX_N
 
 
