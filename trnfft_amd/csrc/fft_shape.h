@@ -57,6 +57,9 @@ __host__ __device__ constexpr bool real_pf(int h) { return h >= 8192; }
 // Elements per thread of the forward STFT's pair transforms (many lanes per transform measured
 // fastest at every n_fft).
 __host__ __device__ constexpr int stft_epth(int n) { return n < 8 ? n : 8; }
+// next-pass twiddle prefetch in the STFT transforms from n_fft = 1024 (8 or fewer pairs per
+// workgroup: n_fft 1024 84 -> 77 us; at 512 it measured 1 % slower)
+__host__ __device__ constexpr bool stft_pf(int n) { return n >= 1024; }
 
 // Elements per thread of the 2-D transform's paired real-row pass 1 and column pass 2 (the
 // many-lanes-per-transform shape that also won for the STFT).
@@ -76,10 +79,14 @@ __host__ __device__ constexpr bool fft2_small_ok(long long h, long long w) {
 // Fused Bluestein launch shape.  m = 2048 (n = 1000): E = 8 with 512-thread workgroups measured
 // 16.2 -> 14.7 us against the batched-c2c shape (E = 16, 256 threads).  m >= 8192 (one row per
 // workgroup, latency-bound): E = 32 / 512 threads with the next-pass twiddle prefetch, m = 16384
-// 30.5 -> 26.9 us against E = 16 without it.  Other lengths keep the batched-c2c shape.
+// 30.5 -> 26.9 us against E = 16 without it.  Other lengths keep the batched-c2c shape.  The
+// prefetch pays from m = 256 (every workgroup runs the same pass at the same time, so each pass's
+// table latency is exposed): C3a 1024 x 1000 12.9 -> 12.3 us, 6990 x 600 66.8 -> 57.0,
+// 8388 x 500 50.1 -> 49.0, 41943 x 100 48.1 -> 46.7.  (The tables staged in LDS once per
+// workgroup instead measured slower, C3a 13.0 -> 17.0 us: the 41 KB copy costs more.)
 __host__ __device__ constexpr int blue_epth(int m) { return m == 2048 ? 8 : m >= 8192 ? 32 : lds_epth(m); }
 __host__ __device__ constexpr int blue_threads(int m) { return m == 2048 || m >= 8192 ? 512 : 256; }
-__host__ __device__ constexpr bool blue_pf(int m) { return m >= 8192; }
+__host__ __device__ constexpr bool blue_pf(int m) { return m >= 256; }
 
 // Inverse-STFT launch shape from a sweep on MI355X (64 x 160000 samples, hop n/2, n_fft 16..4096,
 // E in {4, 8, 16} x 128..1024 threads): E = 8 elements per thread up to n = 2048, 16 at 4096;
@@ -87,6 +94,9 @@ __host__ __device__ constexpr bool blue_pf(int m) { return m >= 8192; }
 // 256: 65 -> 48, 1024: 73 -> 63, 4096: 122 -> 100 against the former shapes).
 __host__ __device__ constexpr int istft_epth(int n) { return n <= 2048 ? 8 : 16; }
 __host__ __device__ constexpr int istft_threads(int n) { return n <= 64 ? 256 : n <= 1024 ? 512 : 1024; }
+// next-pass twiddle prefetch in the inverse STFT from n_fft = 512 (C2's inverse 53.4 -> 52.6 us,
+// n_fft 1024 127 -> 122)
+__host__ __device__ constexpr bool istft_pf(int n) { return n >= 512; }
 
 // Elements per thread of the four-step passes over transforms of length l (128..4096): 32 threads
 // per transform up to l = 1024 (one 32-transform tile = 1024 threads), 32 elements above.

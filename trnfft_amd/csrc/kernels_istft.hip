@@ -86,7 +86,7 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
     }
   }
   exchange_sync<WL>();  // the transform reuses this pair's region
-  LdsFft<NFFT, E, 1, WL, false, true>::run(v, reg, nullptr, tw, tid);  // interleaved exchange
+  LdsFft<NFFT, E, 1, WL, false, true, istft_pf(NFFT)>::run(v, reg, nullptr, tw, tid);  // interleaved exchange
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     reg[tid + T * e] = v[e].x;         // frame 2p

@@ -116,7 +116,7 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS, E_>::THREADS)) void stft_kern
     }
   }
   float2* my = lds2 + pl * PADN;
-  LdsFft<NFFT, E, -1, (T <= 64), false, true>::run(v, reinterpret_cast<float*>(my), nullptr, tw, tid);
+  LdsFft<NFFT, E, -1, (T <= 64), false, true, stft_pf(NFFT)>::run(v, reinterpret_cast<float*>(my), nullptr, tw, tid);
 #pragma unroll
   for (int e = 0; e < E; ++e) my[lds_pad(tid + T * e)] = v[e];
   __syncthreads();
