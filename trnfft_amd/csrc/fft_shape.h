@@ -76,15 +76,16 @@ __host__ __device__ constexpr bool fft2_small_ok(long long h, long long w) {
          h >= fft2_small_epth((int)h, (int)w) && w >= fft2_small_epth((int)h, (int)w);
 }
 
-// Fused Bluestein launch shape.  m = 2048 (n = 1000): E = 8 with 512-thread workgroups measured
-// 16.2 -> 14.7 us against the batched-c2c shape (E = 16, 256 threads).  m >= 8192 (one row per
-// workgroup, latency-bound): E = 32 / 512 threads with the next-pass twiddle prefetch, m = 16384
-// 30.5 -> 26.9 us against E = 16 without it.  Other lengths keep the batched-c2c shape.  The
-// prefetch pays from m = 256 (every workgroup runs the same pass at the same time, so each pass's
-// table latency is exposed): C3a 1024 x 1000 12.9 -> 12.3 us, 6990 x 600 66.8 -> 57.0,
-// 8388 x 500 50.1 -> 49.0, 41943 x 100 48.1 -> 46.7.  (The tables staged in LDS once per
-// workgroup instead measured slower, C3a 13.0 -> 17.0 us: the 41 KB copy costs more.)
-__host__ __device__ constexpr int blue_epth(int m) { return m == 2048 ? 8 : m >= 8192 ? 32 : lds_epth(m); }
+// Fused Bluestein launch shape, from in-run A/B sweeps on MI355X with the next-pass twiddle
+// prefetch on.  E = 8 elements per thread for m = 128..8192: more lanes per row (a row per
+// workgroup from m = 512 at 256/512 threads, 1024 at m = 8192) and ~90 VGPRs, against E = 16/32
+// with 100-244: m = 128 7.2 -> 4.8 us (1024 rows), 256 8.2 -> 5.2, 512 17.0 -> 6.1, 1024 11.5 ->
+// 8.6, 4096 (256 rows) 23.1 -> 9.3, 8192 (256 rows) 27.6 -> 14.7; m = 16384 (C3b) E = 16 with
+// 1024 threads, 31.7 -> 29.5 us against E = 32 / 512.  The prefetch pays from m = 256 (every
+// workgroup runs the same pass at the same time, so each pass's table latency is exposed): C3a
+// 1024 x 1000 12.9 -> 12.3 us.  (Twiddle tables staged in LDS once per workgroup measured
+// slower, C3a 13.0 -> 17.0 us: the 41 KB copy costs more than it saves.)
+__host__ __device__ constexpr int blue_epth(int m) { return m >= 16384 ? 16 : m >= 128 ? 8 : lds_epth(m); }
 __host__ __device__ constexpr int blue_threads(int m) { return m == 2048 || m >= 8192 ? 512 : 256; }
 __host__ __device__ constexpr bool blue_pf(int m) { return m >= 256; }
 
