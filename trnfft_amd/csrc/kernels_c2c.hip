@@ -18,8 +18,9 @@ namespace tfa {
 // LDS-resident batched transform
 // ---------------------------------------------------------------------------------------------
 // TAIL = false: every transform slot of the grid is inside the batch (no guards at all; the
-// guard-free instruction stream measured fastest).  TAIL = true: one workgroup for the ragged
-// remainder, slots past the batch end neither load nor store.
+// guard-free instruction stream measured fastest).  TAIL = true: the launch for a ragged batch,
+// whose slots past the batch end neither load nor store (one launch instead of a full-block
+// launch plus a one-workgroup tail launch: 4095 x 1024 18.2 -> 13.3 us).
 template <int N, int DIR, bool REAL_IN, bool TAIL, int E_ = c2c_epth(N), int THR = c2c_threads(N)>
 __global__ __launch_bounds__((C2cThreads<N, E_, THR>::THREADS)) void c2c_lds_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re,
@@ -131,13 +132,13 @@ __global__ __launch_bounds__(C2cSmallCfg<N>::THREADS) void c2c_small_kernel(
 template <int N, int DIR, bool REAL_IN>
 static hipError_t launch_c2c_small_t(const C2cArgs& a) {
   constexpr int THREADS = C2cSmallCfg<N>::THREADS, XS = C2cSmallCfg<N>::XS;
-  const long long full = a.batch / XS;
-  if (full > 0)
-    hipLaunchKernelGGL((c2c_small_kernel<N, DIR, REAL_IN, false>), dim3((unsigned)full), dim3(THREADS), 0,
+  const long long blocks = (a.batch + XS - 1) / XS;
+  if (blocks * XS == a.batch)
+    hipLaunchKernelGGL((c2c_small_kernel<N, DIR, REAL_IN, false>), dim3((unsigned)blocks), dim3(THREADS), 0,
                        a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, 0LL, a.batch, a.scale);
-  if (full * XS < a.batch)
-    hipLaunchKernelGGL((c2c_small_kernel<N, DIR, REAL_IN, true>), dim3(1), dim3(THREADS), 0, a.stream,
-                       a.in_re, a.in_im, a.out_re, a.out_im, a.tw, full * XS, a.batch, a.scale);
+  else  // ragged batch: one launch whose slots past the end neither load nor store
+    hipLaunchKernelGGL((c2c_small_kernel<N, DIR, REAL_IN, true>), dim3((unsigned)blocks), dim3(THREADS), 0,
+                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, 0LL, a.batch, a.scale);
   return hipGetLastError();
 }
 
@@ -147,13 +148,13 @@ static hipError_t launch_c2c_lds_t(const C2cArgs& a) {
     return launch_c2c_small_t<N, DIR, REAL_IN>(a);
   } else {
     using C = C2cThreads<N>;
-    const long long full = a.batch / C::XF;
-    if (full > 0)
-      hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN, false>), dim3((unsigned)full), dim3(C::THREADS), 0,
+    const long long blocks = (a.batch + C::XF - 1) / C::XF;
+    if (blocks * C::XF == a.batch)
+      hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN, false>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
                          a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, 0LL, a.batch, a.scale);
-    if (full * C::XF < a.batch)
-      hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN, true>), dim3(1), dim3(C::THREADS), 0, a.stream,
-                         a.in_re, a.in_im, a.out_re, a.out_im, a.tw, full * C::XF, a.batch, a.scale);
+    else  // ragged batch: one launch whose slots past the end neither load nor store
+      hipLaunchKernelGGL((c2c_lds_kernel<N, DIR, REAL_IN, true>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
+                         a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw, 0LL, a.batch, a.scale);
     return hipGetLastError();
   }
 }

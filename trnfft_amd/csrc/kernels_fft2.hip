@@ -302,23 +302,22 @@ template <int H, int W, int DIR>
 static hipError_t launch_fft2_small_hw(const Fft2Args& a) {
   if constexpr (fft2_small_ok(H, W)) {
     using C = Fft2SmallCfg<H, W>;
-    const long long full = a.batch / C::IMG;
+    const long long blocks = (a.batch + C::IMG - 1) / C::IMG;
     const bool real_in = a.in_im == nullptr;
-    if (full > 0) {
+    if (blocks * C::IMG == a.batch) {
       if (real_in)
-        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, true, false>), dim3((unsigned)full), dim3(1024), 0, a.stream,
-                           a.in_re, a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, 0LL, a.batch, a.scale);
-      else
-        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, false, false>), dim3((unsigned)full), dim3(1024), 0,
+        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, true, false>), dim3((unsigned)blocks), dim3(1024), 0,
                            a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, 0LL, a.batch, a.scale);
-    }
-    if (full * C::IMG < a.batch) {  // ragged tail: one workgroup
-      if (real_in)
-        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, true, true>), dim3(1), dim3(1024), 0, a.stream, a.in_re,
-                           a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, full * C::IMG, a.batch, a.scale);
       else
-        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, false, true>), dim3(1), dim3(1024), 0, a.stream, a.in_re,
-                           a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, full * C::IMG, a.batch, a.scale);
+        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, false, false>), dim3((unsigned)blocks), dim3(1024), 0,
+                           a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, 0LL, a.batch, a.scale);
+    } else {  // ragged batch: one launch of the guarded variant
+      if (real_in)
+        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, true, true>), dim3((unsigned)blocks), dim3(1024), 0,
+                           a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, 0LL, a.batch, a.scale);
+      else
+        hipLaunchKernelGGL((fft2_small_kernel<H, W, DIR, false, true>), dim3((unsigned)blocks), dim3(1024), 0,
+                           a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.tw_sw, a.tw_sh, 0LL, a.batch, a.scale);
     }
     return hipGetLastError();
   } else {

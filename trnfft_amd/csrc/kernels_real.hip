@@ -22,6 +22,10 @@ struct RealCfg {
   static constexpr int XF = T >= THR ? 1 : THR / T;  // transforms per workgroup
   static constexpr int THREADS = XF * T;
   static constexpr int PADR = lds_pad(H) + 1;  // room for bins 0..H
+  // rows of H+1 bins with H <= 64: a store (r2c) or load (c2r) instruction would cover segments
+  // of 64 bytes or less at odd alignment, one per row; the workgroup's XF rows of bins are one
+  // contiguous run per plane, staged through LDS and moved as such
+  static constexpr bool STAGE = H <= 64 && XF > 1;
 };
 
 __device__ __forceinline__ float2 ld_stream2(const float2* p) {
@@ -58,9 +62,11 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
   constexpr int E = C::E, T = C::T;
   constexpr bool WL = T <= 64;
   __shared__ float2 lds[C::XF * C::PADR];  // interleaved (re, im)
+  __shared__ float2 stage[C::STAGE ? C::XF * (H + 1) : 1];  // the workgroup's bins, row after row
   const int tid = threadIdx.x % T;
   const int xf = threadIdx.x / T;
-  const long long b = first + (long long)blockIdx.x * C::XF + xf;
+  const long long b0 = first + (long long)blockIdx.x * C::XF;
+  const long long b = b0 + xf;
   const bool valid = !TAIL || b < batch;
   float2* m = lds + xf * C::PADR;
   const float2* src = reinterpret_cast<const float2*>(x + (size_t)b * (2 * H)) + tid;
@@ -71,7 +77,7 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
 #pragma unroll
   for (int e = 0; e < E; ++e) m[lds_pad(tid + T * e)] = v[e];
   exchange_sync<WL>();
-  if (!valid) return;
+  if (!C::STAGE && !valid) return;
   float* qr = out_re + (size_t)b * (H + 1) + tid;
   float* qi = out_im + (size_t)b * (H + 1) + tid;
   float2 wk[E];
@@ -85,10 +91,28 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
     const float2 ev = make_float2(0.5f * (a.x + c.x), 0.5f * (a.y + c.y));
     const float2 od = make_float2(0.5f * (a.y - c.y), -0.5f * (a.x - c.x));  // (a - c) / 2i
     const float2 y = cadd(ev, cmul(wk[e], od));
-    st_stream(qr + T * e, y.x);
-    st_stream(qi + T * e, y.y);
+    if constexpr (C::STAGE) {
+      stage[xf * (H + 1) + k] = y;
+    } else {
+      st_stream(qr + T * e, y.x);
+      st_stream(qi + T * e, y.y);
+    }
   }
-  if (tid == 0) {
+  if constexpr (C::STAGE) {
+    if (tid == 0) stage[xf * (H + 1) + H] = make_float2(v[0].x - v[0].y, 0.0f);
+    __syncthreads();
+    // the rows b0 .. b0 + rows - 1 of bins are one contiguous run of rows * (H + 1) floats per plane
+    const long long left = batch - b0;
+    const int rows = TAIL ? (int)(left < C::XF ? left : C::XF) : C::XF;
+    const int count = rows * (H + 1);
+    float* orr = out_re + (size_t)b0 * (H + 1);
+    float* oii = out_im + (size_t)b0 * (H + 1);
+    for (int i = threadIdx.x; i < count; i += C::THREADS) {
+      const float2 y = stage[i];
+      st_stream(orr + i, y.x);
+      st_stream(oii + i, y.y);
+    }
+  } else if (tid == 0) {
     st_stream(qr + H, v[0].x - v[0].y);
     st_stream(qi + H, 0.0f);
   }
@@ -105,20 +129,42 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
   __shared__ float2 lds[C::XF * C::PADR];  // interleaved (re, im)
   const int tid = threadIdx.x % T;
   const int xf = threadIdx.x / T;
-  const long long b = first + (long long)blockIdx.x * C::XF + xf;
+  const long long b0 = first + (long long)blockIdx.x * C::XF;
+  const long long b = b0 + xf;
   const bool valid = !TAIL || b < batch;
   float2* m = lds + xf * C::PADR;
-  const float* pr = in_re + (size_t)b * (H + 1) + tid;
-  const float* pi = in_im + (size_t)b * (H + 1) + tid;
   float2 a[E];
+  if constexpr (C::STAGE) {
+    // the rows b0 .. b0 + rows - 1 of bins are one contiguous run of rows * (H + 1) floats per
+    // plane: loaded as such into each row's LDS area (bin k of row r at r * PADR + lds_pad(k))
+    const long long left = batch - b0;
+    const int rows = TAIL ? (int)(left < C::XF ? left : C::XF) : C::XF;
+    const int count = rows * (H + 1);
+    const float* prr = in_re + (size_t)b0 * (H + 1);
+    const float* pii = in_im + (size_t)b0 * (H + 1);
+    for (int i = threadIdx.x; i < count; i += C::THREADS) {
+      const int r = i / (H + 1), k = i - r * (H + 1);
+      lds[r * C::PADR + lds_pad(k)] = make_float2(ld_stream(prr + i), ld_stream(pii + i));
+    }
+    __syncthreads();
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    a[e] = valid ? make_float2(ld_stream(pr + T * e), ld_stream(pi + T * e)) : make_float2(0.0f, 0.0f);
-    m[lds_pad(tid + T * e)] = a[e];
-  }
-  if (tid == 0) {
-    m[lds_pad(H)] = make_float2(valid ? ld_stream(pr + H) : 0.0f, 0.0f);  // Im X[H] is never read
-    a[0].y = 0.0f;                                                        // Im X[0] drops out
+    for (int e = 0; e < E; ++e) a[e] = valid ? m[lds_pad(tid + T * e)] : make_float2(0.0f, 0.0f);
+    if (tid == 0) {
+      m[lds_pad(H)].y = 0.0f;  // Im X[H] is never read
+      a[0].y = 0.0f;           // Im X[0] drops out
+    }
+  } else {
+    const float* pr = in_re + (size_t)b * (H + 1) + tid;
+    const float* pi = in_im + (size_t)b * (H + 1) + tid;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      a[e] = valid ? make_float2(ld_stream(pr + T * e), ld_stream(pi + T * e)) : make_float2(0.0f, 0.0f);
+      m[lds_pad(tid + T * e)] = a[e];
+    }
+    if (tid == 0) {
+      m[lds_pad(H)] = make_float2(valid ? ld_stream(pr + H) : 0.0f, 0.0f);  // Im X[H] is never read
+      a[0].y = 0.0f;                                                        // Im X[0] drops out
+    }
   }
   exchange_sync<WL>();
   float2 v[E];
@@ -232,22 +278,24 @@ __global__ __launch_bounds__(kRealSmallRows) void c2r_small_kernel(
 
 template <int H>
 static hipError_t launch_real_small(const RealArgs& a) {
-  const long long full = a.batch / kRealSmallRows;
-  const long long first = full * kRealSmallRows;
+  // ragged batches: one launch of the guarded variant (a separate one-workgroup tail launch
+  // measured ~3.5 us extra)
+  const long long blocks = (a.batch + kRealSmallRows - 1) / kRealSmallRows;
+  const bool ragged = blocks * kRealSmallRows != a.batch;
   if (a.inverse) {
-    if (full > 0)
-      hipLaunchKernelGGL((c2r_small_kernel<H, false>), dim3((unsigned)full), dim3(kRealSmallRows), 0, a.stream,
+    if (!ragged)
+      hipLaunchKernelGGL((c2r_small_kernel<H, false>), dim3((unsigned)blocks), dim3(kRealSmallRows), 0, a.stream,
                          a.in_re, a.in_im, a.out_re, a.twr, 0LL, a.batch, a.scale);
-    if (first < a.batch)
-      hipLaunchKernelGGL((c2r_small_kernel<H, true>), dim3(1), dim3(kRealSmallRows), 0, a.stream, a.in_re, a.in_im,
-                         a.out_re, a.twr, first, a.batch, a.scale);
+    else
+      hipLaunchKernelGGL((c2r_small_kernel<H, true>), dim3((unsigned)blocks), dim3(kRealSmallRows), 0, a.stream,
+                         a.in_re, a.in_im, a.out_re, a.twr, 0LL, a.batch, a.scale);
   } else {
-    if (full > 0)
-      hipLaunchKernelGGL((r2c_small_kernel<H, false>), dim3((unsigned)full), dim3(kRealSmallRows), 0, a.stream,
+    if (!ragged)
+      hipLaunchKernelGGL((r2c_small_kernel<H, false>), dim3((unsigned)blocks), dim3(kRealSmallRows), 0, a.stream,
                          a.in_re, a.out_re, a.out_im, a.twr, 0LL, a.batch);
-    if (first < a.batch)
-      hipLaunchKernelGGL((r2c_small_kernel<H, true>), dim3(1), dim3(kRealSmallRows), 0, a.stream, a.in_re,
-                         a.out_re, a.out_im, a.twr, first, a.batch);
+    else
+      hipLaunchKernelGGL((r2c_small_kernel<H, true>), dim3((unsigned)blocks), dim3(kRealSmallRows), 0, a.stream,
+                         a.in_re, a.out_re, a.out_im, a.twr, 0LL, a.batch);
   }
   return hipGetLastError();
 }
@@ -259,24 +307,25 @@ static hipError_t launch_real_h(const RealArgs& a) {
   if constexpr (H >= 4 && H <= 16) {
     return launch_real_small<H>(a);
   } else {
+    // ragged batches: one launch of the guarded variant
     if (a.inverse) {
       using C = RealCfg<H, real_epth(H, true)>;
-      const long long full = a.batch / C::XF;
-      if (full > 0)
-        hipLaunchKernelGGL((c2r_kernel<H, false>), dim3((unsigned)full), dim3(C::THREADS), 0, a.stream, a.in_re,
+      const long long blocks = (a.batch + C::XF - 1) / C::XF;
+      if (blocks * C::XF == a.batch)
+        hipLaunchKernelGGL((c2r_kernel<H, false>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream, a.in_re,
                            a.in_im, a.out_re, a.tw, a.twr, 0LL, a.batch, a.scale);
-      if (full * C::XF < a.batch)
-        hipLaunchKernelGGL((c2r_kernel<H, true>), dim3(1), dim3(C::THREADS), 0, a.stream, a.in_re, a.in_im,
-                           a.out_re, a.tw, a.twr, full * C::XF, a.batch, a.scale);
+      else
+        hipLaunchKernelGGL((c2r_kernel<H, true>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream, a.in_re,
+                           a.in_im, a.out_re, a.tw, a.twr, 0LL, a.batch, a.scale);
     } else {
       using C = RealCfg<H, real_epth(H, false)>;
-      const long long full = a.batch / C::XF;
-      if (full > 0)
-        hipLaunchKernelGGL((r2c_kernel<H, false>), dim3((unsigned)full), dim3(C::THREADS), 0, a.stream, a.in_re,
+      const long long blocks = (a.batch + C::XF - 1) / C::XF;
+      if (blocks * C::XF == a.batch)
+        hipLaunchKernelGGL((r2c_kernel<H, false>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream, a.in_re,
                            a.out_re, a.out_im, a.tw, a.twr, 0LL, a.batch);
-      if (full * C::XF < a.batch)
-        hipLaunchKernelGGL((r2c_kernel<H, true>), dim3(1), dim3(C::THREADS), 0, a.stream, a.in_re, a.out_re,
-                           a.out_im, a.tw, a.twr, full * C::XF, a.batch);
+      else
+        hipLaunchKernelGGL((r2c_kernel<H, true>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream, a.in_re,
+                           a.out_re, a.out_im, a.tw, a.twr, 0LL, a.batch);
     }
     return hipGetLastError();
   }
