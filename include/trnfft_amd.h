@@ -107,7 +107,7 @@ int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, con
  * tfa_execute_strided extended to power-of-two TFA_KIND_C2C axes 4096 < n <= 2^24 with
  * stride >= 4 (>= 8 from n = 2^21): two strided passes (three from 2^21) through `workspace`,
  * whose size tfa_strided_workspace_size reports (2 * 4 * outer * n * stride bytes for such axes,
- * else 0).
+ * else 0).  n = 4096 with stride >= 16 also takes two passes (faster than the single pass there).
  * In place allowed (out_* == in_*); the workspace must not overlap the data.  Every other
  * plan/stride goes to tfa_execute_strided (workspace unused).  Replaces the same transposes of
  * trnfft/api.py:496-516 for long axes.

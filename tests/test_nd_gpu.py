@@ -125,8 +125,9 @@ def test_non_pow2_axis_strided_bluestein(shape):
 # power-of-two axes longer than 4096 along a strided dimension (stride >= 4): the two-pass
 # strided four-step (n = n1 * n2, every split from 64 x 128 up), against numpy float64 at sizes
 # numpy finishes quickly, with ragged strides (down to the minimum of 4) and real input
-@pytest.mark.parametrize("shape", [(3, 8192, 16), (2, 16384, 17), (1, 32768, 48), (2, 65536, 16), (1, 131072, 24),
-                                   (1, 262144, 16), (5, 8192, 4), (3, 65536, 5), (1, 262144, 7)])
+@pytest.mark.parametrize("shape", [(3, 4096, 16), (2, 4096, 40), (3, 8192, 16), (2, 16384, 17), (1, 32768, 48),
+                                   (2, 65536, 16), (1, 131072, 24), (1, 262144, 16), (5, 8192, 4), (3, 65536, 5),
+                                   (1, 262144, 7)])
 def test_long_pow2_axis_strided_fourstep_vs_numpy(shape):
     from trnfft_amd.fft_core import strided_ok
 
@@ -202,9 +203,13 @@ def test_strided_fourstep_abi_in_place_and_workspace():
     torch.cuda.synchronize()
     ref = np.fft.fft(re.astype(np.float64) + 1j * im, axis=1)
     assert rel_l2(d_re, d_im, ref.real, ref.imag) <= tol_pow2(n)
-    # short axes and small strides need no workspace
-    small = native_plan(_lib.KIND_C2C, 4096, False, 0)
+    # short axes and small strides need no workspace; n = 4096 takes the two passes from 16 columns
+    small = native_plan(_lib.KIND_C2C, 2048, False, 0)
     assert lib.tfa_strided_workspace_size(small.handle, outer, stride, ctypes.byref(nbytes)) == 0 and nbytes.value == 0
+    p4096 = native_plan(_lib.KIND_C2C, 4096, False, 0)
+    assert lib.tfa_strided_workspace_size(p4096.handle, outer, 15, ctypes.byref(nbytes)) == 0 and nbytes.value == 0
+    assert lib.tfa_strided_workspace_size(p4096.handle, outer, 16, ctypes.byref(nbytes)) == 0
+    assert nbytes.value == 2 * 4 * outer * 4096 * 16
     assert lib.tfa_strided_workspace_size(plan.handle, outer, 3, ctypes.byref(nbytes)) == 0 and nbytes.value == 0
 
 

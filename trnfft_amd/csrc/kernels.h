@@ -95,12 +95,19 @@ hipError_t launch_strided(int n1, const StridedArgs& a);
 // Longest axis the single-pass strided kernel takes; longer power-of-two axes (up to 2^24) run
 // as two or three strided passes (strided multi-pass four-step) through a workspace.
 constexpr int kMaxStridedN = 4096;
+// Shortest axis that runs the strided multi-pass path (n = 4096 as two passes of 64: its single
+// pass fits only 4 columns per workgroup).
+constexpr int kMinStridedMultiPassN = 4096;
 // Axes of 2^kStridedThreePassLg and more use three factors (each <= 256: 64-column tiles).
 constexpr int kStridedThreePassLg = 21;
 // Smallest trailing stride of the strided multi-pass path: the last pass reads runs of `stride`
-// floats, and below these strides the transpose round trip measured faster (2^22 x 2: 112 vs
-// 167 us; 2^20 x 1: 35 vs 37 us; from 4 / 8 columns the strided passes win 1.3-1.8x).
-__host__ __device__ constexpr long long strided_fs_min_stride(int npass) { return npass >= 3 ? 8 : 4; }
+// floats, and below these strides the alternative measured faster: the transpose round trip
+// above 4096 (2^22 x 2: 112 vs 167 us; 2^20 x 1: 35 vs 37 us; from 4 / 8 columns the strided
+// passes win 1.3-1.8x), the single-pass strided kernel at 4096 (stride 4: 103 vs 159 us; from
+// 16 columns the two passes win 1.16-1.38x, 4 x 4096 x 4096 629 -> 455 us).
+__host__ __device__ constexpr long long strided_fs_min_stride(int npass, long long n) {
+  return n <= 4096 ? 16 : npass >= 3 ? 8 : 4;
+}
 struct StridedFourStepArgs {
   const float* in_re;
   const float* in_im;  // nullptr: real input

@@ -210,9 +210,13 @@ static hipError_t launch_strided_fs_dir(const StridedFourStepArgs& a) {
 }
 
 hipError_t launch_strided_fourstep(const StridedFourStepArgs& a) {
-  if (a.npass < 2 || a.npass > 3 || a.stride < strided_fs_min_stride(a.npass) || a.outer < 1) return hipErrorInvalidValue;
-  for (int i = 0; i < a.npass; ++i)
+  if (a.npass < 2 || a.npass > 3 || a.outer < 1) return hipErrorInvalidValue;
+  long long n = 1;
+  for (int i = 0; i < a.npass; ++i) {
     if (a.len[i] < 64 || a.len[i] > 4096) return hipErrorInvalidValue;
+    n *= a.len[i];
+  }
+  if (a.stride < strided_fs_min_stride(a.npass, n)) return hipErrorInvalidValue;
   return a.dir < 0 ? launch_strided_fs_dir<-1>(a) : launch_strided_fs_dir<1>(a);
 }
 

@@ -70,7 +70,7 @@ struct C2cTables {
   float2* tw_lds = nullptr;  // LDS path, strided / 2-D row kernel layout
   int n1 = 0, n2 = 0, lo_bits = 0;
   float2 *tw1 = nullptr, *tw2 = nullptr, *tw_lo = nullptr, *tw_hi = nullptr;
-  int s_np = 0, s_len[3] = {0, 0, 0};  // strided multi-pass split of n > 4096 (2 or 3 factors)
+  int s_np = 0, s_len[3] = {0, 0, 0};  // strided multi-pass split of n >= 4096 (2 or 3 factors)
   float2* s_tw[3] = {nullptr, nullptr, nullptr};  // its per-factor tables (lds_epth layout)
 };
 
@@ -124,7 +124,7 @@ struct tfa_plan {
       int rc = upload(lds_table((int)n, dir, tfa::c2c_epth((int)n)), &t->tw);
       if (!rc && tfa::c2c_epth((int)n) != tfa::lds_epth((int)n)) rc = upload(lds_table((int)n, dir), &t->tw_lds);
       else t->tw_lds = t->tw;
-      if (rc || n <= tfa::kMaxStridedN) return rc;
+      if (rc || n < tfa::kMinStridedMultiPassN) return rc;
       if ((rc = build_roots(n, dir, t))) return rc;
       return build_strided_split(n, dir, t);
     }
@@ -146,7 +146,7 @@ struct tfa_plan {
     return rc ? rc : upload(hi, &t->tw_hi);
   }
 
-  // factors of a strided axis n > 4096 (multi-pass strided path): two, n1 = 2^floor(lg/2) <= n2,
+  // factors of a strided axis n >= 4096 (multi-pass strided path): two, n1 = 2^floor(lg/2) <= n2,
   // below 2^21; three of 128..256 from 2^21 (every pass with 64-column tiles)
   int build_strided_split(int64_t n, int dir, C2cTables* t) {
     const int lg = tfa::ilog2(n);
@@ -552,9 +552,9 @@ namespace {
 
 // power-of-two C2C axis longer than the single-pass strided kernel: two strided passes
 bool strided_fourstep(const tfa_plan* plan, int64_t stride) {
-  if (plan->d.kind != TFA_KIND_C2C || plan->d.n <= tfa::kMaxStridedN) return false;
+  if (plan->d.kind != TFA_KIND_C2C || plan->d.n < tfa::kMinStridedMultiPassN) return false;
   const C2cTables& t = plan->d.inverse ? plan->inv : plan->fwd;
-  return stride >= tfa::strided_fs_min_stride(t.s_np);
+  return stride >= tfa::strided_fs_min_stride(t.s_np, plan->d.n);
 }
 
 }  // namespace

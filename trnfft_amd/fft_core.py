@@ -149,7 +149,8 @@ def _strided_fs_min_stride(n: int) -> int:
 def execute_strided(re: torch.Tensor, im: torch.Tensor | None, dim: int, inverse: bool) -> ComplexTensor:
     """Transform along a non-last axis `dim` without moving it: power-of-two n <= 4096 and
     other n <= 2048 in one strided pass, power-of-two 4096 < n <= 2^24 (stride >= 4, >= 8 from
-    2^21) as a two- or three-pass strided four-step through a workspace.
+    2^21) as a two- or three-pass strided four-step through a workspace (the library also takes
+    that path for n = 4096 over 16 or more columns: it reports a non-zero workspace then).
 
     The contiguous tensor is viewed as (outer, n, stride); every column is transformed along
     its n elements (replaces trnfft/api.py:496-516's transposes).
