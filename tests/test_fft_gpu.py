@@ -48,18 +48,46 @@ def test_pow2_fourstep_vs_oracle(n, inverse):
     assert rel_l2(*got, *ref) <= tol_pow2(n), (n, inverse)
 
 
-@pytest.mark.parametrize("lg", [22, 23, 24])
-def test_pow2_fourstep_largest_vs_numpy(lg):
-    # splits 2048 x 2048, 2048 x 4096 and 4096 x 4096 (16- and 8-transform tiles): one row
-    # against numpy's float64 FFT (the oracle's radix-2 loop is too slow at these sizes), forward
-    # and inverse
+@pytest.mark.parametrize("lg,batch", [(22, 1), (23, 1), (24, 1), (24, 2)])
+def test_pow2_fourstep_largest_vs_numpy(lg, batch):
+    # splits 2048 x 2048 and 2048 x 4096 (16- and 8-transform tiles), and 2^24 as three strided
+    # passes of 256 with the last pass staged through LDS: rows against numpy's float64 FFT (the
+    # oracle's radix-2 loop is too slow at these sizes), forward and inverse
     n = 1 << lg
-    re, im = seeded_complex(1, n, seed=lg)
+    re, im = seeded_complex(batch, n, seed=lg)
     x = re.double().numpy() + 1j * im.double().numpy()
     for inverse in (False, True):
         got = _gpu_fft(re, im, inverse)
-        ref = np.fft.ifft(x) if inverse else np.fft.fft(x)
+        ref = np.fft.ifft(x, axis=-1) if inverse else np.fft.fft(x, axis=-1)
         assert rel_l2(*got, ref.real, ref.imag) <= tol_pow2(n), (n, inverse)
+
+
+def test_pow2_2_24_real_input_and_in_place():
+    # 2^24 real input (the first strided pass's real-input variant) and an in-place call through
+    # the C ABI (the last pass writes the output after the first has read all input)
+    import ctypes
+
+    from trnfft_amd import _lib
+    from trnfft_amd.dispatch import ptr, stream_handle
+    from trnfft_amd.plan import native_plan
+
+    n = 1 << 24
+    re, im = seeded_complex(1, n, seed=5)
+    X = trnfft_amd.fft(re.cuda())
+    e = np.fft.fft(re.double().numpy(), axis=-1)
+    assert rel_l2(X.real, X.imag, e.real, e.imag) <= tol_pow2(n)
+    plan = native_plan(_lib.KIND_C2C, n, False, 0)
+    nbytes = ctypes.c_size_t(0)
+    lib = _lib.lib()
+    assert lib.tfa_plan_workspace_size(plan.handle, 1, ctypes.byref(nbytes)) == 0
+    ws = torch.empty(nbytes.value // 4, device="cuda")
+    d_re, d_im = re.cuda(), im.cuda()
+    rc = lib.tfa_execute(plan.handle, 1, ptr(d_re), ptr(d_im), ptr(d_re), ptr(d_im), ptr(ws),
+                         stream_handle(torch.device("cuda", 0)))
+    assert rc == 0
+    torch.cuda.synchronize()
+    e = np.fft.fft(re.double().numpy() + 1j * im.double().numpy(), axis=-1)
+    assert rel_l2(d_re, d_im, e.real, e.imag) <= tol_pow2(n)
 
 
 @pytest.mark.parametrize("n", [1 << 15, 1 << 20])

@@ -108,6 +108,12 @@ constexpr int kStridedThreePassLg = 21;
 __host__ __device__ constexpr long long strided_fs_min_stride(int npass, long long n) {
   return n <= 4096 ? 16 : npass >= 3 ? 8 : 4;
 }
+// Contiguous power-of-two lengths from 2^kContigThreePassLg run as the three-pass strided path
+// with stride 1 (factors <= 256) instead of the two-pass four-step, whose 4096-point passes have
+// 8-column tiles: 1 x 2^24 224 -> 199 us (inverse 227 -> 210, real input 207 -> 193).  At 2^23
+// and below it measured no better or slower (1 x 2^23 91 -> 103 us, 4 x 2^22 173 -> 185,
+// 8 x 2^21 145 -> 185): a third HBM pass costs more than the wider tiles gain.
+constexpr int kContigThreePassLg = 24;
 struct StridedFourStepArgs {
   const float* in_re;
   const float* in_im;  // nullptr: real input

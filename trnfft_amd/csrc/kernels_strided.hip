@@ -105,6 +105,49 @@ __global__ __launch_bounds__(C * (L / lds_epth(L))) void strided_fs_kernel(
   }
 }
 
+// Last pass of a contiguous axis (S = 1): column q's LP inputs are one contiguous block, so the
+// per-column loads of strided_fs_kernel would put every lane on its own block.  The workgroup's C
+// blocks are loaded with lanes along the block (coalesced runs of LP floats) into the columns'
+// LDS areas, then transformed and stored as there (lanes across columns: C consecutive outputs).
+template <int L, int DIR, int C = fourstep_tile(L)>
+__global__ __launch_bounds__(C * (L / lds_epth(L))) void strided_fs_last_contig_kernel(
+    const float* in_re, const float* in_im, float* out_re, float* out_im, const float2* __restrict__ tw,
+    SfsPass p) {
+  constexpr int E = lds_epth(L), T = L / E, THREADS = C * T;
+  constexpr int PADN = lds_pad(L) + 1;
+  static_assert(L != 4096, "staged last pass uses the interleaved exchange");
+  __shared__ float2 lds[C * PADN];
+  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
+  const long long o = tile / p.tiles_per_block;
+  const long long q0 = (tile % p.tiles_per_block) * C;
+  const long long qmask = (1LL << p.qa_bits) - 1;
+  const size_t ob = (size_t)(o * p.blk);
+#pragma unroll 4
+  for (int i = threadIdx.x; i < C * L; i += THREADS) {
+    const int c = i / L, j = i % L;
+    const long long q = q0 + c;
+    const size_t src = ob + (size_t)((q & qmask) * p.in_a + (q >> p.qa_bits) * p.in_b) + j;
+    lds[c * PADN + lds_pad(j)] = make_float2(ld_stream(in_re + src), ld_stream(in_im + src));
+  }
+  __syncthreads();
+  const int c = threadIdx.x % C, t = threadIdx.x / C;
+  float2* base = lds + c * PADN;
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = base[lds_pad(t + T * e)];
+  __syncthreads();  // the column areas become the transforms' exchange areas
+  LdsFft<L, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(base), nullptr, tw, t);
+  const long long q = q0 + c;
+  const size_t o0 = ob + (size_t)((q & qmask) * p.out_a + (q >> p.qa_bits) * p.out_b) + (size_t)t * (size_t)p.out_step;
+  const size_t ostep = (size_t)T * (size_t)p.out_step;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float2 y = cscale(v[e], p.scale);
+    st_stream(out_re + o0 + e * ostep, y.x);
+    st_stream(out_im + o0 + e * ostep, y.y);
+  }
+}
+
 template <int L, int DIR>
 static hipError_t launch_sfs_pass_t(const float* in_re, const float* in_im, float* out_re, float* out_im,
                                     const float2* tw, const StridedFourStepArgs& a, long long blocks, bool twiddle,
@@ -112,6 +155,13 @@ static hipError_t launch_sfs_pass_t(const float* in_re, const float* in_im, floa
   constexpr int C = fourstep_tile(L), TH = C * (L / lds_epth(L));
   const long long grid = blocks * p.tiles_per_block;
   if (grid > 0xffffffffLL) return hipErrorInvalidValue;
+  if constexpr (L != 4096) {
+    if (!twiddle && p.S == 1) {
+      hipLaunchKernelGGL((strided_fs_last_contig_kernel<L, DIR>), dim3((unsigned)grid), dim3(TH), 0, s, in_re, in_im,
+                         out_re, out_im, tw, p);
+      return hipGetLastError();
+    }
+  }
   if (twiddle && in_im == nullptr)
     hipLaunchKernelGGL((strided_fs_kernel<L, DIR, true, true>), dim3((unsigned)grid), dim3(TH), 0, s, in_re, in_im,
                        out_re, out_im, tw, a.tw_lo, a.tw_hi, p);
@@ -216,7 +266,10 @@ hipError_t launch_strided_fourstep(const StridedFourStepArgs& a) {
     if (a.len[i] < 64 || a.len[i] > 4096) return hipErrorInvalidValue;
     n *= a.len[i];
   }
-  if (a.stride < strided_fs_min_stride(a.npass, n)) return hipErrorInvalidValue;
+  // stride 1: a contiguous axis (last pass staged through LDS); 4096-point last passes use the
+  // split-plane exchange, which the staged pass does not have
+  if (a.stride == 1 ? a.len[a.npass - 1] == 4096 : a.stride < strided_fs_min_stride(a.npass, n))
+    return hipErrorInvalidValue;
   return a.dir < 0 ? launch_strided_fs_dir<-1>(a) : launch_strided_fs_dir<1>(a);
 }
 

@@ -211,9 +211,17 @@ int run_c2c(const C2cTables& t, int64_t batch, const float* in_re, const float* 
     if (!ws) return fail(TFA_ERR_INVALID, "four-step transform needs a workspace");
     float* t_re = static_cast<float*>(ws);
     float* t_im = t_re + (size_t)batch * (size_t)t.n;
-    tfa::FourStepArgs a{in_re, in_im, t_re, t_im, out_re, out_im, t.tw1, t.tw2, t.tw_lo, t.tw_hi,
-                        t.n1, t.n2, t.lo_bits, batch, scale, t.dir, s};
-    e = tfa::launch_fourstep(a);
+    if (t.s_np == 3 && tfa::ilog2(t.n) >= tfa::kContigThreePassLg) {
+      // three passes over factors <= 256 (64-column tiles) instead of the two-pass four-step,
+      // whose 2048- and 4096-point passes have 16- and 8-column tiles
+      tfa::StridedFourStepArgs a{in_re, in_im, t_re, t_im, out_re, out_im, t.s_np, {t.s_len[0], t.s_len[1], t.s_len[2]},
+                                 {t.s_tw[0], t.s_tw[1], t.s_tw[2]}, t.tw_lo, t.tw_hi, t.lo_bits, batch, 1, scale, t.dir, s};
+      e = tfa::launch_strided_fourstep(a);
+    } else {
+      tfa::FourStepArgs a{in_re, in_im, t_re, t_im, out_re, out_im, t.tw1, t.tw2, t.tw_lo, t.tw_hi,
+                          t.n1, t.n2, t.lo_bits, batch, scale, t.dir, s};
+      e = tfa::launch_fourstep(a);
+    }
   }
   return e == hipSuccess ? TFA_OK : hip_fail(e, "c2c launch");
 }
