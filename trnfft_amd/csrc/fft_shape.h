@@ -88,6 +88,12 @@ __host__ __device__ constexpr bool fft2_small_ok(long long h, long long w) {
 __host__ __device__ constexpr int blue_epth(int m) { return m >= 16384 ? 16 : m >= 128 ? 8 : lds_epth(m); }
 __host__ __device__ constexpr int blue_threads(int m) { return m == 2048 || m >= 8192 ? 512 : 256; }
 __host__ __device__ constexpr bool blue_pf(int m) { return m >= 256; }
+// split Bluestein (m >= 32768, three passes): elements per thread of the column passes (length
+// m1; E = 8 at m1 = 128 measured no better) and next-pass twiddle prefetch in the column and row
+// passes (209 x 20000 147 -> 143 us, 59 x 70000 183 -> 178, 32 x 8193 26.9 -> 25.7; 511 x 8193
+// 1 % slower)
+__host__ __device__ constexpr int blue_col_epth(int m1) { return lds_epth(m1); }
+__host__ __device__ constexpr bool blue_split_pf(int) { return true; }
 
 // Inverse-STFT launch shape from a sweep on MI355X (64 x 160000 samples, hop n/2, n_fft 16..4096,
 // E in {4, 8, 16} x 128..1024 threads): E = 8 elements per thread up to n = 2048, 16 at 4096;

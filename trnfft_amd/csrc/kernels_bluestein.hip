@@ -239,9 +239,10 @@ __device__ __forceinline__ void mul_roots(float2 (&v)[E], const float2* __restri
 // columns), LDS Stockham down the column.
 template <int M1>
 struct BlueColCfg {
-  static constexpr int E = lds_epth(M1);
+  static constexpr int E = blue_col_epth(M1);
   static constexpr int T = M1 / E;
-  static constexpr int C = fourstep_tile(M1);
+  // the strided-pass tile, narrowed when fewer elements per thread need more threads per column
+  static constexpr int C = fourstep_tile(M1) * T > 1024 ? 1024 / T : fourstep_tile(M1);
   static constexpr int PADN = lds_pad(M1) + 1;
 };
 
@@ -269,7 +270,7 @@ __global__ __launch_bounds__((BlueColCfg<M1>::C * BlueColCfg<M1>::T)) void blue_
     }
     v[e] = y;
   }
-  LdsFft<M1, E, -1, false, false, true>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);
+  LdsFft<M1, E, -1, false, false, true, blue_split_pf(M1)>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);
   mul_roots<E, T, false>(v, lo, hi, (unsigned)col, (unsigned)t, m - 1, lo_bits);  // W_m^(col*k1)
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -299,7 +300,7 @@ __global__ __launch_bounds__((BlueColCfg<M1>::C * BlueColCfg<M1>::T)) void blue_
     const size_t s = (size_t)b * m + (size_t)(t + T * e) * m2 + col;
     v[e] = make_float2(ld_stream(ws_re + s), ld_stream(ws_im + s));
   }
-  LdsFft<M1, E, 1, false, false, true>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);
+  LdsFft<M1, E, 1, false, false, true, blue_split_pf(M1)>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int i = (t + T * e) * m2 + col;
@@ -333,11 +334,11 @@ __global__ __launch_bounds__(C2cThreads<M2>::THREADS) void blue_row_kernel(
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = make_float2(pr[T * e], pi[T * e]);
   float* my = reinterpret_cast<float*>(lds + xf * C::PADN);
-  LdsFft<M2, E, -1, WL, false, true>::run(v, my, nullptr, tw_f, tid);
+  LdsFft<M2, E, -1, WL, false, true, blue_split_pf(M2)>::run(v, my, nullptr, tw_f, tid);
   const float2* h = hp + (size_t)k1 * M2 + tid;
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = cmul(v[e], h[T * e]);
-  LdsFft<M2, E, 1, WL, false, true>::run(v, my, nullptr, tw_i, tid);
+  LdsFft<M2, E, 1, WL, false, true, blue_split_pf(M2)>::run(v, my, nullptr, tw_i, tid);
   mul_roots<E, T, true>(v, lo, hi, (unsigned)k1, (unsigned)tid, m - 1, lo_bits);  // W_m^-(n2*k1)
 #pragma unroll
   for (int e = 0; e < E; ++e) {

@@ -354,8 +354,8 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         p->blue_m2 = (int)(m / p->blue_m1);
         p->blue_lo_bits = (lg + 1) / 2;
         const int m1 = p->blue_m1, m2 = p->blue_m2;
-        if ((rc = p->upload(lds_table(m1, -1), &p->b_tw1f))) break;
-        if ((rc = p->upload(lds_table(m1, 1), &p->b_tw1i))) break;
+        if ((rc = p->upload(lds_table(m1, -1, tfa::blue_col_epth(m1)), &p->b_tw1f))) break;
+        if ((rc = p->upload(lds_table(m1, 1, tfa::blue_col_epth(m1)), &p->b_tw1i))) break;
         if ((rc = p->upload(lds_table(m2, -1, tfa::c2c_epth(m2)), &p->b_tw2f))) break;
         if ((rc = p->upload(lds_table(m2, 1, tfa::c2c_epth(m2)), &p->b_tw2i))) break;
         std::vector<float2> lo((size_t)1 << p->blue_lo_bits), hi((size_t)(m >> p->blue_lo_bits));
