@@ -114,3 +114,22 @@ def test_graph_replay_short_rows_small_images_and_strided_axes():
             assert torch.equal(o.real, e.real) and torch.equal(o.imag, e.imag)
         trnfft_amd.fft(a)  # unrelated eager work between replays
         torch.cuda.synchronize()
+
+
+def test_graph_replay_multipass_paths():
+    # the strided multi-pass path (a 2^17 axis down a strided dimension, workspace from the
+    # caching allocator inside the capture) and the 2^24 contiguous three-pass path
+    g0 = torch.Generator().manual_seed(21)
+    vol = ComplexTensor(torch.randn(2, 1 << 17, 8, generator=g0).cuda(), torch.randn(2, 1 << 17, 8, generator=g0).cuda())
+    row = ComplexTensor(torch.randn(1, 1 << 24, generator=g0).cuda(), torch.randn(1, 1 << 24, generator=g0).cuda())
+    e1 = trnfft_amd.fftn(vol, dim=(1,))
+    e2 = trnfft_amd.fft(row)
+    g, (o1, o2) = _capture(lambda: (trnfft_amd.fftn(vol, dim=(1,)), trnfft_amd.fft(row)))
+    other = ComplexTensor(torch.randn(2, 1 << 17, 8, device="cuda"), torch.randn(2, 1 << 17, 8, device="cuda"))
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o1.real, e1.real) and torch.equal(o1.imag, e1.imag)
+        assert torch.equal(o2.real, e2.real) and torch.equal(o2.imag, e2.imag)
+        trnfft_amd.ifftn(other, dim=(1,))  # unrelated eager work between replays
+        torch.cuda.synchronize()
