@@ -41,11 +41,26 @@ def test_pow2_lds_vs_oracle(n, inverse):
 @pytest.mark.parametrize("n", [1 << 15, 1 << 16, 1 << 17, 1 << 18, 1 << 19, 1 << 20, 1 << 21])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_pow2_fourstep_vs_oracle(n, inverse):
-    # every (n1, n2) split of the two-pass path up to 1024 x 2048 (column tile 32, row tile 32/16)
+    # every (n1, n2) split of the two-pass path up to 1024 x 2048; two rows run the narrow
+    # 8-transform tiles below 2^21 (too few workgroups for the wide ones), the wide tiles at 2^21
     re, im = seeded_complex(2, n, seed=n)
     got = _gpu_fft(re, im, inverse)
     ref = oracle.fft_core(re, im, inverse)
     assert rel_l2(*got, *ref) <= tol_pow2(n), (n, inverse)
+
+
+@pytest.mark.parametrize("n,batch", [(1 << 15, 64), (1 << 16, 32), (1 << 17, 16), (1 << 18, 16), (1 << 19, 8),
+                                     (1 << 20, 4), (1 << 20, 3)])
+def test_pow2_fourstep_wide_tiles_vs_numpy(n, batch):
+    # batches large enough for the wide column tiles (32 transforms per workgroup; 4 x 2^20 is
+    # the smallest 2^20 batch on them, 3 x 2^20 the largest on the narrow ones), both directions,
+    # against numpy float64 (the oracle's radix-2 loop is too slow at these batches)
+    re, im = seeded_complex(batch, n, seed=n + batch)
+    x = re.double().numpy() + 1j * im.double().numpy()
+    for inverse in (False, True):
+        got = _gpu_fft(re, im, inverse)
+        ref = np.fft.ifft(x, axis=-1) if inverse else np.fft.fft(x, axis=-1)
+        assert rel_l2(*got, ref.real, ref.imag) <= tol_pow2(n), (n, batch, inverse)
 
 
 @pytest.mark.parametrize("lg,batch", [(22, 1), (23, 1), (24, 1), (24, 2)])

@@ -8,6 +8,8 @@ namespace tfa {
 
 // Per-workgroup LDS budget of gfx950 (160 KiB per CU, all of it addressable by one workgroup).
 constexpr long long kLdsBytes = 163840;
+// Compute units of MI355X (8 XCDs x 32).
+constexpr int kNumCUs = 256;
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Remap the
 // linear block index so that consecutive tiles run on the same XCD at about the same time:

@@ -249,24 +249,28 @@ __global__ __launch_bounds__(C * (N1 / lds_epth(N1))) void strided_kernel(
 // With 32-transform tiles (lengths up to 1024) every HBM side of both passes moves whole 128-byte
 // lines; 2048 and 4096 use 16 and 8 transforms per tile (the LDS holds no more).
 // ---------------------------------------------------------------------------------------------
-template <int L>
+// TILE_ = 0: the wide tile, 1024 threads (32 transforms up to L = 1024, 16 at 2048, 8 at 4096).
+// A narrower tile (TILE_ = kFourStepNarrow) spreads a small batch over more workgroups.
+template <int L, int TILE_ = 0>
 struct FourStepCfg {
-  static constexpr int TILE = L <= 1024 ? 32 : 32768 / L;
   static constexpr int E = fourstep_epth(L);
   static constexpr int T = L / E;
+  static constexpr int TILE = TILE_ ? TILE_ : 1024 / T;
   static constexpr int THREADS = TILE * T;
   static constexpr int PADN = lds_pad(L) + 1;
-  // both planes (interleaved) in LDS when they fit, else the real and imaginary planes take turns
-  static constexpr bool SPLIT = 2LL * TILE * PADN * 4 > kLdsBytes;
-  static_assert(THREADS == 1024 && (SPLIT ? 1LL : 2LL) * TILE * PADN * 4 <= kLdsBytes, "four-step tile");
+  // both planes (interleaved) in LDS when they fit in half of it (two workgroups per CU), else
+  // the real and imaginary planes take turns (L = 512: 64 x 2^18 141 -> 133 us)
+  static constexpr bool SPLIT = 2LL * TILE * PADN * 4 > kLdsBytes / 2;
+  static_assert(THREADS <= 1024 && (SPLIT ? 1LL : 2LL) * TILE * PADN * 4 <= kLdsBytes, "four-step tile");
 };
+constexpr int kFourStepNarrow = 8;
 
-template <int N1, int DIR, bool REAL_IN, int CK>
-__global__ __launch_bounds__(FourStepCfg<N1>::THREADS) void fourstep_col_kernel(
+template <int N1, int DIR, bool REAL_IN, int CK, int TILE_ = 0>
+__global__ __launch_bounds__((FourStepCfg<N1, TILE_>::THREADS)) void fourstep_col_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ tw, const float2* __restrict__ tw_lo,
     const float2* __restrict__ tw_hi, long long stride, int tiles_per_block, int lo_bits, unsigned nmask) {
-  using Cfg = FourStepCfg<N1>;
+  using Cfg = FourStepCfg<N1, TILE_>;
   constexpr int C = Cfg::TILE, E = Cfg::E, T = Cfg::T, THREADS = Cfg::THREADS, PADN = Cfg::PADN;
   constexpr bool SPLIT = Cfg::SPLIT;
   constexpr int TF = E < 4 ? E : 4;  // twiddle factor group
@@ -348,11 +352,11 @@ __global__ __launch_bounds__(FourStepCfg<N1>::THREADS) void fourstep_col_kernel(
   }
 }
 
-template <int N2, int DIR>
-__global__ __launch_bounds__(FourStepCfg<N2>::THREADS) void fourstep_row_kernel(
+template <int N2, int DIR, int TILE_ = 0>
+__global__ __launch_bounds__((FourStepCfg<N2, TILE_>::THREADS)) void fourstep_row_kernel(
     const float* __restrict__ t_re, const float* __restrict__ t_im, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ tw, int n1_len, float scale) {
-  using Cfg = FourStepCfg<N2>;
+  using Cfg = FourStepCfg<N2, TILE_>;
   constexpr int CK = Cfg::TILE, E = Cfg::E, T = Cfg::T, PADN = Cfg::PADN;
   constexpr bool SPLIT = Cfg::SPLIT;
   __shared__ float2 lds[SPLIT ? (CK * PADN + 1) / 2 : CK * PADN];
@@ -489,28 +493,39 @@ hipError_t launch_strided(int n1, const StridedArgs& a) {
   return a.dir < 0 ? launch_strided_dir<-1>(n1, a) : launch_strided_dir<1>(n1, a);
 }
 
-template <int N1, int N2, int DIR>
-static hipError_t launch_fourstep_t(const FourStepArgs& a) {
-  using C1 = FourStepCfg<N1>;
-  using C2 = FourStepCfg<N2>;
+template <int N1, int N2, int DIR, int TILE_>
+static hipError_t launch_fourstep_tiles(const FourStepArgs& a) {
+  using C1 = FourStepCfg<N1, TILE_>;
+  using C2 = FourStepCfg<N2, TILE_>;
   constexpr int CK = C2::TILE;
   static_assert(N2 % C1::TILE == 0 && N1 % CK == 0, "four-step tiles");
   const unsigned nmask = (unsigned)((long long)N1 * N2 - 1);
   const long long cols = a.batch * (N2 / C1::TILE);
   if (a.in_im == nullptr)
-    hipLaunchKernelGGL((fourstep_col_kernel<N1, DIR, true, CK>), dim3((unsigned)cols), dim3(C1::THREADS), 0,
+    hipLaunchKernelGGL((fourstep_col_kernel<N1, DIR, true, CK, TILE_>), dim3((unsigned)cols), dim3(C1::THREADS), 0,
                        a.stream, a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, (long long)N2,
                        N2 / C1::TILE, a.lo_bits, nmask);
   else
-    hipLaunchKernelGGL((fourstep_col_kernel<N1, DIR, false, CK>), dim3((unsigned)cols), dim3(C1::THREADS), 0,
+    hipLaunchKernelGGL((fourstep_col_kernel<N1, DIR, false, CK, TILE_>), dim3((unsigned)cols), dim3(C1::THREADS), 0,
                        a.stream, a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, (long long)N2,
                        N2 / C1::TILE, a.lo_bits, nmask);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const long long rows = a.batch * (N1 / CK);
-  hipLaunchKernelGGL((fourstep_row_kernel<N2, DIR>), dim3((unsigned)rows), dim3(C2::THREADS), 0, a.stream, a.t_re,
-                     a.t_im, a.out_re, a.out_im, a.tw2, N1, a.scale);
+  hipLaunchKernelGGL((fourstep_row_kernel<N2, DIR, TILE_>), dim3((unsigned)rows), dim3(C2::THREADS), 0, a.stream,
+                     a.t_re, a.t_im, a.out_re, a.out_im, a.tw2, N1, a.scale);
   return hipGetLastError();
+}
+
+template <int N1, int N2, int DIR>
+static hipError_t launch_fourstep_t(const FourStepArgs& a) {
+  // a batch whose wide-tile column pass would fill fewer than half the CUs runs narrow tiles
+  // (four times the workgroups): 1 x 2^20 35.5 -> 22.2 us, 1 x 2^16 14.0 -> 9.9, 2 x 2^20 36.3 ->
+  // 26.1; at 4 x 2^20 (128 wide workgroups) the wide tiles stay faster (40.4 against 44.2)
+  if (a.batch * (N2 / FourStepCfg<N1>::TILE) < kNumCUs / 2 && FourStepCfg<N1>::TILE > kFourStepNarrow &&
+      FourStepCfg<N2>::TILE > kFourStepNarrow)
+    return launch_fourstep_tiles<N1, N2, DIR, kFourStepNarrow>(a);
+  return launch_fourstep_tiles<N1, N2, DIR, 0>(a);
 }
 
 // n = n1 * n2 with n1 = 2^floor(lg/2) <= n2 (the plan's split)
