@@ -1,0 +1,112 @@
+"""Seeded randomized parity sweep of the power-of-two paths against numpy / torch float64.
+
+A fixed seed draws 160 cases over every public entry point that runs a power-of-two kernel: c2c
+of random length and batch (LDS, short-row, four-step with narrow and wide tiles), rfft/irfft,
+transforms along a strided axis (single pass, few-column staging, two- and three-pass strided
+four-step, real and complex input), fft2 (single-pass small images, two-pass, axis by axis) and
+stft.  Every case must meet 1e-6 * log2 N relative L2 against float64 (numpy.fft or
+torch.stft), the same bound as the fixed-shape tests.  Non-power-of-two lengths are pinned
+against the oracle elsewhere: the reference's fp32 Bluestein chirp puts its operator itself up
+to ~3e-3 from the exact DFT at large n.
+"""
+
+from __future__ import annotations
+
+import random
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import trnfft_amd
+from conftest import rel_l2, tol_pow2
+from trnfft_amd import ComplexTensor
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(count: int, seed: int):
+    rng = random.Random(seed)
+    kinds = ["c2c", "c2c", "real", "strided", "strided", "fft2", "stft"]
+    out = []
+    for i in range(count):
+        kind = kinds[i % len(kinds)]
+        if kind == "c2c":
+            n = 1 << rng.randrange(0, 22)
+            out.append((kind, n, rng.randrange(1, max(2, min(600, (1 << 21) // n))), rng.random() < 0.5))
+        elif kind == "real":
+            n = 1 << rng.randrange(2, 16)
+            out.append((kind, n, rng.randrange(1, max(2, min(3000, (1 << 20) // n))), False))
+        elif kind == "strided":
+            n = 1 << rng.randrange(1, 22)
+            stride = rng.choice([1, 2, 3, 4, 5, 8, 15, 16, 17, 64, 100])
+            while n > 2 and n * stride > (1 << 22):  # at most 4M elements per case
+                n //= 2
+            outer = rng.randrange(1, max(2, min(5, (1 << 22) // (n * stride) + 1)))
+            out.append((kind, n, (outer, stride, rng.random() < 0.25), rng.random() < 0.5))
+        elif kind == "fft2":
+            h, w = 1 << rng.randrange(2, 12), 1 << rng.randrange(2, 12)
+            out.append((kind, (h, w), rng.randrange(1, max(2, min(5, (1 << 21) // (h * w) + 1))), rng.random() < 0.5))
+        else:
+            n_fft = 1 << rng.randrange(4, 13)
+            out.append((kind, n_fft, (rng.choice([n_fft // 4, n_fft // 2, n_fft]), rng.randrange(n_fft + 1, 30000)),
+                        rng.randrange(1, 4)))
+    return out
+
+
+def _randn(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("case", _cases(160, 2024), ids=lambda c: f"{c[0]}-{c[1]}-{c[2]}-{c[3]}")
+def test_random_pow2_parity(case):
+    kind, n, p, q = case
+    seed = zlib.crc32(repr(case).encode())  # stable across processes (str hash is not)
+    if kind == "c2c":
+        batch, inverse = p, q
+        re, im = _randn((batch, n), seed), _randn((batch, n), seed + 1)
+        x = ComplexTensor(torch.from_numpy(re).cuda(), torch.from_numpy(im).cuda())
+        y = trnfft_amd.ifft(x) if inverse else trnfft_amd.fft(x)
+        z = re.astype(np.float64) + 1j * im
+        ref = np.fft.ifft(z, axis=-1) if inverse else np.fft.fft(z, axis=-1)
+        assert rel_l2(y.real, y.imag, ref.real, ref.imag) <= tol_pow2(n)
+    elif kind == "real":
+        batch = p
+        x = _randn((batch, n), seed)
+        y = trnfft_amd.rfft(torch.from_numpy(x).cuda())
+        ref = np.fft.rfft(x.astype(np.float64), axis=-1)
+        assert rel_l2(y.real, y.imag, ref.real, ref.imag) <= tol_pow2(n)
+        back = trnfft_amd.irfft(y, n=n)
+        rb = np.fft.irfft(ref, n=n, axis=-1)
+        assert rel_l2(back, torch.zeros_like(back), rb, np.zeros_like(rb)) <= 2 * tol_pow2(n)
+    elif kind == "strided":
+        (outer, stride, real_in), inverse = p, q
+        shape = (outer, n, stride)
+        re, im = _randn(shape, seed), _randn(shape, seed + 1)
+        if real_in:
+            xin, z = torch.from_numpy(re).cuda(), re.astype(np.float64)
+        else:
+            xin = ComplexTensor(torch.from_numpy(re).cuda(), torch.from_numpy(im).cuda())
+            z = re.astype(np.float64) + 1j * im
+        y = trnfft_amd.ifftn(xin, dim=(1,)) if inverse else trnfft_amd.fftn(xin, dim=(1,))
+        ref = np.fft.ifft(z, axis=1) if inverse else np.fft.fft(z, axis=1)
+        assert rel_l2(y.real, y.imag, ref.real, ref.imag) <= tol_pow2(n)
+    elif kind == "fft2":
+        (h, w), b, real_in = n, p, q
+        x = _randn((b, h, w), seed)
+        if real_in:
+            y, z = trnfft_amd.fft2(torch.from_numpy(x).cuda()), x.astype(np.float64)
+        else:
+            xi = _randn((b, h, w), seed + 1)
+            y = trnfft_amd.fft2(ComplexTensor(torch.from_numpy(x).cuda(), torch.from_numpy(xi).cuda()))
+            z = x.astype(np.float64) + 1j * xi
+        ref = np.fft.fft2(z)
+        assert rel_l2(y.real, y.imag, ref.real, ref.imag) <= tol_pow2(h * w)
+    else:
+        (hop, length), b = p, q
+        xt = torch.from_numpy(_randn((b, length), seed))
+        y = trnfft_amd.stft(xt.cuda(), n, hop_length=hop)
+        ref = torch.stft(xt.double(), n, hop_length=hop, window=torch.hann_window(n, dtype=torch.float64), center=True,
+                         pad_mode="reflect", return_complex=True).numpy()
+        assert rel_l2(y.real, y.imag, ref.real, ref.imag) <= tol_pow2(n)
