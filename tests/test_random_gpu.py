@@ -5,9 +5,10 @@ of random length and batch (LDS, short-row, four-step with narrow and wide tiles
 transforms along a strided axis (single pass, few-column staging, two- and three-pass strided
 four-step, real and complex input), fft2 (single-pass small images, two-pass, axis by axis) and
 stft.  Every case must meet 1e-6 * log2 N relative L2 against float64 (numpy.fft or
-torch.stft), the same bound as the fixed-shape tests.  Non-power-of-two lengths are pinned
-against the oracle elsewhere: the reference's fp32 Bluestein chirp puts its operator itself up
-to ~3e-3 from the exact DFT at large n.
+torch.stft), the same bound as the fixed-shape tests.  A second seeded sweep (48 cases) draws
+any length (mostly Bluestein) for c2c, rfft, strided axes and fft2 and checks it against the
+oracle's restatement of the reference operator at 1e-5 * log2 N: the reference's fp32 Bluestein
+chirp puts that operator itself up to ~3e-3 from the exact DFT at large n.
 """
 
 from __future__ import annotations
@@ -110,3 +111,63 @@ def test_random_pow2_parity(case):
         ref = torch.stft(xt.double(), n, hop_length=hop, window=torch.hann_window(n, dtype=torch.float64), center=True,
                          pad_mode="reflect", return_complex=True).numpy()
         assert rel_l2(y.real, y.imag, ref.real, ref.imag) <= tol_pow2(n)
+
+
+def _cases_any(count: int, seed: int):
+    rng = random.Random(seed)
+    kinds = ["c2c", "real", "strided", "fft2"]
+    out = []
+    for i in range(count):
+        kind = kinds[i % len(kinds)]
+        if kind == "c2c":
+            out.append((kind, rng.randrange(2, 600), rng.randrange(1, 40), rng.random() < 0.5))
+        elif kind == "real":
+            out.append((kind, rng.randrange(3, 600), rng.randrange(1, 40), False))
+        elif kind == "strided":
+            out.append((kind, rng.randrange(2, 600), (rng.randrange(1, 4), rng.choice([1, 2, 3, 5, 16, 33])),
+                        rng.random() < 0.5))
+        else:
+            out.append((kind, (rng.randrange(3, 200), rng.randrange(3, 200)), rng.randrange(1, 3), rng.random() < 0.5))
+    return out
+
+
+# any length (mostly Bluestein) against the oracle's restatement of the reference operator, fp32
+# chirp included, at sizes its radix-2 loop finishes quickly
+@pytest.mark.parametrize("case", _cases_any(48, 7), ids=lambda c: f"{c[0]}-{c[1]}-{c[2]}-{c[3]}")
+def test_random_any_length_vs_oracle(case):
+    import oracle
+    from conftest import tol_bluestein
+
+    kind, n, p, q = case
+    seed = zlib.crc32(repr(case).encode())
+    if kind == "c2c":
+        batch, inverse = p, q
+        re, im = torch.from_numpy(_randn((batch, n), seed)), torch.from_numpy(_randn((batch, n), seed + 1))
+        x = ComplexTensor(re.cuda(), im.cuda())
+        y = trnfft_amd.ifft(x) if inverse else trnfft_amd.fft(x)
+        ref = oracle.fft_core(re, im, inverse)
+        assert rel_l2(y.real, y.imag, *ref) <= tol_bluestein(n)
+    elif kind == "real":
+        x = torch.from_numpy(_randn((p, n), seed))
+        y = trnfft_amd.rfft(x.cuda())
+        ref = oracle.rfft(x)
+        assert rel_l2(y.real, y.imag, *ref) <= tol_bluestein(n)
+    elif kind == "strided":
+        (outer, stride), inverse = p, q
+        re = torch.from_numpy(_randn((outer, n, stride), seed))
+        im = torch.from_numpy(_randn((outer, n, stride), seed + 1))
+        x = ComplexTensor(re.cuda(), im.cuda())
+        y = trnfft_amd.ifftn(x, dim=(1,)) if inverse else trnfft_amd.fftn(x, dim=(1,))
+        ref = oracle.ifftn((re, im), dim=(1,)) if inverse else oracle.fftn((re, im), dim=(1,))
+        assert rel_l2(y.real, y.imag, *ref) <= tol_bluestein(n)
+    else:
+        (h, w), b, real_in = n, p, q
+        re = torch.from_numpy(_randn((b, h, w), seed))
+        if real_in:
+            y = trnfft_amd.fft2(re.cuda())
+            ref = oracle.fft2(re)
+        else:
+            im = torch.from_numpy(_randn((b, h, w), seed + 1))
+            y = trnfft_amd.fft2(ComplexTensor(re.cuda(), im.cuda()))
+            ref = oracle.fft2((re, im))
+        assert rel_l2(y.real, y.imag, *ref) <= 2 * tol_bluestein(max(h, w))
