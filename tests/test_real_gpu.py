@@ -15,12 +15,13 @@ from trnfft_amd import ComplexTensor
 pytestmark = pytest.mark.gpu
 
 # (n, batch): batches not a multiple of the rows per workgroup run the guarded kernel variant over
-# the whole grid, whose last workgroup is partial (n = 8..32 run one row per thread with 256-row
-# staging tiles: 300, 257, 1000 rows leave a partial tile after full ones; n = 64 and 128 move
-# their bins through LDS as one run per workgroup of 32 / 16 rows: 513 and 77 rows end in a
-# partial run, 1024 rows are whole runs only)
-CASES = [(4, 300), (8, 257), (16, 33), (16, 1000), (32, 65), (64, 7), (64, 513), (64, 1024), (128, 5), (128, 77),
-         (128, 1024), (256, 3), (512, 3), (1024, 5), (2048, 3), (4096, 2), (8192, 2), (16384, 1), (32768, 2)]
+# the whole grid, whose last workgroup is partial (n = 8, 16 run one row per thread with 256-row
+# staging tiles: 300, 257, 1000 rows leave a partial tile after full ones; n = 32, 64 and 128 move
+# their bins through LDS as one run per workgroup of 64 / 32 / 16 rows: 65, 513 and 77 rows end
+# in a partial run, 1024 rows are whole runs only)
+CASES = [(4, 300), (4, 1024), (8, 257), (16, 33), (16, 1000), (32, 65), (32, 1024), (64, 7), (64, 513), (64, 1024),
+         (128, 5), (128, 77), (128, 1024), (256, 3), (512, 3), (1024, 5), (2048, 3), (4096, 2), (8192, 2), (16384, 1),
+         (32768, 2)]
 
 
 @pytest.mark.parametrize("n,batch", CASES)

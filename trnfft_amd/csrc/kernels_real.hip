@@ -186,7 +186,7 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
   for (int e = 0; e < E; ++e) st_stream2(dst + T * e, v[e]);
 }
 
-// Short rows (n = 2H = 8, 16, 32): one thread per row, the half-length transform in registers (the
+// Short rows (n = 2H = 8, 16): one thread per row, the half-length transform in registers (the
 // in-register DFT).  A thread per row would touch one cache line per lane, so the workgroup's
 // XS rows move between HBM and LDS as contiguous runs (rows of n reals, rows of H+1 bins); the
 // input and output staging share the LDS area (a barrier between reading one and writing the
@@ -302,9 +302,10 @@ static hipError_t launch_real_small(const RealArgs& a) {
 
 template <int H>
 static hipError_t launch_real_h(const RealArgs& a) {
-  // the short-row kernels for n = 8, 16, 32 (n = 4 and 64 measured faster on the LDS kernels:
-  // 8.6 vs 11.2 us and 18.3 vs 28.7 us for 4M samples)
-  if constexpr (H >= 4 && H <= 16) {
+  // the short-row kernels for n = 8 and 16; n = 4 and n >= 32 measured faster on the LDS kernels
+  // (n = 4: 8.6 vs 11.2 us for 4M samples; n = 32 with its bins staged through LDS: r2c 17.0 ->
+  // 10.6 us, c2r 12.4 -> 8.7, 1000 rows 11.3 -> 4.7; n = 16 is even there, n = 8 slower)
+  if constexpr (H >= 4 && H <= 8) {
     return launch_real_small<H>(a);
   } else {
     // ragged batches: one launch of the guarded variant
