@@ -445,19 +445,36 @@ __global__ __launch_bounds__(C * (N1 / lds_epth(N1))) void strided_small_kernel(
   }
 }
 
+template <int N1, int DIR, int CS>
+static hipError_t launch_strided_small_c(const StridedArgs& a) {
+  constexpr int T = N1 / lds_epth(N1);
+  const int groups = (int)(CS / a.stride);
+  const long long blocks = (a.outer + groups - 1) / groups;
+  if (a.in_im == nullptr)
+    hipLaunchKernelGGL((strided_small_kernel<N1, DIR, true, CS>), dim3((unsigned)blocks), dim3(CS * T), 0, a.stream,
+                       a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.outer, (int)a.stride, groups, a.scale);
+  else
+    hipLaunchKernelGGL((strided_small_kernel<N1, DIR, false, CS>), dim3((unsigned)blocks), dim3(CS * T), 0, a.stream,
+                       a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.outer, (int)a.stride, groups, a.scale);
+  return hipGetLastError();
+}
+
+// Column tile of the few-column kernel up to n = 1024: the strided kernel's, narrowed until two
+// workgroups fit in a CU's LDS (n = 256 over 3 columns 37.4 -> 30.7 us, 512 55.4 -> 48.8, 1024
+// 40.4 -> 31.9; n = 2048 measured 5 % slower and keeps the full tile)
+__host__ __device__ constexpr int strided_small_tile(int l) {
+  int c = fourstep_tile(l);
+  while (c > 1 && (long long)c * (lds_pad(l) + 1) * 8 > kLdsBytes / 2) c /= 2;
+  return c;
+}
+
 template <int N1, int DIR>
 static hipError_t launch_strided_t(const StridedArgs& a) {
   constexpr int C = fourstep_tile(N1), T = N1 / lds_epth(N1);
   if (2 * a.stride <= C) {
-    const int groups = (int)(C / a.stride);
-    const long long blocks = (a.outer + groups - 1) / groups;
-    if (a.in_im == nullptr)
-      hipLaunchKernelGGL((strided_small_kernel<N1, DIR, true>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream,
-                         a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.outer, (int)a.stride, groups, a.scale);
-    else
-      hipLaunchKernelGGL((strided_small_kernel<N1, DIR, false>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream,
-                         a.in_re, a.in_im, a.out_re, a.out_im, a.tw, a.outer, (int)a.stride, groups, a.scale);
-    return hipGetLastError();
+    constexpr int CS = strided_small_tile(N1);
+    if (N1 <= 1024 && a.stride <= CS) return launch_strided_small_c<N1, DIR, CS>(a);
+    return launch_strided_small_c<N1, DIR, C>(a);
   }
   const long long tiles = (a.stride + C - 1) / C;
   const long long blocks = a.outer * tiles;
