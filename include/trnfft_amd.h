@@ -78,7 +78,7 @@ int64_t tfa_plan_padded_n(const tfa_plan* plan);
  * which dispatches to _cooley_tukey (:53-117, power-of-two n), _bluestein (:1285-1376, other n)
  * and, for TFA_KIND_DFT_GEMM plans, _fft_via_gemm (:221-251).
  * TFA_KIND_FFT2 plans: `batch` arrays of (n2, n) each, transformed over both axes (x 1/(n n2)
- * when inverse), power-of-two 16 <= n <= 2048 and 16 <= n2 <= 4096 (two HBM passes), or
+ * when inverse), power-of-two 16 <= n <= 4096 and 16 <= n2 <= 4096 (two HBM passes), or
  * n * n2 <= 16384 with both axes >= 4 (>= 8 at 8192, >= 16 at 16384; whole images in LDS, one
  * pass); output must not alias the input; replaces trnfft/api.py:105-139 (fft2 -> fftn over
  * (-2, -1)).

@@ -156,9 +156,14 @@ def test_stft_edge_shapes(n_fft, hop, length, batch_shape):
     assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(n_fft)
 
 
-@pytest.mark.parametrize("shape", [(2, 16, 16), (1, 4096, 16), (3, 16, 2048), (2, 512, 1024), (1, 128, 64)])
+@pytest.mark.parametrize("shape", [(2, 16, 16), (1, 4096, 16), (3, 16, 2048), (2, 512, 1024), (1, 128, 64),
+                                   (2, 64, 4096), (1, 512, 4096)])
 def test_fft2_complex_and_inverse(shape):
-    # (16, 16) and (128, 64) take the single-pass small-image kernel, the others the two passes
+    # (16, 16) and (128, 64) take the single-pass small-image kernel; complex input routes the
+    # others to the two single-axis passes, and the two-pass 2-D kernels are checked directly
+    # (4096-wide rows: pass 1 exchanges its 8 rows through LDS one plane at a time)
+    from trnfft_amd.fft_core import execute_fft2
+
     rng = np.random.default_rng(11)
     re = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
     im = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
@@ -166,13 +171,16 @@ def test_fft2_complex_and_inverse(shape):
     ref = oracle.fft2((re, im))
     n = shape[-1] * shape[-2]
     assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(n)
+    direct = execute_fft2(re.cuda(), im.cuda(), False)
+    assert rel_l2(direct.real, direct.imag, *ref) <= tol_pow2(n)
     back = trnfft_amd.ifftn(got, dim=(-2, -1))
     ref_back = oracle.ifftn(ref, dim=(-2, -1))
     assert rel_l2(back.real, back.imag, *ref_back) <= tol_pow2(n)
     assert rel_l2(back.real, back.imag, re, im) <= 2 * tol_pow2(n)
 
 
-@pytest.mark.parametrize("shape", [(2, 16, 16), (1, 4096, 16), (3, 16, 2048), (2, 512, 1024), (1, 128, 64), (2, 64, 32)])
+@pytest.mark.parametrize("shape", [(2, 16, 16), (1, 4096, 16), (3, 16, 2048), (2, 512, 1024), (1, 128, 64), (2, 64, 32),
+                                   (2, 64, 4096), (1, 256, 4096)])
 def test_fft2_real_input(shape):
     # real input.  Two-pass shapes: pass 1 writes columns 0..W/2, pass 2 completes W/2+1..W-1
     # from the 2-D Hermitian symmetry; small images are transformed whole.  Forward and inverse

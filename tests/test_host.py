@@ -66,6 +66,10 @@ def test_fft2_shape_gates():
     for h, w in [(2, 64), (64, 2), (4, 2048), (8, 2048), (256, 128), (12, 16), (3, 3)]:
         assert not fft2_small_ok(h, w), (h, w)
     assert fft2_ok(4, 4) and fft2_ok(16, 2048) and fft2_ok(4096, 16) and not fft2_ok(4, 2048)
+    assert fft2_ok(16, 4096) and fft2_ok(4096, 4096) and not fft2_ok(8192, 16) and not fft2_ok(16, 8192)
+    # complex input: two-pass kernels only for 256 <= w <= 512 with h >= 512; small images always
+    assert fft2_ok(512, 512, False) and fft2_ok(4096, 256, False) and fft2_ok(64, 64, False)
+    assert not fft2_ok(1024, 1024, False) and not fft2_ok(256, 256, False) and not fft2_ok(2048, 64, False)
 
 
 def test_strided_axis_gates():

@@ -147,9 +147,10 @@ def _fftn(input, s, dim, inverse: bool) -> ComplexTensor:
     if s is not None:
         for size, d in zip(s, dim):
             x = _resize_dim_real(x, d, size) if real_in else _resize_dim(x, d, size)
-    if ndim >= 2 and sorted(dim) == [ndim - 2, ndim - 1] and fft2_ok(x.shape[-2], x.shape[-1]):
-        # both trailing axes at once: the two-pass 2-D kernels (the 1-D transforms of the two
-        # axes commute; only rounding differs from the reference's dim -2 then dim -1 order)
+    if ndim >= 2 and sorted(dim) == [ndim - 2, ndim - 1] and fft2_ok(x.shape[-2], x.shape[-1], real_in):
+        # both trailing axes at once: the 2-D kernels where they measured faster than the two
+        # single-axis passes (the 1-D transforms of the two axes commute; only rounding differs
+        # from the reference's dim -2 then dim -1 order)
         _resolve(None)
         _require_hip("fft2")
         if real_in:

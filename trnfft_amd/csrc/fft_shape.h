@@ -63,7 +63,7 @@ __host__ __device__ constexpr bool stft_pf(int n) { return n >= 1024; }
 
 // Elements per thread of the 2-D transform's paired real-row pass 1 and column pass 2 (the
 // many-lanes-per-transform shape that also won for the STFT).
-__host__ __device__ constexpr int fft2_pair_epth(int w) { return w < 8 ? w : 8; }
+__host__ __device__ constexpr int fft2_pair_epth(int w) { return w < 8 ? w : w >= 4096 ? 16 : 8; }
 __host__ __device__ constexpr int fft2_col_epth(int hr) { return hr < 8 ? hr : 8; }
 
 // Single-pass 2-D transform of small images (h*w <= 16384 complex: whole images in LDS).  A

@@ -32,7 +32,10 @@ __global__ __launch_bounds__(Fft2Row<W>::THREADS) void fft2_pass1_kernel(
   using C = Fft2Row<W>;
   constexpr int E = C::E, T = C::T, PADW = C::PADW;
   static_assert(8 * E >= 16 && (W * 8) % C::THREADS == 0, "layout");
-  __shared__ float2 lds[8 * PADW];  // interleaved (re, im)
+  // the 8 rows as interleaved (re, im) entries, or (W = 4096, 8 rows = 278 KB) one plane at a time
+  constexpr bool SPL = 8LL * PADW * 8 > kLdsBytes;
+  __shared__ float2 lds[SPL ? 8 * PADW / 2 : 8 * PADW];
+  float* lre = reinterpret_cast<float*>(lds);
   const long long g = blockIdx.x;
   const long long b = g / HR;
   const int r1 = (int)(g % HR);
@@ -48,12 +51,34 @@ __global__ __launch_bounds__(Fft2Row<W>::THREADS) void fft2_pass1_kernel(
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = make_float2(ld_stream(pr + T * e), REAL_IN ? 0.0f : ld_stream(pi + T * e));
   }
-  LdsFft<W, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + j * PADW), nullptr, tw_w, tid);
-#pragma unroll
-  for (int e = 0; e < E; ++e) lds[j * PADW + lds_pad(tid + T * e)] = v[e];
-  __syncthreads();
   // cross-row 8-point DFT: thread t handles columns k = t + THREADS*m, m < W*8/THREADS/8
   constexpr int KPT = W / C::THREADS;  // columns per thread (>= 1 since W >= THREADS/8 * 8)
+  float2 zc[SPL ? KPT : 1][8];          // split planes: the columns gathered one plane at a time
+  if constexpr (SPL) {
+    LdsFft<W, E, DIR, false, true>::run(v, lre + j * PADW, nullptr, tw_w, tid);
+#pragma unroll
+    for (int plane = 0; plane < 2; ++plane) {
+      __syncthreads();  // the previous reads of the buffer are done
+#pragma unroll
+      for (int e = 0; e < E; ++e) lre[j * PADW + lds_pad(tid + T * e)] = plane ? v[e].y : v[e].x;
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < KPT; ++m) {
+        const int k = threadIdx.x + C::THREADS * m;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float f = lre[jj * PADW + lds_pad(k)];
+          if (plane) zc[m][jj].y = f;
+          else zc[m][jj].x = f;
+        }
+      }
+    }
+  } else {
+    LdsFft<W, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + j * PADW), nullptr, tw_w, tid);
+#pragma unroll
+    for (int e = 0; e < E; ++e) lds[j * PADW + lds_pad(tid + T * e)] = v[e];
+    __syncthreads();
+  }
   float2 tq[8];
 #pragma unroll
   for (int q = 1; q < 8; ++q) tq[q] = tw_h[(r1 * q) & (H - 1)];
@@ -62,7 +87,7 @@ __global__ __launch_bounds__(Fft2Row<W>::THREADS) void fft2_pass1_kernel(
     const int k = threadIdx.x + C::THREADS * m;
     float2 z[8];
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) z[jj] = lds[jj * PADW + lds_pad(k)];
+    for (int jj = 0; jj < 8; ++jj) z[jj] = SPL ? zc[SPL ? m : 0][jj] : lds[jj * PADW + lds_pad(k)];
     Dft<8, DIR>::run(z);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -361,7 +386,7 @@ template <int DIR>
 static hipError_t launch_fft2_dir(const Fft2Args& a) {
   if (fft2_small_ok(a.h, a.w)) return launch_fft2_small<DIR>(a);
   hipError_t e;
-  switch (a.w) {  // 8 rows x W/E threads must fit one 1024-thread workgroup: W <= 2048
+  switch (a.w) {  // 8 rows x W/E threads must fit one 1024-thread workgroup (W = 4096: E = 32, split planes)
     case 16: e = launch_pass1_w<16, DIR>(a); break;
     case 32: e = launch_pass1_w<32, DIR>(a); break;
     case 64: e = launch_pass1_w<64, DIR>(a); break;
@@ -370,6 +395,7 @@ static hipError_t launch_fft2_dir(const Fft2Args& a) {
     case 512: e = launch_pass1_w<512, DIR>(a); break;
     case 1024: e = launch_pass1_w<1024, DIR>(a); break;
     case 2048: e = launch_pass1_w<2048, DIR>(a); break;
+    case 4096: e = launch_pass1_w<4096, DIR>(a); break;
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess) return e;

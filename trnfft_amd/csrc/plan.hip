@@ -408,9 +408,9 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         rc = p->upload(lds_table((int)h, dir, e), &p->tw_sh);
         break;
       }
-      if (!is_pow2(n) || n < 16 || n > 2048 || !is_pow2(h) || h < 16 || h > 4096) {
+      if (!is_pow2(n) || n < 16 || n > 4096 || !is_pow2(h) || h < 16 || h > 4096) {
         rc = fail(TFA_ERR_UNSUPPORTED,
-                  "FFT2 plans need power-of-two 16 <= n <= 2048 and 16 <= n2 <= 4096, or n * n2 <= 16384 "
+                  "FFT2 plans need power-of-two 16 <= n <= 4096 and 16 <= n2 <= 4096, or n * n2 <= 16384 "
                   "with both axes >= 4 (and >= 8 / 16 at n * n2 = 8192 / 16384)");
         break;
       }
