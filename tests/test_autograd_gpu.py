@@ -122,7 +122,8 @@ def test_irfft_general_n_gradient_via_oracle():
     assert rel_l2(a_r.grad, a_i.grad, r_r.grad, r_i.grad) <= 1e-5
 
 
-@pytest.mark.parametrize("shape,real_in", [((2, 64, 128), False), ((2, 64, 128), True), ((3, 16, 2048), False)])
+@pytest.mark.parametrize("shape,real_in", [((2, 64, 128), False), ((2, 64, 128), True), ((3, 16, 2048), False),
+                                           ((1, 512, 256), True), ((1, 64, 4096), True)])
 def test_fft2_gradient(shape, real_in):
     g = torch.Generator().manual_seed(8)
     xr = torch.randn(*shape, generator=g)

@@ -76,7 +76,7 @@ class _C2CFn(torch.autograd.Function):
         elif ctx.mode == "strided":
             g = _fc.execute_strided(g_re, g_im, ctx.dim, adj)
         else:
-            g = _fc.execute_fft2(g_re, g_im, adj)
+            g = _fc.execute_fft2_any(g_re, g_im, adj)
         s = 1.0 / ctx.size if ctx.inverse else float(ctx.size)
         d_re = g.real.mul_(s)
         d_im = None if ctx.real_in else g.imag.mul_(s)

@@ -239,6 +239,17 @@ def execute_fft2(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> Co
     return out if out_dev == dev else out.to(out_dev)
 
 
+def execute_fft2_any(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> ComplexTensor:
+    """2-D transform over the last two axes by whichever route measured faster for this input
+    (``fft2_ok``): the 2-D kernels, or the strided pass over axis -2 then the contiguous pass
+    over axis -1 (used for the adjoint of a real-input fft2, whose gradient is complex)."""
+    h, w = re.shape[-2], re.shape[-1]
+    if fft2_ok(h, w, im is None):
+        return execute_fft2(re, im, inverse)
+    y = execute_strided(re, im, re.dim() - 2, inverse)
+    return execute_1d(y.real, y.imag, inverse)
+
+
 def execute_stft(x: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int, center: bool, normalized: bool,
                  onesided: bool, num_frames: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Fused STFT kernel on device-resident fp32 x (..., L) and window (n_fft): (re, im) planes of
