@@ -10,7 +10,7 @@ import torch
 
 import oracle
 import trnfft_amd
-from conftest import rel_l2, tol_pow2
+from conftest import rel_l2, tol_bluestein, tol_pow2
 from trnfft_amd import ComplexTensor
 from trnfft_amd.fft_core import fft2_small_ok
 
@@ -27,6 +27,37 @@ def test_rfft_irfft():
     back = trnfft_amd.irfft(got, n=128)
     ref_back = oracle.irfft(ref, n=128)
     assert rel_l2(back, torch.zeros_like(back), ref_back, torch.zeros_like(ref_back)) <= tol_pow2(128)
+
+
+@pytest.mark.parametrize("n,bins,batch", [(8, 5, 3), (64, 33, 2), (100, 51, 3), (1024, 513, 4), (1000, 501, 2),
+                                           (256, 129, 1), (100, 60, 2), (64, 40, 3)])
+def test_hfft_ihfft_vs_numpy_and_oracle(n, bins, batch):
+    # hfft = irfft(conj(x), n) * n (trnfft/api.py:71-86).  At the default n = 2*(bins-1) this is
+    # numpy's hfft; for a shorter n the reference's Hermitian completion (trnfft/api.py:49-68)
+    # keeps every given bin and mirrors bins 1..n-bins, which numpy does not, so those cases are
+    # checked against the oracle's restatement of it
+    rng = np.random.default_rng(n + bins)
+    re = rng.standard_normal((batch, bins)).astype(np.float32)
+    im = rng.standard_normal((batch, bins)).astype(np.float32)
+    got = trnfft_amd.hfft(ComplexTensor(torch.from_numpy(re).cuda(), torch.from_numpy(im).cuda()), n=n)
+    tol = tol_pow2(n) if n & (n - 1) == 0 else 3 * tol_bluestein(n)
+    if n == 2 * (bins - 1):
+        ref = np.fft.hfft(re.astype(np.float64) + 1j * im, n=n, axis=-1)
+    else:
+        ref = oracle.irfft((torch.from_numpy(re), -torch.from_numpy(im)), n=n).double().numpy() * n
+    assert rel_l2(got, torch.zeros_like(got), ref, np.zeros_like(ref)) <= tol, (n, bins)
+    x = rng.standard_normal((batch, n)).astype(np.float32)
+    z = trnfft_amd.ihfft(torch.from_numpy(x).cuda())
+    e = np.fft.ihfft(x.astype(np.float64), axis=-1)
+    assert rel_l2(z.real, z.imag, e.real, e.imag) <= tol, n
+
+
+def test_hfft_longer_n_than_the_spectrum_raises_like_the_reference():
+    # n > 2*(bins-1): the reference's completion has no zero padding and fails on the shape
+    # mismatch (trnfft/api.py:64-65); the HIP path raises the same RuntimeError
+    x = ComplexTensor(torch.randn(2, 400).cuda(), torch.randn(2, 400).cuda())
+    with pytest.raises(RuntimeError):
+        trnfft_amd.hfft(x, n=1000)
 
 
 def test_hfft_ihfft_roundtrip():
