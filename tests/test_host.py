@@ -153,3 +153,14 @@ class TestComplexTensor:
         assert x[1].shape == (4,)
         with pytest.raises(AssertionError):
             ComplexTensor(torch.randn(2), torch.randn(3))
+
+
+def test_reference_public_names_are_exported():
+    # every name of the reference's public API (trnfft/__init__.py:36-68, __all__) exists here
+    names = ["fft", "ifft", "rfft", "hfft", "ihfft", "irfft", "fft2", "fftn", "ifftn", "rfft2", "irfft2", "rfftn",
+             "irfftn", "stft", "istft", "ComplexTensor", "complex_matmul", "create_plan", "clear_plan_cache", "FFTPlan",
+             "HAS_NKI", "set_backend", "get_backend", "set_precision", "set_ozaki_product_precision_verified",
+             "get_precision"]
+    missing = [n for n in names if not hasattr(trnfft_amd, n)]
+    assert not missing, missing
+    assert trnfft_amd.HAS_NKI is False

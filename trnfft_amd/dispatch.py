@@ -23,6 +23,8 @@ from . import _lib
 from .complex import ComplexTensor
 
 HAS_HIP = _lib.library_present()
+# the reference's flag (trnfft/nki/dispatch.py:17-24): this backend has no NKI path
+HAS_NKI = False
 
 _backend = "auto"
 
