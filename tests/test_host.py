@@ -41,6 +41,10 @@ def test_abi_rejects_bad_arguments_without_gpu():
     assert lib.tfa_plan_create(ctypes.byref(h), ctypes.byref(desc)) == _lib.TFA_ERR_INVALID
     assert b"length" in lib.tfa_last_error()
     assert lib.tfa_execute(None, 1, None, None, None, None, None, None) == _lib.TFA_ERR_INVALID
+    nbytes = ctypes.c_size_t(7)
+    assert lib.tfa_strided_workspace_size(None, 1, 16, ctypes.byref(nbytes)) == _lib.TFA_ERR_INVALID
+    assert lib.tfa_execute_strided_ws(None, 1, 16, None, None, None, None, None, None) == _lib.TFA_ERR_INVALID
+    assert lib.tfa_execute_strided(None, 1, 16, None, None, None, None, None) == _lib.TFA_ERR_INVALID
     with pytest.raises(ValueError):
         _lib.check(_lib.TFA_ERR_INVALID, "x")
 
