@@ -109,7 +109,8 @@ int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, con
  * whose size tfa_strided_workspace_size reports (2 * 4 * outer * n * stride bytes for such axes,
  * else 0).  n = 4096 with stride >= 16 also takes two passes (faster than the single pass there).
  * In place allowed (out_* == in_*); the workspace must not overlap the data.  Every other
- * plan/stride goes to tfa_execute_strided (workspace unused).  Replaces the same transposes of
+ * plan/stride goes to tfa_execute_strided (workspace unused).  outer = 0 is a no-op on both entry
+ * points (the size query then reports 0 bytes).  Replaces the same transposes of
  * trnfft/api.py:496-516 for long axes.
  */
 int tfa_strided_workspace_size(const tfa_plan* plan, int64_t outer, int64_t stride, size_t* bytes);

@@ -276,3 +276,20 @@ def test_fft2_small_image_known_answers():
     ref = torch.zeros(h, w)
     ref[3, 5] = h * w
     assert torch.allclose(z.real.cpu(), ref, atol=1e-3) and torch.allclose(z.imag.cpu(), torch.zeros(h, w), atol=1e-3)
+
+
+def test_empty_batches():
+    # zero rows / images / outer blocks: every entry point returns an empty result of the right
+    # shape without launching anything (torch.fft gives the same shapes)
+    def c(shape):
+        return ComplexTensor(torch.zeros(shape, device="cuda"), torch.zeros(shape, device="cuda"))
+
+    assert tuple(trnfft_amd.fft(c((0, 1024))).shape) == (0, 1024)
+    assert tuple(trnfft_amd.ifft(c((0, 1000))).shape) == (0, 1000)              # Bluestein
+    assert tuple(trnfft_amd.fft(c((0, 1 << 20))).shape) == (0, 1 << 20)         # four-step
+    assert tuple(trnfft_amd.rfft(torch.zeros(0, 64, device="cuda")).shape) == (0, 33)
+    assert tuple(trnfft_amd.irfft(c((0, 33))).shape) == (0, 64)
+    assert tuple(trnfft_amd.fftn(c((0, 8192, 16)), dim=(1,)).shape) == (0, 8192, 16)  # strided multi-pass
+    assert tuple(trnfft_amd.fftn(c((0, 64, 5)), dim=(1,)).shape) == (0, 64, 5)
+    assert tuple(trnfft_amd.fft2(torch.zeros(0, 64, 64, device="cuda")).shape) == (0, 64, 64)
+    assert tuple(trnfft_amd.fft2(c((0, 256, 512))).shape) == (0, 256, 512)
