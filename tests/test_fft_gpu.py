@@ -228,3 +228,19 @@ def test_bluestein_split_large_vs_oracle(n, batch, inverse):
     got = _gpu_fft(re, im, inverse)
     ref = oracle.fft_core(re, im, inverse)
     assert rel_l2(*got, *ref) <= tol_bluestein(n), (n, inverse)
+
+
+def test_bluestein_largest_length_and_beyond():
+    # the longest Bluestein axis the library takes, n = 2^23 - 1 (padded m = 2^24, the split
+    # three-pass path), against the oracle (fp32 chirp included) in both directions; one sample
+    # more would pad to 2^25 and is refused with NotImplementedError
+    n = (1 << 23) - 1
+    assert trnfft_amd.create_plan(n).padded_n == 1 << 24
+    re, im = seeded_complex(1, n, seed=9)
+    for inverse in (False, True):
+        y = _gpu_fft(re, im, inverse)
+        ref = oracle.fft_core(re, im, inverse)
+        assert rel_l2(*y, *ref) <= tol_bluestein(n), inverse
+    big = (1 << 23) + 1
+    with pytest.raises(NotImplementedError):
+        trnfft_amd.fft(ComplexTensor(torch.zeros(1, big, device="cuda"), torch.zeros(1, big, device="cuda")))
