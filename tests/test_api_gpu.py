@@ -293,3 +293,56 @@ def test_empty_batches():
     assert tuple(trnfft_amd.fftn(c((0, 64, 5)), dim=(1,)).shape) == (0, 64, 5)
     assert tuple(trnfft_amd.fft2(torch.zeros(0, 64, 64, device="cuda")).shape) == (0, 64, 64)
     assert tuple(trnfft_amd.fft2(c((0, 256, 512))).shape) == (0, 256, 512)
+
+
+def test_views_are_transformed_as_their_values():
+    # expanded (stride 0), strided-slice, transposed and offset views: the entry points copy them
+    # to contiguous fp32 first, so each result equals the transform of the materialised values
+    g = torch.Generator(device="cuda").manual_seed(3)
+    base = torch.randn(64, 2048, device="cuda", generator=g)
+    views = [base[:1].expand(32, 2048), base[:, ::2], base[:, :1024].t(), base[5:37, 7:1007], base[:, 1:]]
+    import oracle
+
+    # against the oracle: the 1000-point view is a Bluestein length, where the reference operator's
+    # fp32 chirp sits ~1.2e-4 from the exact DFT
+    for v in views:
+        assert not v.is_contiguous()
+        vc = v.cpu().contiguous()
+        got = trnfft_amd.fft(v)
+        ref = oracle.fft_core(vc, torch.zeros_like(vc), False)
+        assert rel_l2(got.real, got.imag, *ref) <= tol_bluestein(v.shape[-1]), tuple(v.shape)
+        got = trnfft_amd.rfft(v)
+        assert rel_l2(got.real, got.imag, *oracle.rfft(vc)) <= tol_bluestein(v.shape[-1]), tuple(v.shape)
+    z = ComplexTensor(base[:, ::2], base[:, 1::2])
+    got = trnfft_amd.ifft(z)
+    ref = np.fft.ifft(base[:, ::2].cpu().double().numpy() + 1j * base[:, 1::2].cpu().double().numpy(), axis=-1)
+    assert rel_l2(got.real, got.imag, ref.real, ref.imag) <= tol_pow2(1024)
+
+
+def test_one_plan_on_two_streams_at_once():
+    # the cached plans (four-step with its workspace, split Bluestein, STFT) driven from two
+    # streams concurrently give the same results as one stream at a time
+    g = torch.Generator(device="cuda").manual_seed(4)
+    shapes = [(8, 1 << 18), (3, 40000), (64, 1024)]
+    xs = [[ComplexTensor(torch.randn(s, device="cuda", generator=g), torch.randn(s, device="cuda", generator=g))
+           for _ in range(2)] for s in shapes]
+    sig = [torch.randn(16, 50000, device="cuda", generator=g) for _ in range(2)]
+    serial = [[trnfft_amd.fft(x) for x in pair] for pair in xs]
+    serial_s = [trnfft_amd.stft(s, 512, hop_length=128) for s in sig]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[None] * len(shapes) for _ in range(2)]
+    outs_s = [None, None]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for rep in range(3):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                for j in range(len(shapes)):
+                    outs[i][j] = trnfft_amd.fft(xs[j][i])
+                outs_s[i] = trnfft_amd.stft(sig[i], 512, hop_length=128)
+        torch.cuda.synchronize()
+        for i in range(2):
+            for j in range(len(shapes)):
+                assert torch.equal(outs[i][j].real, serial[j][i].real) and torch.equal(outs[i][j].imag, serial[j][i].imag)
+            assert torch.equal(outs_s[i].real, serial_s[i].real) and torch.equal(outs_s[i].imag, serial_s[i].imag)
