@@ -94,6 +94,9 @@ def _traffic_from_profiles(kernel_tag: str):
 # ---------------------------------------------------------------------------------------------
 
 
+ROOFLINE_STEPS = 200  # fixed back-to-back region for roofline.t_launch: 200 steps = 400 launches
+
+
 def bench_headline(steps: int, warmup: int):
     import trnfft_amd
     from trnfft_amd import _lib
@@ -139,62 +142,66 @@ def bench_headline(steps: int, warmup: int):
         if rc:
             _lib.check(rc, "tfa_execute")
 
-    for k in range(warmup):
-        step(k)
-    torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
 
-    # eager: one C-ABI call per launch from Python
-    t0 = time.perf_counter()
-    ev0.record()
-    for k in range(steps):
-        step(k)
-    ev1.record()
-    torch.cuda.synchronize()
-    wall_eager = time.perf_counter() - t0
-    t_eager_launch = ev0.elapsed_time(ev1) * 1e-3 / (2 * steps)
+    def eager_region(k_steps):
+        """Events around k_steps eager steps (one C-ABI call per launch from Python), bracketed by
+        synchronize on both sides; returns (GPU seconds, wall seconds)."""
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev0.record()
+        for k in range(k_steps):
+            step(k)
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) * 1e-3, time.perf_counter() - t0
 
-    # graph: the same K steps captured once into a HIP graph and replayed (no host work between
-    # launches); this is the timed region reported as `value`
+    for k in range(warmup):
+        step(k)
+    torch.cuda.synchronize()
+
+    # the timed region reported as `value`: exactly K steps, three times, median
+    regions = sorted(eager_region(steps) for _ in range(3))
+    t_region, wall = regions[1]
+
+    # roofline.t_launch: a fixed region of ROOFLINE_STEPS steps (2 x ROOFLINE_STEPS back-to-back
+    # launches, alternating directions over the rotated sets), independent of --steps, captured
+    # once into a HIP graph (no host work between launches); 3 warm-up replays, then 3 timed
+    # replays, median
     graph = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream()
     cap.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(cap):
         with torch.cuda.graph(graph, stream=cap):
             strm = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-            for k in range(steps):
+            for k in range(ROOFLINE_STEPS):
                 step(k, strm)
     torch.cuda.current_stream().wait_stream(cap)
-    for _ in range(3):  # warm-up replays (the first replays after capture run measurably slower)
+    for _ in range(3):  # the first replays after capture run measurably slower
         graph.replay()
-    torch.cuda.synchronize()
-    # the K-step region is timed three times (each: synchronize, events around one replay of all
-    # K steps, synchronize); the median region is reported
-    regions = []
+    graph_regions = []
     for _ in range(3):
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
         ev0.record()
         graph.replay()
         ev1.record()
         torch.cuda.synchronize()
-        regions.append((ev0.elapsed_time(ev1) * 1e-3, time.perf_counter() - t0))
-    regions.sort()
-    t_region, wall = regions[1]
-    t_region_launch = t_region / (2 * steps)
+        graph_regions.append(ev0.elapsed_time(ev1) * 1e-3)
+    t_launch = _median(graph_regions) / (2 * ROOFLINE_STEPS)
+    # the same fixed region launched eagerly, for comparison
+    t_launch_eager = _median([eager_region(ROOFLINE_STEPS)[0] for _ in range(3)]) / (2 * ROOFLINE_STEPS)
 
     # per-launch kernel durations (separate pass, event pairs around each launch)
     timer = EventTimer()
-    for k in range(max(20, min(steps, 200))):
+    for k in range(100):
         timer.record(lambda k=k: execute(*args_f[k % sets]))
         timer.record(lambda k=k: execute(*args_i[k % sets]))
     d = timer.durations_s()
-    t_launch = t_region_launch
 
-    # correctness of what was timed: the last step's two outputs (written after every other
-    # access to those buffers in the graph) equal fresh eager transforms, bit for bit
-    kf, ki = (steps - 1) % sets, (steps - 1 + sets // 2) % sets
+    # correctness of what was timed: the last graph step's two outputs (written after every
+    # other access to those buffers in the graph) equal fresh eager transforms, bit for bit
+    kf, ki = (ROOFLINE_STEPS - 1) % sets, (ROOFLINE_STEPS - 1 + sets // 2) % sets
     chk = trnfft_amd.fft(trnfft_amd.ComplexTensor(ins[kf][0], ins[kf][1]))
     chk_i = trnfft_amd.ifft(trnfft_amd.ComplexTensor(ins[ki][0], ins[ki][1]))
     graph.replay()
@@ -210,7 +217,7 @@ def bench_headline(steps: int, warmup: int):
     for k in range(warmup):
         cdst[k % sets].copy_(csrc[k % sets])
     torch.cuda.synchronize()
-    reps = max(20, min(2 * steps, 400))
+    reps = 2 * ROOFLINE_STEPS
     ev0.record()
     for k in range(reps):
         cdst[k % sets].copy_(csrc[(k + 3) % sets])
@@ -223,13 +230,14 @@ def bench_headline(steps: int, warmup: int):
     bytes_launch = 2 * 2 * plane  # read re+im, write re+im
     return {
         "t_copy_s": t_copy,
-        "wall_eager_s": wall_eager,
-        "t_eager_launch_s": t_eager_launch,
+        "t_region_s": t_region,
         "wall_s": wall,
-        "ms_per_step": wall / steps * 1e3,
-        "value": flops_step * steps / wall / 1e9,
+        "ms_per_step": t_region / steps * 1e3,
+        "value": flops_step * steps / t_region / 1e9,
         "regions_ms": [round(r[0] * 1e3, 4) for r in regions],
+        "graph_regions_ms": [round(r * 1e3, 4) for r in graph_regions],
         "t_launch_s": t_launch,
+        "t_launch_eager_s": t_launch_eager,
         "t_launch_median_s": _median(d),
         "bytes_launch": bytes_launch,
         "buffer_sets": sets,
@@ -421,34 +429,101 @@ def bench_secondary():
 # ---------------------------------------------------------------------------------------------
 
 
-def bench_cpu_baseline(reps: int = 3):
+CPU_K_LIMIT = 256  # literal-loop positions timed per stage in the capped samples (the rest extrapolated)
+
+
+def bench_cpu_baseline():
+    """The reference's pytorch CPU path (restated in oracle/, every power-of-two transform through
+    the literal per-k loop of trnfft/fft_core.py:67-117) on this host's cores, for every BASELINE
+    config.  Configs whose full run would take minutes are timed on a stated sample: stages with
+    more than CPU_K_LIMIT butterfly positions run only the first CPU_K_LIMIT (each position of a
+    stage does identical work, so the stage time scales by positions / run), and C4a runs one of
+    its 32 images (scaled x 32)."""
     sys.path.insert(0, ROOT)
     import oracle
 
-    threads = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    batch, n = 4096, 1024
-    re, im = make_c2c_input(batch, n)
-    oracle.cooley_tukey_loop(re[:64], im[:64], False)  # warm-up
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        fr, fi = oracle.cooley_tukey_loop(re, im, False)
-        oracle.cooley_tukey_loop(fr, fi, True)
-        times.append(time.perf_counter() - t0)
-    t = _median(times)
     try:
-        model = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
-        model = next((l.split(":", 1)[1].strip() for l in model.splitlines() if l.startswith("Model name")), "")
+        lscpu = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        model = next((l.split(":", 1)[1].strip() for l in lscpu.splitlines() if l.startswith("Model name")), "")
     except Exception:
         model = ""
+
+    def timed(fn, k_limit=None, reps=1):
+        """Median over reps of the (extrapolated) seconds of fn() under the literal loop."""
+        secs, frac = [], 1.0
+        for _ in range(reps):
+            with oracle.LiteralLoopTiming(k_limit) as t:
+                fn()
+            secs.append(t.seconds)
+            frac = t.positions_run / max(1, t.positions_total)
+        return _median(secs), frac
+
+    configs = {}
+
+    def rec(name, fn, flops, sample, k_limit=None, reps=1, scale=1.0):
+        sec, frac = timed(fn, k_limit, reps)
+        sec *= scale
+        configs[name] = {
+            "seconds": round(sec, 4),
+            "gflops": round(flops / sec / 1e9, 4),
+            "reps": reps,
+            "sample": sample + (f"; literal loop capped at {k_limit} positions per stage "
+                                f"({100 * frac:.1f} % of positions run, rest extrapolated)" if k_limit else ""),
+        }
+
+    # C1: 4096 x 1024 fft + ifft (the headline workload), full, median of 3
+    re, im = make_c2c_input(4096, 1024)
+    oracle.cooley_tukey_loop(re[:64], im[:64], False)  # warm-up
+
+    def c1():
+        fr, fi = oracle.fft_core(re, im, False)
+        oracle.fft_core(fr, fi, True)
+
+    rec("c1_c2c_4096x1024_fwd_inv", c1, 2 * flops_fft(1024, 4096), "full workload (fft then ifft)", reps=3)
+    # C2: STFT 64 x 160000, n_fft 512, hop 256, periodic Hann, reflect centre, onesided (api.py:291-365)
+    x = make_stft_input(64, 160000)
+    win = torch.hann_window(512)
+    rec("c2_stft_64x160000_nfft512", lambda: oracle.stft(x, 512, 256, window=win), 40064 * 5 * 512 * 9,
+        "full workload")
+    # C3: Bluestein (fft_core.py:1285-1376): three m-point transforms per call
+    for n, b, lim in [(1000, 1024, None), (4099, 256, CPU_K_LIMIT)]:
+        re, im = make_c2c_input(b, n)
+        rec(f"c3_bluestein_{b}x{n}", lambda: oracle.fft_core(re, im, False), flops_fft(n, b), "full batch", k_limit=lim)
+    # C4a: fft2 of 32 real 2048 x 2048 images (api.py:105-139, transposes + two axis passes): one image
+    g = torch.Generator().manual_seed(42)
+    img = torch.rand(1, 2048, 2048, generator=g)
+    rec("c4a_fft2_32x2048x2048", lambda: oracle.fft2(img), 32 * 5 * 2048 * 2048 * 22,
+        "1 of the 32 images, time x 32", k_limit=CPU_K_LIMIT, scale=32.0)
+    # C4b: 16 x 2^20 c2c (the reference's CPU path runs the radix-2 loop at any length)
+    re, im = make_c2c_input(16, 1 << 20)
+    rec("c4b_c2c_16x2^20", lambda: oracle.fft_core(re, im, False), flops_fft(1 << 20, 16), "full batch",
+        k_limit=CPU_K_LIMIT)
+    # C5a: ComplexLinear 8192 x 1024 -> 1024, four F.linear (nn.py:43-48), median of 3
+    g = torch.Generator().manual_seed(42)
+    xr, xi = torch.randn(8192, 1024, generator=g), torch.randn(8192, 1024, generator=g)
+    wr = (torch.rand(1024, 1024, generator=g) * 2 - 1).div_(32)
+    wi = (torch.rand(1024, 1024, generator=g) * 2 - 1).div_(32)
+    rec("c5a_complex_linear_8192x1024x1024", lambda: oracle.complex_linear((xr, xi), wr, wi),
+        8.0 * 8192 * 1024 * 1024, "full workload, 4 sgemm (torch CPU)", reps=3)
+    # C5b: 65536 x 256 forward; the reference's CPU path runs the radix-2 loop (DFT-GEMM is NKI-only)
+    re, im = make_c2c_input(65536, 256)
+    rec("c5b_c2c_65536x256", lambda: oracle.fft_core(re, im, False), flops_fft(256, 65536),
+        "full workload (radix-2 loop: the pytorch backend never takes the DFT-GEMM route)")
+    del re, im, x, img, xr, xi
+
+    head = configs["c1_c2c_4096x1024_fwd_inv"]
     return {
-        "value": round(2 * flops_fft(n, batch) / t / 1e9, 4),
+        "value": head["gflops"],
         "unit": "GFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"full workload 4096x{n} fft+ifft, reference radix-2 per-k loop (oracle.cooley_tukey_loop, "
-        f"trnfft/fft_core.py:53-117), torch CPU fp32, median of {reps}, {t:.2f} s/step; host: {model}",
+        "sample": f"C1 full workload 4096x1024 fft+ifft, reference radix-2 per-k loop "
+        f"(oracle.cooley_tukey_loop, trnfft/fft_core.py:53-117), torch CPU fp32, median of 3, "
+        f"{head['seconds']:.2f} s/step; host: {model}",
+        "host": model,
+        "configs": configs,
     }
 
 
@@ -485,12 +560,12 @@ def main(argv=None):
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: N(0,1) re/im, seed 42, 4096x1024 (BASELINE config 1)",
-        "value_eager": round(2 * flops_fft(1024, 4096) * args.steps / head["wall_eager_s"] / 1e9, 1),
         "timed_regions_ms": head["regions_ms"],
+        "ms_per_step_wall": round(head["wall_s"] / args.steps * 1e3, 5),
         "config": {
             "workload": "batched c2c FFT, 4096 x N=1024 fp32 split re/im; step = forward fft of one batch + "
-            "inverse fft of another, buffers rotated over >1 GiB; K steps replayed as one HIP graph, the "
-            "K-step region timed 3 times after 3 warm-up replays, median reported",
+            "inverse fft of another, buffers rotated over >1 GiB; the K-step region (eager launches, events "
+            "around it, synchronize on both sides) timed 3 times, median reported",
             "n": 1024,
             "batch": 4096,
             "buffer_sets": head["buffer_sets"],
@@ -504,8 +579,11 @@ def main(argv=None):
             "frac": round(achieved / HBM_PEAK, 4),
             "traffic": _traffic_from_profiles("c2c_lds_n1024"),
             "t_launch_us": round(head["t_launch_s"] * 1e6, 3),
+            "t_launch_from": f"median of 3 replays of one HIP graph of {2 * ROOFLINE_STEPS} back-to-back launches "
+            "(fixed, independent of --steps)",
+            "graph_regions_ms": head["graph_regions_ms"],
+            "t_launch_eager_us": round(head["t_launch_eager_s"] * 1e6, 3),
             "t_launch_isolated_median_us": round(head["t_launch_median_s"] * 1e6, 3),
-            "t_launch_eager_us": round(head["t_eager_launch_s"] * 1e6, 3),
             "bytes_per_launch": head["bytes_launch"],
             "copy_gbps": round(head["bytes_launch"] / head["t_copy_s"] / 1e9, 1),
             "frac_of_copy": round(head["t_copy_s"] / head["t_launch_s"], 4),

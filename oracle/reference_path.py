@@ -10,6 +10,7 @@ the literal loop and the tests check both forms agree bit for bit.
 from __future__ import annotations
 
 import math
+import time
 
 import numpy as np
 import torch
@@ -20,6 +21,7 @@ __all__ = [
     "bit_reverse_indices_loop",
     "cooley_tukey",
     "cooley_tukey_loop",
+    "LiteralLoopTiming",
     "bluestein",
     "reference_chirp",
     "fft_core",
@@ -82,6 +84,8 @@ def cooley_tukey(re: torch.Tensor, im: torch.Tensor, inverse: bool) -> tuple[tor
     same fp32 operations (t*o products, difference/sum, then e+p and e-p) on every group; here
     all k are processed at once through a (..., n/m, m) view.
     """
+    if _LITERAL_LOOP is not None:
+        return _LITERAL_LOOP.run(re, im, inverse)
     n = re.shape[-1]
     log2n = int(math.log2(n))
     assert 1 << log2n == n, f"Not power of 2: {n}"
@@ -111,11 +115,18 @@ def cooley_tukey(re: torch.Tensor, im: torch.Tensor, inverse: bool) -> tuple[tor
     return re.contiguous(), im.contiguous()
 
 
-def cooley_tukey_loop(re: torch.Tensor, im: torch.Tensor, inverse: bool) -> tuple[torch.Tensor, torch.Tensor]:
+def cooley_tukey_loop(
+    re: torch.Tensor, im: torch.Tensor, inverse: bool, k_limit: int | None = None, stage_log: list | None = None
+) -> tuple[torch.Tensor, torch.Tensor]:
     """Literal restatement of trnfft/fft_core.py:67-117 with its per-k Python loop.
 
     Used to pin ``cooley_tukey`` (bit equality on small sizes) and as the CPU baseline, since
     this loop is where the reference's pytorch path spends its time.
+
+    Timing sample only: with ``k_limit`` each stage runs just its first ``k_limit`` butterfly
+    positions (the result is then NOT a transform) and appends (positions run, positions in the
+    stage, seconds) to ``stage_log``.  Every position of a stage does the same work on tensors
+    of the same size, so the stage's full time is its measured time x positions / run.
     """
     n = re.shape[-1]
     log2n = int(math.log2(n))
@@ -128,7 +139,9 @@ def cooley_tukey_loop(re: torch.Tensor, im: torch.Tensor, inverse: bool) -> tupl
         m = 1 << (s + 1)
         half = m >> 1
         tw_re, tw_im = _twiddles(half, m, sign, re.dtype)
-        for k in range(half):
+        run = half if k_limit is None else min(half, k_limit)
+        t_stage = time.perf_counter()
+        for k in range(run):
             even_idx = list(range(k, n, m))
             odd_idx = list(range(k + half, n, m))
             e_re = re[..., even_idx]
@@ -143,11 +156,59 @@ def cooley_tukey_loop(re: torch.Tensor, im: torch.Tensor, inverse: bool) -> tupl
             im[..., even_idx] = e_im + prod_im
             re[..., odd_idx] = e_re - prod_re
             im[..., odd_idx] = e_im - prod_im
+        if stage_log is not None:
+            stage_log.append((run, half, time.perf_counter() - t_stage))
     if inverse:
         scale = 1.0 / n
         re = re * scale
         im = im * scale
     return re, im
+
+
+class LiteralLoopTiming:
+    """Timing context (CPU baseline only): inside it every power-of-two transform that
+    ``cooley_tukey`` would do (through fft_core, bluestein, fftn, stft, ...) runs the literal
+    per-k loop of trnfft/fft_core.py:67-117 instead, capped at ``k_limit`` positions per stage.
+
+    ``seconds`` = measured wall time of the timed region + the time of the skipped positions
+    (each capped stage's measured time x (positions / run - 1)).  With ``k_limit=None`` nothing
+    is skipped and the outputs are the reference's; with a cap the outputs are meaningless.
+    """
+
+    def __init__(self, k_limit: int | None = None):
+        self.k_limit = k_limit
+        self.skipped_s = 0.0
+        self.positions_run = 0
+        self.positions_total = 0
+        self._t0 = 0.0
+        self.seconds = 0.0
+
+    def run(self, re, im, inverse):
+        log: list = []
+        out = cooley_tukey_loop(re, im, inverse, k_limit=self.k_limit, stage_log=log)
+        for run, half, sec in log:
+            self.positions_run += run
+            self.positions_total += half
+            if run < half:
+                self.skipped_s += sec * (half / run - 1.0)
+        return out
+
+    def __enter__(self):
+        global _LITERAL_LOOP
+        if _LITERAL_LOOP is not None:
+            raise RuntimeError("LiteralLoopTiming does not nest")
+        _LITERAL_LOOP = self
+        self._t0 = time.perf_counter()
+        return self
+
+    def __exit__(self, *exc):
+        global _LITERAL_LOOP
+        self.seconds = time.perf_counter() - self._t0 + self.skipped_s
+        _LITERAL_LOOP = None
+        return False
+
+
+_LITERAL_LOOP: LiteralLoopTiming | None = None
 
 
 def _cmul(ar, ai, br, bi):
