@@ -120,6 +120,53 @@ def test_stft_vs_oracle(n_fft, hop, center, normalized, onesided):
     assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(n_fft)
 
 
+@pytest.mark.parametrize("n_fft,hop,pad_mode,center,onesided,normalized,shape", [
+    (400, 160, "reflect", True, True, False, (2, 16000)),      # 25 ms @ 16 kHz: Bluestein frames (m = 1024)
+    (400, 100, "constant", True, True, True, (3, 5000)),
+    (12, 3, "replicate", True, True, False, (2, 301)),         # n_fft below the fused kernel's range
+    (12, 5, "circular", True, False, False, (1, 200)),         # (1, L): the reference squeezes the batch axis
+    (8192, 2048, "reflect", True, True, False, (2, 30000)),    # above the fused kernel's range
+    (8192, 4096, "constant", True, False, True, (20000,)),
+    (512, 128, "constant", True, True, False, (2, 3, 4000)),   # fused kernel on the device-padded signal
+    (512, 256, "replicate", True, True, True, (4000,)),
+    (1024, 300, "circular", True, False, False, (2, 5000)),
+    (8, 2, "reflect", False, True, False, (2, 100)),
+    (1000, 250, "reflect", False, False, False, (2, 3000)),
+    (2, 1, "constant", True, True, False, (3, 17)),
+])
+def test_stft_any_n_fft_and_pad_mode_vs_oracle(n_fft, hop, pad_mode, center, onesided, normalized, shape):
+    # every stft the reference computes (trnfft/api.py:291-365: F.pad with any mode, any n_fft
+    # through fft_core / Bluestein) runs here too, on the device
+    g = torch.Generator().manual_seed(n_fft + hop)
+    x = torch.randn(*shape, generator=g)
+    got = trnfft_amd.stft(x.cuda(), n_fft=n_fft, hop_length=hop, center=center, pad_mode=pad_mode,
+                          normalized=normalized, onesided=onesided)
+    ref = oracle.stft(x, n_fft=n_fft, hop_length=hop, center=center, pad_mode=pad_mode, normalized=normalized,
+                      onesided=onesided)
+    assert got.shape == ref[0].shape
+    tol = tol_pow2(n_fft) if n_fft & (n_fft - 1) == 0 else tol_bluestein(n_fft)
+    assert rel_l2(got.real, got.imag, *ref) <= tol
+
+
+def test_stft_win_length_below_n_fft_and_custom_window_composed():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 6000, generator=g)
+    w = torch.rand(300, generator=g)
+    got = trnfft_amd.stft(x.cuda(), n_fft=400, hop_length=128, win_length=300, window=w.cuda())
+    ref = oracle.stft(x, n_fft=400, hop_length=128, win_length=300, window=w)
+    assert got.shape == ref[0].shape
+    assert rel_l2(got.real, got.imag, *ref) <= tol_bluestein(400)
+
+
+def test_stft_no_whole_frame_returns_empty_like_the_reference():
+    # center=False and a signal shorter than n_fft by less than a hop: num_frames = 0, and the
+    # reference's frame index is empty (trnfft/api.py:321-327)
+    x = torch.randn(2, 300)
+    got = trnfft_amd.stft(x.cuda(), n_fft=400, hop_length=200, center=False)
+    ref = oracle.stft(x, n_fft=400, hop_length=200, center=False)
+    assert got.shape == ref[0].shape == (2, 201, 0)
+
+
 def test_stft_config2_full_size():
     # 64 x 160000 samples, 3 sinusoids + N(0, 0.1) noise, n_fft 512, hop 256
     from bench import make_stft_input

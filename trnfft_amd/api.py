@@ -255,6 +255,10 @@ def _effective_window(window: torch.Tensor | None, n_fft: int, win_length: int, 
     return window
 
 
+def _fused_stft_ok(n_fft: int) -> bool:
+    return 16 <= n_fft <= 4096 and n_fft & (n_fft - 1) == 0
+
+
 def stft(
     input: torch.Tensor,
     n_fft: int,
@@ -268,8 +272,12 @@ def stft(
 ) -> ComplexTensor:
     """Short-time Fourier transform, output (..., freq, time) (trnfft/api.py:291-365).
 
-    Power-of-two n_fft with reflect padding runs as one fused kernel that reads the raw
-    waveform (framing, padding, window, transform and the (freq, time) transpose in one pass).
+    Power-of-two n_fft in [16, 4096] runs as one fused kernel that reads the raw waveform
+    (framing, padding, window, transform and the (freq, time) transpose in one pass); with a
+    pad_mode other than "reflect" the signal is padded on the device first (the reference's
+    F.pad) and the fused kernel frames the padded signal.  Other n_fft keep the reference's
+    composition on the device: pad, frame gather, window, then the transform kernels (Bluestein
+    for non-power-of-two n_fft) and the onesided slice.
     """
     if hop_length is None:
         hop_length = n_fft // 4
@@ -282,21 +290,50 @@ def stft(
     out_dev = input.device
     x = to_device_f32(input, dev)
     win = to_device_f32(win, dev)
-    length = x.shape[-1]
-    if center and pad_mode != "reflect":
-        raise NotImplementedError(f"stft pad_mode={pad_mode!r}: only 'reflect' is implemented")
-    if center and length <= n_fft // 2:
-        raise ValueError(f"reflect padding of {n_fft // 2} needs more than {n_fft // 2} samples; got {length}")
-    num_frames = stft_num_frames(length, n_fft, hop_length, center)
-    if num_frames < 1:
-        raise ValueError(f"signal of {length} samples is shorter than n_fft={n_fft}")
-    out = _ag.stft(x, win, n_fft, hop_length, center, normalized, onesided, num_frames)
-    out_re, out_im = out.real, out.imag
-    if center and x.dim() == 2 and x.shape[0] == 1:
-        # the reference squeezes a (1, L) signal to 1-D after padding (trnfft/api.py:313-315),
-        # so its result has no batch axis; keep that shape for drop-in compatibility
-        out_re, out_im = out_re[0], out_im[0]
-    out = ComplexTensor._wrap(out_re, out_im)
+    if center and pad_mode == "reflect" and _fused_stft_ok(n_fft):
+        length = x.shape[-1]
+        if length <= n_fft // 2:
+            raise ValueError(f"reflect padding of {n_fft // 2} needs more than {n_fft // 2} samples; got {length}")
+        num_frames = stft_num_frames(length, n_fft, hop_length, center)
+        out = _ag.stft(x, win, n_fft, hop_length, True, normalized, onesided, num_frames)
+        out_re, out_im = out.real, out.imag
+        if x.dim() == 2 and x.shape[0] == 1:
+            # the reference squeezes a (1, L) signal to 1-D after padding (trnfft/api.py:313-315),
+            # so its result has no batch axis; keep that shape for drop-in compatibility
+            out_re, out_im = out_re[0], out_im[0]
+        out = ComplexTensor._wrap(out_re, out_im)
+        return out if out_dev == dev else out.to(out_dev)
+    if center:
+        # trnfft/api.py:310-315, on the device: F.pad needs a 2-D+ input; (1, L') is squeezed back
+        pad_amount = n_fft // 2
+        x = x.unsqueeze(0) if x.dim() == 1 else x
+        x = torch.nn.functional.pad(x, (pad_amount, pad_amount), mode=pad_mode)
+        x = x.squeeze(0) if x.dim() == 2 and x.shape[0] == 1 else x
+    padded_length = x.shape[-1]
+    num_frames = 1 + (padded_length - n_fft) // hop_length
+    if num_frames < 0:
+        raise ValueError(f"signal of {padded_length} samples (after padding) is shorter than n_fft={n_fft}")
+    bins = n_fft // 2 + 1 if onesided else n_fft
+    if num_frames == 0:
+        empty = torch.empty(*x.shape[:-1], bins, 0, dtype=torch.float32, device=dev)
+        out = ComplexTensor._wrap(empty, empty.clone())
+        return out if out_dev == dev else out.to(out_dev)
+    if _fused_stft_ok(n_fft):
+        # the padded signal through the fused kernel (no centre padding of its own)
+        out = _ag.stft(x.contiguous(), win, n_fft, hop_length, False, normalized, onesided, num_frames)
+        return out if out_dev == dev else out.to(out_dev)
+    # trnfft/api.py:321-363 on the device: frame gather, window, transform of real frames,
+    # onesided slice, (freq, time) transpose, normalisation
+    frame_idx = (torch.arange(n_fft, device=dev).unsqueeze(0)
+                 + torch.arange(num_frames, device=dev).unsqueeze(1) * hop_length)
+    frames = (x[..., frame_idx] * win).contiguous()  # (..., T, n_fft)
+    spec = rfft(frames) if onesided else _real_1d(frames, inverse=False)
+    out_re = spec.real.transpose(-2, -1)
+    out_im = spec.imag.transpose(-2, -1)
+    if normalized:
+        scale = 1.0 / math.sqrt(n_fft)
+        out_re, out_im = out_re * scale, out_im * scale
+    out = ComplexTensor._wrap(out_re.contiguous(), out_im.contiguous())
     return out if out_dev == dev else out.to(out_dev)
 
 
