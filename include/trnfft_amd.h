@@ -173,6 +173,20 @@ int tfa_complex_gemm_ex(int64_t m, int64_t n, int64_t k, const float* a_re, cons
                         const float* bias_re, const float* bias_im, float* c_re, float* c_im, int64_t ldc,
                         tfa_stream stream);
 
+/*
+ * Strided-batched form of tfa_complex_gemm_ex: for b in [0, batch),
+ *   C_b = alpha * op(A_b) @ op(B_b) + bias,  X_b = X + b * stride_x (floats, both planes).
+ * A stride of 0 shares that operand across the batch (broadcast); C's stride must separate the
+ * output matrices.  Replaces the batched and broadcast torch.matmul products of
+ * trnfft/complex.py:142-150 (complex_matmul / ComplexTensor.__matmul__: four real matmuls of
+ * (..., m, k) @ (..., k, n) operands), one launch for all four products of every matrix pair.
+ */
+int tfa_complex_gemm_batched(int64_t batch, int64_t m, int64_t n, int64_t k, const float* a_re, const float* a_im,
+                             int64_t lda, int64_t stride_a, int32_t a_op, const float* b_re, const float* b_im,
+                             int64_t ldb, int64_t stride_b, int32_t b_op, float alpha, const float* bias_re,
+                             const float* bias_im, float* c_re, float* c_im, int64_t ldc, int64_t stride_c,
+                             tfa_stream stream);
+
 /* Thread-local message describing the last failure on this thread ("" if none). */
 const char* tfa_last_error(void);
 

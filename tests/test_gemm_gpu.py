@@ -40,6 +40,40 @@ def test_complex_gemm_vs_float64(m, k, n):
     assert rel_l2(got.real, got.imag, *ref) <= _tol_k(k), (m, k, n)
 
 
+@pytest.mark.parametrize("sa,sb", [
+    ((4, 50, 33), (4, 33, 70)),        # batched
+    ((4, 50, 33), (33, 70)),           # batched A, shared 2-D B (one GEMM over all rows)
+    ((50, 33), (3, 33, 70)),           # shared A, batched B
+    ((2, 1, 17, 9), (3, 9, 20)),       # broadcast batch axes -> (2, 3, 17, 20)
+    ((2, 3, 17, 9), (1, 3, 9, 20)),
+    ((33,), (33, 70)),                 # vector @ matrix
+    ((50, 33), (33,)),                 # matrix @ vector
+    ((5, 50, 33), (33,)),              # batched matrix @ vector
+    ((33,), (4, 33, 7)),               # vector @ batched matrix
+    ((33,), (33,)),                    # dot product -> 0-d
+    ((0, 8, 5), (0, 5, 3)),            # empty batch
+    ((70000, 2, 3), (70000, 3, 2)),    # more products than one launch's grid.y (65535)
+])
+def test_complex_matmul_torch_matmul_shapes(sa, sb):
+    # the reference's complex_matmul is four torch.matmul (trnfft/complex.py:142-150), so it takes
+    # every torch.matmul shape; the result and its shape match the same formula in float64
+    g = torch.Generator().manual_seed(len(sa) * 10 + len(sb))
+    a = _planes(sa, g)
+    b = _planes(sb, g)
+    got = ComplexTensor(a[0].cuda(), a[1].cuda()) @ ComplexTensor(b[0].cuda(), b[1].cuda())
+    ref = oracle.complex_matmul((a[0].double(), a[1].double()), (b[0].double(), b[1].double()))
+    assert tuple(got.real.shape) == tuple(ref[0].shape)
+    if ref[0].numel():
+        assert rel_l2(got.real, got.imag, *ref) <= _tol_k(sa[-1]), (sa, sb)
+
+
+def test_complex_matmul_shape_mismatch_raises_like_torch():
+    a = ComplexTensor(torch.randn(4, 5).cuda(), torch.randn(4, 5).cuda())
+    b = ComplexTensor(torch.randn(2, 6, 3).cuda(), torch.randn(2, 6, 3).cuda())
+    with pytest.raises(RuntimeError):
+        a @ b
+
+
 def test_complex_gemm_kat():
     a = ComplexTensor(torch.tensor([[1.0]]).cuda(), torch.tensor([[2.0]]).cuda())
     b = ComplexTensor(torch.tensor([[3.0]]).cuda(), torch.tensor([[4.0]]).cuda())

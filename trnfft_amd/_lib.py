@@ -47,6 +47,7 @@ EXPORTS = (
     "tfa_istft_execute",
     "tfa_complex_gemm",
     "tfa_complex_gemm_ex",
+    "tfa_complex_gemm_batched",
     "tfa_last_error",
     "tfa_abi_version",
 )
@@ -101,6 +102,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tfa_complex_gemm_ex.argtypes = [_i64, _i64, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i32, ctypes.c_float,
                                         _vp, _vp, _vp, _vp, _i64, _vp]
     lib.tfa_complex_gemm_ex.restype = ctypes.c_int
+    lib.tfa_complex_gemm_batched.argtypes = [_i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i32, _vp, _vp, _i64, _i64,
+                                             _i32, ctypes.c_float, _vp, _vp, _vp, _vp, _i64, _i64, _vp]
+    lib.tfa_complex_gemm_batched.restype = ctypes.c_int
     lib.tfa_last_error.argtypes = []
     lib.tfa_last_error.restype = ctypes.c_char_p
     lib.tfa_abi_version.argtypes = []

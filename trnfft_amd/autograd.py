@@ -288,6 +288,60 @@ def gemm(a_re, a_im, b_re, b_im, b_trans: bool, bias_re=None, bias_im=None, what
                    what=what)
 
 
+class _ComplexBMMFn(torch.autograd.Function):
+    """C_b = A_b @ B_b for b < batch; A (batch or 1, m, k), B (batch or 1, k, n) (1: shared)."""
+
+    @staticmethod
+    def forward(ctx, a_re, a_im, b_re, b_im, batch: int):
+        from .dispatch import gemm_batched
+
+        ctx.save_for_backward(a_re, a_im, b_re, b_im)
+        ctx.batch = batch
+        return gemm_batched(a_re, a_im, _lib.OP_N, b_re, b_im, _lib.OP_N, batch)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, g_re, g_im):
+        from .dispatch import gemm_batched, gemm_ex
+
+        a_re, a_im, b_re, b_im = ctx.saved_tensors
+        g_re, g_im = _c(g_re), _c(g_im)
+        batch = ctx.batch
+        need = ctx.needs_input_grad
+        da_re = da_im = db_re = db_im = None
+        if need[0] or need[1]:
+            # dA_b = dC_b B_b^H, summed over the batch when A is shared
+            da_re, da_im = gemm_batched(g_re, g_im, _lib.OP_N, b_re, b_im, _lib.OP_C, batch,
+                                        what="complex_matmul backward dA")
+            if a_re.shape[0] == 1 and batch > 1:
+                da_re, da_im = da_re.sum(0, keepdim=True), da_im.sum(0, keepdim=True)
+        if need[2] or need[3]:
+            # dB_b = A_b^H dC_b, summed over the batch when B is shared
+            if b_re.shape[0] == batch or batch == 1:
+                db_re, db_im = gemm_batched(a_re, a_im, _lib.OP_C, g_re, g_im, _lib.OP_N, batch,
+                                            what="complex_matmul backward dB")
+            elif a_re.shape[0] == batch:
+                # sum_b A_b^H dC_b = A_flat^H dC_flat with the batch stacked along the rows
+                m, k = a_re.shape[1:]
+                db_re, db_im = gemm_ex(a_re.reshape(batch * m, k), a_im.reshape(batch * m, k), _lib.OP_C,
+                                       g_re.reshape(batch * m, -1), g_im.reshape(batch * m, -1), _lib.OP_N,
+                                       what="complex_matmul backward dB")
+                db_re, db_im = db_re.unsqueeze(0), db_im.unsqueeze(0)
+            else:
+                db_re, db_im = gemm_batched(a_re, a_im, _lib.OP_C, g_re.sum(0, keepdim=True),
+                                            g_im.sum(0, keepdim=True), _lib.OP_N, 1, what="complex_matmul backward dB")
+        return da_re, da_im, db_re, db_im, None
+
+
+def bmm(a_re, a_im, b_re, b_im, batch: int):
+    """(c_re, c_im) = batched A @ B, (batch, m, n); differentiable."""
+    if _grad_on(a_re, a_im, b_re, b_im):
+        return _ComplexBMMFn.apply(a_re, a_im, b_re, b_im, batch)
+    from .dispatch import gemm_batched
+
+    return gemm_batched(a_re, a_im, _lib.OP_N, b_re, b_im, _lib.OP_N, batch)
+
+
 def fft_autograd(x_real: torch.Tensor, x_imag: torch.Tensor, inverse: bool, precision: str = "fast"):
     """(y_re, y_im) of the last-axis transform, differentiable (trnfft/nki/autograd.py:204-205)."""
     y = c2c(x_real, x_imag, inverse)

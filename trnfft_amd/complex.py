@@ -145,7 +145,8 @@ class ComplexTensor:
 
 
 def complex_matmul(a: ComplexTensor, b: ComplexTensor) -> ComplexTensor:
-    """C = A @ B on the HIP complex GEMM (replaces the four torch.matmul of trnfft/complex.py:142-150)."""
-    from .dispatch import complex_gemm
+    """C = A @ B on the HIP complex GEMM with torch.matmul's shape rules: 1-D, 2-D, batched and
+    broadcast operands (replaces the four torch.matmul of trnfft/complex.py:142-150)."""
+    from .dispatch import complex_matmul as _matmul
 
-    return complex_gemm(a, b)
+    return _matmul(a, b)

@@ -293,6 +293,8 @@ struct GemmArgs {
   long long ldc;
   float alpha;
   hipStream_t stream;
+  long long batch = 1;            // matrix triples (grid.y)
+  long long sa = 0, sb = 0, sc = 0;  // batch strides in floats (0: operand shared by the batch)
 };
 hipError_t launch_cgemm(const GemmArgs& a);
 

@@ -10,6 +10,8 @@
 // "stationary reuse" idea, trnfft/nki/dispatch.py:121-200 and :267-345, in CDNA4 form).
 // Workgroup tile 128 x 128 (per plane), 4 waves of 64 x 64, BK = 16 k per LDS stage with the
 // next stage prefetched into registers while the current one is consumed.
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace tfa {
@@ -119,9 +121,21 @@ __global__ __launch_bounds__(256, 2) void cgemm_kernel(int M, int N, int K, cons
                                                     const float* __restrict__ B_re, const float* __restrict__ B_im,
                                                     long long ldb, float b_sim, const float* __restrict__ bias_re,
                                                     const float* __restrict__ bias_im, float* __restrict__ C_re,
-                                                    float* __restrict__ C_im, long long ldc, float alpha) {
+                                                    float* __restrict__ C_im, long long ldc, float alpha,
+                                                    long long sa, long long sb, long long sc) {
   __shared__ float As[2][GBK][GLD];
   __shared__ float Bs[2][GBK][GLD];
+  // batched products: blockIdx.y selects the matrix triple (batch strides in floats; a stride of 0
+  // broadcasts one operand over the batch)
+  {
+    const size_t bz = blockIdx.y;
+    A_re += bz * sa;
+    A_im += bz * sa;
+    B_re += bz * sb;
+    B_im += bz * sb;
+    C_re += bz * sc;
+    C_im += bz * sc;
+  }
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int w = t >> 6;
@@ -210,9 +224,14 @@ template <bool A_T, bool B_T>
 static void launch_cgemm_t(const GemmArgs& a, long long tiles) {
   const float a_sim = (a.a_op == 2 || a.a_op == 3) ? -1.0f : 1.0f;
   const float b_sim = (a.b_op == 2 || a.b_op == 3) ? -1.0f : 1.0f;
-  hipLaunchKernelGGL((cgemm_kernel<A_T, B_T>), dim3((unsigned)tiles), dim3(256), 0, a.stream, (int)a.m, (int)a.n,
-                     (int)a.k, a.a_re, a.a_im, a.lda, a_sim, a.b_re, a.b_im, a.ldb, b_sim, a.bias_re, a.bias_im,
-                     a.c_re, a.c_im, a.ldc, a.alpha);
+  constexpr long long kMaxGridY = 65535;
+  for (long long b0 = 0; b0 < a.batch; b0 += kMaxGridY) {
+    const unsigned nb = (unsigned)std::min(kMaxGridY, a.batch - b0);
+    hipLaunchKernelGGL((cgemm_kernel<A_T, B_T>), dim3((unsigned)tiles, nb), dim3(256), 0, a.stream, (int)a.m,
+                       (int)a.n, (int)a.k, a.a_re + b0 * a.sa, a.a_im + b0 * a.sa, a.lda, a_sim, a.b_re + b0 * a.sb,
+                       a.b_im + b0 * a.sb, a.ldb, b_sim, a.bias_re, a.bias_im, a.c_re + b0 * a.sc,
+                       a.c_im + b0 * a.sc, a.ldc, a.alpha, a.sa, a.sb, a.sc);
+  }
 }
 
 hipError_t launch_cgemm(const GemmArgs& a) {

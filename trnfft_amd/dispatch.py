@@ -131,6 +131,32 @@ def gemm_ex(a_re, a_im, a_op: int, b_re, b_im, b_op: int, alpha: float = 1.0, bi
     return c_re, c_im
 
 
+def gemm_batched(a_re, a_im, a_op: int, b_re, b_im, b_op: int, batch: int, alpha: float = 1.0,
+                 what: str = "complex_matmul"):
+    """C_b = alpha * op(A_b) @ op(B_b) for b < batch on the MFMA kernel; A and B are 3-D device fp32
+    planes whose first axis is `batch` or 1 (1: the matrix is shared by every product).  Returns
+    (c_re, c_im) of shape (batch, m, n)."""
+    dev = a_re.device
+    a_re, a_im, b_re, b_im = (t.contiguous() for t in (a_re, a_im, b_re, b_im))
+    at = a_op in (_lib.OP_T, _lib.OP_C)
+    bt = b_op in (_lib.OP_T, _lib.OP_C)
+    m, k = (a_re.shape[2], a_re.shape[1]) if at else a_re.shape[1:]
+    kb, n = (b_re.shape[2], b_re.shape[1]) if bt else b_re.shape[1:]
+    if kb != k:
+        raise RuntimeError(f"{what}: inner dimensions differ ({k} vs {kb})")
+    sa = 0 if a_re.shape[0] == 1 else a_re.shape[1] * a_re.shape[2]
+    sb = 0 if b_re.shape[0] == 1 else b_re.shape[1] * b_re.shape[2]
+    c_re = torch.empty(batch, m, n, device=dev, dtype=torch.float32)
+    c_im = torch.empty(batch, m, n, device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_complex_gemm_batched(
+            batch, m, n, k, ptr(a_re), ptr(a_im), a_re.shape[2], sa, a_op, ptr(b_re), ptr(b_im), b_re.shape[2], sb,
+            b_op, float(alpha), ptr(None), ptr(None), ptr(c_re), ptr(c_im), n, m * n, stream_handle(dev),
+        )
+    _lib.check(rc, what)
+    return c_re, c_im
+
+
 def _gemm(a_re, a_im, b_re, b_im, b_trans: bool, bias_re=None, bias_im=None, what="complex_gemm"):
     """op(B) = B or B^T; A's leading dimensions are batch rows.  Differentiable (the adjoint
     products run on the same kernel)."""
@@ -149,6 +175,76 @@ def _gemm(a_re, a_im, b_re, b_im, b_trans: bool, bias_re=None, bias_im=None, wha
     c_re, c_im = _ag.gemm(a_re.reshape(-1, k), a_im.reshape(-1, k), b_re, b_im, b_trans, bias_re, bias_im, what)
     out = ComplexTensor._wrap(c_re.reshape(*lead, c_re.shape[-1]), c_im.reshape(*lead, c_im.shape[-1]))
     return out if out_dev == dev else out.to(out_dev)
+
+
+def complex_matmul(a: ComplexTensor, b: ComplexTensor) -> ComplexTensor:
+    """A @ B with torch.matmul's shape rules (trnfft/complex.py:142-150 runs four torch.matmul):
+    1-D operands are promoted and the added axis removed, a 2-D right operand makes A's leading
+    axes rows of one GEMM, and batched operands broadcast over their leading axes and run as one
+    strided-batched launch.  Every product runs on the MFMA kernel."""
+    ar, ai, br, bi = a.real, a.imag, b.real, b.imag
+    if ar.dim() == 0 or br.dim() == 0:
+        raise RuntimeError("complex_matmul: both arguments need to be at least 1-D")
+    pre, post = ar.dim() == 1, br.dim() == 1
+    if pre:
+        ar, ai = ar.unsqueeze(0), ai.unsqueeze(0)
+    if post:
+        br, bi = br.unsqueeze(-1), bi.unsqueeze(-1)
+    if ar.shape[-1] != br.shape[-2]:
+        raise RuntimeError(
+            f"complex_matmul: shapes {tuple(a.real.shape)} and {tuple(b.real.shape)} cannot be multiplied"
+        )
+    if br.dim() == 2:
+        out = _gemm(ar, ai, br, bi, False, what="complex_matmul")
+        re, im = out.real, out.imag
+    else:
+        re, im = _bmm(ar, ai, br, bi)
+    if post:
+        re, im = re.squeeze(-1), im.squeeze(-1)
+    if pre:
+        d = -1 if post else -2
+        re, im = re.squeeze(d), im.squeeze(d)
+    return ComplexTensor._wrap(re, im)
+
+
+def _bmm(a_re, a_im, b_re, b_im):
+    """Broadcast batched product of (..., m, k) and (..., k, n) planes (b at least 3-D)."""
+    from . import autograd as _ag
+
+    _require_hip("complex_matmul")
+    dev = target_device(a_re, b_re)
+    out_dev = a_re.device
+    a_re, a_im = to_device_f32(a_re, dev), to_device_f32(a_im, dev)
+    b_re, b_im = to_device_f32(b_re, dev), to_device_f32(b_im, dev)
+    m, k = a_re.shape[-2:]
+    n = b_re.shape[-1]
+    bshape = torch.broadcast_shapes(a_re.shape[:-2], b_re.shape[:-2])
+    batch = 1
+    for d in bshape:
+        batch *= d
+
+    def batched(x_re, x_im, rows, cols):
+        # a matrix shared by the whole batch keeps a batch axis of 1 (stride 0 in the launch);
+        # otherwise the operand is broadcast to the full batch
+        own = 1
+        for d in x_re.shape[:-2]:
+            own *= d
+        if own == 1:
+            return x_re.reshape(1, rows, cols), x_im.reshape(1, rows, cols)
+        return (x_re.expand(*bshape, rows, cols).reshape(batch, rows, cols),
+                x_im.expand(*bshape, rows, cols).reshape(batch, rows, cols))
+
+    if batch == 0 or m == 0 or n == 0:
+        z = torch.zeros(*bshape, m, n, device=dev, dtype=torch.float32)
+        re, im = z, z.clone()
+    else:
+        a3 = batched(a_re, a_im, m, k)
+        b3 = batched(b_re, b_im, k, n)
+        c_re, c_im = _ag.bmm(a3[0], a3[1], b3[0], b3[1], batch)
+        re, im = c_re.reshape(*bshape, m, n), c_im.reshape(*bshape, m, n)
+    if out_dev != dev:
+        re, im = re.to(out_dev), im.to(out_dev)
+    return re, im
 
 
 def complex_gemm(a: ComplexTensor, b: ComplexTensor) -> ComplexTensor:
