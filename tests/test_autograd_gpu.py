@@ -211,6 +211,40 @@ def test_stft_gradient(n_fft, hop, center, normalized, onesided):
     assert _rel(aw.grad, rw.grad) <= TOL
 
 
+@pytest.mark.parametrize("n_fft,hop,pad_mode", [(8192, 2048, "replicate"), (512, 128, "circular"), (12, 4, "constant")])
+def test_stft_gradient_composed_pow2(n_fft, hop, pad_mode):
+    # power-of-two n_fft outside the fused kernel's range or with a non-reflect pad: device F.pad +
+    # (fused kernel or frame gather + transform kernels), against torch.stft in float64
+    g = torch.Generator().manual_seed(15)
+    x = torch.randn(2, 20000 if n_fft > 1000 else 900, generator=g)
+    a = _leaf(x)
+    y = trnfft_amd.stft(a, n_fft, hop_length=hop, pad_mode=pad_mode)
+    cr, ci = _cotangent(tuple(y.shape), 16)
+    (y.real * cr.float().cuda() + y.imag * ci.float().cuda()).sum().backward()
+    r = x.double().requires_grad_(True)
+    z = torch.stft(r, n_fft, hop_length=hop, window=torch.hann_window(n_fft, dtype=torch.float64), center=True,
+                   pad_mode=pad_mode, onesided=True, return_complex=True)
+    assert tuple(z.shape) == tuple(y.shape)
+    (z.real * cr + z.imag * ci).sum().backward()
+    assert _rel(a.grad, r.grad) <= TOL
+
+
+def test_stft_gradient_composed_bluestein():
+    # n_fft = 400 (Bluestein frames): against autograd through the oracle's restatement of the
+    # reference's own pytorch path in fp32 (its fp32 chirp differs from the exact DFT)
+    g = torch.Generator().manual_seed(17)
+    x = torch.randn(2, 4000, generator=g)
+    a = _leaf(x)
+    y = trnfft_amd.stft(a, 400, hop_length=160, pad_mode="constant")
+    cr, ci = _cotangent(tuple(y.shape), 18)
+    (y.real * cr.float().cuda() + y.imag * ci.float().cuda()).sum().backward()
+    r = x.clone().requires_grad_(True)
+    zr, zi = oracle.stft(r, 400, hop_length=160, pad_mode="constant")
+    assert tuple(zr.shape) == tuple(y.shape)
+    (zr * cr.float() + zi * ci.float()).sum().backward()
+    assert _rel(a.grad, r.grad) <= tol_bluestein(400)
+
+
 def test_stft_gradient_matches_reference_test():
     # trnfft tests/test_nn.py:88-96
     signal = torch.randn(512, requires_grad=True, device="cuda")
@@ -242,6 +276,27 @@ def test_complex_linear_gradients():
     assert rel_l2(a_r.grad, a_i.grad, r_r.grad, r_i.grad) <= TOL
     assert rel_l2(layer.W_re.weight.grad, layer.W_im.weight.grad, wr.grad, wi.grad) <= TOL
     assert rel_l2(layer.bias_re.grad, layer.bias_im.grad, br.grad, bi.grad) <= TOL
+
+
+@pytest.mark.parametrize("sa,sb", [((3, 20, 13), (3, 13, 30)), ((3, 20, 13), (13, 30)), ((20, 13), (4, 13, 30)),
+                                   ((2, 1, 9, 13), (3, 13, 6)), ((13,), (2, 13, 5)), ((4, 20, 13), (13,))])
+def test_complex_matmul_batched_gradients(sa, sb):
+    # batched / broadcast products: the adjoints run on the batched kernel and are summed over
+    # the axes an operand was broadcast along, as torch.matmul's autograd does
+    g = torch.Generator().manual_seed(len(sa) + 3 * len(sb))
+    ar, ai = torch.randn(*sa, generator=g), torch.randn(*sa, generator=g)
+    br, bi = torch.randn(*sb, generator=g), torch.randn(*sb, generator=g)
+    A = torch.complex(ar.double(), ai.double()).requires_grad_(True)
+    B = torch.complex(br.double(), bi.double()).requires_grad_(True)
+    z = torch.matmul(A, B)
+    cr, ci = _cotangent(tuple(z.shape), 19)
+    (z.real * cr + z.imag * ci).sum().backward()
+    l_ar, l_ai, l_br, l_bi = (_leaf(t) for t in (ar, ai, br, bi))
+    c = trnfft_amd.complex_matmul(ComplexTensor(l_ar, l_ai), ComplexTensor(l_br, l_bi))
+    assert tuple(c.real.shape) == tuple(z.shape)
+    (c.real * cr.float().cuda() + c.imag * ci.float().cuda()).sum().backward()
+    assert rel_l2(l_ar.grad, l_ai.grad, A.grad.real, A.grad.imag) <= TOL
+    assert rel_l2(l_br.grad, l_bi.grad, B.grad.real, B.grad.imag) <= TOL
 
 
 def test_complex_matmul_gradients():

@@ -133,3 +133,28 @@ def test_graph_replay_multipass_paths():
         assert torch.equal(o2.real, e2.real) and torch.equal(o2.imag, e2.imag)
         trnfft_amd.ifftn(other, dim=(1,))  # unrelated eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("n,batch", [(1024, 256), (1 << 18, 2), (4099, 4)])
+def test_graph_replay_after_plan_cache_clear(n, batch):
+    # a captured graph holds the plan's device tables: clearing the cache (and collecting the
+    # Python plan objects) must not free them while the graph can still be replayed
+    import gc
+
+    from trnfft_amd.plan import clear_plan_cache
+
+    clear_plan_cache()
+    re, im = seeded_complex(batch, n, seed=6)
+    x = ComplexTensor(re.cuda(), im.cuda())
+    eager = trnfft_amd.fft(x)
+    g, out = _capture(lambda: trnfft_amd.fft(x))
+    clear_plan_cache()
+    gc.collect()
+    # new plans of other lengths allocate device tables after the clear
+    for m in (2048, 999, 1 << 17):
+        trnfft_amd.fft(ComplexTensor(torch.randn(2, m, device="cuda"), torch.randn(2, m, device="cuda")))
+    torch.cuda.synchronize()
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.real, eager.real) and torch.equal(out.imag, eager.imag)

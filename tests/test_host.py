@@ -168,3 +168,56 @@ def test_reference_public_names_are_exported():
     missing = [n for n in names if not hasattr(trnfft_amd, n)]
     assert not missing, missing
     assert trnfft_amd.HAS_NKI is False
+
+
+class _FakePlan:
+    """Stand-in for NativePlan (no device): records its own release."""
+
+    released: list = []
+
+    def __init__(self, kind, n, inverse, device, hop=0, flags=0, n2=0):
+        self.key = (kind, n, inverse)
+
+    def __del__(self):
+        _FakePlan.released.append(self.key)
+
+
+def test_plan_cache_keeps_a_held_plan_alive_across_clear():
+    # a caller that fetched a plan keeps it until it drops the reference: clear_plan_cache only
+    # drops the cache's own reference (no explicit destroy under a running call)
+    import gc
+
+    from trnfft_amd import plan as P
+
+    P.clear_plan_cache()
+    _FakePlan.released.clear()
+    held = P.native_plan(99, 8, False, 0, _factory=_FakePlan)
+    assert P.native_plan(99, 8, False, 0, _factory=_FakePlan) is held
+    P.clear_plan_cache()
+    gc.collect()
+    assert _FakePlan.released == []
+    del held
+    gc.collect()
+    assert _FakePlan.released == [(99, 8, False)]
+
+
+def test_plan_cache_is_bounded_lru():
+    import gc
+
+    from trnfft_amd import plan as P
+
+    P.clear_plan_cache()
+    _FakePlan.released.clear()
+    first = [P.native_plan(98, n, False, 0, _factory=_FakePlan) for n in range(P.NATIVE_CACHE_MAX)]
+    keep = first[0]
+    P.native_plan(98, 0, False, 0, _factory=_FakePlan)  # touch: most recently used now
+    del first
+    extra = [P.native_plan(98, 1000 + i, False, 0, _factory=_FakePlan) for i in range(5)]
+    gc.collect()
+    assert len(P._native_cache) == P.NATIVE_CACHE_MAX
+    # the five least recently used (1..5) were evicted; 0 was touched and is held anyway
+    assert sorted(k[1] for k in _FakePlan.released) == [1, 2, 3, 4, 5]
+    assert (98, 0, False, 0, 0, 0, 0) in P._native_cache
+    del keep, extra
+    P.clear_plan_cache()
+    gc.collect()

@@ -1,8 +1,10 @@
 // Host side of the C ABI (include/trnfft_amd.h): plan construction (algorithm choice and device
 // tables), workspace sizing and execution dispatch.
+#include <atomic>
 #include <cmath>
 #include <complex>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -97,6 +99,9 @@ struct tfa_plan {
   float* w_re = nullptr;  // DFT-GEMM matrix
   float* w_im = nullptr;
   std::vector<void*> allocs;
+  // set once the plan has been executed on a stream under graph capture: the captured kernels
+  // hold raw pointers to these tables, so tfa_plan_destroy must not free them
+  mutable std::atomic<bool> captured{false};
 
   ~tfa_plan() {
     for (void* p : allocs) (void)hipFree(p);
@@ -267,11 +272,31 @@ std::vector<float2> reference_chirp(int64_t n, int sign) {
   return c;
 }
 
+std::mutex g_retained_mu;
+
+// plans destroyed after use under graph capture (never freed; see tfa_plan_destroy)
+std::vector<tfa_plan*>& retained_plans() {
+  static std::vector<tfa_plan*>* v = new std::vector<tfa_plan*>();
+  return *v;
+}
+
+// Marks the plan as referenced by a captured graph when `stream` is capturing.  The null stream
+// never captures (and querying it while another stream captures in global mode is an error).
+void note_capture(const tfa_plan* plan, tfa_stream stream) {
+  if (!stream || plan->captured.load(std::memory_order_relaxed)) return;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &st) != hipSuccess) {
+    (void)hipGetLastError();  // leave no error behind for the launch check that follows
+    return;
+  }
+  if (st != hipStreamCaptureStatusNone) plan->captured.store(true, std::memory_order_release);
+}
+
 }  // namespace
 
 extern "C" {
 
-int32_t tfa_abi_version(void) { return (1 << 16) | 1; }
+int32_t tfa_abi_version(void) { return (1 << 16) | 2; }
 
 const char* tfa_last_error(void) { return g_last_error.c_str(); }
 
@@ -468,7 +493,16 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
   return TFA_OK;
 }
 
-void tfa_plan_destroy(tfa_plan* plan) { delete plan; }
+void tfa_plan_destroy(tfa_plan* plan) {
+  if (!plan) return;
+  if (plan->captured.load(std::memory_order_acquire)) {
+    // a captured graph may still be replayed: keep the tables for the life of the process
+    std::lock_guard<std::mutex> g(g_retained_mu);
+    retained_plans().push_back(plan);
+    return;
+  }
+  delete plan;
+}
 
 int64_t tfa_plan_padded_n(const tfa_plan* plan) { return plan ? plan->m : 0; }
 
@@ -498,6 +532,7 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
     return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  note_capture(plan, stream);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t n = plan->d.n;
   const float scale = plan->d.inverse ? (float)(1.0 / (double)n) : 1.0f;
@@ -586,6 +621,7 @@ int tfa_execute_strided_ws(const tfa_plan* plan, int64_t outer, int64_t stride, 
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
     return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  note_capture(plan, stream);
   const C2cTables& t = plan->d.inverse ? plan->inv : plan->fwd;
   const size_t plane = (size_t)outer * (size_t)plan->d.n * (size_t)stride;
   float* t_re = static_cast<float*>(workspace);
@@ -615,6 +651,7 @@ int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, con
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
     return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  note_capture(plan, stream);
   if (blue) {
     const float bscale = plan->d.inverse ? (float)(1.0 / (double)plan->d.n) : 1.0f;
     tfa::StridedBlueArgs ba{in_re, in_im, out_re, out_im, plan->chirp, plan->hs, plan->b_tw_sf, plan->b_tw_si,
@@ -648,6 +685,7 @@ int tfa_stft_execute(const tfa_plan* plan, int64_t batch, int64_t num_samples, c
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
     return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  note_capture(plan, stream);
   const int64_t n_fft = plan->d.n;
   const bool center = plan->d.flags & TFA_STFT_CENTER;
   const int64_t pad = center ? n_fft / 2 : 0;
@@ -685,6 +723,7 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
     return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  note_capture(plan, stream);
   int64_t out_len = 0;
   int rc = tfa_istft_length(plan, n_frames, length, &out_len);
   if (rc) return rc;
@@ -721,6 +760,33 @@ int tfa_complex_gemm_ex(int64_t m, int64_t n, int64_t k, const float* a_re, cons
                   c_re, c_im, ldc, alpha, static_cast<hipStream_t>(stream)};
   hipError_t e = tfa::launch_cgemm(g);
   return e == hipSuccess ? TFA_OK : hip_fail(e, "complex gemm launch");
+}
+
+int tfa_complex_gemm_batched(int64_t batch, int64_t m, int64_t n, int64_t k, const float* a_re, const float* a_im,
+                             int64_t lda, int64_t stride_a, int32_t a_op, const float* b_re, const float* b_im,
+                             int64_t ldb, int64_t stride_b, int32_t b_op, float alpha, const float* bias_re,
+                             const float* bias_im, float* c_re, float* c_im, int64_t ldc, int64_t stride_c,
+                             tfa_stream stream) {
+  if (batch < 0 || m < 0 || n < 0 || k < 0) return fail(TFA_ERR_INVALID, "negative dimension");
+  if (stride_a < 0 || stride_b < 0 || stride_c < 0) return fail(TFA_ERR_INVALID, "negative batch stride");
+  if (a_op < TFA_OP_N || a_op > TFA_OP_R || b_op < TFA_OP_N || b_op > TFA_OP_R)
+    return fail(TFA_ERR_INVALID, "operand op must be TFA_OP_N, _T, _C or _R");
+  if (batch == 0 || m == 0 || n == 0) return TFA_OK;
+  if (!a_re || !a_im || !b_re || !b_im || !c_re || !c_im) return fail(TFA_ERR_INVALID, "null data pointer");
+  if ((bias_re == nullptr) != (bias_im == nullptr)) return fail(TFA_ERR_INVALID, "bias needs both planes or neither");
+  const bool at = a_op == TFA_OP_T || a_op == TFA_OP_C, bt = b_op == TFA_OP_T || b_op == TFA_OP_C;
+  if (lda < (at ? m : k) || ldb < (bt ? k : n) || ldc < n) return fail(TFA_ERR_INVALID, "leading dimension too small");
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return fail(TFA_ERR_UNSUPPORTED, "dimension above 2^31");
+  // distinct outputs per batch entry: C's batch stride must cover one (m, ldc) matrix
+  if (batch > 1 && stride_c < (m - 1) * ldc + n) return fail(TFA_ERR_INVALID, "output batch stride overlaps matrices");
+  tfa::GemmArgs g{m, n, k, a_re, a_im, lda, a_op, b_re, b_im, ldb, b_op, bias_re, bias_im,
+                  c_re, c_im, ldc, alpha, static_cast<hipStream_t>(stream)};
+  g.batch = batch;
+  g.sa = stride_a;
+  g.sb = stride_b;
+  g.sc = stride_c;
+  hipError_t e = tfa::launch_cgemm(g);
+  return e == hipSuccess ? TFA_OK : hip_fail(e, "batched complex gemm launch");
 }
 
 int tfa_complex_gemm(int64_t m, int64_t n, int64_t k, const float* a_re, const float* a_im,

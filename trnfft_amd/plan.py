@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+from collections import OrderedDict
 from dataclasses import dataclass
 from enum import Enum, auto
 
@@ -36,8 +37,15 @@ class FFTPlan:
 
 
 _plan_cache: dict[tuple, FFTPlan] = {}
-_native_cache: dict[tuple, NativePlan] = {}
 _lock = threading.Lock()
+
+# Native plans kept alive by the cache (least recently used evicted first).  Plans own device
+# tables (up to ~130 MB for the longest Bluestein lengths); a plan leaves memory only when the
+# last Python reference to it is gone, so a call that fetched a plan keeps it valid until it
+# returns, whatever another thread does to the cache meanwhile.  A plan used under HIP-graph
+# capture is retained by the native library itself until the process exits (tfa_plan_destroy
+# does not free a captured plan's tables), so replays stay valid after an eviction or a clear.
+NATIVE_CACHE_MAX = 64
 
 
 def create_plan(n: int, inverse: bool = False) -> FFTPlan:
@@ -57,13 +65,11 @@ def create_plan(n: int, inverse: bool = False) -> FFTPlan:
 
 
 def clear_plan_cache():
-    """Drop every cached plan, releasing the native plans' device tables."""
+    """Drop every cached plan (trnfft/plan.py:49-50).  Native plans release their device tables
+    once no caller still holds them (captured plans stay with the native library)."""
     with _lock:
         _plan_cache.clear()
-        natives = list(_native_cache.values())
         _native_cache.clear()
-    for p in natives:
-        p.destroy()
 
 
 class NativePlan:
@@ -101,14 +107,46 @@ class NativePlan:
             pass
 
 
-def native_plan(kind: int, n: int, inverse: bool, device: int, hop: int = 0, flags: int = 0, n2: int = 0) -> NativePlan:
-    key = (kind, n, bool(inverse), device, hop, flags, n2)
-    p = _native_cache.get(key)
-    if p is not None:
+class _LruCache:
+    """Bounded key -> plan map; the least recently used entry is dropped past `limit`."""
+
+    def __init__(self, limit: int):
+        self.limit = limit
+        self._d: OrderedDict = OrderedDict()
+
+    def get(self, key):
+        p = self._d.get(key)
+        if p is not None:
+            self._d.move_to_end(key)
         return p
+
+    def put(self, key, plan) -> None:
+        self._d[key] = plan
+        self._d.move_to_end(key)
+        while len(self._d) > self.limit:
+            self._d.popitem(last=False)
+
+    def clear(self) -> None:
+        self._d.clear()
+
+    def __len__(self) -> int:
+        return len(self._d)
+
+    def __contains__(self, key) -> bool:
+        return key in self._d
+
+
+_native_cache = _LruCache(NATIVE_CACHE_MAX)
+
+
+def native_plan(kind: int, n: int, inverse: bool, device: int, hop: int = 0, flags: int = 0, n2: int = 0,
+                _factory=None) -> NativePlan:
+    """The cached native plan for this key, created on first use.  The returned object keeps the
+    plan alive for as long as the caller holds it."""
+    key = (kind, n, bool(inverse), device, hop, flags, n2)
     with _lock:
         p = _native_cache.get(key)
         if p is None:
-            p = NativePlan(kind, n, inverse, device, hop, flags, n2)
-            _native_cache[key] = p
+            p = (_factory or NativePlan)(kind, n, inverse, device, hop, flags, n2)
+            _native_cache.put(key, p)
     return p
