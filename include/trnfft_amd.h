@@ -94,6 +94,19 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
                 float* out_re, float* out_im, void* workspace, tfa_stream stream);
 
 /*
+ * tfa_execute without a workspace argument and without any device allocation: the scratch the
+ * four-step (n > 16384) and split-Bluestein kernels need comes from a static device array of
+ * 64 MiB per GPU, part of the library's code object and held until the process ends.  No
+ * counterpart in the reference; it is for callers that cannot allocate device memory (code under
+ * HIP-graph capture, serving loops, harnesses that forbid hipMalloc).  A call whose scratch
+ * (tfa_plan_workspace_size) exceeds 64 MiB fails with TFA_ERR_INVALID; plans that need no scratch
+ * run exactly as tfa_execute.  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (concurrent streams) race and must be serialised by the caller.
+ */
+int tfa_execute_noalloc(const tfa_plan* plan, int64_t batch, const float* in_re, const float* in_im,
+                        float* out_re, float* out_im, tfa_stream stream);
+
+/*
  * Batched 1-D transform along a strided axis, in place allowed: data viewed as (outer, n, stride)
  * row-major, each of the outer*stride columns transformed along its n elements (element stride
  * `stride`).  TFA_KIND_C2C plans with n <= 4096, or TFA_KIND_BLUESTEIN plans with n <= 2048

@@ -38,6 +38,7 @@ EXPORTS = (
     "tfa_plan_workspace_size",
     "tfa_plan_padded_n",
     "tfa_execute",
+    "tfa_execute_noalloc",
     "tfa_execute_strided",
     "tfa_strided_workspace_size",
     "tfa_execute_strided_ws",
@@ -105,6 +106,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tfa_complex_gemm_batched.argtypes = [_i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i32, _vp, _vp, _i64, _i64,
                                              _i32, ctypes.c_float, _vp, _vp, _vp, _vp, _i64, _i64, _vp]
     lib.tfa_complex_gemm_batched.restype = ctypes.c_int
+    lib.tfa_execute_noalloc.argtypes = [_vp, _i64, _vp, _vp, _vp, _vp, _vp]
+    lib.tfa_execute_noalloc.restype = ctypes.c_int
     lib.tfa_last_error.argtypes = []
     lib.tfa_last_error.restype = ctypes.c_char_p
     lib.tfa_abi_version.argtypes = []

@@ -14,6 +14,13 @@
 
 using tfa::LdsShape;
 
+// Scratch of the allocation-free entry point (tfa_execute_noalloc): device memory of the loaded
+// code object, one copy per GPU, held until the process ends.  Host code must never pass this
+// name to a kernel (it is a host-side stand-in); it uses the per-device address from
+// hipGetSymbolAddress (scratch_for_device below).
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -290,6 +297,26 @@ void note_capture(const tfa_plan* plan, tfa_stream stream) {
     return;
   }
   if (st != hipStreamCaptureStatusNone) plan->captured.store(true, std::memory_order_release);
+}
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on `dev`, which must be the current device; resolved on the first
+// call on each device and kept.
+int scratch_for_device(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxScratchDevices) return fail(TFA_ERR_UNSUPPORTED, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(TFA_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TFA_OK;
 }
 
 }  // namespace
@@ -607,6 +634,29 @@ int tfa_strided_workspace_size(const tfa_plan* plan, int64_t outer, int64_t stri
   if (outer < 0 || stride < 1) return fail(TFA_ERR_INVALID, "bad outer/stride");
   *bytes = strided_fourstep(plan, stride) ? (size_t)2 * sizeof(float) * (size_t)outer * (size_t)plan->d.n * (size_t)stride : 0;
   return TFA_OK;
+}
+
+int tfa_execute_noalloc(const tfa_plan* plan, int64_t batch, const float* in_re, const float* in_im,
+                        float* out_re, float* out_im, tfa_stream stream) {
+  if (!plan) return fail(TFA_ERR_INVALID, "null plan");
+  if (batch < 0) return fail(TFA_ERR_INVALID, "negative batch");
+  size_t need = 0;
+  int rc = tfa_plan_workspace_size(plan, batch, &need);
+  if (rc) return rc;
+  if (need > kNoAllocScratchBytes)
+    return fail(TFA_ERR_INVALID, "tfa_execute_noalloc: this transform needs " + std::to_string(need) +
+                                     " bytes of scratch, above the static scratch of " +
+                                     std::to_string(kNoAllocScratchBytes) + " bytes (use tfa_execute with a workspace)");
+  void* ws = nullptr;
+  if (need > 0) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
+      return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+    if ((rc = scratch_for_device(dev, &ws))) return rc;
+  }
+  // the same kernels as tfa_execute; every kernel writes the scratch it later reads, so nothing
+  // needs clearing between calls
+  return tfa_execute(plan, batch, in_re, in_im, out_re, out_im, ws, stream);
 }
 
 int tfa_execute_strided_ws(const tfa_plan* plan, int64_t outer, int64_t stride, const float* in_re,
