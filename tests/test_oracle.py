@@ -176,6 +176,71 @@ def test_istft_roundtrip():
     np.testing.assert_allclose(y.numpy(), x.numpy(), atol=1e-3)
 
 
+@pytest.mark.parametrize("n_fft,hop,center,normalized,onesided,length,win", [
+    (256, 64, True, False, True, None, "hann"),
+    (512, 128, True, True, True, 3000, "hann"),
+    (512, 200, True, False, True, 2500, "hann"),      # hop not dividing n_fft
+    (128, 32, False, False, True, None, "hann+0.1"),  # no zero in the envelope without centring
+    (64, 16, True, False, False, None, "hann"),       # two-sided spectrum (real part kept)
+])
+def test_istft_vs_torch_istft_float64(n_fft, hop, center, normalized, onesided, length, win):
+    # torch.istft divides the overlap-add by the same squared-window envelope; with a window that
+    # meets NOLA the reference's raw-sum branch (trnfft/api.py:450-452) is never taken
+    g = torch.Generator().manual_seed(n_fft + hop)
+    x = torch.randn(2, 3000, generator=g, dtype=torch.float64)
+    w = torch.hann_window(n_fft, dtype=torch.float64)
+    if win == "hann+0.1":
+        w = w + 0.1
+    spec = torch.stft(x, n_fft, hop_length=hop, window=w, center=center, normalized=normalized,
+                      onesided=onesided, return_complex=True)
+    spec = spec + 0.01 * torch.randn(spec.shape, generator=g, dtype=torch.complex128)  # not an exact STFT
+    got = oracle.istft((spec.real.float(), spec.imag.float()), n_fft=n_fft, hop_length=hop, window=w.float(),
+                       center=center, normalized=normalized, onesided=onesided, length=length)
+    ref = torch.istft(spec, n_fft, hop_length=hop, window=w, center=center, normalized=normalized,
+                      onesided=onesided, length=length, return_complex=not onesided)
+    ref = ref.real if torch.is_complex(ref) else ref
+    assert got.shape == ref.shape
+    assert rel_l2(got, torch.zeros_like(got), ref, torch.zeros_like(ref)) < 1e-6
+
+
+def test_istft_raw_sum_branch_closed_form():
+    # hop = n_fft (frames do not overlap) and a window with zero ends: the envelope is w[j]^2, so
+    # every sample is frame[j] * w[j] / w[j]^2 except where w[j] = 0, where the reference returns
+    # the raw overlap-add, i.e. the inverse-transformed frame sample itself (trnfft/api.py:446-452)
+    n, frames = 64, 5
+    g = torch.Generator().manual_seed(3)
+    f = torch.randn(2, frames, n, generator=g, dtype=torch.float64)
+    w = torch.ones(n, dtype=torch.float64)
+    w[0] = w[-1] = 0.0
+    w[1] = w[-2] = 0.5
+    spec = torch.fft.fft(f, dim=-1).transpose(-2, -1)  # (2, n, frames), two-sided
+    got = oracle.istft((spec.real.float(), spec.imag.float()), n_fft=n, hop_length=n, window=w.float(),
+                       center=False, onesided=False)
+    expect = torch.where(w > 0, f / torch.where(w > 0, w, torch.ones_like(w)), f).reshape(2, frames * n)
+    assert got.shape == expect.shape
+    assert rel_l2(got, torch.zeros_like(got), expect, torch.zeros_like(expect)) < 1e-6
+    # the zero-window samples are exactly the raw frame samples
+    raw = got.reshape(2, frames, n)[..., [0, n - 1]].double()
+    assert torch.allclose(raw, f[..., [0, n - 1]], atol=1e-5)
+
+
+@pytest.mark.parametrize("sa,sb", [((6, 5), (5, 7)), ((3, 6, 5), (3, 5, 7)), ((2, 1, 6, 5), (4, 5, 7)), ((5,), (5, 7)),
+                                   ((6, 5), (5,)), ((5,), (5,)), ((3, 6, 5), (5, 7))])
+def test_complex_matmul_vs_numpy_complex(sa, sb):
+    # the four-real-matmul formula of trnfft/complex.py:142-150 against complex matmul in numpy:
+    # float64 operands agree to rounding, float32 ones within fp32 accumulation error
+    rng = np.random.default_rng(len(sa) * 7 + len(sb))
+    ar, ai = rng.standard_normal(sa), rng.standard_normal(sa)
+    br, bi = rng.standard_normal(sb), rng.standard_normal(sb)
+    e = np.matmul(ar + 1j * ai, br + 1j * bi)
+    r, i = oracle.complex_matmul((torch.from_numpy(ar), torch.from_numpy(ai)), (torch.from_numpy(br), torch.from_numpy(bi)))
+    assert tuple(r.shape) == e.shape
+    assert rel_l2(r, i, e.real, e.imag) < 1e-14
+    f = lambda a: torch.from_numpy(a.astype(np.float32))  # noqa: E731
+    r, i = oracle.complex_matmul((f(ar), f(ai)), (f(br), f(bi)))
+    assert rel_l2(r, i, e.real, e.imag) < 1e-6
+
+
 # --- complex linear / DFT-GEMM / row-column --------------------------------------------------
 
 
