@@ -184,6 +184,9 @@ def test_bluestein_vs_reference_golden(direction):
 
 
 @pytest.mark.parametrize("n,batch", [(1000, 1024), (4099, 256), (3, 5), (17, 33), (8193, 4), (20000, 2),
+                                     # the mixed-radix fused length 9216 = 12^2 * 64 covers
+                                     # 4096 < n <= 4608 (reference m = 16384); 4609 pads to 16384
+                                     (4097, 3), (4097, 300), (4608, 70), (4609, 70), (4609, 5),
                                      # short rows (m <= 256, staged per workgroup): full tiles plus a
                                      # ragged one, every padded length 4..256 and real input below
                                      (2, 600), (5, 1000), (7, 257), (12, 300), (31, 513), (33, 129),
@@ -204,18 +207,19 @@ def test_bluestein_short_rows_real_input(n):
     assert rel_l2(X.real, X.imag, *ref) <= tol_bluestein(n)
 
 
+@pytest.mark.parametrize("n", [4099, 6000])
 @pytest.mark.parametrize("inverse", [False, True])
-def test_bluestein_fused_and_split_paths_agree(inverse):
-    # m = 16384 (n = 4099) runs the fused one-row-per-workgroup kernel for large batches and the
-    # split three-pass path for small ones; rows must agree across the two paths, and the fused
-    # batch is checked against the oracle on a few rows
-    re, im = seeded_complex(2048, 4099, seed=11)
+def test_bluestein_fused_and_split_paths_agree(n, inverse):
+    # n = 6000 (m = 16384) runs the fused one-row-per-workgroup kernel for large batches and the
+    # split three-pass path for small ones; n = 4099 runs the 9216-point fused kernel at every
+    # batch; rows must agree across batch sizes, and both are checked against the oracle
+    re, im = seeded_complex(2048, n, seed=11)
     fused = _gpu_fft(re, im, inverse)  # 2048 rows: fused kernel
-    split = _gpu_fft(re[:5], im[:5], inverse)  # 5 rows: split path
-    assert rel_l2(fused[0][:5], fused[1][:5], *split) <= tol_bluestein(4099)
+    small = _gpu_fft(re[:5], im[:5], inverse)  # 5 rows: split path for n = 6000
+    assert rel_l2(fused[0][:5], fused[1][:5], *small) <= tol_bluestein(n)
     ref = oracle.fft_core(re[:5], im[:5], inverse)
-    assert rel_l2(fused[0][:5], fused[1][:5], *ref) <= tol_bluestein(4099)
-    assert rel_l2(*split, *ref) <= tol_bluestein(4099)
+    assert rel_l2(fused[0][:5], fused[1][:5], *ref) <= tol_bluestein(n)
+    assert rel_l2(*small, *ref) <= tol_bluestein(n)
 
 
 @pytest.mark.parametrize("n,batch", [(70000, 1), ((1 << 20) + 1, 1)])

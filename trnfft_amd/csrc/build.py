@@ -42,8 +42,14 @@ FLAGS = [
 ]
 
 
+# per-source extra flags: the fused Bluestein kernel feeds compile-time zeros (the zero-padded
+# half of its forward input) into its first pass; ignoring the sign of zero lets the compiler drop
+# the additions of those zeros (x + 0 -> x), which changes no result beyond the sign of a zero
+EXTRA_FLAGS = {"kernels_bluestein.hip": ["-fno-signed-zeros"]}
+
+
 def _compile(src: str, obj: str) -> None:
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(HERE, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(HERE, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")

@@ -123,6 +123,20 @@ struct Dft<4, DIR> {
   }
 };
 
+// Radix 3: a0 + a1 + a2, and a0 - (a1 + a2)/2 -/+ (sqrt(3)/2) (DIR i)(a1 - a2) for outputs 1, 2.
+template <int DIR>
+struct Dft<3, DIR> {
+  __device__ __forceinline__ static void run(float2* a) {
+    constexpr float s3 = 0.866025403784438646763723170752936f;
+    const float2 t1 = cadd(a[1], a[2]);
+    const float2 t2 = make_float2(a[0].x - 0.5f * t1.x, a[0].y - 0.5f * t1.y);
+    const float2 t3 = cscale(mul_diri<DIR>(csub(a[1], a[2])), s3);
+    a[0] = cadd(a[0], t1);
+    a[1] = cadd(t2, t3);
+    a[2] = csub(t2, t3);
+  }
+};
+
 // R = R1 * R2: DFT_R2 over the stride-R1 subsequences, twiddle W_R^{l q}, then DFT_R1.
 template <int R1, int R2, int DIR>
 struct DftSplit {
@@ -171,6 +185,19 @@ template <int DIR>
 struct Dft<32, DIR> {
   __device__ __forceinline__ static void run(float2* a) { DftSplit<4, 8, DIR>::run(a); }
 };
+// radices with a factor 3 (mixed-radix lengths 3 * 2^k and 9 * 2^k)
+template <int DIR>
+struct Dft<6, DIR> {
+  __device__ __forceinline__ static void run(float2* a) { DftSplit<2, 3, DIR>::run(a); }
+};
+template <int DIR>
+struct Dft<12, DIR> {
+  __device__ __forceinline__ static void run(float2* a) { DftSplit<4, 3, DIR>::run(a); }
+};
+template <int DIR>
+struct Dft<24, DIR> {
+  __device__ __forceinline__ static void run(float2* a) { DftSplit<8, 3, DIR>::run(a); }
+};
 
 // Synchronisation between the LDS write and read halves of a pass exchange.  When a transform
 // lives inside one wavefront (T <= 64) program order within the wave suffices and only the
@@ -197,10 +224,21 @@ __device__ __forceinline__ void exchange_sync() {
 // consecutive float2 in the cycles of a ds_read_b32, so this halves LDS time as well).
 // PF: each pass requests the next pass's twiddles before its exchange barriers, so their table
 // latency overlaps the exchange instead of following it (E/2 float4 more registers live there).
-template <int N, int E, int DIR, bool WAVE_LOCAL, bool SPLIT = false, bool IL = false, bool PF = false>
+// DB: double-buffered exchange (IL only): pass p writes and reads LDS buffer p % 2, the second one
+// 2 * lds_pad(N) floats after `lre`, so one workgroup barrier per exchange suffices (a buffer is
+// rewritten two passes later, after every thread has passed the intervening barrier, which
+// follows its reads of that buffer); run() starts with a barrier so that back-to-back transforms
+// in one kernel do not overwrite a buffer another thread is still reading.  Nothing after run()
+// may use the LDS without its own barrier.
+template <int N, int E, int DIR, bool WAVE_LOCAL, bool SPLIT = false, bool IL = false, bool PF = false,
+          bool DB = false>
 struct LdsFft {
   static constexpr LdsShape S = make_shape(N, E);
   static constexpr int T = N / E;
+  static_assert(!DB || (IL && !SPLIT && !WAVE_LOCAL), "double buffering is for the interleaved workgroup exchange");
+  static constexpr int PADP = lds_pad_period(N, E);  // LDS pad period (16 for power-of-two shapes)
+  static constexpr int DBOFF = 2 * lds_entries(N, E);  // floats between the two buffers
+  __device__ __forceinline__ static int pad(int i) { return lds_pad_p(i, PADP); }
   static constexpr int TQ = PF ? (E / 2 > 0 ? E / 2 : 1) : 1;  // float4 twiddles per thread per pass
 
   template <int P>
@@ -209,16 +247,18 @@ struct LdsFft {
     if constexpr (P < S.npass) {
       constexpr int R = S.radix[P];
       constexpr int NB = E / R;
+      static_assert(E % R == 0, "each pass radix must divide the elements per thread");
+      static_assert(P == 0 || R % 2 == 0, "twiddled passes read their table as float4 pairs (even radix)");
       constexpr int LS = S.ls[P];
       constexpr bool LAST = (P == S.npass - 1);
       // the pass's LDS write index is linear in u when the radix (first pass) or the span LS
       // (later passes) is a multiple of the 16-word padding period
-      constexpr bool LIN_W = (LS == 1) ? (R % 16 == 0) : (LS % 16 == 0);
+      constexpr bool LIN_W = (LS == 1) ? (R % PADP == 0) : (LS % PADP == 0);
       float2 w[NB][R];
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const int j = tid + b * T;
-        const int k = j & (LS - 1);
+        const int k = (int)((unsigned)j % (unsigned)LS);
 #pragma unroll
         for (int r = 0; r < R; ++r) w[b][r] = v[b + r * NB];
         if constexpr (P > 0) {
@@ -235,7 +275,7 @@ struct LdsFft {
 #pragma unroll
           for (int u = 0; u < R; ++u) v[b + u * NB] = w[b][u];
         } else if constexpr (!SPLIT) {
-          store_pass<R, LS, LIN_W>(w[b], lre, lim, j, k, IL ? 3 : 2);
+          store_pass<R, LS, LIN_W>(w[b], (DB && (P & 1)) ? lre + DBOFF : lre, lim, j, k, IL ? 3 : 2);
         }
       }
       if constexpr (!LAST) {
@@ -244,7 +284,7 @@ struct LdsFft {
           constexpr int R1 = S.radix[P + 1], NB1 = E / R1, LS1 = S.ls[P + 1];
 #pragma unroll
           for (int b = 0; b < NB1; ++b) {
-            const int k1 = (tid + b * T) & (LS1 - 1);
+            const int k1 = (int)((unsigned)(tid + b * T) % (unsigned)LS1);
             const float4* t4 = reinterpret_cast<const float4*>(tw + S.twoff[P + 1] + k1 * R1);
 #pragma unroll
             for (int r2 = 0; r2 < R1 / 2; ++r2) tn[b * (R1 / 2) + r2] = t4[r2];
@@ -252,15 +292,15 @@ struct LdsFft {
         }
         if constexpr (!SPLIT) {
           exchange_sync<WAVE_LOCAL>();
-          load_pass(v, lre, lim, tid, IL ? 3 : 2);
-          exchange_sync<WAVE_LOCAL>();
+          load_pass(v, (DB && (P & 1)) ? lre + DBOFF : lre, lim, tid, IL ? 3 : 2);
+          if constexpr (!DB) exchange_sync<WAVE_LOCAL>();
         } else {
 #pragma unroll
           for (int plane = 0; plane < 2; ++plane) {
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
               const int j = tid + b * T;
-              store_pass<R, LS, LIN_W>(w[b], lre, lre, j, j & (LS - 1), plane);
+              store_pass<R, LS, LIN_W>(w[b], lre, lre, j, (int)((unsigned)j % (unsigned)LS), plane);
             }
             exchange_sync<WAVE_LOCAL>();
             load_pass(v, lre, lre, tid, plane);
@@ -279,10 +319,10 @@ struct LdsFft {
                                                     int which) {
     if constexpr (LIN_W) {
       // padded index = base + compile-time offset per u (immediate-offset LDS stores)
-      const int base = LS == 1 ? j * (R + R / 16) : lds_pad((j - k) * R) + k + (k >> 4);
+      const int base = LS == 1 ? j * (R + R / PADP) : pad((j - k) * R) + k + (int)((unsigned)k / (unsigned)PADP);
 #pragma unroll
       for (int u = 0; u < R; ++u) {
-        const int off = LS == 1 ? u + (u >> 4) : u * (LS + LS / 16);
+        const int off = LS == 1 ? u + u / PADP : u * (LS + LS / PADP);
         if (which == 3) {
           reinterpret_cast<float2*>(a)[base + off] = w[u];
         } else if (which == 2) {
@@ -296,7 +336,7 @@ struct LdsFft {
       const int base = (j - k) * R + k;
 #pragma unroll
       for (int u = 0; u < R; ++u) {
-        const int idx = lds_pad(base + u * LS);
+        const int idx = pad(base + u * LS);
         if (which == 3) {
           reinterpret_cast<float2*>(a)[idx] = w[u];
         } else if (which == 2) {
@@ -311,11 +351,11 @@ struct LdsFft {
 
   __device__ __forceinline__ static void load_pass(float2 (&v)[E], const float* a, const float* b, int tid,
                                                    int which) {
-    if constexpr (T % 16 == 0) {
-      const int rb = tid + (tid >> 4);
+    if constexpr (T % PADP == 0) {
+      const int rb = tid + (int)((unsigned)tid / (unsigned)PADP);
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        const int idx = rb + e * (T + T / 16);
+        const int idx = rb + e * (T + T / PADP);
         if (which == 3) v[e] = reinterpret_cast<const float2*>(a)[idx];
         else if (which == 2) v[e] = make_float2(a[idx], b[idx]);
         else if (which == 0) v[e].x = a[idx];
@@ -324,7 +364,7 @@ struct LdsFft {
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        const int idx = lds_pad(tid + T * e);
+        const int idx = pad(tid + T * e);
         if (which == 3) v[e] = reinterpret_cast<const float2*>(a)[idx];
         else if (which == 2) v[e] = make_float2(a[idx], b[idx]);
         else if (which == 0) v[e].x = a[idx];
@@ -336,6 +376,7 @@ struct LdsFft {
   __device__ __forceinline__ static void run(float2 (&v)[E], float* lre, float* lim,
                                              const float2* __restrict__ tw, int tid) {
     const float4 none[TQ] = {};
+    if constexpr (DB) exchange_sync<false>();
     pass<0>(v, lre, lim, tw, tid, none);
   }
 };

@@ -85,9 +85,22 @@ __host__ __device__ constexpr bool fft2_small_ok(long long h, long long w) {
 // workgroup runs the same pass at the same time, so each pass's table latency is exposed): C3a
 // 1024 x 1000 12.9 -> 12.3 us.  (Twiddle tables staged in LDS once per workgroup measured
 // slower, C3a 13.0 -> 17.0 us: the 41 KB copy costs more than it saves.)
-__host__ __device__ constexpr int blue_epth(int m) { return m >= 16384 ? 16 : m >= 128 ? 8 : lds_epth(m); }
-__host__ __device__ constexpr int blue_threads(int m) { return m == 2048 || m >= 8192 ? 512 : 256; }
+// Mixed-radix length 9216 = 12 * 12 * 4 * 4 * 4 (C3b's n = 4099): E = 12 with 768 threads per row
+// measured 18.2 us against 22.6 us for E = 24 / 384 threads (181 VGPRs), 24.9 us for E = 24 forced
+// to two workgroups per CU and 26.7 us for E = 24 without the twiddle prefetch (the former
+// power-of-two m = 16384 kernel: 29.0 us).  Timing probes of that kernel: the LDS exchanges cost
+// 3.5 us and the twiddle-table reads 1.4 us of the 18.9; the rest is VALU (1536 instructions per
+// wave, each 4 cycles on a 16-lane SIMD) and the load latencies.
+__host__ __device__ constexpr int blue_epth(int m) {
+  return m % 3 == 0 ? 12 : m >= 16384 ? 16 : m >= 128 ? 8 : lds_epth(m);
+}
+__host__ __device__ constexpr int blue_threads(int m) {
+  return m % 3 == 0 ? m / 12 : m == 2048 || m >= 8192 ? 512 : 256;
+}
 __host__ __device__ constexpr bool blue_pf(int m) { return m >= 256; }
+// double-buffered LDS exchange in the fused kernel (one barrier per pass exchange) where two
+// buffers fit the CU's LDS: C3a (m = 2048) 12.8 -> 12.2 us; no change at m = 9216
+__host__ __device__ constexpr bool blue_db(int m) { return m % 3 == 0 || (m >= 1024 && m <= 8192); }
 // split Bluestein (m >= 32768, three passes): elements per thread of the column passes (length
 // m1; E = 8 at m1 = 128 measured no better) and next-pass twiddle prefetch in the column and row
 // passes (209 x 20000 147 -> 143 us, 59 x 70000 183 -> 178, 32 x 8193 26.9 -> 25.7; 511 x 8193
@@ -109,6 +122,15 @@ __host__ __device__ constexpr bool istft_pf(int n) { return n >= 512; }
 // per transform up to l = 1024 (one 32-transform tile = 1024 threads), 32 elements above.
 __host__ __device__ constexpr int fourstep_epth(int l) { return l <= 1024 ? (l >= 128 ? l / 32 : 4) : 32; }
 
+__host__ __device__ constexpr int gcd_c(int a, int b) {
+  while (b) {
+    const int t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
 struct LdsShape {
   int n, e, t, npass;
   int radix[kMaxPasses];
@@ -125,7 +147,10 @@ __host__ __device__ constexpr LdsShape make_shape(int n, int e) {
   s.t = n / e;
   int rem = n, p = 0, ls = 1, off = 0;
   while (rem > 1) {
-    int r = rem >= e ? e : rem;
+    // the largest radix dividing both the remaining length and E (E itself while it divides; for
+    // powers of two this is min(E, rem))
+    int r = gcd_c(e, rem);
+    if (r <= 1) r = rem;  // no common factor: one pass of the rest (rejected by the device code)
     s.radix[p] = r;
     s.ls[p] = ls;
     s.twoff[p] = off;
@@ -141,5 +166,17 @@ __host__ __device__ constexpr LdsShape make_shape(int n, int e) {
 
 // LDS word index with one pad word per 16 to keep the strided pass writes bank-conflict free.
 __host__ __device__ constexpr int lds_pad(int i) { return i + (i >> 4); }
+
+// Pad period of the LDS exchange of the (n, e) Stockham shape: 16 for power-of-two radices; for a
+// shape that starts with a radix divisible by 3 (mixed-radix lengths) the first radix R0, so the
+// first pass's stride-R0 writes land on stride R0 + 1 entries, the second pass's runs of R0
+// consecutive entries (when its span is R0) stay contiguous across 16 lanes, and the later passes
+// write near-contiguous runs.
+__host__ __device__ constexpr int lds_pad_period(int n, int e) {
+  return (make_shape(n, e).radix[0] % 3 == 0) ? make_shape(n, e).radix[0] : 16;
+}
+__host__ __device__ constexpr int lds_pad_p(int i, int period) { return i + (int)((unsigned)i / (unsigned)period); }
+// LDS entries (float2 when interleaved) one transform of the (n, e) shape occupies
+__host__ __device__ constexpr int lds_entries(int n, int e) { return lds_pad_p(n, lds_pad_period(n, e)); }
 
 }  // namespace tfa

@@ -29,7 +29,9 @@ struct BlueCfg {
   static constexpr int T = M / E;
   static constexpr int XF = T >= THR ? 1 : THR / T;
   static constexpr int THREADS = XF * T;
-  static constexpr int PADN = lds_pad(M) > 1 ? lds_pad(M) : 1;
+  static constexpr int PADN = lds_entries(M, E_) > 1 ? lds_entries(M, E_) : 1;
+  static constexpr bool DB = blue_db(M) && T > 64;  // double-buffered exchange (two LDS buffers per row)
+  static constexpr int NBUF = DB ? 2 : 1;
 };
 
 template <int M, bool REAL_IN, int E_ = blue_epth(M), int THR = blue_threads(M)>
@@ -40,47 +42,61 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
     float scale) {
   using C = BlueCfg<M, E_, THR>;
   constexpr int E = C::E, T = C::T;
-  __shared__ float2 lds[C::XF * C::PADN];  // interleaved (re, im) exchange
-  const int tid = threadIdx.x & (T - 1);
+  __shared__ float2 lds[C::XF * C::PADN * C::NBUF];  // interleaved (re, im) exchange
+  const int tid = threadIdx.x % T;
   const int xf = threadIdx.x / T;
   const long long b = (long long)blockIdx.x * C::XF + xf;
   const bool valid = b < batch;
   const size_t base = (size_t)b * n;
 
   // every workgroup of the launch runs the same phase at the same time, so nothing hides a
-  // table load issued where it is used: the chirp is loaded once (it multiplies both the input
-  // and the output) and the filter spectrum is requested before the forward transform
-  // (with 16 or more elements per thread the extra registers would spill: both tables are then
-  // read where they are used)
+  // table load issued where it is used: with up to 8 elements per thread the chirp is loaded
+  // once (it multiplies both the input and the output) and the filter spectrum is requested
+  // before the forward transform; with 12 (the mixed-radix lengths) the filter spectrum is
+  // requested before the forward transform and the output chirp before the inverse one; with 16
+  // the extra registers would spill, and both tables are read where they are used.
+  // n <= M/2 (M >= 2n - 1), so element e of a thread can hold a sample only for e < E/2: the
+  // upper half of the forward input is zero at compile time and the upper half of the inverse
+  // output is never needed (its last-pass arithmetic is dead code).
+  constexpr int EH = E / 2 > 0 ? E / 2 : 1;
   constexpr bool PRE = E <= 8;
-  float2 v[E], ch[PRE ? E : 1], hv[PRE ? E : 1];
+  constexpr bool PRE2 = E == 12;
+  float2 v[E], ch[PRE ? EH : 1], hv[PRE || PRE2 ? E : 1];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int i = tid + T * e;
-    const float2 c = i < n ? chirp[i] : make_float2(0.0f, 0.0f);
-    if constexpr (PRE) {
-      ch[e] = c;
-      hv[e] = hs[i];
-    }
+    if constexpr (PRE || PRE2) hv[e] = hs[i];
     float2 y = make_float2(0.0f, 0.0f);
-    if (valid && i < n) {
-      const float2 x = make_float2(in_re[base + i], REAL_IN ? 0.0f : in_im[base + i]);
-      y = cmul(x, c);
+    if (e < EH) {
+      const float2 c = i < n ? chirp[i] : make_float2(0.0f, 0.0f);
+      if constexpr (PRE) ch[PRE ? e : 0] = c;
+      if (valid && i < n) {
+        const float2 x = make_float2(in_re[base + i], REAL_IN ? 0.0f : in_im[base + i]);
+        y = cmul(x, c);
+      }
     }
     v[e] = y;
   }
-  float* my = reinterpret_cast<float*>(lds + xf * C::PADN);
+  float* my = reinterpret_cast<float*>(lds + xf * C::PADN * C::NBUF);
   constexpr bool PF = blue_pf(M);
-  LdsFft<M, E, -1, (T <= 64), false, true, PF>::run(v, my, nullptr, tw_f, tid);
+  LdsFft<M, E, -1, (T <= 64), false, true, PF, C::DB>::run(v, my, nullptr, tw_f, tid);
 #pragma unroll
-  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], PRE ? hv[PRE ? e : 0] : hs[tid + T * e]);
-  LdsFft<M, E, 1, (T <= 64), false, true, PF>::run(v, my, nullptr, tw_i, tid);
+  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], PRE || PRE2 ? hv[PRE || PRE2 ? e : 0] : hs[tid + T * e]);
+  float2 ch2[PRE2 ? EH : 1];
+  if constexpr (PRE2) {
+#pragma unroll
+    for (int e = 0; e < EH; ++e) {
+      const int i = tid + T * e;
+      ch2[e] = i < n ? chirp[i] : make_float2(0.0f, 0.0f);
+    }
+  }
+  LdsFft<M, E, 1, (T <= 64), false, true, PF, C::DB>::run(v, my, nullptr, tw_i, tid);
   if (valid) {
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
+    for (int e = 0; e < EH; ++e) {
       const int i = tid + T * e;
       if (i < n) {
-        const float2 y = cmul(v[e], PRE ? ch[PRE ? e : 0] : chirp[i]);
+        const float2 y = cmul(v[e], PRE ? ch[PRE ? e : 0] : PRE2 ? ch2[PRE2 ? e : 0] : chirp[i]);
         out_re[base + i] = y.x * scale;
         out_im[base + i] = y.y * scale;
       }
@@ -202,6 +218,7 @@ hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a) {
     case 4096: return launch_blue_m<4096>(a);
     case 8192: return launch_blue_m<8192>(a);
     case 16384: return launch_blue_m<16384>(a);
+    case 9216: return launch_blue_m<9216>(a);
     default: return hipErrorInvalidValue;
   }
 }

@@ -88,7 +88,8 @@ struct C2cTables {
 struct tfa_plan {
   tfa_plan_desc d{};
   int device = 0;
-  int64_t m = 0;  // padded length (Bluestein), else n
+  int64_t m = 0;  // padded length (Bluestein: the reference's, trnfft/plan.py:42), else n
+  int64_t mf = 0;  // Bluestein: internal length of the fused kernel (m, or a shorter mixed-radix length)
   C2cTables fwd, inv;  // C2C uses the one for its direction; Bluestein uses both (length m)
   bool blue_fused = false;  // Bluestein: fused one-launch kernel available (m <= 16384)
   bool blue_split = false;  // Bluestein: split three-pass path available (m >= 16384)
@@ -204,9 +205,20 @@ namespace {
 // Bluestein path choice: the fused kernel holds one row per workgroup, so with fewer than
 // kBlueSplitRows rows it leaves most of the GPU idle and the split three-pass path (each row
 // spread over many workgroups per pass) takes over; above 16384 only the split path exists.
+// Internal length of the fused Bluestein kernel for n whose reference padded length is m: the
+// circular convolution needs only L >= 2n - 1, and where m overshoots that by most, a
+// mixed-radix length (3^2 * 2^10 = 9216 for 4096 < n <= 4608, against m = 16384) halves the
+// transforms and the LDS (two workgroups per CU instead of one).
+int64_t blue_fused_length(int64_t n, int64_t m) {
+  if (m == 16384 && 2 * n - 1 <= 9216) return 9216;
+  return m;
+}
+
 bool blue_use_split(const tfa_plan* p, int64_t batch) {
   if (!p->blue_fused) return true;
-  return p->blue_split && batch < kBlueSplitRows;
+  // the mixed-radix fused kernel (half the LDS, two rows' latency per CU) beats the split path
+  // at every row count: 1 x 4099 12.7 vs 13.9 us, 16 x 4099 13.8 vs 16.2, 63 x 4099 14.7 vs 23.0
+  return p->blue_split && batch < kBlueSplitRows && p->mf == p->m;
 }
 
 size_t c2c_workspace(const C2cTables& t, int64_t batch) {
@@ -239,6 +251,33 @@ int run_c2c(const C2cTables& t, int64_t batch, const float* in_re, const float* 
 }
 
 // Host fp64 radix-2 FFT (forward, in place) used only to build the Bluestein filter spectrum.
+void host_fft(std::vector<std::complex<double>>& a);
+
+// Host fp64 forward DFT of a power-of-two length, or of 3^a * 2^b (one radix-3 split per factor 3
+// down to the radix-2 FFT); builds the filter spectrum of the mixed-radix fused lengths.
+void host_dft(std::vector<std::complex<double>>& a) {
+  const size_t n = a.size();
+  if (n % 3 != 0) {
+    host_fft(a);
+    return;
+  }
+  const size_t q = n / 3;
+  std::vector<std::complex<double>> s[3];
+  for (int r = 0; r < 3; ++r) {
+    s[r].resize(q);
+    for (size_t j = 0; j < q; ++j) s[r][j] = a[3 * j + r];
+    host_dft(s[r]);
+  }
+  for (size_t k = 0; k < n; ++k) {
+    std::complex<double> acc = s[0][k % q];
+    for (int r = 1; r < 3; ++r) {
+      const double ang = -2.0 * M_PI * (double)((r * k) % n) / (double)n;
+      acc += s[r][k % q] * std::complex<double>(std::cos(ang), std::sin(ang));
+    }
+    a[k] = acc;
+  }
+}
+
 void host_fft(std::vector<std::complex<double>>& a) {
   const size_t n = a.size();
   for (size_t i = 1, j = 0; i < n; ++i) {
@@ -367,13 +406,15 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       }
       p->blue_fused = m <= kMaxLdsN;
       p->blue_split = m >= kMinBlueSplitM;
+      p->mf = p->blue_fused ? blue_fused_length(n, m) : 0;
       if (p->blue_fused) {
         // the fused kernel's own launch shape (tfa::blue_epth) fixes its table layout
-        p->fwd.n = p->inv.n = m;
+        const int mf = (int)p->mf;
+        p->fwd.n = p->inv.n = mf;
         p->fwd.dir = -1;
         p->inv.dir = 1;
-        if ((rc = p->upload(lds_table((int)m, -1, tfa::blue_epth((int)m)), &p->fwd.tw))) break;
-        if ((rc = p->upload(lds_table((int)m, 1, tfa::blue_epth((int)m)), &p->inv.tw))) break;
+        if ((rc = p->upload(lds_table(mf, -1, tfa::blue_epth(mf)), &p->fwd.tw))) break;
+        if ((rc = p->upload(lds_table(mf, 1, tfa::blue_epth(mf)), &p->inv.tw))) break;
         if (m <= tfa::kMaxStridedBlueM) {  // the strided-axis kernel's layout (tfa::lds_epth)
           if (tfa::blue_epth((int)m) == tfa::lds_epth((int)m)) {
             p->b_tw_sf = p->fwd.tw;
@@ -385,19 +426,25 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         }
       }
       const std::vector<float2> chirp = reference_chirp(n, dir);
-      // h = conj(chirp) circularly wrapped (trnfft/fft_core.py:1337-1345); H = FFT_m(h) / m
-      std::vector<std::complex<double>> h((size_t)m, {0.0, 0.0});
-      for (int64_t i = 0; i < n; ++i) {
-        const std::complex<double> hc(chirp[(size_t)i].x, -(double)chirp[(size_t)i].y);
-        h[(size_t)i] = hc;
-        if (i > 0) h[(size_t)(m - i)] = hc;
-      }
-      host_fft(h);
-      std::vector<float2> hs((size_t)m);
-      for (int64_t i = 0; i < m; ++i)
-        hs[(size_t)i] = make_float2((float)(h[(size_t)i].real() / (double)m), (float)(h[(size_t)i].imag() / (double)m));
+      // h = conj(chirp) circularly wrapped (trnfft/fft_core.py:1337-1345) to the circular
+      // convolution length L; H = FFT_L(h) / L.  Any L >= 2n - 1 gives the same convolution, so
+      // the fused kernel may use a shorter mixed-radix length than the reference's m.
+      auto filter_spectrum = [&](int64_t L) {
+        std::vector<std::complex<double>> h((size_t)L, {0.0, 0.0});
+        for (int64_t i = 0; i < n; ++i) {
+          const std::complex<double> hc(chirp[(size_t)i].x, -(double)chirp[(size_t)i].y);
+          h[(size_t)i] = hc;
+          if (i > 0) h[(size_t)(L - i)] = hc;
+        }
+        host_dft(h);
+        std::vector<float2> hs((size_t)L);
+        for (int64_t i = 0; i < L; ++i)
+          hs[(size_t)i] = make_float2((float)(h[(size_t)i].real() / (double)L), (float)(h[(size_t)i].imag() / (double)L));
+        return hs;
+      };
+      const std::vector<float2> hs = filter_spectrum(m);
       if ((rc = p->upload(chirp, &p->chirp))) break;
-      if ((rc = p->upload(hs, &p->hs))) break;
+      if ((rc = p->upload(p->blue_fused && p->mf != m ? filter_spectrum(p->mf) : hs, &p->hs))) break;
       if (p->blue_split) {
         // m = m1 * m2 (m1 = 2^floor(log2 m / 2)); tables of the three passes, H/m permuted to
         // the transposed spectrum order hp[k1*m2 + k2] = H[k1 + m1*k2] / m
@@ -569,10 +616,10 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
                      workspace, scale, s);
     case TFA_KIND_BLUESTEIN: {
       tfa::BluesteinArgs a{in_re, in_im, out_re, out_im, plan->chirp, plan->hs, plan->fwd.tw,
-                           plan->inv.tw, (int)n, (int)plan->m, batch, scale, s};
+                           plan->inv.tw, (int)n, (int)plan->mf, batch, scale, s};
       hipError_t e;
       if (!blue_use_split(plan, batch)) {
-        e = tfa::launch_bluestein_fused((int)plan->m, a);
+        e = tfa::launch_bluestein_fused((int)plan->mf, a);
         return e == hipSuccess ? TFA_OK : hip_fail(e, "bluestein launch");
       }
       if (!workspace) return fail(TFA_ERR_INVALID, "split Bluestein needs a workspace (tfa_plan_workspace_size)");
