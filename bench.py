@@ -374,20 +374,24 @@ def bench_secondary():
     rec("c4a_fft2_32x2048x2048", t, 32 * 5 * 2048 * 2048 * 22, 32 * 2048 * 2048 * (4 + 8), sets=1,
         note="two HBM passes; algorithmic bytes = real read + complex write")
     del img, yr, yi
-    # C5a: ComplexLinear 8192 x 1024 -> 1024 (Kaiming-uniform U(+-1/32) weights, zero bias); MFMA-bound
+    # C5a: ComplexLinear 8192 x 1024 -> 1024 (Kaiming-uniform U(+-1/32) weights, zero bias); MFMA-bound.
+    # Buffer sets (x, W, y: 142.6 MB each) rotated past the Infinity Cache like the other configs
+    nbytes = 142614528
+    S = _n_sets(nbytes)
     g = torch.Generator().manual_seed(42)
-    xr = torch.randn(8192, 1024, generator=g).to(dev)
-    xi = torch.randn(8192, 1024, generator=g).to(dev)
-    wr = (torch.rand(1024, 1024, generator=g) * 2 - 1).div_(32).to(dev)
-    wi = (torch.rand(1024, 1024, generator=g) * 2 - 1).div_(32).to(dev)
+    xr0, xi0 = torch.randn(8192, 1024, generator=g), torch.randn(8192, 1024, generator=g)
+    wr0 = (torch.rand(1024, 1024, generator=g) * 2 - 1).div_(32)
+    wi0 = (torch.rand(1024, 1024, generator=g) * 2 - 1).div_(32)
+    xs = list(zip(rolled(xr0, S), rolled(xi0, S)))
+    ws = list(zip(rolled(wr0, S), rolled(wi0, S)))
     br = torch.zeros(1024, device=dev)
     bi = torch.zeros(1024, device=dev)
-    yr = torch.empty(8192, 1024, device=dev)
-    yi = torch.empty_like(yr)
-    t = _time_rot(lambda k, st: chk(L.tfa_complex_gemm(8192, 1024, 1024, P(xr), P(xi), 1024, P(wr), P(wi), 1024, 1,
-                                                   P(br), P(bi), P(yr), P(yi), 1024, st)), 1)
-    rec("c5a_complex_linear_8192x1024x1024", t, 8.0 * 8192 * 1024 * 1024, 142614528, kind="mfma")
-    del xr, xi, yr, yi
+    ys = [(torch.empty(8192, 1024, device=dev), torch.empty(8192, 1024, device=dev)) for _ in range(S)]
+    t = _time_rot(lambda k, st: chk(L.tfa_complex_gemm(8192, 1024, 1024, P(xs[k][0]), P(xs[k][1]), 1024, P(ws[k][0]),
+                                                   P(ws[k][1]), 1024, 1, P(br), P(bi), P(ys[k][0]), P(ys[k][1]),
+                                                   1024, st)), S)
+    rec("c5a_complex_linear_8192x1024x1024", t, 8.0 * 8192 * 1024 * 1024, nbytes, kind="mfma", sets=S)
+    del xs, ws, ys
     # C5b: DFT-as-GEMM, 65536 x N=256 forward, and the same shape on the Stockham kernel
     nbytes = 4 * 65536 * 256 * 4
     S = _n_sets(nbytes)

@@ -57,18 +57,32 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
   for (int i = threadIdx.x; i < NFFT; i += THREADS) wl[i] = win[i];
   // 1. stage bins: region of pair p = [re_a | im_a | re_b | im_b], F floats each
   const size_t sbase = (size_t)b * F * n_frames + ta;
-  for (int i = threadIdx.x; i < F * FR; i += THREADS) {
+  // every load of the tile is issued before the first LDS write (a load-then-store loop would
+  // wait out the full memory latency once per iteration)
+  constexpr int SI = (F * FR + THREADS - 1) / THREADS;
+  float sr[SI], si[SI];
+#pragma unroll
+  for (int it = 0; it < SI; ++it) {
+    const int i = (int)threadIdx.x + it * THREADS;
     const int f = i % FR, k = i / FR;
-    float re = 0.0f, im = 0.0f;
-    if (f < nf) {
+    sr[it] = 0.0f;
+    si[it] = 0.0f;
+    if (i < F * FR && f < nf) {
       // plain loads: a bin row segment is FR frames (64 bytes at n_fft 512), so a cache line is
       // shared with the neighbouring tile, which then finds it in L2 (measured 4 % faster)
-      re = sre[sbase + (size_t)k * n_frames + f];
-      im = sim[sbase + (size_t)k * n_frames + f];
+      sr[it] = sre[sbase + (size_t)k * n_frames + f];
+      si[it] = sim[sbase + (size_t)k * n_frames + f];
     }
-    float* reg = lds + (f >> 1) * RP + (f & 1) * 2 * F;
-    reg[k] = re;
-    reg[F + k] = (k == 0 || k == NFFT / 2) ? 0.0f : im;
+  }
+#pragma unroll
+  for (int it = 0; it < SI; ++it) {
+    const int i = (int)threadIdx.x + it * THREADS;
+    const int f = i % FR, k = i / FR;
+    if (i < F * FR) {
+      float* reg = lds + (f >> 1) * RP + (f & 1) * 2 * F;
+      reg[k] = sr[it];
+      reg[F + k] = (k == 0 || k == NFFT / 2) ? 0.0f : si[it];
+    }
   }
   __syncthreads();
   // 2. one complex inverse transform per frame pair
@@ -101,6 +115,40 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
   const int s_hi = (t0 + owned >= n_frames || s_end > expected_len) ? expected_len : (int)s_end;
   float* dst = out + (size_t)b * out_pitch;
   const int t_end = ta + nf - 1;
+  if (THREADS % hop == 0 && halo < 4 && t0 >= halo && t0 + owned < n_frames && s_end <= expected_len) {
+    // interior tile (every owned sample has all its covering frames in the tile) and a hop that
+    // divides the thread count: each thread keeps one phase r = s mod hop, so its covering frames
+    // t, t-1, ... meet it at the fixed offsets r, r + hop, ... of their windows; the window
+    // values and the envelope (summed in the same order as below) are computed once per thread
+    // and the envelope division becomes one reciprocal per thread
+    const int r = (int)threadIdx.x % hop;
+    const int tstep = THREADS / hop;
+    const int nc = (NFFT - 1 - r) / hop + 1;  // covering frames of phase r (<= halo + 1 <= 4)
+    float wv[4], env = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      wv[m] = m < nc ? wl[r + m * hop] : 0.0f;
+      if (m < nc) env += wv[m] * wv[m];
+    }
+    const bool norm = env > 1e-8f;
+    const float inv = 1.0f / env;
+    for (int t = t0 + (int)threadIdx.x / hop; t < t0 + owned; t += tstep) {
+      const int o = t * hop + r - (int)start;
+      if (o < 0 || o >= write_len) continue;
+      float acc = 0.0f, raw = 0.0f;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m < nc) {
+          const int f = t - m - ta;
+          const float x = lds[(f >> 1) * RP + (f & 1) * NFFT + r + m * hop];
+          acc += x * wv[m];
+          raw += x;
+        }
+      }
+      dst[o] = norm ? acc * inv : raw;
+    }
+    return;  // not the last tile: no zero fill
+  }
   for (int s = s_lo + (int)threadIdx.x; s < s_hi; s += THREADS) {
     const int o = s - start;
     if (o < 0 || o >= write_len) continue;

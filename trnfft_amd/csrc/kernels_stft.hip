@@ -67,13 +67,27 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS, E_>::THREADS)) void stft_kern
     // 1. stage the span (block-uniform branch)
     if (start >= 0 && start + span <= length && ((reinterpret_cast<size_t>(x + start) & 15) == 0)) {
       const float4* src = reinterpret_cast<const float4*>(x + start);
-      for (int q = threadIdx.x; q < span / 4; q += THREADS) {
-        const float4 s4 = ld_stream4(src + q);
-        const int a = stage_pad(4 * q);  // 4q % 32 <= 28: the 4 words share one pad period
-        lds[a] = s4.x;
-        lds[a + 1] = s4.y;
-        lds[a + 2] = s4.z;
-        lds[a + 3] = s4.w;
+      // three float4 loads in flight per thread before the LDS writes (a load-then-store loop waits
+      // out the memory latency once per iteration): n_fft 256 64.8 -> 61.7 us, 1024 75.0 -> 73.4
+      constexpr int U = 3;
+      for (int q0 = threadIdx.x; q0 < span / 4; q0 += U * THREADS) {
+        float4 s4[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int q = q0 + u * THREADS;
+          if (q < span / 4) s4[u] = ld_stream4(src + q);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int q = q0 + u * THREADS;
+          if (q < span / 4) {
+            const int a = stage_pad(4 * q);  // 4q % 32 <= 28: the 4 words share one pad period
+            lds[a] = s4[u].x;
+            lds[a + 1] = s4[u].y;
+            lds[a + 2] = s4[u].z;
+            lds[a + 3] = s4[u].w;
+          }
+        }
       }
       for (int i = (span / 4) * 4 + threadIdx.x; i < span; i += THREADS) lds[stage_pad(i)] = x[start + i];
     } else {
