@@ -71,7 +71,8 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
       const float2 c = i < n ? chirp[i] : make_float2(0.0f, 0.0f);
       if constexpr (PRE) ch[PRE ? e : 0] = c;
       if (valid && i < n) {
-        const float2 x = make_float2(in_re[base + i], REAL_IN ? 0.0f : in_im[base + i]);
+        // non-temporal: every row is read and written once (C3b 18.4 -> 17.3 us, C3a 12.0 -> 11.4)
+        const float2 x = make_float2(ld_stream(in_re + base + i), REAL_IN ? 0.0f : ld_stream(in_im + base + i));
         y = cmul(x, c);
       }
     }
@@ -97,8 +98,8 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
       const int i = tid + T * e;
       if (i < n) {
         const float2 y = cmul(v[e], PRE ? ch[PRE ? e : 0] : PRE2 ? ch2[PRE2 ? e : 0] : chirp[i]);
-        out_re[base + i] = y.x * scale;
-        out_im[base + i] = y.y * scale;
+        st_stream(out_re + base + i, y.x * scale);
+        st_stream(out_im + base + i, y.y * scale);
       }
     }
   }

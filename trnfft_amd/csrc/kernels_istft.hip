@@ -145,7 +145,7 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
           raw += x;
         }
       }
-      dst[o] = norm ? acc * inv : raw;
+      st_stream(dst + o, norm ? acc * inv : raw);  // non-temporal: whole output rows (C2 inverse 41.5 -> 38.6 us)
     }
     return;  // not the last tile: no zero fill
   }
