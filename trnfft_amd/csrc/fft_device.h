@@ -236,9 +236,7 @@ struct LdsFft {
   static constexpr LdsShape S = make_shape(N, E);
   static constexpr int T = N / E;
   static_assert(!DB || (IL && !SPLIT && !WAVE_LOCAL), "double buffering is for the interleaved workgroup exchange");
-  static constexpr int PADP = lds_pad_period(N, E);  // LDS pad period (16 for power-of-two shapes)
-  static constexpr int DBOFF = 2 * lds_entries(N, E);  // floats between the two buffers
-  __device__ __forceinline__ static int pad(int i) { return lds_pad_p(i, PADP); }
+  static constexpr int DBOFF = 2 * lds_pad(N);  // floats between the two buffers
   static constexpr int TQ = PF ? (E / 2 > 0 ? E / 2 : 1) : 1;  // float4 twiddles per thread per pass
 
   template <int P>
@@ -253,7 +251,7 @@ struct LdsFft {
       constexpr bool LAST = (P == S.npass - 1);
       // the pass's LDS write index is linear in u when the radix (first pass) or the span LS
       // (later passes) is a multiple of the 16-word padding period
-      constexpr bool LIN_W = (LS == 1) ? (R % PADP == 0) : (LS % PADP == 0);
+      constexpr bool LIN_W = (LS == 1) ? (R % 16 == 0) : (LS % 16 == 0);
       float2 w[NB][R];
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
@@ -319,10 +317,10 @@ struct LdsFft {
                                                     int which) {
     if constexpr (LIN_W) {
       // padded index = base + compile-time offset per u (immediate-offset LDS stores)
-      const int base = LS == 1 ? j * (R + R / PADP) : pad((j - k) * R) + k + (int)((unsigned)k / (unsigned)PADP);
+      const int base = LS == 1 ? j * (R + R / 16) : lds_pad((j - k) * R) + k + (k >> 4);
 #pragma unroll
       for (int u = 0; u < R; ++u) {
-        const int off = LS == 1 ? u + u / PADP : u * (LS + LS / PADP);
+        const int off = LS == 1 ? u + (u >> 4) : u * (LS + LS / 16);
         if (which == 3) {
           reinterpret_cast<float2*>(a)[base + off] = w[u];
         } else if (which == 2) {
@@ -336,7 +334,7 @@ struct LdsFft {
       const int base = (j - k) * R + k;
 #pragma unroll
       for (int u = 0; u < R; ++u) {
-        const int idx = pad(base + u * LS);
+        const int idx = lds_pad(base + u * LS);
         if (which == 3) {
           reinterpret_cast<float2*>(a)[idx] = w[u];
         } else if (which == 2) {
@@ -351,11 +349,11 @@ struct LdsFft {
 
   __device__ __forceinline__ static void load_pass(float2 (&v)[E], const float* a, const float* b, int tid,
                                                    int which) {
-    if constexpr (T % PADP == 0) {
-      const int rb = tid + (int)((unsigned)tid / (unsigned)PADP);
+    if constexpr (T % 16 == 0) {
+      const int rb = tid + (tid >> 4);
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        const int idx = rb + e * (T + T / PADP);
+        const int idx = rb + e * (T + T / 16);
         if (which == 3) v[e] = reinterpret_cast<const float2*>(a)[idx];
         else if (which == 2) v[e] = make_float2(a[idx], b[idx]);
         else if (which == 0) v[e].x = a[idx];
@@ -364,7 +362,7 @@ struct LdsFft {
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        const int idx = pad(tid + T * e);
+        const int idx = lds_pad(tid + T * e);
         if (which == 3) v[e] = reinterpret_cast<const float2*>(a)[idx];
         else if (which == 2) v[e] = make_float2(a[idx], b[idx]);
         else if (which == 0) v[e].x = a[idx];

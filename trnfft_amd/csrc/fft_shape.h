@@ -167,16 +167,6 @@ __host__ __device__ constexpr LdsShape make_shape(int n, int e) {
 // LDS word index with one pad word per 16 to keep the strided pass writes bank-conflict free.
 __host__ __device__ constexpr int lds_pad(int i) { return i + (i >> 4); }
 
-// Pad period of the LDS exchange of the (n, e) Stockham shape: 16 for power-of-two radices; for a
-// shape that starts with a radix divisible by 3 (mixed-radix lengths) the first radix R0, so the
-// first pass's stride-R0 writes land on stride R0 + 1 entries, the second pass's runs of R0
-// consecutive entries (when its span is R0) stay contiguous across 16 lanes, and the later passes
-// write near-contiguous runs.
-__host__ __device__ constexpr int lds_pad_period(int n, int e) {
-  return (make_shape(n, e).radix[0] % 3 == 0) ? make_shape(n, e).radix[0] : 16;
-}
-__host__ __device__ constexpr int lds_pad_p(int i, int period) { return i + (int)((unsigned)i / (unsigned)period); }
-// LDS entries (float2 when interleaved) one transform of the (n, e) shape occupies
-__host__ __device__ constexpr int lds_entries(int n, int e) { return lds_pad_p(n, lds_pad_period(n, e)); }
+
 
 }  // namespace tfa

@@ -29,7 +29,7 @@ struct BlueCfg {
   static constexpr int T = M / E;
   static constexpr int XF = T >= THR ? 1 : THR / T;
   static constexpr int THREADS = XF * T;
-  static constexpr int PADN = lds_entries(M, E_) > 1 ? lds_entries(M, E_) : 1;
+  static constexpr int PADN = lds_pad(M) > 1 ? lds_pad(M) : 1;
   static constexpr bool DB = blue_db(M) && T > 64;  // double-buffered exchange (two LDS buffers per row)
   static constexpr int NBUF = DB ? 2 : 1;
 };
