@@ -340,12 +340,15 @@ __global__ __launch_bounds__((FourStepCfg<N1, TILE_>::THREADS)) void fourstep_co
       const int idx = (w / CK) * PADN +
                       (CK % 16 == 0 ? lds_pad(kk) + kb * (CK + CK / 16) : lds_pad(kb * CK + kk));
       const size_t o = obase + (size_t)(threadIdx.x / RUN) * stride * CK + w + (size_t)(RPI * i) * stride * CK;
+      // plain stores (and plain loads in the row pass): the workspace is written and read once
+      // within one transform and stays in the Infinity Cache between the passes when it fits
+      // (16 x 2^20: 128 MB; C4b 121.9 -> 106.4 us against streaming accesses)
       if constexpr (SPLIT) {
-        st_stream((plane ? out_im : out_re) + o, lre[idx]);
+        (plane ? out_im : out_re)[o] = lre[idx];
       } else {
         const float2 y = lds[idx];
-        st_stream(out_re + o, y.x);
-        st_stream(out_im + o, y.y);
+        out_re[o] = y.x;
+        out_im[o] = y.y;
       }
     }
     if (SPLIT && plane == 0) __syncthreads();
@@ -373,7 +376,7 @@ __global__ __launch_bounds__((FourStepCfg<N2, TILE_>::THREADS)) void fourstep_ro
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const size_t i = ibase + (size_t)e * (T * CK);
-    v[e] = make_float2(ld_stream(t_re + i), ld_stream(t_im + i));
+    v[e] = make_float2(t_re[i], t_im[i]);
   }
   if constexpr (SPLIT)
     LdsFft<N2, E, DIR, false, true>::run(v, lre + r * PADN, nullptr, tw, t);
