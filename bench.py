@@ -257,33 +257,28 @@ def _n_sets(set_bytes: int) -> int:
     return max(1, math.ceil(ROTATE_BYTES / set_bytes))
 
 
-def _time_rot(fn, n_sets: int, reps: int = 30, warm: int = 3) -> float:
+def _time_rot(fn, n_sets: int, reps: int = 100, warm: int = 3) -> float:
     """Average launch duration of fn(k, stream) over `reps` back-to-back launches (k = buffer set
-    k % n_sets), captured once into a HIP graph and timed with HIP events around one replay, so
-    host launch overhead neither adds to nor starves the timed kernels."""
+    k % n_sets) on the current stream, HIP events around the region, synchronize on both sides;
+    median of three regions.  Eager launches: the host enqueues faster than these kernels run,
+    so the region is the kernels' own time (a captured graph adds ~100 us per replay)."""
     cur = torch.cuda.current_stream()
+    h = ctypes.c_void_p(cur.cuda_stream)
     for k in range(warm):
-        fn(k % n_sets, ctypes.c_void_p(cur.cuda_stream))
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream()
-    cap.wait_stream(cur)
-    with torch.cuda.stream(cap):
-        with torch.cuda.graph(graph, stream=cap):
-            h = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-            for k in range(reps):
-                fn(k % n_sets, h)
-    cur.wait_stream(cap)
-    graph.replay()
+        fn(k % n_sets, h)
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    graph.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    del graph
-    return ev0.elapsed_time(ev1) * 1e-3 / reps
+    regions = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        ev0.record()
+        for k in range(reps):
+            fn(k % n_sets, h)
+        ev1.record()
+        torch.cuda.synchronize()
+        regions.append(ev0.elapsed_time(ev1) * 1e-3 / reps)
+    return _median(regions)
 
 
 def bench_secondary():
@@ -360,7 +355,7 @@ def bench_secondary():
     pl = native_plan(_lib.KIND_C2C, 1 << 20, False, dev.index)
     ws = torch.empty(pl.workspace_bytes(16) // 4, device=dev)
     t = _time_rot(lambda k, st: chk(L.tfa_execute(pl.handle, 16, P(ins[k][0]), P(ins[k][1]), P(outs[k][0]),
-                                              P(outs[k][1]), P(ws), st)), S, reps=20)
+                                              P(outs[k][1]), P(ws), st)), S)
     rec("c4b_fourstep_16x2^20", t, flops_fft(1 << 20, 16), nbytes, sets=S,
         note="two HBM passes; algorithmic bytes = one read + one write")
     del ins, outs, ws
@@ -370,7 +365,7 @@ def bench_secondary():
     yr = torch.empty_like(img)
     yi = torch.empty_like(img)
     pl = native_plan(_lib.KIND_FFT2, 2048, False, dev.index, n2=2048)
-    t = _time_rot(lambda k, st: chk(L.tfa_execute(pl.handle, 32, P(img), None, P(yr), P(yi), None, st)), 1, reps=5, warm=1)
+    t = _time_rot(lambda k, st: chk(L.tfa_execute(pl.handle, 32, P(img), None, P(yr), P(yi), None, st)), 1, reps=30, warm=1)
     rec("c4a_fft2_32x2048x2048", t, 32 * 5 * 2048 * 2048 * 22, 32 * 2048 * 2048 * (4 + 8), sets=1,
         note="two HBM passes; algorithmic bytes = real read + complex write")
     del img, yr, yi
