@@ -60,6 +60,10 @@ __host__ __device__ constexpr int stft_epth(int n) { return n < 8 ? n : 8; }
 // next-pass twiddle prefetch in the STFT transforms from n_fft = 1024 (8 or fewer pairs per
 // workgroup: n_fft 1024 84 -> 77 us; at 512 it measured 1 % slower)
 __host__ __device__ constexpr bool stft_pf(int n) { return n >= 1024; }
+// Dynamic LDS (bytes, unused by the kernel) added to the STFT launch to hold it to one 1024-thread
+// workgroup per CU: at n_fft = 512 (64 x 160000 samples, hop 256) one workgroup per CU measured
+// 39.5 us against 43.3 us for two (the output's bin-row segments reach HBM in a better order).
+__host__ __device__ constexpr unsigned stft_lds_extra(int n) { return n == 512 ? 16384u : 0u; }
 
 // Elements per thread of the 2-D transform's paired real-row pass 1 and column pass 2 (the
 // many-lanes-per-transform shape that also won for the STFT).

@@ -5,52 +5,55 @@
 // The frames are real, so two of them share one complex transform: z = w*x_a + i*w*x_b gives
 // X_a[k] = (Z[k] + conj(Z[n-k])) / 2 and X_b[k] = (Z[k] - conj(Z[n-k])) / (2i).
 // One workgroup takes FR consecutive frames of one signal (FR/2 complex LDS transforms):
-//   1. the samples the tile covers ((FR-1)*hop + n_fft, reflect-padded at the signal edges) are
-//      staged into LDS with wide coalesced loads, the window too;
-//   2. each frame pair is windowed out of LDS and transformed (LDS Stockham);
-//   3. the spectra go to LDS; the two real spectra are separated there while lanes run over
-//      consecutive frames, so every store instruction writes FR contiguous floats of one bin row
-//      of the (batch, bins, frames) output.
+//   1. the threads of each frame pair load the pair's two frames straight from the waveform
+//      (coalesced runs of consecutive samples, reflect padding at the signal edges) and window them;
+//      the half-hop overlap between neighbouring frames is served by L2;
+//   2. each pair is transformed (LDS Stockham; one wavefront per pair at n_fft = 512);
+//   3. each pair stores its spectrum as packed entries (Z[k], Z[n-k]), k <= n/2, one float4 each;
+//      lanes then run over consecutive frames and read one entry per output bin, so every store
+//      instruction writes FR contiguous floats of bin rows of the (batch, bins, frames) output.
+// The window is pre-scaled by scale/2 (the 1/2 of the pair separation, and the normalisation), so
+// the separation is two additions per output value.
 #include "kernels.h"
 
 namespace tfa {
 
-// Launch shape from a sweep on MI355X (64 waveforms x 160000 samples, hop n_fft/2, buffers
-// rotated past the Infinity Cache, n_fft 64..4096): E = 8 elements per thread (many lanes per
-// transform) is fastest at every length, with 8192/n_fft frame pairs per workgroup (~70 KB of LDS,
-// two workgroups per CU, 256..1024 threads); stft_epth (fft_shape.h) gives E.
+// Frame pairs per workgroup: 8192 / n_fft (1024 threads from n_fft = 256 up), between 2 and 32.
 template <int NFFT>
-constexpr int stft_default_pairs() {
+constexpr int stft_pairs() {
   constexpr int p = 8192 / NFFT;
   return p < 2 ? 2 : p > 32 ? 32 : p;
 }
-template <int NFFT, int PAIRS_ = stft_default_pairs<NFFT>(), int E_ = stft_epth(NFFT)>
+// Floats of LDS per frame pair: the interleaved exchange area of the transform, which also holds
+// the packed spectrum (4 * (n/2 + 1) floats) afterwards; a multiple of 4 floats (float4 entries)
+// that is 4 more than a multiple of 64, so the pair regions start on successive bank quads.
+constexpr int stft_area(int n) {
+  int a = (2 * (lds_pad(n) + 1) + 3) / 4 * 4;
+  while (a % 64 != 4) a += 4;
+  return a;
+}
+
+template <int NFFT>
 struct StftCfg {
-  static constexpr int E = E_;
-  static constexpr int T = NFFT / E;
-  static constexpr int PADN = lds_pad(NFFT) + 1;  // odd pitch: pair regions start on different banks
-  static constexpr int PAIRS = PAIRS_;             // complex transforms per workgroup
-  static constexpr int FR = 2 * PAIRS;             // frames per workgroup
+  static constexpr int E = stft_epth(NFFT);
+  static constexpr int T = NFFT / E;  // threads per frame pair
+  static constexpr int PAIRS = stft_pairs<NFFT>();
+  static constexpr int FR = 2 * PAIRS;  // frames per workgroup
   static constexpr int THREADS = PAIRS * T;
-  static constexpr int LDSF = 2 * PAIRS * PADN;  // floats of the spectra area (also the staging area)
-  // the spectra are interleaved (re, im) float2 entries: PADN per pair
-  static_assert((long long)LDSF * 4 + NFFT * 4 <= kLdsBytes, "STFT tile exceeds LDS");
-  static_assert(THREADS > 0 && (FR & (FR - 1)) == 0, "frame tile must be a power of two");
+  static constexpr int AREA = stft_area(NFFT);
+  static constexpr int NB1 = NFFT / 2 + 1;  // onesided bins = packed entries per pair
+  static_assert(PAIRS * AREA * 4 <= kLdsBytes, "STFT tile exceeds LDS");
+  static_assert(THREADS % FR == 0, "the output stage maps lanes to (bin, frame)");
 };
 
-// staging-area word of sample i of the tile span (one pad word per 32 spreads frame starts over banks)
-__device__ __forceinline__ int stage_pad(int i) { return i + (i >> 5); }
-
-template <int NFFT, int PAIRS = stft_default_pairs<NFFT>(), int E_ = stft_epth(NFFT)>
-__global__ __launch_bounds__((StftCfg<NFFT, PAIRS, E_>::THREADS)) void stft_kernel(
+template <int NFFT>
+__global__ __launch_bounds__((StftCfg<NFFT>::THREADS)) void stft_kernel(
     const float* __restrict__ sig, const float* __restrict__ win, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ tw, int length, int hop, int pad,
-    int n_frames, int n_bins, int tiles_per_signal, float scale) {
-  using C = StftCfg<NFFT, PAIRS, E_>;
-  constexpr int E = C::E, T = C::T, FR = C::FR, PADN = C::PADN, THREADS = C::THREADS;
-  __shared__ float2 lds2[C::LDSF / 2];
-  __shared__ float wl[NFFT];
-  float* lds = reinterpret_cast<float*>(lds2);
+    int n_frames, int n_bins, int tiles_per_signal, float hs) {
+  using C = StftCfg<NFFT>;
+  constexpr int E = C::E, T = C::T, FR = C::FR, AREA = C::AREA, THREADS = C::THREADS, NB1 = C::NB1;
+  __shared__ __attribute__((aligned(16))) float lds[C::PAIRS * AREA];
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
   const long long b = tile / tiles_per_signal;
   const int f0 = (int)(tile % tiles_per_signal) * FR;
@@ -58,102 +61,95 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS, E_>::THREADS)) void stft_kern
   const int pl = threadIdx.x / T;
   const int fa = f0 + 2 * pl;  // frames fa (real part) and fa + 1 (imaginary part)
   const float* x = sig + (size_t)b * length;
-
-  for (int i = threadIdx.x; i < NFFT; i += THREADS) wl[i] = win[i];
   const int start = f0 * hop - pad;  // padded-signal origin of the tile's first frame
   const int span = (FR - 1) * hop + NFFT;
+  float wv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) wv[e] = win[tid + T * e] * hs;
   float2 v[E];
-  if (stage_pad(span) <= C::LDSF) {
-    // 1. stage the span (block-uniform branch)
-    if (start >= 0 && start + span <= length && ((reinterpret_cast<size_t>(x + start) & 15) == 0)) {
-      const float4* src = reinterpret_cast<const float4*>(x + start);
-      // three float4 loads in flight per thread before the LDS writes (a load-then-store loop waits
-      // out the memory latency once per iteration): n_fft 256 64.8 -> 61.7 us, 1024 75.0 -> 73.4
-      constexpr int U = 3;
-      for (int q0 = threadIdx.x; q0 < span / 4; q0 += U * THREADS) {
-        float4 s4[U];
+  if (start >= 0 && start + span <= length) {  // block-uniform: no padding inside the tile
+    const float* p0 = x + (start + 2 * pl * hop) + tid;
+    const float* p1 = p0 + hop;
+    float a[E], c[E];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int q = q0 + u * THREADS;
-          if (q < span / 4) s4[u] = ld_stream4(src + q);
-        }
+    for (int e = 0; e < E; ++e) a[e] = ld_stream(p0 + T * e);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int q = q0 + u * THREADS;
-          if (q < span / 4) {
-            const int a = stage_pad(4 * q);  // 4q % 32 <= 28: the 4 words share one pad period
-            lds[a] = s4[u].x;
-            lds[a + 1] = s4[u].y;
-            lds[a + 2] = s4[u].z;
-            lds[a + 3] = s4[u].w;
-          }
-        }
-      }
-      for (int i = (span / 4) * 4 + threadIdx.x; i < span; i += THREADS) lds[stage_pad(i)] = x[start + i];
-    } else {
-      for (int i = threadIdx.x; i < span; i += THREADS) {
-        int idx = start + i;
+    for (int e = 0; e < E; ++e) c[e] = ld_stream(p1 + T * e);
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = make_float2(a[e] * wv[e], c[e] * wv[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int j = tid + T * e;
+      float s[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int idx = (fa + h) * hop + j - pad;
         // reflect without repeating the edge sample (torch.nn.functional.pad mode="reflect");
         // positions that only frames past the end would read are clamped (never stored)
         idx = idx < 0 ? -idx : idx;
         idx = idx >= length ? 2 * (length - 1) - idx : idx;
         idx = idx < 0 ? 0 : (idx >= length ? length - 1 : idx);
-        lds[stage_pad(i)] = x[idx];
-      }
-    }
-    __syncthreads();
-    // 2. window the pair's two frames out of LDS
-    const int oa = 2 * pl * hop;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int j = tid + T * e;
-      const float w = wl[j];
-      v[e] = make_float2(lds[stage_pad(oa + j)] * w, lds[stage_pad(oa + hop + j)] * w);
-    }
-    __syncthreads();  // the transform below reuses the staging area
-  } else {
-    // span too long for LDS (hop much larger than n_fft): per-frame loads
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const int j = tid + T * e;
-      const float w = win[j];
-      float s[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        int idx = (fa + h) * hop + j - pad;
-        idx = idx < 0 ? -idx : idx;
-        idx = idx >= length ? 2 * (length - 1) - idx : idx;
-        idx = idx < 0 ? 0 : (idx >= length ? length - 1 : idx);
-        s[h] = x[idx] * w;
+        s[h] = x[idx] * wv[e];
       }
       v[e] = make_float2(s[0], s[1]);
     }
   }
-  float2* my = lds2 + pl * PADN;
-  LdsFft<NFFT, E, -1, (T <= 64), false, true, stft_pf(NFFT)>::run(v, reinterpret_cast<float*>(my), nullptr, tw, tid);
+  float* my = lds + pl * AREA;
+  LdsFft<NFFT, E, -1, (T <= 64), false, true, stft_pf(NFFT)>::run(v, my, nullptr, tw, tid);
+  // a transform spread over several wavefronts may still be reading its last exchange
+  if constexpr (T > 64) __syncthreads();
+  // packed spectrum: entry k (0..n/2) = (Z[k], Z[n-k mod n]) as one float4
+  float2* sp = reinterpret_cast<float2*>(my);
 #pragma unroll
-  for (int e = 0; e < E; ++e) my[lds_pad(tid + T * e)] = v[e];
+  for (int e = 0; e < E; ++e) {
+    const int k = tid + T * e;
+    if (e < E / 2) sp[2 * k] = v[e];              // k < n/2: first half of entry k
+    else sp[2 * (NFFT - k) + 1] = v[e];           // k >= n/2: second half of entry n - k
+  }
+  if (tid == 0) {
+    sp[1] = v[0];                  // entry 0: Z[n - 0 mod n] = Z[0]
+    sp[2 * (NFFT / 2)] = v[E / 2]; // entry n/2: Z[n/2] in both halves
+  }
   __syncthreads();
-  // 3. lanes over consecutive frames fr: frame fr = 2p (+1) is the real (imaginary) part of pair p.
-  //    Flat loop over (bin, frame) so any FR / THREADS ratio is covered; every iteration advances.
-  const float hs = 0.5f * scale;
+  // lanes over consecutive frames fr: frame fr = 2p (+1) is the real (imaginary) part of pair p
+  constexpr int KS = THREADS / FR;  // bins per step
+  const int fr = threadIdx.x % FR;
+  const int kb = threadIdx.x / FR;
+  if (f0 + fr >= n_frames) return;
+  const float* pbase = lds + (fr >> 1) * AREA;
+  const bool odd = fr & 1;
   const size_t ob = (size_t)b * n_bins * n_frames + f0;
-  const int total = n_bins * FR;
-  for (int i = threadIdx.x; i < total; i += THREADS) {
-    const int fr = i % FR;
-    const int k = i / FR;
-    if (f0 + fr >= n_frames) continue;
-    const float2* zp = lds2 + (fr >> 1) * PADN;
-    const float2 z = zp[lds_pad(k)], y = zp[lds_pad((NFFT - k) & (NFFT - 1))];
-    const float zr = z.x, zi = z.y, yr = y.x, yi = y.y;
-    const bool odd = fr & 1;
-    const float re = odd ? (zi + yi) : (zr + yr);
-    const float im = odd ? (yr - zr) : (zi - yi);
-    const size_t o = ob + (size_t)k * n_frames + fr;
-    // plain (not streaming) stores: a workgroup's row segments rarely start on a cache line,
-    // and L2 merges the partial lines the neighbouring workgroups write (measured 1.4x faster)
-    out_re[o] = re * hs;
-    out_im[o] = im * hs;
+  // byte offsets from the wave-uniform row bases (scalar base + 32-bit vector offset stores)
+  char* bre = reinterpret_cast<char*>(out_re + ob);
+  char* bim = reinterpret_cast<char*>(out_im + ob);
+  if (n_bins == NB1) {
+    const float4* e4 = reinterpret_cast<const float4*>(pbase) + kb;
+    unsigned off = (unsigned)(fr + kb * n_frames) * 4u;
+    const unsigned step = (unsigned)(KS * n_frames) * 4u;
+#pragma unroll
+    for (int i = 0; i < (NB1 + KS - 1) / KS; ++i) {
+      if (kb + KS * i < NB1) {
+        const float4 q = e4[KS * i];  // (zr, zi, yr, yi) = (Z[k], Z[n-k])
+        const float re = odd ? (q.y + q.w) : (q.x + q.z);
+        const float im = odd ? (q.z - q.x) : (q.y - q.w);
+        *reinterpret_cast<float*>(bre + off) = re;
+        *reinterpret_cast<float*>(bim + off) = im;
+      }
+      off += step;
+    }
+  } else {
+    // two-sided: bins above n/2 read entry n - k with its halves swapped
+    for (int k = kb; k < n_bins; k += KS) {
+      const bool hi = k > NFFT / 2;
+      const float4 q = reinterpret_cast<const float4*>(pbase)[hi ? NFFT - k : k];
+      const float zr = hi ? q.z : q.x, zi = hi ? q.w : q.y, yr = hi ? q.x : q.z, yi = hi ? q.y : q.w;
+      const float re = odd ? (zi + yi) : (zr + yr);
+      const float im = odd ? (yr - zr) : (zi - yi);
+      const unsigned o = (unsigned)(fr + k * n_frames) * 4u;
+      *reinterpret_cast<float*>(bre + o) = re;
+      *reinterpret_cast<float*>(bim + o) = im;
+    }
   }
 }
 
@@ -162,8 +158,11 @@ static hipError_t launch_stft_n(const StftArgs& a) {
   using C = StftCfg<NFFT>;
   const int tiles = (a.n_frames + C::FR - 1) / C::FR;
   const long long blocks = a.batch * (long long)tiles;
-  hipLaunchKernelGGL((stft_kernel<NFFT>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream, a.signal, a.window,
-                     a.out_re, a.out_im, a.tw, a.length, a.hop, a.pad, a.n_frames, a.n_bins, tiles, a.scale);
+  // stft_lds_extra: unused dynamic LDS that holds the workgroups resident per CU to one where that
+  // measured faster
+  hipLaunchKernelGGL((stft_kernel<NFFT>), dim3((unsigned)blocks), dim3(C::THREADS), stft_lds_extra(NFFT), a.stream,
+                     a.signal, a.window, a.out_re, a.out_im, a.tw, a.length, a.hop, a.pad, a.n_frames, a.n_bins, tiles,
+                     0.5f * a.scale);
   return hipGetLastError();
 }
 
