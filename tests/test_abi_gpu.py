@@ -97,11 +97,12 @@ def test_gemm_ex_argument_checks():
 def test_bluestein_split_needs_workspace():
     lib = _lib.lib()
     st = VP(torch.cuda.current_stream().cuda_stream)
-    rc, p = _plan(_lib.KIND_BLUESTEIN, 8193)  # m = 32768: split path only
+    # m = 32768: split path only (n = 8193..8200 wrap the fused kernel's 16384-point convolution)
+    rc, p = _plan(_lib.KIND_BLUESTEIN, 8201)
     assert rc == 0
     size = ctypes.c_size_t()
     assert lib.tfa_plan_workspace_size(p, 2, ctypes.byref(size)) == 0 and size.value == 2 * 4 * 2 * 32768
-    x = torch.randn(2, 8193, device="cuda")
+    x = torch.randn(2, 8201, device="cuda")
     y = torch.empty_like(x)
     assert lib.tfa_execute(p, 2, P(x), P(x), P(y), P(y), None, st) == _lib.TFA_ERR_INVALID
     assert "workspace" in _err()

@@ -185,8 +185,9 @@ def test_bluestein_vs_reference_golden(direction):
 
 @pytest.mark.parametrize("n,batch", [(1000, 1024), (4099, 256), (3, 5), (17, 33), (8193, 4), (20000, 2),
                                      # the mixed-radix fused length 9216 = 12^2 * 64 covers
-                                     # 4096 < n <= 4608 (reference m = 16384); 4609 pads to 16384
-                                     (4097, 3), (4097, 300), (4608, 70), (4609, 70), (4609, 5),
+                                     # 4104 < n <= 4608 (reference m = 16384; 4097..4104 wrap at
+                                     # 8192); 4609 pads to 16384
+                                     (4097, 3), (4097, 300), (4200, 9), (4608, 70), (4609, 70), (4609, 5),
                                      # short rows (m <= 256, staged per workgroup): full tiles plus a
                                      # ragged one, every padded length 4..256 and real input below
                                      (2, 600), (5, 1000), (7, 257), (12, 300), (31, 513), (33, 129),
@@ -207,12 +208,47 @@ def test_bluestein_short_rows_real_input(n):
     assert rel_l2(X.real, X.imag, *ref) <= tol_bluestein(n)
 
 
+@pytest.mark.parametrize("n,batch", [(129, 300), (136, 64), (1025, 40), (1032, 7), (2049, 33), (2056, 3),
+                                     (4097, 256), (4099, 256), (4104, 5), (8193, 3), (8200, 20)])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_bluestein_wrapped_lengths_vs_oracle(n, batch, inverse):
+    # n = 2^k + 1 .. 2^k + 8: the fused kernel convolves circularly at 2^(k+1) < 2n - 1 and corrects
+    # the 2 * (2n - 1 - 2^(k+1)) outputs the wrapped filter taps reach (wrap 1 .. 15)
+    re, im = seeded_complex(batch, n, seed=n + 5)
+    got = _gpu_fft(re, im, inverse)
+    ref = oracle.fft_core(re, im, inverse)
+    assert rel_l2(*got, *ref) <= tol_bluestein(n), (n, inverse)
+    # the corrected outputs at both ends, against the exact DFT of the same rows (the fp32 chirp's
+    # deviation is spread over all bins, so the ends must not stand out from the rest)
+    x = re.double().numpy() + 1j * im.double().numpy()
+    exact = np.fft.ifft(x, axis=-1) if inverse else np.fft.fft(x, axis=-1)
+    g = got[0].double().numpy() + 1j * got[1].double().numpy()
+    ends = np.r_[0:16, n - 16:n]
+    e_ends = np.linalg.norm(g[:, ends] - exact[:, ends]) / np.linalg.norm(exact[:, ends])
+    e_all = np.linalg.norm(g - exact) / np.linalg.norm(exact)
+    assert e_ends <= 3 * e_all + 1e-6, (n, e_ends, e_all)
+
+
+@pytest.mark.parametrize("n", [1027, 4099])
+def test_bluestein_wrapped_real_input_and_strided_axis(n):
+    # real input through the wrapped fused kernel, and a strided axis (n = 1027: m = 4096 runs the
+    # strided-axis kernel at the reference's length while the contiguous rows wrap at 2048)
+    re, _ = seeded_complex(9, n, seed=3)
+    X = trnfft_amd.fft(re.cuda())
+    ref = oracle.fft_core(re, torch.zeros_like(re), False)
+    assert rel_l2(X.real, X.imag, *ref) <= tol_bluestein(n)
+    if n <= 4096:
+        xt = re.t().contiguous()  # (n, 9): transform along dim 0
+        Y = trnfft_amd.fftn(xt.cuda(), dim=(0,))
+        assert rel_l2(Y.real.t(), Y.imag.t(), *ref) <= tol_bluestein(n)
+
+
 @pytest.mark.parametrize("n", [4099, 6000])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_bluestein_fused_and_split_paths_agree(n, inverse):
     # n = 6000 (m = 16384) runs the fused one-row-per-workgroup kernel for large batches and the
-    # split three-pass path for small ones; n = 4099 runs the 9216-point fused kernel at every
-    # batch; rows must agree across batch sizes, and both are checked against the oracle
+    # split three-pass path for small ones; n = 4099 runs the wrapped 8192-point fused kernel at
+    # every batch; rows must agree across batch sizes, and both are checked against the oracle
     re, im = seeded_complex(2048, n, seed=11)
     fused = _gpu_fft(re, im, inverse)  # 2048 rows: fused kernel
     small = _gpu_fft(re[:5], im[:5], inverse)  # 5 rows: split path for n = 6000

@@ -70,7 +70,7 @@ def test_graph_replay_real_istft_and_split_bluestein():
     rows = torch.randn(64, 1024, generator=g0).cuda()
     bins = ComplexTensor(torch.randn(64, 513, generator=g0).cuda(), torch.randn(64, 513, generator=g0).cuda())
     spec = trnfft_amd.stft(torch.randn(3, 12000, generator=g0).cuda(), n_fft=512, hop_length=128)
-    few = ComplexTensor(torch.randn(3, 8193, generator=g0).cuda(), torch.randn(3, 8193, generator=g0).cuda())
+    few = ComplexTensor(torch.randn(3, 8201, generator=g0).cuda(), torch.randn(3, 8201, generator=g0).cuda())
 
     def ops():
         return (trnfft_amd.rfft(rows), trnfft_amd.irfft(bins), trnfft_amd.istft(spec, n_fft=512, hop_length=128),

@@ -221,3 +221,41 @@ def test_plan_cache_is_bounded_lru():
     del keep, extra
     P.clear_plan_cache()
     gc.collect()
+
+
+def _wrapped_bluestein(x, m, sign=-1):
+    """Bluestein at a circular length m < 2n - 1 with the colliding filter taps summed and the
+    outputs they reach corrected (the fused kernel's wrapped lengths), in float64."""
+    n = len(x)
+    d = 2 * n - 1 - m
+    k = np.arange(n)
+    chirp = np.exp(sign * 1j * np.pi * ((k * k) % (2 * n)) / n)
+    y = x * chirp
+    h = np.zeros(m, complex)
+    for i in range(n):
+        h[i] += np.conj(chirp[i])
+        if i > 0:
+            h[m - i] += np.conj(chirp[i])
+    yp = np.zeros(m, complex)
+    yp[:n] = y
+    conv = np.fft.ifft(np.fft.fft(yp) * np.fft.fft(h))[:n]
+    lo = n - d
+    yl, yh, ct = y[:d], y[lo:n], chirp[lo:n]
+    for i in range(min(d, n)):  # outputs k < d: extra taps from y[lo + c], c >= k
+        conv[i] -= sum(yh[c] * np.conj(ct[d - 1 + i - c]) for c in range(i, d))
+    for i in range(lo, n):  # outputs k >= n - d: extra taps from y[j], j <= k - lo
+        a = i - lo
+        conv[i] -= sum(yl[j] * np.conj(ct[d - 1 - a + j]) for j in range(a + 1))
+    return conv * chirp
+
+
+@pytest.mark.parametrize("n,m", [(3, 4), (5, 8), (7, 8), (65, 128), (72, 128), (129, 256), (4099, 8192),
+                                 (4104, 8192)])
+def test_wrapped_bluestein_correction_is_exact(n, m):
+    # the identity the fused kernel's wrapped lengths rely on, against numpy's DFT (float64);
+    # dropping either correction (or flipping a conjugate) leaves errors of order 1e-3 at the ends
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n) + 1j * rng.standard_normal(n)
+    got = _wrapped_bluestein(x, m)
+    ref = np.fft.fft(x)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-13

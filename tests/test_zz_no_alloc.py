@@ -42,7 +42,7 @@ def _run_both(plan, batch, n_in, n_out, seed):
 @pytest.mark.parametrize("kind,n,batches", [
     (_lib.KIND_C2C, 1 << 20, (6, 2)),     # four-step: 48 MiB then 16 MiB of scratch
     (_lib.KIND_C2C, 1 << 24, (1, 1)),     # 2^24 three-pass path: 128 MiB -> rejected (checked below)
-    (_lib.KIND_BLUESTEIN, 4099, (40, 3)),  # split Bluestein below 64 rows (m = 16384)
+    (_lib.KIND_BLUESTEIN, 6000, (40, 3)),  # split Bluestein below 64 rows (m = 16384)
     (_lib.KIND_BLUESTEIN, 20000, (4, 1)),  # split Bluestein, m = 65536
     (_lib.KIND_C2C, 1024, (64, 8)),       # no scratch: plain tfa_execute
 ])

@@ -105,6 +105,9 @@ __host__ __device__ constexpr bool blue_pf(int m) { return m >= 256; }
 // double-buffered LDS exchange in the fused kernel (one barrier per pass exchange) where two
 // buffers fit the CU's LDS: C3a (m = 2048) 12.8 -> 12.2 us; no change at m = 9216
 __host__ __device__ constexpr bool blue_db(int m) { return m % 3 == 0 || (m >= 1024 && m <= 8192); }
+// wrapped-convolution lengths of the fused kernel (power-of-two M = 2n - 1 - wrap, 1 <= wrap <= 15):
+// from 128 (16 threads per row, so the corrected outputs k < wrap are all in element 0)
+__host__ __device__ constexpr bool blue_wrap_ok(int m) { return m >= 128 && m <= 16384 && (m & (m - 1)) == 0; }
 // split Bluestein (m >= 32768, three passes): elements per thread of the column passes (length
 // m1; E = 8 at m1 = 128 measured no better) and next-pass twiddle prefetch in the column and row
 // passes (209 x 20000 147 -> 143 us, 59 x 70000 183 -> 178, 32 x 8193 26.9 -> 25.7; 511 x 8193

@@ -168,8 +168,14 @@ struct BluesteinArgs {
   long long batch;
   float scale;
   hipStream_t stream;
+  // wrapped convolution length (fused path): m = 2n - 1 - wrap < 2n - 1, 0 < wrap <= kBlueWrapMax;
+  // hs then holds the filter with its wrap colliding taps summed, and the kernel corrects the
+  // 2 * wrap outputs they reach
+  int wrap = 0;
 };
 hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a);
+// Largest wrap (2n - 1 - m) of the fused Bluestein kernel's wrapped-convolution lengths.
+constexpr int kBlueWrapMax = 15;
 
 // Bluestein down a strided axis (x viewed as (outer, n, stride)), m <= kMaxStridedBlueM.
 constexpr int kMaxStridedBlueM = 4096;

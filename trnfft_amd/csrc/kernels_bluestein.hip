@@ -34,20 +34,31 @@ struct BlueCfg {
   static constexpr int NBUF = DB ? 2 : 1;
 };
 
-template <int M, bool REAL_IN, int E_ = blue_epth(M), int THR = blue_threads(M)>
+// WRAP: the circular convolution length M is shorter than 2n - 1 by wrap = 2n - 1 - M
+// (1..kBlueWrapMax).  The filter taps t and t - M (t = M - n + 1 .. n - 1) then share a slot of the
+// filter (the plan sums them), which adds one extra term y[j] conj(chirp[M - k + j]) (j <= k - L,
+// L = n - wrap) to the outputs k >= L and y[j] conj(chirp[k - j + M]) (j >= k + L) to the outputs
+// k < wrap; both are subtracted after the inverse transform from the chirped input ends y[0, wrap),
+// y[L, n) and chirp[L, n), kept in LDS.  n then exceeds M/2 by at most 8, so one more element per
+// thread can hold a sample.
+template <int M, bool REAL_IN, bool WRAP = false, int E_ = blue_epth(M), int THR = blue_threads(M)>
 __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fused_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re,
     float* out_im, const float2* __restrict__ chirp, const float2* __restrict__ hs,
     const float2* __restrict__ tw_f, const float2* __restrict__ tw_i, int n, long long batch,
-    float scale) {
+    float scale, int wrap) {
   using C = BlueCfg<M, E_, THR>;
   constexpr int E = C::E, T = C::T;
+  static_assert(!WRAP || (T > kBlueWrapMax && E >= 2), "wrapped lengths: the corrected outputs are elements 0 and E/2");
   __shared__ float2 lds[C::XF * C::PADN * C::NBUF];  // interleaved (re, im) exchange
+  __shared__ float2 ends_all[WRAP ? C::XF * 3 * kBlueWrapMax : 1];  // per row: y[0, wrap), y[L, n), chirp[L, n)
   const int tid = threadIdx.x % T;
   const int xf = threadIdx.x / T;
   const long long b = (long long)blockIdx.x * C::XF + xf;
   const bool valid = b < batch;
   const size_t base = (size_t)b * n;
+  const int L = n - wrap;
+  float2* ends = ends_all + (WRAP ? xf * 3 * kBlueWrapMax : 0);
 
   // every workgroup of the launch runs the same phase at the same time, so nothing hides a
   // table load issued where it is used: with up to 8 elements per thread the chirp is loaded
@@ -58,7 +69,7 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   // n <= M/2 (M >= 2n - 1), so element e of a thread can hold a sample only for e < E/2: the
   // upper half of the forward input is zero at compile time and the upper half of the inverse
   // output is never needed (its last-pass arithmetic is dead code).
-  constexpr int EH = E / 2 > 0 ? E / 2 : 1;
+  constexpr int EH = (E / 2 > 0 ? E / 2 : 1) + (WRAP ? 1 : 0);
   constexpr bool PRE = E <= 8;
   constexpr bool PRE2 = E == 12;
   float2 v[E], ch[PRE ? EH : 1], hv[PRE || PRE2 ? E : 1];
@@ -74,6 +85,14 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
         // non-temporal: every row is read and written once (C3b 18.4 -> 17.3 us, C3a 12.0 -> 11.4)
         const float2 x = make_float2(ld_stream(in_re + base + i), REAL_IN ? 0.0f : ld_stream(in_im + base + i));
         y = cmul(x, c);
+      }
+      if constexpr (WRAP) {
+        // (read after the transforms, whose exchanges synchronise the workgroup)
+        if (i < wrap) ends[i] = y;
+        if (i >= L && i < n) {
+          ends[kBlueWrapMax + i - L] = y;
+          ends[2 * kBlueWrapMax + i - L] = c;
+        }
       }
     }
     v[e] = y;
@@ -97,7 +116,26 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
     for (int e = 0; e < EH; ++e) {
       const int i = tid + T * e;
       if (i < n) {
-        const float2 y = cmul(v[e], PRE ? ch[PRE ? e : 0] : PRE2 ? ch2[PRE2 ? e : 0] : chirp[i]);
+        float2 cv = v[e];
+        if constexpr (WRAP) {
+          const float2* yl = ends;
+          const float2* yh = ends + kBlueWrapMax;
+          const float2* ct = ends + 2 * kBlueWrapMax;
+          if (i < wrap) {  // extra terms y[L + c] conj(chirp[L + wrap - 1 + i - c]), c = i .. wrap-1
+            for (int c = i; c < wrap; ++c) {
+              const float2 t = ct[wrap - 1 + i - c];
+              cv = csub(cv, cmul(yh[c], make_float2(t.x, -t.y)));
+            }
+          }
+          if (i >= L) {  // extra terms y[j] conj(chirp[L + wrap - 1 - a + j]), j = 0 .. a, a = i - L
+            const int a = i - L;
+            for (int j = 0; j <= a; ++j) {
+              const float2 t = ct[wrap - 1 - a + j];
+              cv = csub(cv, cmul(yl[j], make_float2(t.x, -t.y)));
+            }
+          }
+        }
+        const float2 y = cmul(cv, PRE ? ch[PRE ? e : 0] : PRE2 ? ch2[PRE2 ? e : 0] : chirp[i]);
         st_stream(out_re + base + i, y.x * scale);
         st_stream(out_im + base + i, y.y * scale);
       }
@@ -105,19 +143,31 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   }
 }
 
-template <int M>
-static hipError_t launch_blue_m(const BluesteinArgs& a) {
+template <int M, bool WRAP>
+static hipError_t launch_blue_mw(const BluesteinArgs& a) {
   using C = BlueCfg<M, blue_epth(M), blue_threads(M)>;
   const long long blocks = (a.batch + C::XF - 1) / C::XF;
   if (a.in_im == nullptr)
-    hipLaunchKernelGGL((bluestein_fused_kernel<M, true>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
+    hipLaunchKernelGGL((bluestein_fused_kernel<M, true, WRAP>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
                        a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i,
-                       a.n, a.batch, a.scale);
+                       a.n, a.batch, a.scale, a.wrap);
   else
-    hipLaunchKernelGGL((bluestein_fused_kernel<M, false>), dim3((unsigned)blocks), dim3(C::THREADS),
+    hipLaunchKernelGGL((bluestein_fused_kernel<M, false, WRAP>), dim3((unsigned)blocks), dim3(C::THREADS),
                        0, a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f,
-                       a.tw_i, a.n, a.batch, a.scale);
+                       a.tw_i, a.n, a.batch, a.scale, a.wrap);
   return hipGetLastError();
+}
+
+template <int M>
+static hipError_t launch_blue_m(const BluesteinArgs& a) {
+  if (a.wrap == 0) return launch_blue_mw<M, false>(a);
+  if constexpr (blue_wrap_ok(M)) {
+    // wrapped lengths: n = (M + 1 + wrap) / 2 holds one element per thread beyond M/2
+    if (a.wrap < 0 || a.wrap > kBlueWrapMax || 2 * a.n - 1 - a.wrap != M) return hipErrorInvalidValue;
+    return launch_blue_mw<M, true>(a);
+  } else {
+    return hipErrorInvalidValue;
+  }
 }
 
 // Bluestein down a strided axis: x viewed as (outer, n, S); every column of n elements at stride

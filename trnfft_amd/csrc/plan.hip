@@ -1,5 +1,6 @@
 // Host side of the C ABI (include/trnfft_amd.h): plan construction (algorithm choice and device
 // tables), workspace sizing and execution dispatch.
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <complex>
@@ -99,6 +100,8 @@ struct tfa_plan {
   float2* chirp = nullptr;
   float2* hs = nullptr;
   float2 *b_tw_sf = nullptr, *b_tw_si = nullptr;  // Bluestein m <= 4096: strided-axis kernel tables
+  float2* b_hs_s = nullptr;  // Bluestein m <= 4096: strided-axis filter spectrum (length m; hs when mf == m)
+  int blue_wrap = 0;         // Bluestein: 2n - 1 - mf when the fused length wraps the convolution
   C2cTables col;          // FFT2: LDS table for n2/8 (pass 2)
   float2* tw_h = nullptr;  // FFT2: W_{n2}^i, i < n2
   float2* tw_w_pair = nullptr;  // FFT2: row table in the paired-real-row layout
@@ -205,11 +208,16 @@ namespace {
 // Bluestein path choice: the fused kernel holds one row per workgroup, so with fewer than
 // kBlueSplitRows rows it leaves most of the GPU idle and the split three-pass path (each row
 // spread over many workgroups per pass) takes over; above 16384 only the split path exists.
-// Internal length of the fused Bluestein kernel for n whose reference padded length is m: the
-// circular convolution needs only L >= 2n - 1, and where m overshoots that by most, a
+// Internal length of the fused Bluestein kernel for n whose reference padded length is m (the
+// smallest power of two >= 2n - 1).  Where 2n - 1 exceeds m/2 by at most kBlueWrapMax (n just
+// above a power of two, e.g. C3b's 4099 = 4096 + 3), the kernel convolves circularly at m/2 and
+// corrects the 2 * (2n - 1 - m/2) outputs the wrapped filter taps reach (exact, see the kernel):
+// half the transform length (4099: 8192 points against 9216 or the reference's 16384).
+// Otherwise the circular convolution needs L >= 2n - 1, and where m overshoots that by most, a
 // mixed-radix length (3^2 * 2^10 = 9216 for 4096 < n <= 4608, against m = 16384) halves the
 // transforms and the LDS (two workgroups per CU instead of one).
 int64_t blue_fused_length(int64_t n, int64_t m) {
+  if (tfa::blue_wrap_ok((int)std::min<int64_t>(m / 2, 1 << 30)) && 2 * n - 1 - m / 2 <= tfa::kBlueWrapMax) return m / 2;
   if (m == 16384 && 2 * n - 1 <= 9216) return 9216;
   return m;
 }
@@ -404,9 +412,11 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         rc = fail(TFA_ERR_UNSUPPORTED, "Bluestein padded length above 2^24 not supported");
         break;
       }
-      p->blue_fused = m <= kMaxLdsN;
+      p->mf = blue_fused_length(n, m);
+      p->blue_fused = p->mf <= kMaxLdsN;
       p->blue_split = m >= kMinBlueSplitM;
-      p->mf = p->blue_fused ? blue_fused_length(n, m) : 0;
+      if (!p->blue_fused) p->mf = 0;
+      p->blue_wrap = p->blue_fused && p->mf < 2 * n - 1 ? (int)(2 * n - 1 - p->mf) : 0;
       if (p->blue_fused) {
         // the fused kernel's own launch shape (tfa::blue_epth) fixes its table layout
         const int mf = (int)p->mf;
@@ -416,7 +426,7 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         if ((rc = p->upload(lds_table(mf, -1, tfa::blue_epth(mf)), &p->fwd.tw))) break;
         if ((rc = p->upload(lds_table(mf, 1, tfa::blue_epth(mf)), &p->inv.tw))) break;
         if (m <= tfa::kMaxStridedBlueM) {  // the strided-axis kernel's layout (tfa::lds_epth)
-          if (tfa::blue_epth((int)m) == tfa::lds_epth((int)m)) {
+          if (p->mf == m && tfa::blue_epth((int)m) == tfa::lds_epth((int)m)) {
             p->b_tw_sf = p->fwd.tw;
             p->b_tw_si = p->inv.tw;
           } else {
@@ -428,13 +438,15 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       const std::vector<float2> chirp = reference_chirp(n, dir);
       // h = conj(chirp) circularly wrapped (trnfft/fft_core.py:1337-1345) to the circular
       // convolution length L; H = FFT_L(h) / L.  Any L >= 2n - 1 gives the same convolution, so
-      // the fused kernel may use a shorter mixed-radix length than the reference's m.
+      // the fused kernel may use a shorter mixed-radix length than the reference's m; below
+      // 2n - 1 the taps i and L - i (i > L - n) share a slot and are summed (the wrapped
+      // fused kernel corrects the outputs they reach).
       auto filter_spectrum = [&](int64_t L) {
         std::vector<std::complex<double>> h((size_t)L, {0.0, 0.0});
         for (int64_t i = 0; i < n; ++i) {
           const std::complex<double> hc(chirp[(size_t)i].x, -(double)chirp[(size_t)i].y);
-          h[(size_t)i] = hc;
-          if (i > 0) h[(size_t)(L - i)] = hc;
+          h[(size_t)i] += hc;
+          if (i > 0) h[(size_t)(L - i)] += hc;
         }
         host_dft(h);
         std::vector<float2> hs((size_t)L);
@@ -445,6 +457,10 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       const std::vector<float2> hs = filter_spectrum(m);
       if ((rc = p->upload(chirp, &p->chirp))) break;
       if ((rc = p->upload(p->blue_fused && p->mf != m ? filter_spectrum(p->mf) : hs, &p->hs))) break;
+      if (m <= tfa::kMaxStridedBlueM) {
+        if (p->mf == m) p->b_hs_s = p->hs;
+        else if ((rc = p->upload(hs, &p->b_hs_s))) break;
+      }
       if (p->blue_split) {
         // m = m1 * m2 (m1 = 2^floor(log2 m / 2)); tables of the three passes, H/m permuted to
         // the transposed spectrum order hp[k1*m2 + k2] = H[k1 + m1*k2] / m
@@ -616,7 +632,7 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
                      workspace, scale, s);
     case TFA_KIND_BLUESTEIN: {
       tfa::BluesteinArgs a{in_re, in_im, out_re, out_im, plan->chirp, plan->hs, plan->fwd.tw,
-                           plan->inv.tw, (int)n, (int)plan->mf, batch, scale, s};
+                           plan->inv.tw, (int)n, (int)plan->mf, batch, scale, s, plan->blue_wrap};
       hipError_t e;
       if (!blue_use_split(plan, batch)) {
         e = tfa::launch_bluestein_fused((int)plan->mf, a);
@@ -751,7 +767,7 @@ int tfa_execute_strided(const tfa_plan* plan, int64_t outer, int64_t stride, con
   note_capture(plan, stream);
   if (blue) {
     const float bscale = plan->d.inverse ? (float)(1.0 / (double)plan->d.n) : 1.0f;
-    tfa::StridedBlueArgs ba{in_re, in_im, out_re, out_im, plan->chirp, plan->hs, plan->b_tw_sf, plan->b_tw_si,
+    tfa::StridedBlueArgs ba{in_re, in_im, out_re, out_im, plan->chirp, plan->b_hs_s, plan->b_tw_sf, plan->b_tw_si,
                             outer, stride, (int)plan->d.n, bscale, static_cast<hipStream_t>(stream)};
     hipError_t be = tfa::launch_strided_bluestein((int)plan->m, ba);
     return be == hipSuccess ? TFA_OK : hip_fail(be, "strided Bluestein launch");
