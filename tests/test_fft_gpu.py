@@ -209,7 +209,9 @@ def test_bluestein_short_rows_real_input(n):
 
 
 @pytest.mark.parametrize("n,batch", [(129, 300), (136, 64), (1025, 40), (1032, 7), (2049, 33), (2056, 3),
-                                     (4097, 256), (4099, 256), (4104, 5), (8193, 3), (8200, 20)])
+                                     (4097, 256), (4099, 256), (4104, 5), (8193, 64), (8200, 70),
+                                     # below 64 rows n = 8193..8200 take the split path at 32768
+                                     (8193, 3), (8200, 20)])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_bluestein_wrapped_lengths_vs_oracle(n, batch, inverse):
     # n = 2^k + 1 .. 2^k + 8: the fused kernel convolves circularly at 2^(k+1) < 2n - 1 and corrects

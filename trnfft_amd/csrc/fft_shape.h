@@ -84,12 +84,13 @@ __host__ __device__ constexpr bool fft2_small_ok(long long h, long long w) {
 // prefetch on.  E = 8 elements per thread for m = 128..8192: more lanes per row (a row per
 // workgroup from m = 512 at 256/512 threads, 1024 at m = 8192) and ~90 VGPRs, against E = 16/32
 // with 100-244: m = 128 7.2 -> 4.8 us (1024 rows), 256 8.2 -> 5.2, 512 17.0 -> 6.1, 1024 11.5 ->
-// 8.6, 4096 (256 rows) 23.1 -> 9.3, 8192 (256 rows) 27.6 -> 14.7; m = 16384 (C3b) E = 16 with
+// 8.6, 4096 (256 rows) 23.1 -> 9.3, 8192 (256 rows) 27.6 -> 14.7; m = 16384 (256 x 4099) E = 16 with
 // 1024 threads, 31.7 -> 29.5 us against E = 32 / 512.  The prefetch pays from m = 256 (every
 // workgroup runs the same pass at the same time, so each pass's table latency is exposed): C3a
 // 1024 x 1000 12.9 -> 12.3 us.  (Twiddle tables staged in LDS once per workgroup measured
 // slower, C3a 13.0 -> 17.0 us: the 41 KB copy costs more than it saves.)
-// Mixed-radix length 9216 = 12 * 12 * 4 * 4 * 4 (C3b's n = 4099): E = 12 with 768 threads per row
+// Mixed-radix length 9216 = 12 * 12 * 4 * 4 * 4 (4104 < n <= 4608; measured at n = 4099, 256 rows, before
+// the wrapped 8192-point length took that n over): E = 12 with 768 threads per row
 // measured 18.2 us against 22.6 us for E = 24 / 384 threads (181 VGPRs), 24.9 us for E = 24 forced
 // to two workgroups per CU and 26.7 us for E = 24 without the twiddle prefetch (the former
 // power-of-two m = 16384 kernel: 29.0 us).  Timing probes of that kernel: the LDS exchanges cost

@@ -224,9 +224,12 @@ int64_t blue_fused_length(int64_t n, int64_t m) {
 
 bool blue_use_split(const tfa_plan* p, int64_t batch) {
   if (!p->blue_fused) return true;
-  // the mixed-radix fused kernel (half the LDS, two rows' latency per CU) beats the split path
-  // at every row count: 1 x 4099 12.7 vs 13.9 us, 16 x 4099 13.8 vs 16.2, 63 x 4099 14.7 vs 23.0
-  return p->blue_split && batch < kBlueSplitRows && p->mf == p->m;
+  // With few rows the fused kernel's shorter internal lengths still win where they are at most
+  // 9216 points: n = 4099 at 9216 points, 1 row 12.7 vs 13.9 us for the split path at 16384, 16 rows
+  // 13.8 vs 16.2, 63 rows 14.7 vs 23.0 (the wrapped 8192-point length: 10.8 us at 1 row).  A wrapped
+  // 16384-point row (n = 8193..8200) takes one CU 26-29 us, against 18-21 us for the split path at
+  // 32768 below 64 rows (at 256 rows: 32 against 82 us).
+  return p->blue_split && batch < kBlueSplitRows && (p->mf == p->m || p->mf >= 16384);
 }
 
 size_t c2c_workspace(const C2cTables& t, int64_t batch) {
