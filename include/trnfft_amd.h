@@ -135,7 +135,11 @@ int tfa_execute_strided_ws(const tfa_plan* plan, int64_t outer, int64_t stride, 
  * of n_fft samples every hop, after reflect padding when TFA_STFT_CENTER; each frame is
  * multiplied by window (device pointer, n_fft floats, already centre-padded to n_fft) and
  * transformed; output planes are (batch, n_bins, n_frames) row-major with n_bins = n_fft/2+1
- * when TFA_STFT_ONESIDED else n_fft.  Replaces trnfft/api.py:291-365 (stft).
+ * when TFA_STFT_ONESIDED else n_fft.  Replaces trnfft/api.py:291-365 (stft).  n_fft: a power
+ * of two in [16, 4096], or any other n_fft from 9 up to 2731 (onesided) or 2048 (two-sided),
+ * forward only: each frame then goes through the reference's Bluestein chain
+ * (trnfft/fft_core.py:1285-1376), convolved at the shortest power of two or 3 * 2^k that holds
+ * n_fft + n_bins - 1 points.
  */
 int tfa_stft_frames(const tfa_plan* plan, int64_t num_samples, int64_t* n_frames);
 int tfa_stft_execute(const tfa_plan* plan, int64_t batch, int64_t num_samples, const float* signal,

@@ -121,16 +121,16 @@ def test_stft_vs_oracle(n_fft, hop, center, normalized, onesided):
 
 
 @pytest.mark.parametrize("n_fft,hop,pad_mode,center,onesided,normalized,shape", [
-    (400, 160, "reflect", True, True, False, (2, 16000)),      # 25 ms @ 16 kHz: Bluestein frames (m = 1024)
+    (400, 160, "reflect", True, True, False, (2, 16000)),      # 25 ms @ 16 kHz: a Bluestein transform per frame
     (400, 100, "constant", True, True, True, (3, 5000)),
-    (12, 3, "replicate", True, True, False, (2, 301)),         # n_fft below the fused kernel's range
+    (12, 3, "replicate", True, True, False, (2, 301)),         # the fused kernel's shortest convolution (32)
     (12, 5, "circular", True, False, False, (1, 200)),         # (1, L): the reference squeezes the batch axis
     (8192, 2048, "reflect", True, True, False, (2, 30000)),    # above the fused kernel's range
     (8192, 4096, "constant", True, False, True, (20000,)),
     (512, 128, "constant", True, True, False, (2, 3, 4000)),   # fused kernel on the device-padded signal
     (512, 256, "replicate", True, True, True, (4000,)),
     (1024, 300, "circular", True, False, False, (2, 5000)),
-    (8, 2, "reflect", False, True, False, (2, 100)),
+    (8, 2, "reflect", False, True, False, (2, 100)),           # below the fused kernels' range
     (1000, 250, "reflect", False, False, False, (2, 3000)),
     (2, 1, "constant", True, True, False, (3, 17)),
 ])
@@ -146,6 +146,57 @@ def test_stft_any_n_fft_and_pad_mode_vs_oracle(n_fft, hop, pad_mode, center, one
     assert got.shape == ref[0].shape
     tol = tol_pow2(n_fft) if n_fft & (n_fft - 1) == 0 else tol_bluestein(n_fft)
     assert rel_l2(got.real, got.imag, *ref) <= tol
+
+
+@pytest.mark.parametrize("n_fft,hop,center,onesided,normalized,shape", [
+    # convolution length m: the shortest power of two or 3 * 2^k >= n_fft + n_bins - 1
+    (9, 3, True, True, False, (2, 500)),         # m = 32
+    (12, 4, False, False, False, (3, 257)),      # m = 32, two-sided
+    (20, 7, True, True, True, (2, 1000)),        # m = 32 (30 points)
+    (30, 12, True, True, False, (2, 1500)),      # m = 64
+    (33, 11, True, False, False, (1, 999)),      # m = 96, two-sided
+    (50, 20, True, True, False, (2, 2000)),      # m = 96
+    (80, 30, False, True, False, (2, 2500)),     # m = 128
+    (100, 40, True, True, False, (4, 3001)),     # m = 192
+    (150, 60, True, True, True, (2, 4000)),      # m = 256
+    (200, 64, True, True, False, (2, 8000)),     # m = 384
+    (257, 128, True, True, False, (2, 5000)),    # m = 512
+    (300, 450, False, True, False, (2, 9000)),   # m = 512, hop > n_fft
+    (400, 160, True, True, False, (3, 16000)),   # m = 768
+    (400, 160, True, True, False, (2, 201)),     # every frame reaches into the reflect padding
+    (640, 160, False, True, True, (2, 9000)),    # m = 1024
+    (1000, 250, True, True, False, (2, 7000)),   # m = 1536
+    (1000, 250, True, False, False, (2, 7000)),  # m = 2048, two-sided
+    (1025, 300, True, True, False, (2, 9000)),   # m = 2048
+    (2000, 500, True, True, False, (1, 20000)),  # m = 3072
+    (2500, 600, True, True, False, (1, 20000)),  # m = 4096
+    (2047, 512, True, False, False, (1, 20000)), # m = 4096, two-sided
+])
+def test_stft_fused_bluestein_frames_vs_oracle(n_fft, hop, center, onesided, normalized, shape):
+    # n_fft that is not a power of two, without autograd: one fused kernel with a Bluestein
+    # transform per frame (the reference's chain, trnfft/api.py:339-349 -> fft_core.py:1285-1376)
+    g = torch.Generator().manual_seed(n_fft * 7 + hop)
+    x = torch.randn(*shape, generator=g)
+    got = trnfft_amd.stft(x.cuda(), n_fft=n_fft, hop_length=hop, center=center, normalized=normalized,
+                          onesided=onesided)
+    ref = oracle.stft(x, n_fft=n_fft, hop_length=hop, center=center, normalized=normalized, onesided=onesided)
+    assert got.shape == ref[0].shape
+    assert rel_l2(got.real, got.imag, *ref) <= tol_bluestein(n_fft)
+
+
+@pytest.mark.parametrize("n_fft,hop,pad_mode", [(400, 160, "reflect"), (1000, 256, "constant"), (99, 33, "circular")])
+def test_stft_fused_bluestein_matches_composed_path(n_fft, hop, pad_mode):
+    # the same call under autograd takes the composed path (frame gather + Bluestein rows); both
+    # run the reference's chain, so they agree to fp32 rounding
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(3, 12000, generator=g).cuda()
+    with torch.no_grad():
+        fused = trnfft_amd.stft(x, n_fft=n_fft, hop_length=hop, pad_mode=pad_mode)
+    xg = x.clone().requires_grad_(True)
+    comp = trnfft_amd.stft(xg, n_fft=n_fft, hop_length=hop, pad_mode=pad_mode)
+    assert comp.real.requires_grad
+    assert fused.shape == comp.shape
+    assert rel_l2(fused.real, fused.imag, comp.real.detach(), comp.imag.detach()) <= tol_bluestein(n_fft) / 4
 
 
 def test_stft_win_length_below_n_fft_and_custom_window_composed():
@@ -217,6 +268,20 @@ def test_fftn_strided_axes_vs_oracle(shape, dim):
     assert rel_l2(got.real, got.imag, *ref) <= 1e-5 * math.log2(total)
     back = trnfft_amd.ifftn(got, dim=dim)
     assert rel_l2(back.real, back.imag, re, im) <= 1e-5 * math.log2(total)
+
+
+@pytest.mark.parametrize("n_fft", [512, 400])
+def test_stft_hop_beyond_the_signal(n_fft):
+    # one frame per signal; a hop beyond 32 bits is clamped on the host and the kernels' tile
+    # bounds are 64-bit, so no frame offset wraps
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(2, 3000, generator=g)
+    tol = tol_pow2(n_fft) if n_fft & (n_fft - 1) == 0 else tol_bluestein(n_fft)
+    for hop, center in [(5000, True), (3_000_000_000, True), (3_000_000_000, False)]:
+        got = trnfft_amd.stft(x.cuda(), n_fft=n_fft, hop_length=hop, center=center)
+        ref = oracle.stft(x, n_fft=n_fft, hop_length=hop, center=center)
+        assert got.shape == ref[0].shape == (2, n_fft // 2 + 1, 1)
+        assert rel_l2(got.real, got.imag, *ref) <= tol
 
 
 @pytest.mark.parametrize("n_fft,hop,length,batch_shape", [

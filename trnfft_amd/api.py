@@ -255,8 +255,19 @@ def _effective_window(window: torch.Tensor | None, n_fft: int, win_length: int, 
     return window
 
 
-def _fused_stft_ok(n_fft: int) -> bool:
-    return 16 <= n_fft <= 4096 and n_fft & (n_fft - 1) == 0
+# longest non-power-of-two n_fft of the fused per-frame Bluestein STFT (4096-point convolution:
+# n + n/2 <= 4096 onesided, 2n - 1 <= 4096 two-sided)
+_STFT_BLUE_MAX_N = {True: 2731, False: 2048}
+
+
+def _fused_stft_ok(n_fft: int, onesided: bool = True, needs_grad: bool = False) -> bool:
+    """Whether the fused STFT kernel takes this n_fft: a power of two in [16, 4096] (two real
+    frames per transform, differentiable), or any other n_fft from 9 up to 2731 (onesided) or
+    2048 (two-sided) (one Bluestein transform per frame, forward only: calls that need
+    gradients keep the composed path)."""
+    if n_fft & (n_fft - 1) == 0:
+        return 16 <= n_fft <= 4096
+    return 9 <= n_fft <= _STFT_BLUE_MAX_N[bool(onesided)] and not needs_grad
 
 
 def stft(
@@ -272,12 +283,14 @@ def stft(
 ) -> ComplexTensor:
     """Short-time Fourier transform, output (..., freq, time) (trnfft/api.py:291-365).
 
-    Power-of-two n_fft in [16, 4096] runs as one fused kernel that reads the raw waveform
-    (framing, padding, window, transform and the (freq, time) transpose in one pass); with a
-    pad_mode other than "reflect" the signal is padded on the device first (the reference's
-    F.pad) and the fused kernel frames the padded signal.  Other n_fft keep the reference's
-    composition on the device: pad, frame gather, window, then the transform kernels (Bluestein
-    for non-power-of-two n_fft) and the onesided slice.
+    Power-of-two n_fft in [16, 4096], and other n_fft from 9 to 2731 (2048 two-sided) when no
+    gradient is needed, run as one fused kernel that reads the raw waveform (framing, padding,
+    window, transform -- one Bluestein chain per frame for non-power-of-two n_fft -- and the
+    (freq, time) transpose in one pass); with a pad_mode other than "reflect" the signal is padded on the device first
+    (the reference's F.pad) and the fused kernel frames the padded signal.  Other n_fft, and
+    non-power-of-two n_fft under autograd, keep the reference's composition on the device: pad,
+    frame gather, window, then the transform kernels (Bluestein for non-power-of-two n_fft) and
+    the onesided slice.
     """
     if hop_length is None:
         hop_length = n_fft // 4
@@ -290,7 +303,9 @@ def stft(
     out_dev = input.device
     x = to_device_f32(input, dev)
     win = to_device_f32(win, dev)
-    if center and pad_mode == "reflect" and _fused_stft_ok(n_fft):
+    needs_grad = torch.is_grad_enabled() and (x.requires_grad or win.requires_grad)
+    fused = _fused_stft_ok(n_fft, onesided, needs_grad)
+    if center and pad_mode == "reflect" and fused:
         length = x.shape[-1]
         if length <= n_fft // 2:
             raise ValueError(f"reflect padding of {n_fft // 2} needs more than {n_fft // 2} samples; got {length}")
@@ -318,7 +333,7 @@ def stft(
         empty = torch.empty(*x.shape[:-1], bins, 0, dtype=torch.float32, device=dev)
         out = ComplexTensor._wrap(empty, empty.clone())
         return out if out_dev == dev else out.to(out_dev)
-    if _fused_stft_ok(n_fft):
+    if fused:
         # the padded signal through the fused kernel (no centre padding of its own)
         out = _ag.stft(x.contiguous(), win, n_fft, hop_length, False, normalized, onesided, num_frames)
         return out if out_dev == dev else out.to(out_dev)

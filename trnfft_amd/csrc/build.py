@@ -20,6 +20,7 @@ SOURCES = [
     "kernels_strided.hip",
     "kernels_bluestein.hip",
     "kernels_stft.hip",
+    "kernels_stft_blue.hip",
     "kernels_gemm.hip",
     "kernels_fft2.hip",
     "kernels_real.hip",
@@ -42,10 +43,10 @@ FLAGS = [
 ]
 
 
-# per-source extra flags: the fused Bluestein kernel feeds compile-time zeros (the zero-padded
+# per-source extra flags: the fused Bluestein kernels feed compile-time zeros (the zero-padded
 # half of its forward input) into its first pass; ignoring the sign of zero lets the compiler drop
 # the additions of those zeros (x + 0 -> x), which changes no result beyond the sign of a zero
-EXTRA_FLAGS = {"kernels_bluestein.hip": ["-fno-signed-zeros"]}
+EXTRA_FLAGS = {"kernels_bluestein.hip": ["-fno-signed-zeros"], "kernels_stft_blue.hip": ["-fno-signed-zeros"]}
 
 
 def _compile(src: str, obj: str) -> None:

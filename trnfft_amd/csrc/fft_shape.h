@@ -175,6 +175,42 @@ __host__ __device__ constexpr LdsShape make_shape(int n, int e) {
 // LDS word index with one pad word per 16 to keep the strided pass writes bank-conflict free.
 __host__ __device__ constexpr int lds_pad(int i) { return i + (i >> 4); }
 
-
+// Non-power-of-two STFT: one Bluestein transform of length m per frame, m a power of two
+// (32..4096) or 3 * 2^k (96..3072), the shortest with n + n_bins - 1 <= m.
+constexpr int kStftBlueMinM = 32;
+constexpr int kStftBlueMaxM = 4096;
+__host__ __device__ constexpr bool stft_blue_len_ok(long long m) {
+  if (m < kStftBlueMinM || m > kStftBlueMaxM) return false;
+  const long long q = m % 3 == 0 ? m / 3 : m;
+  return q >= 32 && (q & (q - 1)) == 0;
+}
+// largest n_fft a length-m transform serves (onesided: n + n/2 <= m)
+__host__ __device__ constexpr int stft_blue_nmax(int m) {
+  int n = 2 * m / 3 + 2;
+  while (n + n / 2 > m) --n;
+  return n;
+}
+// Launch shape (elements per thread, frames per workgroup) from a sweep on MI355X (64 x 160000
+// samples, hop 2n/5, every E in {4..32} dividing m and 2..64 frames per workgroup; the kernel is
+// VALU-bound, ~1 wavefront-instruction per 64 points per pass): n_fft 30 (m 64) 128 us, 100 (192)
+// 148, 200 (384) 177, 257 (512) 177, 400 (768) 186, 600 (1024) 188, 1000 (1536) 199, 1300 (2048)
+// 187, 2000 (3072) 232.  (m = 1024 at E = 16 / 16 frames, the first shape: 270 us for n_fft 400;
+// the shortest-length rule with the truncated filter took n_fft 400 from 1024 to 768 points,
+// 320 from 1024 to 512 and 600 from 2048 to 1024.)
+__host__ __device__ constexpr int stft_blue_epth(int m) {
+  return (m == 384 || m == 768 || m == 1536) ? 24 : m % 3 == 0 ? 12 : 8;
+}
+__host__ __device__ constexpr int stft_blue_frames(int m) {
+  return m <= 32 ? 32 : m <= 512 ? 16 : m <= 1024 ? 8 : m <= 2048 ? 4 : 2;
+}
+// Floats of LDS per frame: the exchange buffer of the m-point transform (its spectrum, at most
+// m/2 float2, is staged there afterwards), rounded so that successive frames start g banks apart,
+// g = 128 / frames: the output stage reads bin k of `frames` consecutive frames per instruction.
+__host__ __device__ constexpr int stft_blue_area(int m, int frames) {
+  const int g = frames >= 32 ? 4 : (128 / frames) % 64;
+  int a = 2 * lds_pad(m);
+  while (a % 64 != g) a += 4;
+  return a;
+}
 
 }  // namespace tfa

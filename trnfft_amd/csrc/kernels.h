@@ -228,8 +228,15 @@ struct StftArgs {
   long long batch;
   float scale;
   hipStream_t stream;
+  // non-power-of-two n_fft (Bluestein per frame, padded length m): tw above is the forward table
+  // for m, these the inverse table, the chirp (n_fft) and the filter spectrum H/m (m)
+  const float2* tw_i = nullptr;
+  const float2* chirp = nullptr;
+  const float2* hs = nullptr;
+  int m = 0;
 };
 hipError_t launch_stft(int n_fft, const StftArgs& a);
+hipError_t launch_stft_blue(int n_fft, const StftArgs& a);  // a.m != 0
 
 struct RealArgs {
   const float* in_re;  // forward: (batch, n) real rows; inverse: (batch, n/2+1) bins

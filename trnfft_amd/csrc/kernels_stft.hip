@@ -62,12 +62,12 @@ __global__ __launch_bounds__((StftCfg<NFFT>::THREADS)) void stft_kernel(
   const int fa = f0 + 2 * pl;  // frames fa (real part) and fa + 1 (imaginary part)
   const float* x = sig + (size_t)b * length;
   const int start = f0 * hop - pad;  // padded-signal origin of the tile's first frame
-  const int span = (FR - 1) * hop + NFFT;
+  const long long span = (long long)(FR - 1) * hop + NFFT;  // (frames past the end count)
   float wv[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) wv[e] = win[tid + T * e] * hs;
   float2 v[E];
-  if (start >= 0 && start + span <= length) {  // block-uniform: no padding inside the tile
+  if (start >= 0 && (long long)start + span <= length) {  // block-uniform: no padding inside the tile
     const float* p0 = x + (start + 2 * pl * hop) + tid;
     const float* p1 = p0 + hop;
     float a[E], c[E];
@@ -84,9 +84,10 @@ __global__ __launch_bounds__((StftCfg<NFFT>::THREADS)) void stft_kernel(
       float s[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        int idx = (fa + h) * hop + j - pad;
-        // reflect without repeating the edge sample (torch.nn.functional.pad mode="reflect");
-        // positions that only frames past the end would read are clamped (never stored)
+        // frames past the end (never stored) read the last frame's samples
+        const int fi = fa + h < n_frames ? fa + h : n_frames - 1;
+        int idx = fi * hop + j - pad;
+        // reflect without repeating the edge sample (torch.nn.functional.pad mode="reflect")
         idx = idx < 0 ? -idx : idx;
         idx = idx >= length ? 2 * (length - 1) - idx : idx;
         idx = idx < 0 ? 0 : (idx >= length ? length - 1 : idx);
@@ -167,6 +168,7 @@ static hipError_t launch_stft_n(const StftArgs& a) {
 }
 
 hipError_t launch_stft(int n_fft, const StftArgs& a) {
+  if (a.m != 0) return launch_stft_blue(n_fft, a);
   switch (n_fft) {
     case 16: return launch_stft_n<16>(a);
     case 32: return launch_stft_n<32>(a);

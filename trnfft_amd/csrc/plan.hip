@@ -329,6 +329,28 @@ std::vector<float2> reference_chirp(int64_t n, int sign) {
   return c;
 }
 
+// Bluestein filter spectrum: h = conj(chirp) circularly wrapped (trnfft/fft_core.py:1337-1345)
+// to the circular convolution length L; H = FFT_L(h) / L.  Any L >= 2n - 1 gives the same
+// convolution, so the fused kernel may use a shorter mixed-radix length than the reference's m;
+// below 2n - 1 the taps i and L - i (i > L - n) share a slot and are summed (the wrapped fused
+// kernel corrects the outputs they reach).  kmax < n keeps only the taps -(n-1) .. kmax-1, all
+// that outputs k < kmax read: then any L >= n + kmax - 1 gives their values without wrap-around.
+std::vector<float2> blue_filter_spectrum(const std::vector<float2>& chirp, int64_t L, int64_t kmax = -1) {
+  const int64_t n = (int64_t)chirp.size();
+  if (kmax < 0) kmax = n;
+  std::vector<std::complex<double>> h((size_t)L, {0.0, 0.0});
+  for (int64_t i = 0; i < n; ++i) {
+    const std::complex<double> hc(chirp[(size_t)i].x, -(double)chirp[(size_t)i].y);
+    if (i < kmax) h[(size_t)i] += hc;
+    if (i > 0) h[(size_t)(L - i)] += hc;
+  }
+  host_dft(h);
+  std::vector<float2> hs((size_t)L);
+  for (int64_t i = 0; i < L; ++i)
+    hs[(size_t)i] = make_float2((float)(h[(size_t)i].real() / (double)L), (float)(h[(size_t)i].imag() / (double)L));
+  return hs;
+}
+
 std::mutex g_retained_mu;
 
 // plans destroyed after use under graph capture (never freed; see tfa_plan_destroy)
@@ -439,24 +461,7 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         }
       }
       const std::vector<float2> chirp = reference_chirp(n, dir);
-      // h = conj(chirp) circularly wrapped (trnfft/fft_core.py:1337-1345) to the circular
-      // convolution length L; H = FFT_L(h) / L.  Any L >= 2n - 1 gives the same convolution, so
-      // the fused kernel may use a shorter mixed-radix length than the reference's m; below
-      // 2n - 1 the taps i and L - i (i > L - n) share a slot and are summed (the wrapped
-      // fused kernel corrects the outputs they reach).
-      auto filter_spectrum = [&](int64_t L) {
-        std::vector<std::complex<double>> h((size_t)L, {0.0, 0.0});
-        for (int64_t i = 0; i < n; ++i) {
-          const std::complex<double> hc(chirp[(size_t)i].x, -(double)chirp[(size_t)i].y);
-          h[(size_t)i] += hc;
-          if (i > 0) h[(size_t)(L - i)] += hc;
-        }
-        host_dft(h);
-        std::vector<float2> hs((size_t)L);
-        for (int64_t i = 0; i < L; ++i)
-          hs[(size_t)i] = make_float2((float)(h[(size_t)i].real() / (double)L), (float)(h[(size_t)i].imag() / (double)L));
-        return hs;
-      };
+      auto filter_spectrum = [&](int64_t L) { return blue_filter_spectrum(chirp, L); };
       const std::vector<float2> hs = filter_spectrum(m);
       if ((rc = p->upload(chirp, &p->chirp))) break;
       if ((rc = p->upload(p->blue_fused && p->mf != m ? filter_spectrum(p->mf) : hs, &p->hs))) break;
@@ -489,12 +494,36 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       break;
     }
     case TFA_KIND_STFT:
-      if (!is_pow2(n) || n < 16 || n > 4096) {
-        rc = fail(TFA_ERR_UNSUPPORTED, "fused STFT needs a power-of-two n_fft in [16, 4096]");
-        break;
-      }
       if (desc->hop < 1) {
         rc = fail(TFA_ERR_INVALID, "hop_length must be >= 1");
+        break;
+      }
+      if (!is_pow2(n)) {
+        // forward STFT with one Bluestein transform per frame (the reference's chain,
+        // trnfft/fft_core.py:1285-1376): chirp, the filter spectrum H/m of the taps that the kept
+        // bins read, and the two m-point LDS tables; m is the shortest power of two or 3 * 2^k
+        // with n + n_bins - 1 <= m (the reference pads to the power of two >= 2n - 1)
+        const int64_t bins = (desc->flags & TFA_STFT_ONESIDED) ? n / 2 + 1 : n;
+        int64_t m = 0;
+        for (int64_t c = tfa::kStftBlueMinM; c <= tfa::kStftBlueMaxM && !m; ++c)
+          if (tfa::stft_blue_len_ok(c) && n + bins - 1 <= c && n <= tfa::stft_blue_nmax((int)c)) m = c;
+        if (desc->inverse || n < 9 || m == 0) {
+          rc = fail(TFA_ERR_UNSUPPORTED, "fused STFT: forward only for n_fft that is not a power of two, 9..2731 onesided or 9..2048 two-sided");
+          break;
+        }
+        p->m = p->mf = m;
+        p->fwd.n = p->inv.n = m;
+        p->fwd.dir = -1;
+        p->inv.dir = 1;
+        const std::vector<float2> chirp = reference_chirp(n, -1);
+        if ((rc = p->upload(lds_table((int)m, -1, tfa::stft_blue_epth((int)m)), &p->fwd.tw))) break;
+        if ((rc = p->upload(lds_table((int)m, 1, tfa::stft_blue_epth((int)m)), &p->inv.tw))) break;
+        if ((rc = p->upload(chirp, &p->chirp))) break;
+        rc = p->upload(blue_filter_spectrum(chirp, m, bins), &p->hs);
+        break;
+      }
+      if (n < 16 || n > 4096) {
+        rc = fail(TFA_ERR_UNSUPPORTED, "fused STFT needs a power-of-two n_fft in [16, 4096]");
         break;
       }
       if (desc->inverse) {
@@ -812,8 +841,16 @@ int tfa_stft_execute(const tfa_plan* plan, int64_t batch, int64_t num_samples, c
   if (rc) return rc;
   const int n_bins = (plan->d.flags & TFA_STFT_ONESIDED) ? (int)(n_fft / 2 + 1) : (int)n_fft;
   const float scale = (plan->d.flags & TFA_STFT_NORMALIZED) ? (float)(1.0 / std::sqrt((double)n_fft)) : 1.0f;
-  tfa::StftArgs a{signal, window, out_re, out_im, plan->fwd.tw, (int)num_samples, (int)plan->d.hop,
+  // a hop beyond the padded signal leaves one frame, whatever its value: keep it within int
+  const int64_t hop = std::min<int64_t>(plan->d.hop, num_samples + 2 * pad);
+  tfa::StftArgs a{signal, window, out_re, out_im, plan->fwd.tw, (int)num_samples, (int)hop,
                   (int)pad, (int)frames, n_bins, batch, scale, static_cast<hipStream_t>(stream)};
+  if (!is_pow2(n_fft)) {
+    a.tw_i = plan->inv.tw;
+    a.chirp = plan->chirp;
+    a.hs = plan->hs;
+    a.m = (int)plan->m;
+  }
   hipError_t e = tfa::launch_stft((int)n_fft, a);
   return e == hipSuccess ? TFA_OK : hip_fail(e, "stft launch");
 }
