@@ -330,7 +330,18 @@ def bench_secondary():
                                                         P(ys[k]), 160000, st)), S)
     rec("c2_istft_64x257x626_nfft512", t, 40064 * 5 * 512 * 9, nbytes, sets=S,
         note="inverse of c2: spectra in, 64 x 160000 samples out")
-    del xs, os_, ys
+    del os_, ys
+    # C2's signals at n_fft 400 (25 ms at 16 kHz), hop 160: one Bluestein chain per frame
+    w400 = torch.hann_window(400).to(dev)
+    p400 = native_plan(_lib.KIND_STFT, 400, False, dev.index, hop=160, flags=_lib.STFT_CENTER | _lib.STFT_ONESIDED)
+    frames = 1 + 160000 // 160
+    nbytes = 64 * 160000 * 4 + 2 * 64 * 201 * frames * 4
+    os_ = [(torch.empty(64, 201, frames, device=dev), torch.empty(64, 201, frames, device=dev)) for _ in range(S)]
+    t = _time_rot(lambda k, st: chk(L.tfa_stft_execute(p400.handle, 64, 160000, P(xs[k]), P(w400), P(os_[k][0]),
+                                                   P(os_[k][1]), st)), S)
+    rec("stft_64x160000_nfft400", t, 64 * frames * 2 * 5 * 768 * math.log2(768), nbytes, sets=S,
+        note="non-power-of-two n_fft: two 768-point transforms per frame (gflops counts those), VALU-bound")
+    del xs, os_
     # C3: Bluestein (fused, one launch)
     for n, b in [(1000, 1024), (4099, 256)]:
         nbytes = 4 * b * n * 4
