@@ -171,6 +171,23 @@ int tfa_istft_length(const tfa_plan* plan, int64_t n_frames, int64_t length, int
 int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, const float* spec_re,
                       const float* spec_im, const float* window, float* out, int64_t length, tfa_stream stream);
 
+/*
+ * Gradient of the onesided forward STFT with respect to its padded signal: grad_re/grad_im
+ * (batch, n/2+1, n_frames), the gradient of tfa_stft_execute's output planes, -> grad_padded
+ * (batch, padded_len), padded_len = num_samples + 2*(n/2) when CENTER else num_samples, n_frames
+ * = 1 + (padded_len - n)/hop.  Per frame the adjoint of the r2c transform (interior bins halved,
+ * Hermitian-completed inverse transform, unscaled; 1/sqrt(n) when NORMALIZED), times the window,
+ * overlap-added; samples no frame covers get zero.  Undoing the centre padding (the reflected
+ * edges folded back) is left to the caller.  Runs on the inverse STFT plan of the same n, hop
+ * and flags (its table and tile shape; hops the inverse plan refuses are refused there).
+ * Replaces the backward that torch autograd derives for trnfft/api.py:310-349 (pad, frame index,
+ * window multiply, per-frame transform): a gather-transpose of the gradient, an inverse transform
+ * per frame and an index_add/fold overlap-add.
+ */
+int tfa_stft_backward_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, const float* grad_re,
+                              const float* grad_im, const float* window, float* grad_padded, int64_t padded_len,
+                              tfa_stream stream);
+
 /* Operand ops of tfa_complex_gemm_ex (BLAS-style, plus conjugation without transpose). */
 #define TFA_OP_N 0 /* op(X) = X          */
 #define TFA_OP_T 1 /* op(X) = X^T        */

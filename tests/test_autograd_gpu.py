@@ -211,6 +211,63 @@ def test_stft_gradient(n_fft, hop, center, normalized, onesided):
     assert _rel(aw.grad, rw.grad) <= TOL
 
 
+@pytest.mark.parametrize("n_fft,hop,center,normalized,shape", [
+    (512, 256, True, False, (3, 4000)),
+    (512, 128, True, True, (2, 3, 3000)),     # leading dims
+    (256, 100, False, False, (2, 5000)),      # no centre padding; samples past the last frame
+    (16, 4, True, False, (2, 301)),
+    (1024, 256, True, False, (1, 9000)),
+    (2048, 512, False, True, (2, 10000)),
+    (4096, 1024, True, False, (1, 20000)),
+    (512, 600, True, False, (2, 3000)),       # hop > n_fft: gaps between frames
+    (512, 256, True, False, (2, 257)),        # every frame reaches into both reflected edges
+])
+def test_stft_gradient_fused_backward(n_fft, hop, center, normalized, shape, monkeypatch):
+    # window without gradient: the signal gradient is one fused kernel (r2c adjoint per frame,
+    # window, overlap-add) plus the reflected-edge fold; against torch.stft in float64
+    from trnfft_amd import fft_core
+
+    calls = []
+    real = fft_core.execute_stft_backward
+
+    def counted(*args, **kw):
+        out = real(*args, **kw)
+        calls.append(out is not None)
+        return out
+
+    monkeypatch.setattr(fft_core, "execute_stft_backward", counted)
+    g = torch.Generator().manual_seed(n_fft + hop)
+    x = torch.randn(*shape, generator=g)
+    w = torch.hann_window(n_fft) + 0.1 * torch.rand(n_fft, generator=g)
+    a = _leaf(x)
+    y = trnfft_amd.stft(a, n_fft, hop_length=hop, window=w.cuda(), center=center, normalized=normalized)
+    cr, ci = _cotangent(tuple(y.shape), 21)
+    (y.real * cr.float().cuda() + y.imag * ci.float().cuda()).sum().backward()
+    assert calls == [True]
+    r = x.double().requires_grad_(True)
+    z = torch.stft(r.reshape(-1, shape[-1]), n_fft, hop_length=hop, window=w.double(), center=center,
+                   pad_mode="reflect", normalized=normalized, onesided=True, return_complex=True)
+    # (a (1, L) signal comes back without its batch axis, as in the reference)
+    z = z.reshape(tuple(y.shape))
+    (z.real * cr + z.imag * ci).sum().backward()
+    assert _rel(a.grad, r.grad) <= TOL
+
+
+def test_stft_gradient_short_hop_composes():
+    # a hop the inverse-STFT tile refuses: the backward falls back to the composed adjoint
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 1500, generator=g)
+    a = _leaf(x)
+    y = trnfft_amd.stft(a, 512, hop_length=2)
+    cr, ci = _cotangent(tuple(y.shape), 4)
+    (y.real * cr.float().cuda() + y.imag * ci.float().cuda()).sum().backward()
+    r = x.double().requires_grad_(True)
+    z = torch.stft(r, 512, hop_length=2, window=torch.hann_window(512, dtype=torch.float64), center=True,
+                   pad_mode="reflect", onesided=True, return_complex=True)
+    (z.real * cr + z.imag * ci).sum().backward()
+    assert _rel(a.grad, r.grad) <= TOL
+
+
 @pytest.mark.parametrize("n_fft,hop,pad_mode", [(8192, 2048, "replicate"), (512, 128, "circular"), (12, 4, "constant")])
 def test_stft_gradient_composed_pow2(n_fft, hop, pad_mode):
     # power-of-two n_fft outside the fused kernel's range or with a non-reflect pad: device F.pad +

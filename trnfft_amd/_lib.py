@@ -46,6 +46,7 @@ EXPORTS = (
     "tfa_stft_execute",
     "tfa_istft_length",
     "tfa_istft_execute",
+    "tfa_stft_backward_execute",
     "tfa_complex_gemm",
     "tfa_complex_gemm_ex",
     "tfa_complex_gemm_batched",
@@ -98,6 +99,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tfa_istft_length.restype = ctypes.c_int
     lib.tfa_istft_execute.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp]
     lib.tfa_istft_execute.restype = ctypes.c_int
+    lib.tfa_stft_backward_execute.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _vp]
+    lib.tfa_stft_backward_execute.restype = ctypes.c_int
     lib.tfa_complex_gemm.argtypes = [_i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _i64, _vp]
     lib.tfa_complex_gemm.restype = ctypes.c_int
     lib.tfa_complex_gemm_ex.argtypes = [_i64, _i64, _i64, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i32, ctypes.c_float,

@@ -193,6 +193,13 @@ class _StftFn(torch.autograd.Function):
         lead = x.shape[:-1]
         b = x.numel() // length
         bins = g_re.shape[-2]
+        pad = n_fft // 2 if center else 0
+        if onesided and ctx.needs_input_grad[0] and not ctx.needs_input_grad[1] and g_re.is_cuda:
+            # no window gradient: one fused kernel (r2c adjoint per frame, window, overlap-add)
+            d_xp = _fc.execute_stft_backward(g_re.reshape(b, bins, frames), g_im.reshape(b, bins, frames), win,
+                                             n_fft, hop, center, normalized, length + 2 * pad)
+            if d_xp is not None:
+                return _unpad_reflect(d_xp, pad, length).reshape(*lead, length), None, None, None, None, None, None, None
         # (..., bins, frames) -> (b, frames, bins): one spectrum per row
         gr = g_re.reshape(b, bins, frames).transpose(1, 2).contiguous()
         gi = g_im.reshape(b, bins, frames).transpose(1, 2).contiguous()
@@ -202,7 +209,6 @@ class _StftFn(torch.autograd.Function):
             fg = _fc.execute_1d(gr, gi, True).real.mul_(float(n_fft))
         if normalized:
             fg.mul_(1.0 / math.sqrt(n_fft))
-        pad = n_fft // 2 if center else 0
         if center:
             xp = F.pad(x.reshape(b, 1, length), (pad, pad), mode="reflect").reshape(b, -1)
         else:
@@ -217,15 +223,19 @@ class _StftFn(torch.autograd.Function):
             fg.mul_(win)
             d_xp = F.fold(fg.transpose(1, 2), output_size=(1, lp), kernel_size=(1, n_fft), stride=(1, hop))
             d_xp = d_xp.reshape(b, lp)
-            if center:
-                # x_pad[i] = x[pad - i] (i < pad), x_pad[pad + j] = x[j], x_pad[pad + L + i] = x[L - 2 - i]
-                d_x = d_xp[:, pad : pad + length].clone()
-                d_x[:, 1 : pad + 1] += d_xp[:, :pad].flip(-1)
-                d_x[:, length - 1 - pad : length - 1] += d_xp[:, pad + length :].flip(-1)
-            else:
-                d_x = d_xp[:, :length].contiguous()
-            d_x = d_x.reshape(*lead, length)
+            d_x = _unpad_reflect(d_xp, pad, length).reshape(*lead, length)
         return d_x, d_win, None, None, None, None, None, None
+
+
+def _unpad_reflect(d_xp: torch.Tensor, pad: int, length: int) -> torch.Tensor:
+    """Adjoint of the reflect padding x_pad[i] = x[pad - i] (i < pad), x_pad[pad + j] = x[j],
+    x_pad[pad + L + i] = x[L - 2 - i]: the kept span, with the reflected edges folded back in
+    place (a view of d_xp's rows; pad = 0 is the plain prefix)."""
+    d_x = d_xp[:, pad : pad + length]
+    if pad:
+        d_x[:, 1 : pad + 1] += d_xp[:, :pad].flip(-1)
+        d_x[:, length - 1 - pad : length - 1] += d_xp[:, pad + length :].flip(-1)
+    return d_x
 
 
 def stft(x, win, n_fft, hop, center, normalized, onesided, num_frames) -> ComplexTensor:

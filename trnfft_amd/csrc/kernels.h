@@ -266,6 +266,10 @@ struct IstftArgs {
   long long out_pitch;
   float scale;  // 1/n_fft (x sqrt(n_fft) when normalized)
   hipStream_t stream;
+  // adjoint of the forward STFT instead of its inverse: bins 0 and n_fft/2 count twice against
+  // the others (scale 1/2 then gives the r2c adjoint), the windowed sum is written as it is (no
+  // envelope division, no raw-sum branch)
+  bool adjoint = false;
 };
 hipError_t launch_istft(int n_fft, const IstftArgs& a);
 int istft_frames_per_tile(int n_fft);

@@ -16,6 +16,11 @@
 // A sample is covered by frames t with t*hop <= s < t*hop + n, so a workgroup that owns the
 // samples of frames [t0, t0 + FR') also transforms the H = floor((n-1)/hop) frames before t0
 // (recomputed halo, no atomics and no second pass).
+//
+// ADJ: the same kernel computes the gradient of the forward STFT with respect to its (padded)
+// signal, the adjoint of frame gather + window + onesided transform: per frame the adjoint of the
+// r2c transform (a Hermitian-completed inverse transform with the interior bins halved against
+// bins 0 and n/2, unscaled), times the window, overlap-added without the envelope division.
 #include "kernels.h"
 
 namespace tfa {
@@ -36,7 +41,7 @@ struct IstftCfg {
   static_assert(PAIRS >= 1 && RP >= 4 * F && RP >= 2 * NFFT, "istft tile");
 };
 
-template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = istft_threads(NFFT) / (NFFT / E_)>
+template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = istft_threads(NFFT) / (NFFT / E_), bool ADJ = false>
 __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_kernel(
     const float* __restrict__ sre, const float* __restrict__ sim, const float* __restrict__ win,
     float* __restrict__ out, const float2* __restrict__ tw, int n_frames, int hop, int halo, int owned,
@@ -80,7 +85,7 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
     const int f = i % FR, k = i / FR;
     if (i < F * FR) {
       float* reg = lds + (f >> 1) * RP + (f & 1) * 2 * F;
-      reg[k] = sr[it];
+      reg[k] = (ADJ && (k == 0 || k == NFFT / 2)) ? 2.0f * sr[it] : sr[it];
       reg[F + k] = (k == 0 || k == NFFT / 2) ? 0.0f : si[it];
     }
   }
@@ -145,7 +150,7 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
           raw += x;
         }
       }
-      st_stream(dst + o, norm ? acc * inv : raw);  // non-temporal: whole output rows (C2 inverse 41.5 -> 38.6 us)
+      st_stream(dst + o, ADJ ? acc : norm ? acc * inv : raw);  // non-temporal: whole output rows (C2 inverse 41.5 -> 38.6 us)
     }
     return;  // not the last tile: no zero fill
   }
@@ -163,7 +168,7 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
       raw += x;
       env += w * w;
     }
-    dst[o] = env > 1e-8f ? acc / env : raw;
+    dst[o] = ADJ ? acc : env > 1e-8f ? acc / env : raw;
   }
   // samples past the end of the signal up to the requested length are zero
   if (t0 + owned >= n_frames)
@@ -177,9 +182,14 @@ static hipError_t launch_istft_cfg(const IstftArgs& a) {
   if (owned < 1) return hipErrorInvalidValue;
   const int tiles = (a.n_frames + owned - 1) / owned;
   const long long blocks = a.batch * (long long)tiles;
-  hipLaunchKernelGGL((istft_kernel<NFFT, istft_epth(NFFT), MAXP>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
-                     a.stream, a.spec_re, a.spec_im, a.window, a.out, a.tw, a.n_frames, a.hop, a.halo, owned, tiles,
-                     (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale);
+  if (a.adjoint)
+    hipLaunchKernelGGL((istft_kernel<NFFT, istft_epth(NFFT), MAXP, true>), dim3((unsigned)blocks), dim3(C::THREADS),
+                       0, a.stream, a.spec_re, a.spec_im, a.window, a.out, a.tw, a.n_frames, a.hop, a.halo, owned,
+                       tiles, (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale);
+  else
+    hipLaunchKernelGGL((istft_kernel<NFFT, istft_epth(NFFT), MAXP>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
+                       a.stream, a.spec_re, a.spec_im, a.window, a.out, a.tw, a.n_frames, a.hop, a.halo, owned, tiles,
+                       (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale);
   return hipGetLastError();
 }
 

@@ -895,6 +895,34 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
   return e == hipSuccess ? TFA_OK : hip_fail(e, "istft launch");
 }
 
+int tfa_stft_backward_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, const float* grad_re,
+                              const float* grad_im, const float* window, float* grad_padded, int64_t padded_len,
+                              tfa_stream stream) {
+  if (!plan || plan->d.kind != TFA_KIND_STFT || !plan->d.inverse)
+    return fail(TFA_ERR_INVALID, "the STFT backward runs on an inverse STFT plan");
+  if (batch < 0) return fail(TFA_ERR_INVALID, "negative batch");
+  if (batch == 0) return TFA_OK;
+  if (!grad_re || !grad_im || !window || !grad_padded) return fail(TFA_ERR_INVALID, "null data pointer");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
+    return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  const int64_t n_fft = plan->d.n, hop = plan->d.hop;
+  if (n_frames < 1) return fail(TFA_ERR_INVALID, "need at least one frame");
+  // frames n_fft + (n_frames - 1) * hop long reach into the padded signal; the rest has no gradient
+  const int64_t covered = n_fft + (n_frames - 1) * hop;
+  if (covered > padded_len || n_frames != 1 + (padded_len - n_fft) / hop)
+    return fail(TFA_ERR_INVALID, "n_frames does not match padded_len");
+  if (padded_len > INT32_MAX / 2) return fail(TFA_ERR_UNSUPPORTED, "signal too long");
+  note_capture(plan, stream);
+  const double sc = 0.5 * ((plan->d.flags & TFA_STFT_NORMALIZED) ? 1.0 / std::sqrt((double)n_fft) : 1.0);
+  tfa::IstftArgs a{grad_re, grad_im, window, grad_padded, plan->inv.tw, (int)n_frames, (int)hop,
+                   (int)((n_fft - 1) / hop), batch, covered, 0, covered, padded_len, (float)sc,
+                   static_cast<hipStream_t>(stream)};
+  a.adjoint = true;
+  hipError_t e = tfa::launch_istft((int)n_fft, a);
+  return e == hipSuccess ? TFA_OK : hip_fail(e, "stft backward launch");
+}
+
 int tfa_complex_gemm_ex(int64_t m, int64_t n, int64_t k, const float* a_re, const float* a_im, int64_t lda,
                         int32_t a_op, const float* b_re, const float* b_im, int64_t ldb, int32_t b_op, float alpha,
                         const float* bias_re, const float* bias_im, float* c_re, float* c_im, int64_t ldc,

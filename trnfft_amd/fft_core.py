@@ -275,6 +275,28 @@ def execute_stft(x: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int, cente
     return out_re, out_im
 
 
+def execute_stft_backward(g_re: torch.Tensor, g_im: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int,
+                          center: bool, normalized: bool, padded_len: int) -> torch.Tensor | None:
+    """Gradient of the onesided fused STFT with respect to its padded signal, (b, padded_len),
+    from the output gradient planes (b, bins, frames): one fused kernel (per-frame r2c adjoint,
+    window, overlap-add; replaces the autograd of trnfft/api.py:310-349's frame gather, window and
+    per-frame transform).  None when the inverse-STFT tile refuses the hop (the caller composes)."""
+    flags = _lib.STFT_ONESIDED | (_lib.STFT_CENTER if center else 0) | (_lib.STFT_NORMALIZED if normalized else 0)
+    dev = g_re.device
+    try:
+        plan = native_plan(_lib.KIND_STFT, n_fft, True, dev.index, hop=hop, flags=flags)
+    except NotImplementedError:
+        return None
+    g_re, g_im, win = g_re.contiguous(), g_im.contiguous(), win.contiguous()
+    b, frames = g_re.shape[0], g_re.shape[-1]
+    out = torch.empty(b, padded_len, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tfa_stft_backward_execute(plan.handle, b, frames, ptr(g_re), ptr(g_im), ptr(win), ptr(out),
+                                                  padded_len, stream_handle(dev))
+    _lib.check(rc, "tfa_stft_backward_execute")
+    return out
+
+
 def strided_ok(n: int, stride: int) -> bool:
     if stride < 1 or n < 2:
         return False
