@@ -35,7 +35,9 @@ def test_plan_kind_limits():
     for kind, n, extra in [(_lib.KIND_REAL, 3, {}), (_lib.KIND_REAL, 65536, {}), (_lib.KIND_C2C, 1000, {}),
                            (_lib.KIND_STFT, 3000, {"hop": 10}), (_lib.KIND_STFT, 6, {"hop": 2}),
                            (_lib.KIND_STFT, 2049, {"hop": 10}),  # two-sided: 4097 points
-                           (_lib.KIND_STFT, 400, {"hop": 100, "inverse": 1, "flags": _lib.STFT_ONESIDED}),
+                           (_lib.KIND_STFT, 400, {"hop": 100, "inverse": 1}),  # two-sided inverse
+                           (_lib.KIND_STFT, 400, {"hop": 10, "inverse": 1, "flags": _lib.STFT_ONESIDED}),  # halo
+                           (_lib.KIND_STFT, 2049, {"hop": 500, "inverse": 1, "flags": _lib.STFT_ONESIDED}),
                            (_lib.KIND_STFT, 8192, {"hop": 10}), (_lib.KIND_FFT2, 8192, {"n2": 64}),
                            (_lib.KIND_STFT, 512, {"hop": 0}), (_lib.KIND_DFT_GEMM, 8192, {}), (99, 8, {})]:
         rc, h = _plan(kind, n, **extra)

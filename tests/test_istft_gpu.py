@@ -99,3 +99,65 @@ def test_istft_small_hop_falls_back_to_composition():
     got = trnfft_amd.istft(ComplexTensor(re.cuda(), im.cuda()), n_fft, hop_length=hop)
     ref = oracle.istft((re, im), n_fft, hop_length=hop)
     assert _rel(got, ref) <= 1e-4
+
+
+BLUE_CASES = [
+    # n_fft, hop, frames, center, normalized, length; m = the inverse chain's length (>= 2 n_fft - 1)
+    (400, 160, 101, True, False, None),     # m 1024
+    (400, 100, 60, True, True, None),
+    (320, 160, 50, True, False, 9000),      # m 768; longer length: zero fill
+    (9, 2, 40, True, False, None),          # m 32
+    (12, 3, 80, True, False, None),
+    (30, 7, 70, False, False, None),        # m 64
+    (40, 10, 50, True, False, None),        # m 96
+    (50, 60, 20, False, False, None),       # m 128; hop > n_fft
+    (90, 30, 40, True, False, None),        # m 192
+    (99, 33, 30, True, False, None),        # m 256; odd n_fft
+    (100, 25, 40, True, False, 900),        # shorter length: truncation
+    (150, 50, 30, True, True, None),        # m 384
+    (200, 80, 30, True, False, None),       # m 512
+    (600, 150, 20, True, False, None),      # m 1536
+    (1000, 250, 12, False, True, None),     # m 2048
+    (1500, 750, 9, True, False, None),      # m 3072
+    (2047, 1024, 6, True, False, None),     # m 4096
+]
+
+
+@pytest.mark.parametrize("n_fft,hop,frames,center,normalized,length", BLUE_CASES)
+def test_istft_non_pow2_matches_reference(n_fft, hop, frames, center, normalized, length):
+    # one inverse Bluestein chain per frame (the reference's fp32 chirp), fused with the
+    # completion, window, overlap-add and envelope
+    from conftest import tol_bluestein
+
+    re, im = _spec((3,), n_fft, frames, seed=n_fft * 3 + hop)
+    x = ComplexTensor(re.cuda(), im.cuda())
+    got = trnfft_amd.istft(x, n_fft, hop_length=hop, center=center, normalized=normalized, length=length)
+    ref = oracle.istft((re, im), n_fft, hop_length=hop, center=center, normalized=normalized, length=length)
+    assert got.shape == ref.shape
+    assert _rel(got, ref) <= tol_bluestein(n_fft)
+    assert trnfft_amd.api._istft_fused(x, n_fft, hop, n_fft, None, center, normalized, True, length) is not None
+
+
+@pytest.mark.parametrize("n_fft,hop,frames", [(400, 10, 120), (2047, 512, 8)])
+def test_istft_non_pow2_small_hop_composes(n_fft, hop, frames):
+    # a halo of more than half the fused tile: the composed path (frame inverse transforms +
+    # overlap-add)
+    from conftest import tol_bluestein
+
+    re, im = _spec((2,), n_fft, frames, seed=6)
+    x = ComplexTensor(re.cuda(), im.cuda())
+    assert trnfft_amd.api._istft_fused(x, n_fft, hop, n_fft, None, True, False, True, None) is None
+    got = trnfft_amd.istft(x, n_fft, hop_length=hop)
+    ref = oracle.istft((re, im), n_fft, hop_length=hop)
+    assert _rel(got, ref) <= tol_bluestein(n_fft)
+
+
+def test_stft_istft_roundtrip_non_pow2():
+    # C2's signals at n_fft 400 / hop 160 through both fused per-frame Bluestein kernels
+    from bench import make_stft_input
+
+    x = make_stft_input(8, 160000).cuda()
+    spec = trnfft_amd.stft(x, n_fft=400, hop_length=160)
+    y = trnfft_amd.istft(spec, n_fft=400, hop_length=160, length=160000)
+    assert y.shape == x.shape
+    assert _rel(y, x) <= 1e-4

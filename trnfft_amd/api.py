@@ -365,9 +365,11 @@ def istft(
 ) -> torch.Tensor:
     """Inverse STFT by overlap-add with window-sum normalisation (trnfft/api.py:368-470).
 
-    Onesided spectra of power-of-two n_fft run as one fused kernel (completion, inverse
-    transform, window, overlap-add, envelope division, trim); when gradients are needed, or for
-    two-sided input, the same steps run as a composition of the differentiable kernels.
+    Onesided spectra run as one fused kernel (completion, inverse transform -- two frames per
+    transform for power-of-two n_fft in [16, 4096], one inverse Bluestein chain per frame for other
+    n_fft in [9, 2048] -- window, overlap-add, envelope division, trim); when gradients are
+    needed, for two-sided input, other n_fft or hops too short for the kernel's frame tile, the
+    same steps run as a composition of the differentiable kernels.
     """
     if hop_length is None:
         hop_length = n_fft // 4
@@ -433,8 +435,11 @@ def _istft_fused(spec, n_fft, hop, win_length, window, center, normalized, onesi
     from .plan import native_plan
 
     re, im = spec.real, spec.imag
-    if (not onesided or n_fft < 16 or n_fft > 4096 or n_fft & (n_fft - 1) or re.dim() < 2
-            or re.shape[-2] != n_fft // 2 + 1 or re.shape[-1] < 1 or _ag._grad_on(re, im, window)):
+    # power-of-two n_fft in [16, 4096] (two frames per inverse transform), other n_fft in
+    # [9, 2048] (one inverse Bluestein chain per frame)
+    pow2 = n_fft & (n_fft - 1) == 0
+    if (not onesided or (pow2 and not 16 <= n_fft <= 4096) or (not pow2 and not 9 <= n_fft <= 2048)
+            or re.dim() < 2 or re.shape[-2] != n_fft // 2 + 1 or re.shape[-1] < 1 or _ag._grad_on(re, im, window)):
         return None
     _resolve(None)
     _require_hip("istft")

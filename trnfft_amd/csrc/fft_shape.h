@@ -212,5 +212,22 @@ __host__ __device__ constexpr int stft_blue_area(int m, int frames) {
   while (a % 64 != g) a += 4;
   return a;
 }
+// Inverse STFT at n_fft that is not a power of two (one inverse Bluestein chain per frame, m >=
+// 2n - 1 since every sample of a frame is kept): elements per thread and frames per workgroup
+// (owned frames + the recomputed halo of floor((n-1)/hop) frames; up to 1024 threads within the
+// LDS, which also holds the window).  Measured on MI355X (64 signals, 160000 output samples):
+// n_fft 400 / hop 160 (m 1024) E = 16 with 16 frames 321 us against 355 for E = 8 with 8 and 336
+// for E = 32 with 16 (hop 100: 526 / 649 / 559); n_fft 320 (m 768) E = 12 with 8 frames 219 us
+// against 229-258 for the others; n_fft 1000 / hop 250 (m 2048) E = 16 with 8 frames 662 us
+// against 711 for E = 32 (fewer frames per workgroup recompute more halo: 1348-1660).
+__host__ __device__ constexpr int istft_blue_epth(int m) {
+  return m == 768 ? 12 : m % 3 == 0 ? stft_blue_epth(m) : m >= 1024 ? 16 : 8;
+}
+__host__ __device__ constexpr int istft_blue_frames(int m) {
+  int f = m == 768 ? 8 : 1024 / (m / istft_blue_epth(m));
+  f = f > 64 ? 64 : f < 1 ? 1 : f;
+  while (f > 1 && f * stft_blue_area(m, f) * 4 + m * 2 > 160 * 1024) f /= 2;
+  return f;
+}
 
 }  // namespace tfa

@@ -270,9 +270,17 @@ struct IstftArgs {
   // the others (scale 1/2 then gives the r2c adjoint), the windowed sum is written as it is (no
   // envelope division, no raw-sum branch)
   bool adjoint = false;
+  // n_fft that is not a power of two (one inverse Bluestein chain per frame, length m): forward
+  // and inverse m-point tables, the inverse chirp (n_fft) and its filter spectrum H/m (m)
+  const float2* blue_tw_f = nullptr;
+  const float2* blue_tw_i = nullptr;
+  const float2* chirp = nullptr;
+  const float2* hs = nullptr;
+  int m = 0;
 };
 hipError_t launch_istft(int n_fft, const IstftArgs& a);
 int istft_frames_per_tile(int n_fft);
+hipError_t launch_istft_blue(int n_fft, const IstftArgs& a);  // a.m != 0
 
 struct Fft2Args {
   const float* in_re;

@@ -1,5 +1,6 @@
-// Fused STFT for n_fft that is not a power of two: framing + reflect padding + window + one
-// Bluestein transform per frame + onesided slice + (freq, time) layout in one kernel.
+// Fused STFT and inverse STFT for n_fft that is not a power of two: one Bluestein chain per frame
+// (framing, padding, window and the (freq, time) layout fused in the forward kernel; completion,
+// window, overlap-add and envelope in the inverse kernel).
 #include "kernels.h"
 
 namespace tfa {
@@ -135,6 +136,167 @@ hipError_t launch_stft_blue(int n_fft, const StftArgs& a) {
     case 2048: return launch_stft_blue_m<2048>(n_fft, a);
     case 3072: return launch_stft_blue_m<3072>(n_fft, a);
     case 4096: return launch_stft_blue_m<4096>(n_fft, a);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Inverse STFT of onesided spectra at n_fft that is not a power of two (trnfft/api.py:368-470:
+// Hermitian completion, an inverse transform per frame -- the reference's Bluestein chain with
+// its fp32 chirp of sign +1 -- real part, window, overlap-add, envelope division or raw sum,
+// centre trim).  The tiling is the power-of-two inverse kernel's: a workgroup owns the output
+// samples of `owned` frames and also transforms the halo = floor((n-1)/hop) frames before them.
+//   1. the bins of FR consecutive frames are staged in the frames' LDS areas (lanes over frames:
+//      each load reads consecutive frames of one bin row);
+//   2. each frame's T threads form the completed spectrum times the chirp (X[n-k] = conj X[k];
+//      the imaginary parts of bins 0 and n/2 are kept, as the reference keeps them), transform
+//      forward, multiply by H/M, transform back, and keep Re(w[t] chirp[t]) * scale, t < n;
+//   3. every owned sample gathers its covering frames from LDS (windowed sum, raw sum, envelope).
+// M >= 2n - 1 (all n outputs of each frame are kept), so inputs and outputs are the elements
+// e < E/2 of each thread.
+template <int M, int E, int FR>
+struct IstftBlueCfg {
+  static constexpr int T = M / E;
+  static constexpr bool WL = T <= 64;
+  static constexpr int AREA = stft_blue_area(M, FR);
+  static constexpr int THREADS = FR * T;
+  static_assert(FR * AREA * 4 + (M / 2) * 4 <= kLdsBytes, "inverse STFT frame tile exceeds LDS");
+};
+
+template <int M, int E, int FR>
+__global__ __launch_bounds__((IstftBlueCfg<M, E, FR>::THREADS)) void istft_blue_kernel(
+    const float* __restrict__ sre, const float* __restrict__ sim, const float* __restrict__ win,
+    float* __restrict__ out, const float2* __restrict__ chirp, const float2* __restrict__ hs,
+    const float2* __restrict__ tw_f, const float2* __restrict__ tw_i, int n, int n_frames, int hop, int halo,
+    int owned, int tiles_per_signal, int expected_len, int start, int write_len, int out_pitch, float scale) {
+  using C = IstftBlueCfg<M, E, FR>;
+  constexpr int T = C::T, EH = E / 2, AREA = C::AREA, THREADS = C::THREADS;
+  __shared__ __attribute__((aligned(16))) float lds[FR * AREA];
+  __shared__ float wl[M / 2];
+  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
+  const long long b = tile / tiles_per_signal;
+  const int t0 = (int)(tile % tiles_per_signal) * owned;  // first owned frame
+  const int ta = t0 - halo > 0 ? t0 - halo : 0;          // first frame of the tile
+  const int nf = (t0 + owned < n_frames ? t0 + owned : n_frames) - ta;  // frames in the tile (<= FR)
+  const int K = n / 2 + 1;  // onesided bins
+
+  for (int i = threadIdx.x; i < n; i += THREADS) wl[i] = win[i];
+  // 1. stage bins: frame f's area = [re (K) | im (K)]; four loads in flight per thread
+  const size_t sbase = (size_t)b * K * n_frames + ta;
+  for (int i0 = threadIdx.x; i0 < K * FR; i0 += 4 * THREADS) {
+    float sr[4], si[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * THREADS, f = i % FR, k = i / FR;
+      sr[u] = 0.0f;
+      si[u] = 0.0f;
+      if (i < K * FR && f < nf) {
+        sr[u] = sre[sbase + (size_t)k * n_frames + f];
+        si[u] = sim[sbase + (size_t)k * n_frames + f];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * THREADS, f = i % FR, k = i / FR;
+      if (i < K * FR) {
+        lds[f * AREA + k] = sr[u];
+        lds[f * AREA + K + k] = si[u];
+      }
+    }
+  }
+  __syncthreads();
+  // 2. completed spectrum times the chirp, Bluestein chain
+  const int fl = threadIdx.x / T, tid = threadIdx.x % T;
+  float* my = lds + fl * AREA;
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int j = tid + T * e;
+    float2 y = make_float2(0.0f, 0.0f);
+    if (e < EH && j < n) {
+      const float2 x = j < K ? make_float2(my[j], my[K + j]) : make_float2(my[n - j], -my[K + n - j]);
+      y = cmul(x, chirp[j]);
+    }
+    v[e] = y;
+  }
+  // the transform reuses the frame's area
+  if constexpr (C::WL) exchange_sync<true>();
+  else __syncthreads();
+  constexpr bool PF = blue_pf(M);
+  LdsFft<M, E, -1, C::WL, false, true, PF>::run(v, my, nullptr, tw_f, tid);
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], hs[tid + T * e]);
+  LdsFft<M, E, 1, C::WL, false, true, PF>::run(v, my, nullptr, tw_i, tid);
+  if constexpr (!C::WL) __syncthreads();
+#pragma unroll
+  for (int e = 0; e < EH; ++e) {
+    const int t = tid + T * e;
+    if (t < n) {
+      const float2 c = chirp[t];
+      my[t] = (v[e].x * c.x - v[e].y * c.y) * scale;  // Re(w[t] chirp[t]) / n
+    }
+  }
+  __syncthreads();
+  // 3. owned samples [t0*hop, (t0+owned)*hop), the last tile up to the end of the signal; each
+  //    gathers its covering frames t, t-1, ... (offsets s - t*hop < n)
+  const int s_lo = t0 * hop;
+  const long long s_end = (long long)(t0 + owned) * hop;
+  const int s_hi = (t0 + owned >= n_frames || s_end > expected_len) ? expected_len : (int)s_end;
+  float* dst = out + (size_t)b * out_pitch;
+  const int t_end = ta + nf - 1;
+  for (int s = s_lo + (int)threadIdx.x; s < s_hi; s += THREADS) {
+    const int o = s - start;
+    if (o < 0 || o >= write_len) continue;
+    int t = (int)((unsigned)s / (unsigned)hop);
+    if (t > t_end) t = t_end;
+    float acc = 0.0f, raw = 0.0f, env = 0.0f;
+    for (int j = s - t * hop; t >= ta && j < n; --t, j += hop) {
+      const float x = lds[(t - ta) * AREA + j];
+      const float w = wl[j];
+      acc += x * w;
+      raw += x;
+      env += w * w;
+    }
+    dst[o] = env > 1e-8f ? acc / env : raw;
+  }
+  // samples past the end of the signal up to the requested length are zero
+  if (t0 + owned >= n_frames)
+    for (int o = write_len + (int)threadIdx.x; o < out_pitch; o += THREADS) dst[o] = 0.0f;
+}
+
+template <int M>
+static hipError_t launch_istft_blue_m(int n_fft, const IstftArgs& a) {
+  constexpr int E = istft_blue_epth(M);
+  constexpr int FR = istft_blue_frames(M);
+  using C = IstftBlueCfg<M, E, FR>;
+  if (2 * n_fft - 1 > M || a.halo < 0 || a.hop < 1) return hipErrorInvalidValue;
+  const int owned = FR - a.halo;
+  if (owned < 1) return hipErrorInvalidValue;
+  const int tiles = (a.n_frames + owned - 1) / owned;
+  const long long blocks = a.batch * (long long)tiles;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((istft_blue_kernel<M, E, FR>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream,
+                     a.spec_re, a.spec_im, a.window, a.out, a.chirp, a.hs, a.blue_tw_f, a.blue_tw_i, n_fft,
+                     a.n_frames, a.hop, a.halo, owned, tiles, (int)a.expected_len, (int)a.start, (int)a.write_len,
+                     (int)a.out_pitch, a.scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_istft_blue(int n_fft, const IstftArgs& a) {
+  switch (a.m) {
+    case 32: return launch_istft_blue_m<32>(n_fft, a);
+    case 64: return launch_istft_blue_m<64>(n_fft, a);
+    case 96: return launch_istft_blue_m<96>(n_fft, a);
+    case 128: return launch_istft_blue_m<128>(n_fft, a);
+    case 192: return launch_istft_blue_m<192>(n_fft, a);
+    case 256: return launch_istft_blue_m<256>(n_fft, a);
+    case 384: return launch_istft_blue_m<384>(n_fft, a);
+    case 512: return launch_istft_blue_m<512>(n_fft, a);
+    case 768: return launch_istft_blue_m<768>(n_fft, a);
+    case 1024: return launch_istft_blue_m<1024>(n_fft, a);
+    case 1536: return launch_istft_blue_m<1536>(n_fft, a);
+    case 2048: return launch_istft_blue_m<2048>(n_fft, a);
+    case 3072: return launch_istft_blue_m<3072>(n_fft, a);
+    case 4096: return launch_istft_blue_m<4096>(n_fft, a);
     default: return hipErrorInvalidValue;
   }
 }

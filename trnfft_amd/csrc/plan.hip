@@ -503,23 +503,41 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         // trnfft/fft_core.py:1285-1376): chirp, the filter spectrum H/m of the taps that the kept
         // bins read, and the two m-point LDS tables; m is the shortest power of two or 3 * 2^k
         // with n + n_bins - 1 <= m (the reference pads to the power of two >= 2n - 1)
+        // (inverse: every sample of a frame is kept, so m >= 2n - 1, with the chirp of sign +1,
+        // trnfft/api.py:412-417 -> fft_core.py:1285-1376)
         const int64_t bins = (desc->flags & TFA_STFT_ONESIDED) ? n / 2 + 1 : n;
+        const int64_t conv = desc->inverse ? 2 * n - 1 : n + bins - 1;
         int64_t m = 0;
         for (int64_t c = tfa::kStftBlueMinM; c <= tfa::kStftBlueMaxM && !m; ++c)
-          if (tfa::stft_blue_len_ok(c) && n + bins - 1 <= c && n <= tfa::stft_blue_nmax((int)c)) m = c;
-        if (desc->inverse || n < 9 || m == 0) {
-          rc = fail(TFA_ERR_UNSUPPORTED, "fused STFT: forward only for n_fft that is not a power of two, 9..2731 onesided or 9..2048 two-sided");
+          if (tfa::stft_blue_len_ok(c) && conv <= c && n <= tfa::stft_blue_nmax((int)c)) m = c;
+        if (n < 9 || m == 0) {
+          rc = fail(TFA_ERR_UNSUPPORTED, desc->inverse
+                        ? "fused inverse STFT: n_fft that is not a power of two must lie in 9..2048"
+                        : "fused STFT: n_fft that is not a power of two must lie in 9..2731 onesided or 9..2048 two-sided");
           break;
         }
+        if (desc->inverse) {
+          if (!(desc->flags & TFA_STFT_ONESIDED)) {
+            rc = fail(TFA_ERR_UNSUPPORTED, "fused inverse STFT takes onesided spectra");
+            break;
+          }
+          // a halo of more than half the tile recomputes more frames than it owns: the composed
+          // path is faster there
+          if (2 * ((n - 1) / desc->hop) > tfa::istft_blue_frames((int)m)) {
+            rc = fail(TFA_ERR_UNSUPPORTED, "hop_length too small for the fused inverse STFT tile");
+            break;
+          }
+        }
+        const int e = desc->inverse ? tfa::istft_blue_epth((int)m) : tfa::stft_blue_epth((int)m);
         p->m = p->mf = m;
         p->fwd.n = p->inv.n = m;
         p->fwd.dir = -1;
         p->inv.dir = 1;
-        const std::vector<float2> chirp = reference_chirp(n, -1);
-        if ((rc = p->upload(lds_table((int)m, -1, tfa::stft_blue_epth((int)m)), &p->fwd.tw))) break;
-        if ((rc = p->upload(lds_table((int)m, 1, tfa::stft_blue_epth((int)m)), &p->inv.tw))) break;
+        const std::vector<float2> chirp = reference_chirp(n, desc->inverse ? 1 : -1);
+        if ((rc = p->upload(lds_table((int)m, -1, e), &p->fwd.tw))) break;
+        if ((rc = p->upload(lds_table((int)m, 1, e), &p->inv.tw))) break;
         if ((rc = p->upload(chirp, &p->chirp))) break;
-        rc = p->upload(blue_filter_spectrum(chirp, m, bins), &p->hs);
+        rc = p->upload(blue_filter_spectrum(chirp, m, desc->inverse ? n : bins), &p->hs);
         break;
       }
       if (n < 16 || n > 4096) {
@@ -891,7 +909,17 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
   tfa::IstftArgs a{spec_re, spec_im, window, out, plan->inv.tw, (int)n_frames, (int)hop, (int)((n_fft - 1) / hop),
                    batch, expected, start, cur < out_len ? cur : out_len, out_len, (float)sc,
                    static_cast<hipStream_t>(stream)};
-  hipError_t e = tfa::launch_istft((int)n_fft, a);
+  hipError_t e;
+  if (!is_pow2(n_fft)) {
+    a.blue_tw_f = plan->fwd.tw;
+    a.blue_tw_i = plan->inv.tw;
+    a.chirp = plan->chirp;
+    a.hs = plan->hs;
+    a.m = (int)plan->m;
+    e = tfa::launch_istft_blue((int)n_fft, a);
+  } else {
+    e = tfa::launch_istft((int)n_fft, a);
+  }
   return e == hipSuccess ? TFA_OK : hip_fail(e, "istft launch");
 }
 
@@ -900,6 +928,7 @@ int tfa_stft_backward_execute(const tfa_plan* plan, int64_t batch, int64_t n_fra
                               tfa_stream stream) {
   if (!plan || plan->d.kind != TFA_KIND_STFT || !plan->d.inverse)
     return fail(TFA_ERR_INVALID, "the STFT backward runs on an inverse STFT plan");
+  if (!is_pow2(plan->d.n)) return fail(TFA_ERR_UNSUPPORTED, "the fused STFT backward takes a power-of-two n_fft");
   if (batch < 0) return fail(TFA_ERR_INVALID, "negative batch");
   if (batch == 0) return TFA_OK;
   if (!grad_re || !grad_im || !window || !grad_padded) return fail(TFA_ERR_INVALID, "null data pointer");
