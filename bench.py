@@ -341,7 +341,14 @@ def bench_secondary():
                                                    P(os_[k][1]), st)), S)
     rec("stft_64x160000_nfft400", t, 64 * frames * 2 * 5 * 768 * math.log2(768), nbytes, sets=S,
         note="non-power-of-two n_fft: two 768-point transforms per frame (gflops counts those), VALU-bound")
-    del xs, os_
+    # its inverse: one inverse Bluestein chain per frame (1024 points: every sample is kept)
+    ip400 = native_plan(_lib.KIND_STFT, 400, True, dev.index, hop=160, flags=_lib.STFT_CENTER | _lib.STFT_ONESIDED)
+    ys = [torch.empty(64, 160000, device=dev) for _ in range(S)]
+    t = _time_rot(lambda k, st: chk(L.tfa_istft_execute(ip400.handle, 64, frames, P(os_[k][0]), P(os_[k][1]),
+                                                        P(w400), P(ys[k]), 160000, st)), S)
+    rec("istft_64x201x1001_nfft400", t, 64 * frames * 2 * 5 * 1024 * 10, nbytes, sets=S,
+        note="inverse of the n_fft 400 line: two 1024-point transforms per frame (gflops counts those), VALU-bound")
+    del xs, os_, ys
     # C3: Bluestein (fused, one launch)
     for n, b in [(1000, 1024), (4099, 256)]:
         nbytes = 4 * b * n * 4
