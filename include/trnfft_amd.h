@@ -177,12 +177,15 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
  * (batch, padded_len), padded_len = num_samples + 2*(n/2) when CENTER else num_samples, n_frames
  * = 1 + (padded_len - n)/hop.  Per frame the adjoint of the r2c transform (interior bins halved,
  * Hermitian-completed inverse transform, unscaled; 1/sqrt(n) when NORMALIZED), times the window,
- * overlap-added; samples no frame covers get zero.  Undoing the centre padding (the reflected
- * edges folded back) is left to the caller.  Runs on the inverse STFT plan of the same n, hop
- * and flags (its table and tile shape; hops the inverse plan refuses are refused there).
- * Replaces the backward that torch autograd derives for trnfft/api.py:310-349 (pad, frame index,
- * window multiply, per-frame transform): a gather-transpose of the gradient, an inverse transform
- * per frame and an index_add/fold overlap-add.
+ * overlap-added; samples no frame covers get zero.  n_fft that is not a power of two: per frame
+ * the adjoint of the Bluestein chain the forward kernel runs (conj(chirp) times the gradient,
+ * convolved with chirp[|s|], times conj(chirp)).  Undoing the centre padding (the reflected edges
+ * folded back) is left to the caller.  Runs on the forward STFT plan of the call being
+ * differentiated (ONESIDED required); a hop whose recomputed halo frames would fill the kernel's
+ * frame tile returns TFA_ERR_UNSUPPORTED.  Replaces the backward that torch autograd derives for
+ * trnfft/api.py:310-349 (pad, frame index, window multiply, per-frame transform): a
+ * gather-transpose of the gradient, an inverse transform per frame and an index_add/fold
+ * overlap-add.
  */
 int tfa_stft_backward_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, const float* grad_re,
                               const float* grad_im, const float* window, float* grad_padded, int64_t padded_len,

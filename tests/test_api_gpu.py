@@ -186,17 +186,18 @@ def test_stft_fused_bluestein_frames_vs_oracle(n_fft, hop, center, onesided, nor
 
 @pytest.mark.parametrize("n_fft,hop,pad_mode", [(400, 160, "reflect"), (1000, 256, "constant"), (99, 33, "circular")])
 def test_stft_fused_bluestein_matches_composed_path(n_fft, hop, pad_mode):
-    # the same call under autograd takes the composed path (frame gather + Bluestein rows); both
-    # run the reference's chain, so they agree to fp32 rounding
+    # the reference's composition on the device (pad, frame gather, window, Bluestein rows of
+    # rfft, transpose) against the fused kernel: both run the reference's chain, so they agree
+    # to fp32 rounding
     g = torch.Generator().manual_seed(13)
     x = torch.randn(3, 12000, generator=g).cuda()
-    with torch.no_grad():
-        fused = trnfft_amd.stft(x, n_fft=n_fft, hop_length=hop, pad_mode=pad_mode)
-    xg = x.clone().requires_grad_(True)
-    comp = trnfft_amd.stft(xg, n_fft=n_fft, hop_length=hop, pad_mode=pad_mode)
-    assert comp.real.requires_grad
-    assert fused.shape == comp.shape
-    assert rel_l2(fused.real, fused.imag, comp.real.detach(), comp.imag.detach()) <= tol_bluestein(n_fft) / 4
+    fused = trnfft_amd.stft(x, n_fft=n_fft, hop_length=hop, pad_mode=pad_mode)
+    w = torch.hann_window(n_fft, device="cuda")
+    xp = torch.nn.functional.pad(x.unsqueeze(1), (n_fft // 2, n_fft // 2), mode=pad_mode).squeeze(1)
+    spec = trnfft_amd.rfft((xp.unfold(-1, n_fft, hop) * w).contiguous())
+    assert fused.shape == spec.real.transpose(-2, -1).shape
+    assert rel_l2(fused.real, fused.imag, spec.real.transpose(-2, -1), spec.imag.transpose(-2, -1)) \
+        <= tol_bluestein(n_fft) / 4
 
 
 def test_stft_win_length_below_n_fft_and_custom_window_composed():

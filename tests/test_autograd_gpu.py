@@ -253,6 +253,66 @@ def test_stft_gradient_fused_backward(n_fft, hop, center, normalized, shape, mon
     assert _rel(a.grad, r.grad) <= TOL
 
 
+@pytest.mark.parametrize("n_fft,hop,center,normalized,shape", [
+    (400, 160, True, False, (2, 4000)),       # convolution length 768
+    (400, 100, False, True, (2, 3, 3000)),
+    (12, 4, True, False, (2, 301)),           # 32
+    (30, 10, True, False, (2, 500)),          # 64
+    (100, 40, True, False, (2, 2000)),        # 192
+    (257, 128, True, False, (2, 3000)),       # 512
+    (600, 200, True, False, (1, 5000)),       # 1024
+    (1000, 300, True, True, (1, 6000)),       # 1536
+    (2000, 1000, True, False, (1, 9000)),     # 3072
+    (400, 500, True, False, (2, 2000)),       # hop > n_fft
+])
+def test_stft_gradient_fused_backward_non_pow2(n_fft, hop, center, normalized, shape, monkeypatch):
+    # n_fft that is not a power of two, window without gradient: the adjoint Bluestein chain per
+    # frame in one kernel, against autograd through the oracle's restatement of the reference's
+    # pytorch path (the reference's operator carries its fp32 chirp)
+    from trnfft_amd import fft_core
+
+    calls = []
+    real = fft_core.execute_stft_backward
+
+    def counted(*args, **kw):
+        out = real(*args, **kw)
+        calls.append(out is not None)
+        return out
+
+    monkeypatch.setattr(fft_core, "execute_stft_backward", counted)
+    g = torch.Generator().manual_seed(n_fft + hop)
+    x = torch.randn(*shape, generator=g)
+    w = torch.hann_window(n_fft) + 0.1 * torch.rand(n_fft, generator=g)
+    a = _leaf(x)
+    y = trnfft_amd.stft(a, n_fft, hop_length=hop, window=w.cuda(), center=center, normalized=normalized)
+    cr, ci = _cotangent(tuple(y.shape), 22)
+    (y.real * cr.float().cuda() + y.imag * ci.float().cuda()).sum().backward()
+    assert calls == [True]
+    r = x.clone().requires_grad_(True)
+    zr, zi = oracle.stft(r, n_fft, hop_length=hop, window=w, center=center, normalized=normalized)
+    assert tuple(zr.shape) == tuple(y.shape)
+    (zr * cr.float() + zi * ci.float()).sum().backward()
+    assert _rel(a.grad, r.grad) <= tol_bluestein(n_fft)
+
+
+@pytest.mark.parametrize("onesided", [True, False])
+def test_stft_gradient_non_pow2_window_and_two_sided_compose(onesided):
+    # window gradients (and two-sided spectra) take the composed adjoint, which zero-fills the
+    # bins above n/2 before the inverse transform when n_fft is not a power of two
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(2, 3000, generator=g)
+    w = torch.hann_window(400) + 0.1 * torch.rand(400, generator=g)
+    a, aw = _leaf(x), _leaf(w)
+    y = trnfft_amd.stft(a, 400, hop_length=160, window=aw, onesided=onesided)
+    cr, ci = _cotangent(tuple(y.shape), 24)
+    (y.real * cr.float().cuda() + y.imag * ci.float().cuda()).sum().backward()
+    r, rw = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    zr, zi = oracle.stft(r, 400, hop_length=160, window=rw, onesided=onesided)
+    (zr * cr.float() + zi * ci.float()).sum().backward()
+    assert _rel(a.grad, r.grad) <= tol_bluestein(400)
+    assert _rel(aw.grad, rw.grad) <= tol_bluestein(400)
+
+
 def test_stft_gradient_short_hop_composes():
     # a hop the inverse-STFT tile refuses: the backward falls back to the composed adjoint
     g = torch.Generator().manual_seed(3)

@@ -260,14 +260,14 @@ def _effective_window(window: torch.Tensor | None, n_fft: int, win_length: int, 
 _STFT_BLUE_MAX_N = {True: 2731, False: 2048}
 
 
-def _fused_stft_ok(n_fft: int, onesided: bool = True, needs_grad: bool = False) -> bool:
+def _fused_stft_ok(n_fft: int, onesided: bool = True) -> bool:
     """Whether the fused STFT kernel takes this n_fft: a power of two in [16, 4096] (two real
-    frames per transform, differentiable), or any other n_fft from 9 up to 2731 (onesided) or
-    2048 (two-sided) (one Bluestein transform per frame, forward only: calls that need
-    gradients keep the composed path)."""
+    frames per transform), or any other n_fft from 9 up to 2731 (onesided) or 2048 (two-sided)
+    (one Bluestein transform per frame).  Both are differentiable: the signal gradient is one
+    fused adjoint kernel where its tile allows, the composed adjoint otherwise."""
     if n_fft & (n_fft - 1) == 0:
         return 16 <= n_fft <= 4096
-    return 9 <= n_fft <= _STFT_BLUE_MAX_N[bool(onesided)] and not needs_grad
+    return 9 <= n_fft <= _STFT_BLUE_MAX_N[bool(onesided)]
 
 
 def stft(
@@ -283,14 +283,13 @@ def stft(
 ) -> ComplexTensor:
     """Short-time Fourier transform, output (..., freq, time) (trnfft/api.py:291-365).
 
-    Power-of-two n_fft in [16, 4096], and other n_fft from 9 to 2731 (2048 two-sided) when no
-    gradient is needed, run as one fused kernel that reads the raw waveform (framing, padding,
-    window, transform -- one Bluestein chain per frame for non-power-of-two n_fft -- and the
-    (freq, time) transpose in one pass); with a pad_mode other than "reflect" the signal is padded on the device first
-    (the reference's F.pad) and the fused kernel frames the padded signal.  Other n_fft, and
-    non-power-of-two n_fft under autograd, keep the reference's composition on the device: pad,
-    frame gather, window, then the transform kernels (Bluestein for non-power-of-two n_fft) and
-    the onesided slice.
+    Power-of-two n_fft in [16, 4096], and other n_fft from 9 to 2731 (2048 two-sided), run as
+    one fused kernel that reads the raw waveform (framing, padding, window, transform -- one
+    Bluestein chain per frame for non-power-of-two n_fft -- and the (freq, time) transpose in one
+    pass); with a pad_mode other than "reflect" the signal is padded on the device first (the
+    reference's F.pad) and the fused kernel frames the padded signal.  Other n_fft keep the
+    reference's composition on the device: pad, frame gather, window, then the transform kernels
+    (Bluestein for non-power-of-two n_fft) and the onesided slice.
     """
     if hop_length is None:
         hop_length = n_fft // 4
@@ -303,8 +302,7 @@ def stft(
     out_dev = input.device
     x = to_device_f32(input, dev)
     win = to_device_f32(win, dev)
-    needs_grad = torch.is_grad_enabled() and (x.requires_grad or win.requires_grad)
-    fused = _fused_stft_ok(n_fft, onesided, needs_grad)
+    fused = _fused_stft_ok(n_fft, onesided)
     if center and pad_mode == "reflect" and fused:
         length = x.shape[-1]
         if length <= n_fft // 2:

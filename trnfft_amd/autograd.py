@@ -195,7 +195,7 @@ class _StftFn(torch.autograd.Function):
         bins = g_re.shape[-2]
         pad = n_fft // 2 if center else 0
         if onesided and ctx.needs_input_grad[0] and not ctx.needs_input_grad[1] and g_re.is_cuda:
-            # no window gradient: one fused kernel (r2c adjoint per frame, window, overlap-add)
+            # no window gradient: one fused kernel (per-frame transform adjoint, window, overlap-add)
             d_xp = _fc.execute_stft_backward(g_re.reshape(b, bins, frames), g_im.reshape(b, bins, frames), win,
                                              n_fft, hop, center, normalized, length + 2 * pad)
             if d_xp is not None:
@@ -203,9 +203,14 @@ class _StftFn(torch.autograd.Function):
         # (..., bins, frames) -> (b, frames, bins): one spectrum per row
         gr = g_re.reshape(b, bins, frames).transpose(1, 2).contiguous()
         gi = g_im.reshape(b, bins, frames).transpose(1, 2).contiguous()
-        if onesided:
+        if onesided and n_fft & (n_fft - 1) == 0:
             fg = _r2c_adjoint(gr, gi, n_fft)  # (b, frames, n_fft)
         else:
+            if bins < n_fft:
+                # onesided, n_fft not a power of two: the adjoint of keeping bins < n_fft/2 + 1 of
+                # the complex transform is zero-filling the rest before its adjoint
+                gr = F.pad(gr, (0, n_fft - bins))
+                gi = F.pad(gi, (0, n_fft - bins))
             fg = _fc.execute_1d(gr, gi, True).real.mul_(float(n_fft))
         if normalized:
             fg.mul_(1.0 / math.sqrt(n_fft))

@@ -229,5 +229,14 @@ __host__ __device__ constexpr int istft_blue_frames(int m) {
   while (f > 1 && f * stft_blue_area(m, f) * 4 + m * 2 > 160 * 1024) f /= 2;
   return f;
 }
+// The forward STFT's signal gradient at such n_fft (the inverse kernel's tiling on the forward
+// plan's length and elements per thread): frames per workgroup, up to 1024 threads within the LDS
+// (which holds the window of up to stft_blue_nmax(m) samples).
+__host__ __device__ constexpr int stft_blue_adj_frames(int m) {
+  int f = 1024 / (m / stft_blue_epth(m));
+  f = f > 64 ? 64 : f < 1 ? 1 : f;
+  while (f > 1 && f * stft_blue_area(m, f) * 4 + stft_blue_nmax(m) * 4 > 160 * 1024) f /= 2;
+  return f;
+}
 
 }  // namespace tfa

@@ -153,25 +153,35 @@ hipError_t launch_stft_blue(int n_fft, const StftArgs& a) {
 //   3. every owned sample gathers its covering frames from LDS (windowed sum, raw sum, envelope).
 // M >= 2n - 1 (all n outputs of each frame are kept), so inputs and outputs are the elements
 // e < E/2 of each thread.
-template <int M, int E, int FR>
+//
+// ADJ: the same tiling computes the gradient of the forward kernel above with respect to its
+// padded signal (the forward plan's M and tables).  The forward map per frame is
+// X[k] = chirp[k] sum_j w[j] x[j] chirp[j] conj(chirp[|k-j|]) (k < n_bins), so the adjoint takes
+// u[k] = conj(chirp[k]) G[k] (k < n_bins, G the output gradient), convolves it with chirp[|s|]
+// over s = -(n_bins-1) .. n-1 (the plan's adjoint filter spectrum; M >= n + n_bins - 1 holds it
+// without wrap-around), keeps Re(conj(chirp[j]) v[j]) for j < n and overlap-adds it times the
+// window (no envelope).  Outputs j < n then reach the elements e < EIN (n <= 2M/3).
+template <int M, int E, int FR, bool ADJ = false>
 struct IstftBlueCfg {
   static constexpr int T = M / E;
   static constexpr bool WL = T <= 64;
   static constexpr int AREA = stft_blue_area(M, FR);
   static constexpr int THREADS = FR * T;
-  static_assert(FR * AREA * 4 + (M / 2) * 4 <= kLdsBytes, "inverse STFT frame tile exceeds LDS");
+  static constexpr int NW = ADJ ? stft_blue_nmax(M) : M / 2;  // longest n_fft: window floats in LDS
+  static constexpr int EOUT = ADJ ? StftBlueCfg<M, E, 1>::EIN : E / 2;
+  static_assert(FR * AREA * 4 + NW * 4 <= kLdsBytes, "inverse STFT frame tile exceeds LDS");
 };
 
-template <int M, int E, int FR>
-__global__ __launch_bounds__((IstftBlueCfg<M, E, FR>::THREADS)) void istft_blue_kernel(
+template <int M, int E, int FR, bool ADJ = false>
+__global__ __launch_bounds__((IstftBlueCfg<M, E, FR, ADJ>::THREADS)) void istft_blue_kernel(
     const float* __restrict__ sre, const float* __restrict__ sim, const float* __restrict__ win,
     float* __restrict__ out, const float2* __restrict__ chirp, const float2* __restrict__ hs,
     const float2* __restrict__ tw_f, const float2* __restrict__ tw_i, int n, int n_frames, int hop, int halo,
     int owned, int tiles_per_signal, int expected_len, int start, int write_len, int out_pitch, float scale) {
-  using C = IstftBlueCfg<M, E, FR>;
-  constexpr int T = C::T, EH = E / 2, AREA = C::AREA, THREADS = C::THREADS;
+  using C = IstftBlueCfg<M, E, FR, ADJ>;
+  constexpr int T = C::T, EH = E / 2, EOUT = C::EOUT, AREA = C::AREA, THREADS = C::THREADS;
   __shared__ __attribute__((aligned(16))) float lds[FR * AREA];
-  __shared__ float wl[M / 2];
+  __shared__ float wl[C::NW];
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
   const long long b = tile / tiles_per_signal;
   const int t0 = (int)(tile % tiles_per_signal) * owned;  // first owned frame
@@ -212,7 +222,12 @@ __global__ __launch_bounds__((IstftBlueCfg<M, E, FR>::THREADS)) void istft_blue_
   for (int e = 0; e < E; ++e) {
     const int j = tid + T * e;
     float2 y = make_float2(0.0f, 0.0f);
-    if (e < EH && j < n) {
+    if constexpr (ADJ) {
+      if (e < EH && j < K) {  // conj(chirp[k]) G[k]
+        const float2 c = chirp[j];
+        y = cmul(make_float2(my[j], my[K + j]), make_float2(c.x, -c.y));
+      }
+    } else if (e < EH && j < n) {
       const float2 x = j < K ? make_float2(my[j], my[K + j]) : make_float2(my[n - j], -my[K + n - j]);
       y = cmul(x, chirp[j]);
     }
@@ -228,11 +243,12 @@ __global__ __launch_bounds__((IstftBlueCfg<M, E, FR>::THREADS)) void istft_blue_
   LdsFft<M, E, 1, C::WL, false, true, PF>::run(v, my, nullptr, tw_i, tid);
   if constexpr (!C::WL) __syncthreads();
 #pragma unroll
-  for (int e = 0; e < EH; ++e) {
+  for (int e = 0; e < EOUT; ++e) {
     const int t = tid + T * e;
     if (t < n) {
       const float2 c = chirp[t];
-      my[t] = (v[e].x * c.x - v[e].y * c.y) * scale;  // Re(w[t] chirp[t]) / n
+      // inverse: Re(w[t] chirp[t]) / n; adjoint: Re(conj(chirp[t]) v[t])
+      my[t] = (ADJ ? v[e].x * c.x + v[e].y * c.y : v[e].x * c.x - v[e].y * c.y) * scale;
     }
   }
   __syncthreads();
@@ -256,29 +272,36 @@ __global__ __launch_bounds__((IstftBlueCfg<M, E, FR>::THREADS)) void istft_blue_
       raw += x;
       env += w * w;
     }
-    dst[o] = env > 1e-8f ? acc / env : raw;
+    dst[o] = ADJ ? acc : env > 1e-8f ? acc / env : raw;
   }
   // samples past the end of the signal up to the requested length are zero
   if (t0 + owned >= n_frames)
     for (int o = write_len + (int)threadIdx.x; o < out_pitch; o += THREADS) dst[o] = 0.0f;
 }
 
-template <int M>
-static hipError_t launch_istft_blue_m(int n_fft, const IstftArgs& a) {
-  constexpr int E = istft_blue_epth(M);
-  constexpr int FR = istft_blue_frames(M);
-  using C = IstftBlueCfg<M, E, FR>;
-  if (2 * n_fft - 1 > M || a.halo < 0 || a.hop < 1) return hipErrorInvalidValue;
+template <int M, int E, int FR, bool ADJ>
+static hipError_t launch_istft_blue_cfg(int n_fft, const IstftArgs& a) {
+  using C = IstftBlueCfg<M, E, FR, ADJ>;
+  const int bins = n_fft / 2 + 1;
+  if (ADJ ? (n_fft + bins - 1 > M || n_fft > stft_blue_nmax(M)) : 2 * n_fft - 1 > M) return hipErrorInvalidValue;
+  if (a.halo < 0 || a.hop < 1) return hipErrorInvalidValue;
   const int owned = FR - a.halo;
   if (owned < 1) return hipErrorInvalidValue;
   const int tiles = (a.n_frames + owned - 1) / owned;
   const long long blocks = a.batch * (long long)tiles;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((istft_blue_kernel<M, E, FR>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream,
+  hipLaunchKernelGGL((istft_blue_kernel<M, E, FR, ADJ>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream,
                      a.spec_re, a.spec_im, a.window, a.out, a.chirp, a.hs, a.blue_tw_f, a.blue_tw_i, n_fft,
                      a.n_frames, a.hop, a.halo, owned, tiles, (int)a.expected_len, (int)a.start, (int)a.write_len,
                      (int)a.out_pitch, a.scale);
   return hipGetLastError();
+}
+
+template <int M>
+static hipError_t launch_istft_blue_m(int n_fft, const IstftArgs& a) {
+  // the adjoint runs on the forward plan's tables (the forward kernel's elements per thread)
+  if (a.adjoint) return launch_istft_blue_cfg<M, stft_blue_epth(M), stft_blue_adj_frames(M), true>(n_fft, a);
+  return launch_istft_blue_cfg<M, istft_blue_epth(M), istft_blue_frames(M), false>(n_fft, a);
 }
 
 hipError_t launch_istft_blue(int n_fft, const IstftArgs& a) {

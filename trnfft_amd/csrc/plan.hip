@@ -101,6 +101,7 @@ struct tfa_plan {
   float2* hs = nullptr;
   float2 *b_tw_sf = nullptr, *b_tw_si = nullptr;  // Bluestein m <= 4096: strided-axis kernel tables
   float2* b_hs_s = nullptr;  // Bluestein m <= 4096: strided-axis filter spectrum (length m; hs when mf == m)
+  float2* stft_hs_adj = nullptr;  // forward STFT, n_fft not a power of two: the adjoint chain's filter spectrum
   int blue_wrap = 0;         // Bluestein: 2n - 1 - mf when the fused length wraps the convolution
   C2cTables col;          // FFT2: LDS table for n2/8 (pass 2)
   float2* tw_h = nullptr;  // FFT2: W_{n2}^i, i < n2
@@ -335,20 +336,31 @@ std::vector<float2> reference_chirp(int64_t n, int sign) {
 // below 2n - 1 the taps i and L - i (i > L - n) share a slot and are summed (the wrapped fused
 // kernel corrects the outputs they reach).  kmax < n keeps only the taps -(n-1) .. kmax-1, all
 // that outputs k < kmax read: then any L >= n + kmax - 1 gives their values without wrap-around.
-std::vector<float2> blue_filter_spectrum(const std::vector<float2>& chirp, int64_t L, int64_t kmax = -1) {
-  const int64_t n = (int64_t)chirp.size();
-  if (kmax < 0) kmax = n;
+std::vector<float2> blue_taps_spectrum(const std::vector<float2>& chirp, int64_t L, int64_t pos, int64_t neg,
+                                       bool conj_taps) {
   std::vector<std::complex<double>> h((size_t)L, {0.0, 0.0});
-  for (int64_t i = 0; i < n; ++i) {
-    const std::complex<double> hc(chirp[(size_t)i].x, -(double)chirp[(size_t)i].y);
-    if (i < kmax) h[(size_t)i] += hc;
-    if (i > 0) h[(size_t)(L - i)] += hc;
+  for (int64_t i = 0; i < (int64_t)chirp.size(); ++i) {
+    const std::complex<double> hc(chirp[(size_t)i].x, conj_taps ? -(double)chirp[(size_t)i].y : (double)chirp[(size_t)i].y);
+    if (i < pos) h[(size_t)i] += hc;
+    if (i > 0 && i < neg) h[(size_t)(L - i)] += hc;
   }
   host_dft(h);
   std::vector<float2> hs((size_t)L);
   for (int64_t i = 0; i < L; ++i)
     hs[(size_t)i] = make_float2((float)(h[(size_t)i].real() / (double)L), (float)(h[(size_t)i].imag() / (double)L));
   return hs;
+}
+
+std::vector<float2> blue_filter_spectrum(const std::vector<float2>& chirp, int64_t L, int64_t kmax = -1) {
+  const int64_t n = (int64_t)chirp.size();
+  return blue_taps_spectrum(chirp, L, kmax < 0 ? n : kmax, n, true);
+}
+
+// Filter spectrum of the adjoint of the truncated chain (outputs k < kmax): the adjoint maps
+// u_k (k < kmax) to v_j = sum_k u_k chirp[|j - k|] (j < n), a convolution with the taps
+// -(kmax-1) .. n-1 of chirp[|s|] (not conjugated), also / L.
+std::vector<float2> blue_adjoint_spectrum(const std::vector<float2>& chirp, int64_t L, int64_t kmax) {
+  return blue_taps_spectrum(chirp, L, (int64_t)chirp.size(), kmax, false);
 }
 
 std::mutex g_retained_mu;
@@ -537,7 +549,10 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         if ((rc = p->upload(lds_table((int)m, -1, e), &p->fwd.tw))) break;
         if ((rc = p->upload(lds_table((int)m, 1, e), &p->inv.tw))) break;
         if ((rc = p->upload(chirp, &p->chirp))) break;
-        rc = p->upload(blue_filter_spectrum(chirp, m, desc->inverse ? n : bins), &p->hs);
+        if ((rc = p->upload(blue_filter_spectrum(chirp, m, desc->inverse ? n : bins), &p->hs))) break;
+        // the forward plan also serves the signal gradient (tfa_stft_backward_execute), onesided
+        if (!desc->inverse && (desc->flags & TFA_STFT_ONESIDED))
+          rc = p->upload(blue_adjoint_spectrum(chirp, m, bins), &p->stft_hs_adj);
         break;
       }
       if (n < 16 || n > 4096) {
@@ -561,7 +576,11 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       }
       p->fwd.n = n;
       p->fwd.dir = -1;
-      rc = p->upload(lds_table((int)n, -1, tfa::stft_epth((int)n)), &p->fwd.tw);
+      if ((rc = p->upload(lds_table((int)n, -1, tfa::stft_epth((int)n)), &p->fwd.tw))) break;
+      // the signal gradient (tfa_stft_backward_execute) runs on the inverse kernel's layout
+      p->inv.n = n;
+      p->inv.dir = 1;
+      rc = p->upload(lds_table((int)n, 1, tfa::istft_epth((int)n)), &p->inv.tw);
       break;
     case TFA_KIND_FFT2: {
       const int64_t h = desc->n2;
@@ -926,16 +945,21 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
 int tfa_stft_backward_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, const float* grad_re,
                               const float* grad_im, const float* window, float* grad_padded, int64_t padded_len,
                               tfa_stream stream) {
-  if (!plan || plan->d.kind != TFA_KIND_STFT || !plan->d.inverse)
-    return fail(TFA_ERR_INVALID, "the STFT backward runs on an inverse STFT plan");
-  if (!is_pow2(plan->d.n)) return fail(TFA_ERR_UNSUPPORTED, "the fused STFT backward takes a power-of-two n_fft");
+  if (!plan || plan->d.kind != TFA_KIND_STFT || plan->d.inverse)
+    return fail(TFA_ERR_INVALID, "the STFT backward runs on the forward STFT plan");
+  if (!(plan->d.flags & TFA_STFT_ONESIDED)) return fail(TFA_ERR_UNSUPPORTED, "the fused STFT backward takes onesided spectra");
   if (batch < 0) return fail(TFA_ERR_INVALID, "negative batch");
+  const int64_t n_fft = plan->d.n, hop = plan->d.hop;
+  const bool pow2 = is_pow2(n_fft);
+  // the adjoint kernels tile like the inverse ones: a halo of floor((n-1)/hop) recomputed frames
+  const int64_t halo = (n_fft - 1) / hop;
+  if (pow2 ? halo >= tfa::istft_frames_per_tile((int)n_fft) : 2 * halo > tfa::stft_blue_adj_frames((int)plan->m))
+    return fail(TFA_ERR_UNSUPPORTED, "hop_length too small for the fused STFT backward tile");
   if (batch == 0) return TFA_OK;
   if (!grad_re || !grad_im || !window || !grad_padded) return fail(TFA_ERR_INVALID, "null data pointer");
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
     return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
-  const int64_t n_fft = plan->d.n, hop = plan->d.hop;
   if (n_frames < 1) return fail(TFA_ERR_INVALID, "need at least one frame");
   // frames n_fft + (n_frames - 1) * hop long reach into the padded signal; the rest has no gradient
   const int64_t covered = n_fft + (n_frames - 1) * hop;
@@ -943,12 +967,23 @@ int tfa_stft_backward_execute(const tfa_plan* plan, int64_t batch, int64_t n_fra
     return fail(TFA_ERR_INVALID, "n_frames does not match padded_len");
   if (padded_len > INT32_MAX / 2) return fail(TFA_ERR_UNSUPPORTED, "signal too long");
   note_capture(plan, stream);
-  const double sc = 0.5 * ((plan->d.flags & TFA_STFT_NORMALIZED) ? 1.0 / std::sqrt((double)n_fft) : 1.0);
-  tfa::IstftArgs a{grad_re, grad_im, window, grad_padded, plan->inv.tw, (int)n_frames, (int)hop,
-                   (int)((n_fft - 1) / hop), batch, covered, 0, covered, padded_len, (float)sc,
+  const double norm = (plan->d.flags & TFA_STFT_NORMALIZED) ? 1.0 / std::sqrt((double)n_fft) : 1.0;
+  // power of two: r2c adjoint = interior bins halved (scale 1/2, bins 0 and n/2 doubled in the kernel)
+  tfa::IstftArgs a{grad_re, grad_im, window, grad_padded, plan->inv.tw, (int)n_frames, (int)hop, (int)halo,
+                   batch, covered, 0, covered, padded_len, (float)(pow2 ? 0.5 * norm : norm),
                    static_cast<hipStream_t>(stream)};
   a.adjoint = true;
-  hipError_t e = tfa::launch_istft((int)n_fft, a);
+  hipError_t e;
+  if (pow2) {
+    e = tfa::launch_istft((int)n_fft, a);
+  } else {
+    a.blue_tw_f = plan->fwd.tw;
+    a.blue_tw_i = plan->inv.tw;
+    a.chirp = plan->chirp;
+    a.hs = plan->stft_hs_adj;
+    a.m = (int)plan->m;
+    e = tfa::launch_istft_blue((int)n_fft, a);
+  }
   return e == hipSuccess ? TFA_OK : hip_fail(e, "stft backward launch");
 }
 

@@ -278,21 +278,22 @@ def execute_stft(x: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int, cente
 def execute_stft_backward(g_re: torch.Tensor, g_im: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int,
                           center: bool, normalized: bool, padded_len: int) -> torch.Tensor | None:
     """Gradient of the onesided fused STFT with respect to its padded signal, (b, padded_len),
-    from the output gradient planes (b, bins, frames): one fused kernel (per-frame r2c adjoint,
-    window, overlap-add; replaces the autograd of trnfft/api.py:310-349's frame gather, window and
-    per-frame transform).  None when the inverse-STFT tile refuses the hop (the caller composes)."""
+    from the output gradient planes (b, bins, frames): one fused kernel on the forward plan (per
+    frame the adjoint of the transform -- the r2c adjoint, or the adjoint Bluestein chain for
+    n_fft that is not a power of two -- window, overlap-add; replaces the autograd of
+    trnfft/api.py:310-349's frame gather, window and per-frame transform).  None when the kernel's
+    frame tile refuses the hop (the caller composes)."""
     flags = _lib.STFT_ONESIDED | (_lib.STFT_CENTER if center else 0) | (_lib.STFT_NORMALIZED if normalized else 0)
     dev = g_re.device
-    try:
-        plan = native_plan(_lib.KIND_STFT, n_fft, True, dev.index, hop=hop, flags=flags)
-    except NotImplementedError:
-        return None
+    plan = native_plan(_lib.KIND_STFT, n_fft, False, dev.index, hop=hop, flags=flags)
     g_re, g_im, win = g_re.contiguous(), g_im.contiguous(), win.contiguous()
     b, frames = g_re.shape[0], g_re.shape[-1]
     out = torch.empty(b, padded_len, dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         rc = _lib.lib().tfa_stft_backward_execute(plan.handle, b, frames, ptr(g_re), ptr(g_im), ptr(win), ptr(out),
                                                   padded_len, stream_handle(dev))
+    if rc == _lib.TFA_ERR_UNSUPPORTED:
+        return None
     _lib.check(rc, "tfa_stft_backward_execute")
     return out
 
