@@ -220,6 +220,8 @@ def test_stft_gradient(n_fft, hop, center, normalized, onesided):
     (2048, 512, False, True, (2, 10000)),
     (4096, 1024, True, False, (1, 20000)),
     (512, 600, True, False, (2, 3000)),       # hop > n_fft: gaps between frames
+    (512, 130, True, False, (2, 5000)),       # a hop that is not a multiple of 4: one sample per thread
+    (512, 128, False, False, (2, 5001)),      # a padded length that is not
     (512, 256, True, False, (2, 257)),        # every frame reaches into both reflected edges
 ])
 def test_stft_gradient_fused_backward(n_fft, hop, center, normalized, shape, monkeypatch):

@@ -43,6 +43,10 @@ CASES = [
     (512, 40, 30, True, False, None),        # long halo (12 frames): the widest tile
     (1024, 128, 40, True, False, None),      # halo 7 > half the measured 8-frame tile: widest tile
     (32, 16, 300, True, False, None),
+    # interior tiles write four samples per thread when hop, trim, pitch and length allow; these
+    # take the one-sample path: a hop that is not a multiple of 4, a length that is not
+    (512, 126, 60, True, False, None),
+    (512, 128, 60, True, False, 5001),
 ]
 
 

@@ -20,10 +20,23 @@ __device__ __forceinline__ long long xcd_tile_remap(long long i, long long g) {
   return (i % 8) * per + i / 8;
 }
 
+// 32-bit form for grids below 2^31 workgroups (the launchers check): the tile index then divides
+// in a few 32-bit operations instead of a 64-bit division sequence.
+__device__ __forceinline__ unsigned xcd_tile_remap32(unsigned i, unsigned g) {
+  const unsigned per = g / 8;
+  if (i >= per * 8) return i;
+  return (i % 8) * per + i / 8;
+}
+
 // Streaming (non-temporal) global accesses: every element of a batched transform is read once
 // and written once, so it should not displace other lines in L2 / the Infinity Cache.
 __device__ __forceinline__ float ld_stream(const float* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_stream(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void st_stream4(float* p, float4 v) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<f4v*>(p));
+}
 __device__ __forceinline__ float4 ld_stream4(const float4* p) {
   typedef float f4v __attribute__((ext_vector_type(4)));
   const f4v r = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(p));
@@ -270,6 +283,9 @@ struct IstftArgs {
   // the others (scale 1/2 then gives the r2c adjoint), the windowed sum is written as it is (no
   // envelope division, no raw-sum branch)
   bool adjoint = false;
+  // hop, start, out_pitch and write_len multiples of 4 and out 16-byte aligned: interior tiles
+  // write four consecutive samples per thread (host-checked)
+  bool vec4 = false;
   // n_fft that is not a power of two (one inverse Bluestein chain per frame, length m): forward
   // and inverse m-point tables, the inverse chirp (n_fft) and its filter spectrum H/m (m)
   const float2* blue_tw_f = nullptr;

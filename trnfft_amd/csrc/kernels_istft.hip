@@ -46,47 +46,60 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
     const float* __restrict__ sre, const float* __restrict__ sim, const float* __restrict__ win,
     float* __restrict__ out, const float2* __restrict__ tw, int n_frames, int hop, int halo, int owned,
     int tiles_per_signal, long long expected_len, long long start, long long write_len, long long out_pitch,
-    float scale) {
+    float scale, int vec4) {
   using C = IstftCfg<NFFT, E_, MAXP>;
   constexpr int E = C::E, T = C::T, F = C::F, RP = C::RP, FR = C::FR, THREADS = C::THREADS;
   constexpr bool WL = T <= 64;
-  __shared__ float2 lds2[C::PAIRS * RP / 2];  // RP is even: every pair region is 8-byte aligned
-  __shared__ float wl[NFFT];
+  // RP is a multiple of 4: every pair region and frame row is 16-byte aligned
+  __shared__ __attribute__((aligned(16))) float2 lds2[C::PAIRS * RP / 2];
+  __shared__ __attribute__((aligned(16))) float wl[NFFT];
   float* lds = reinterpret_cast<float*>(lds2);
-  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
-  const long long b = tile / tiles_per_signal;
-  const int t0 = (int)(tile % tiles_per_signal) * owned;  // first owned frame
+  // 32-bit tile arithmetic (the launcher keeps the grid below 2^31 and the host keeps a signal's
+  // bins * frames below 2^31)
+  const unsigned tile = xcd_tile_remap32(blockIdx.x, gridDim.x);
+  const unsigned b = tile / (unsigned)tiles_per_signal;
+  const int t0 = (int)(tile - b * (unsigned)tiles_per_signal) * owned;  // first owned frame
   const int ta = t0 - halo > 0 ? t0 - halo : 0;          // first frame of the tile
   const int nf = (t0 + owned < n_frames ? t0 + owned : n_frames) - ta;  // frames in the tile (<= FR)
 
   for (int i = threadIdx.x; i < NFFT; i += THREADS) wl[i] = win[i];
-  // 1. stage bins: region of pair p = [re_a | im_a | re_b | im_b], F floats each
-  const size_t sbase = (size_t)b * F * n_frames + ta;
+  // 1. stage bins: region of pair p = [re_a | im_a | re_b | im_b], F floats each.  Lane fs of
+  //    every KS-lane group reads frame fs of bin rows k0, k0 + KS, ... (THREADS is a multiple
+  //    of FR, so a lane keeps its frame): one 32-bit offset step per load from the signal's base
+  //    (the former per-load 64-bit index arithmetic was a quarter of the kernel's VALU work)
+  constexpr int KS = THREADS / FR;
+  static_assert(THREADS % FR == 0, "lanes keep their frame across the staging steps");
+  const int fs = (int)threadIdx.x % FR, k0 = (int)threadIdx.x / FR;
+  const float* bre = sre + (size_t)b * F * n_frames + ta;
+  const float* bim = sim + (size_t)b * F * n_frames + ta;
   // every load of the tile is issued before the first LDS write (a load-then-store loop would
   // wait out the full memory latency once per iteration)
-  constexpr int SI = (F * FR + THREADS - 1) / THREADS;
+  constexpr int SI = (F + KS - 1) / KS;
   float sr[SI], si[SI];
+  {
+    unsigned off = (unsigned)(fs + k0 * n_frames);
+    const unsigned step = (unsigned)(KS * n_frames);
+    const bool fok = fs < nf;
 #pragma unroll
-  for (int it = 0; it < SI; ++it) {
-    const int i = (int)threadIdx.x + it * THREADS;
-    const int f = i % FR, k = i / FR;
-    sr[it] = 0.0f;
-    si[it] = 0.0f;
-    if (i < F * FR && f < nf) {
-      // plain loads: a bin row segment is FR frames (64 bytes at n_fft 512), so a cache line is
-      // shared with the neighbouring tile, which then finds it in L2 (measured 4 % faster)
-      sr[it] = sre[sbase + (size_t)k * n_frames + f];
-      si[it] = sim[sbase + (size_t)k * n_frames + f];
+    for (int it = 0; it < SI; ++it) {
+      sr[it] = 0.0f;
+      si[it] = 0.0f;
+      if (k0 + KS * it < F && fok) {
+        // plain loads: a bin row segment is FR frames (64 bytes at n_fft 512), so a cache line is
+        // shared with the neighbouring tile, which then finds it in L2 (measured 4 % faster)
+        sr[it] = bre[off];
+        si[it] = bim[off];
+      }
+      off += step;
     }
   }
+  float* sreg = lds + (fs >> 1) * RP + (fs & 1) * 2 * F + k0;
 #pragma unroll
   for (int it = 0; it < SI; ++it) {
-    const int i = (int)threadIdx.x + it * THREADS;
-    const int f = i % FR, k = i / FR;
-    if (i < F * FR) {
-      float* reg = lds + (f >> 1) * RP + (f & 1) * 2 * F;
-      reg[k] = (ADJ && (k == 0 || k == NFFT / 2)) ? 2.0f * sr[it] : sr[it];
-      reg[F + k] = (k == 0 || k == NFFT / 2) ? 0.0f : si[it];
+    const int k = k0 + KS * it;
+    if (k < F) {
+      sreg[KS * it] = (ADJ && (k == 0 || k == NFFT / 2)) ? 2.0f * sr[it] : sr[it];
+      sreg[F + KS * it] = (k == 0 || k == NFFT / 2) ? 0.0f : si[it];
     }
   }
   __syncthreads();
@@ -120,7 +133,61 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
   const int s_hi = (t0 + owned >= n_frames || s_end > expected_len) ? expected_len : (int)s_end;
   float* dst = out + (size_t)b * out_pitch;
   const int t_end = ta + nf - 1;
-  if (THREADS % hop == 0 && halo < 4 && t0 >= halo && t0 + owned < n_frames && s_end <= expected_len) {
+  const bool interior = halo < 4 && t0 >= halo && t0 + owned < n_frames && s_end <= expected_len;
+  if (vec4 && interior && THREADS % (hop >> 2) == 0) {
+    // the interior path below with four consecutive samples per thread (phase r = 4 * (thread
+    // mod hop/4)): one 16-byte LDS read per covering frame and one 16-byte store per four
+    // samples; hop being a multiple of 4, the four samples have the same covering frames
+    const int q = hop >> 2;
+    int rq;
+    const int tq = divmod_small((int)threadIdx.x, q, 1.0f / (float)q, rq);
+    const int r = 4 * rq;
+    const int tstep = THREADS / q;
+    const int nc = (NFFT - 1 - r) / hop + 1;
+    float4 wv[4];
+    float4 env = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      wv[m] = m < nc ? *reinterpret_cast<const float4*>(wl + r + m * hop) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (m < nc) {
+        env.x += wv[m].x * wv[m].x;
+        env.y += wv[m].y * wv[m].y;
+        env.z += wv[m].z * wv[m].z;
+        env.w += wv[m].w * wv[m].w;
+      }
+    }
+    const float4 inv = make_float4(1.0f / env.x, 1.0f / env.y, 1.0f / env.z, 1.0f / env.w);
+    for (int t = t0 + tq; t < t0 + owned; t += tstep) {
+      const int o = t * hop + r - (int)start;
+      if (o < 0 || o >= write_len) continue;
+      float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f), raw = acc;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m < nc) {
+          const int f = t - m - ta;
+          const float4 x = *reinterpret_cast<const float4*>(lds + (f >> 1) * RP + (f & 1) * NFFT + r + m * hop);
+          acc.x += x.x * wv[m].x;
+          acc.y += x.y * wv[m].y;
+          acc.z += x.z * wv[m].z;
+          acc.w += x.w * wv[m].w;
+          raw.x += x.x;
+          raw.y += x.y;
+          raw.z += x.z;
+          raw.w += x.w;
+        }
+      }
+      float4 y = acc;
+      if constexpr (!ADJ) {
+        y.x = env.x > 1e-8f ? acc.x * inv.x : raw.x;
+        y.y = env.y > 1e-8f ? acc.y * inv.y : raw.y;
+        y.z = env.z > 1e-8f ? acc.z * inv.z : raw.z;
+        y.w = env.w > 1e-8f ? acc.w * inv.w : raw.w;
+      }
+      st_stream4(dst + o, y);
+    }
+    return;  // not the last tile: no zero fill
+  }
+  if (THREADS % hop == 0 && interior) {
     // interior tile (every owned sample has all its covering frames in the tile) and a hop that
     // divides the thread count: each thread keeps one phase r = s mod hop, so its covering frames
     // t, t-1, ... meet it at the fixed offsets r, r + hop, ... of their windows; the window
@@ -182,14 +249,16 @@ static hipError_t launch_istft_cfg(const IstftArgs& a) {
   if (owned < 1) return hipErrorInvalidValue;
   const int tiles = (a.n_frames + owned - 1) / owned;
   const long long blocks = a.batch * (long long)tiles;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
   if (a.adjoint)
     hipLaunchKernelGGL((istft_kernel<NFFT, istft_epth(NFFT), MAXP, true>), dim3((unsigned)blocks), dim3(C::THREADS),
                        0, a.stream, a.spec_re, a.spec_im, a.window, a.out, a.tw, a.n_frames, a.hop, a.halo, owned,
-                       tiles, (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale);
+                       tiles, (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale,
+                       (int)a.vec4);
   else
     hipLaunchKernelGGL((istft_kernel<NFFT, istft_epth(NFFT), MAXP>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
                        a.stream, a.spec_re, a.spec_im, a.window, a.out, a.tw, a.n_frames, a.hop, a.halo, owned, tiles,
-                       (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale);
+                       (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale, (int)a.vec4);
   return hipGetLastError();
 }
 

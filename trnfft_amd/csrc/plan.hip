@@ -892,6 +892,12 @@ int tfa_stft_execute(const tfa_plan* plan, int64_t batch, int64_t num_samples, c
   return e == hipSuccess ? TFA_OK : hip_fail(e, "stft launch");
 }
 
+// the inverse-STFT kernels' four-samples-per-thread output path: whole 16-byte groups everywhere
+static bool vec4_ok(const tfa::IstftArgs& a, const float* out) {
+  return a.hop % 4 == 0 && a.start % 4 == 0 && a.out_pitch % 4 == 0 && a.write_len % 4 == 0 &&
+         (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+}
+
 int tfa_istft_length(const tfa_plan* plan, int64_t n_frames, int64_t length, int64_t* out_len) {
   if (!plan || !out_len || plan->d.kind != TFA_KIND_STFT || !plan->d.inverse)
     return fail(TFA_ERR_INVALID, "not an inverse STFT plan");
@@ -919,7 +925,8 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
   if (rc) return rc;
   const int64_t n_fft = plan->d.n, hop = plan->d.hop;
   const int64_t expected = n_fft + (n_frames - 1) * hop;
-  if (expected > INT32_MAX / 2 || n_frames > INT32_MAX / 2 || out_len > INT32_MAX / 2)
+  if (expected > INT32_MAX / 2 || n_frames > INT32_MAX / 2 || out_len > INT32_MAX / 2 ||
+      (n_fft / 2 + 1) * n_frames > INT32_MAX)
     return fail(TFA_ERR_UNSUPPORTED, "signal too long");
   const int64_t start = (plan->d.flags & TFA_STFT_CENTER) ? n_fft / 2 : 0;
   int64_t cur = expected - start;
@@ -928,6 +935,7 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
   tfa::IstftArgs a{spec_re, spec_im, window, out, plan->inv.tw, (int)n_frames, (int)hop, (int)((n_fft - 1) / hop),
                    batch, expected, start, cur < out_len ? cur : out_len, out_len, (float)sc,
                    static_cast<hipStream_t>(stream)};
+  a.vec4 = vec4_ok(a, out);
   hipError_t e;
   if (!is_pow2(n_fft)) {
     a.blue_tw_f = plan->fwd.tw;
@@ -965,7 +973,8 @@ int tfa_stft_backward_execute(const tfa_plan* plan, int64_t batch, int64_t n_fra
   const int64_t covered = n_fft + (n_frames - 1) * hop;
   if (covered > padded_len || n_frames != 1 + (padded_len - n_fft) / hop)
     return fail(TFA_ERR_INVALID, "n_frames does not match padded_len");
-  if (padded_len > INT32_MAX / 2) return fail(TFA_ERR_UNSUPPORTED, "signal too long");
+  if (padded_len > INT32_MAX / 2 || (n_fft / 2 + 1) * n_frames > INT32_MAX)
+    return fail(TFA_ERR_UNSUPPORTED, "signal too long");
   note_capture(plan, stream);
   const double norm = (plan->d.flags & TFA_STFT_NORMALIZED) ? 1.0 / std::sqrt((double)n_fft) : 1.0;
   // power of two: r2c adjoint = interior bins halved (scale 1/2, bins 0 and n/2 doubled in the kernel)
@@ -973,6 +982,7 @@ int tfa_stft_backward_execute(const tfa_plan* plan, int64_t batch, int64_t n_fra
                    batch, covered, 0, covered, padded_len, (float)(pow2 ? 0.5 * norm : norm),
                    static_cast<hipStream_t>(stream)};
   a.adjoint = true;
+  a.vec4 = vec4_ok(a, grad_padded);
   hipError_t e;
   if (pow2) {
     e = tfa::launch_istft((int)n_fft, a);
