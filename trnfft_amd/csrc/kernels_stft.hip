@@ -54,9 +54,9 @@ __global__ __launch_bounds__((StftCfg<NFFT>::THREADS)) void stft_kernel(
   using C = StftCfg<NFFT>;
   constexpr int E = C::E, T = C::T, FR = C::FR, AREA = C::AREA, THREADS = C::THREADS, NB1 = C::NB1;
   __shared__ __attribute__((aligned(16))) float lds[C::PAIRS * AREA];
-  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
-  const long long b = tile / tiles_per_signal;
-  const int f0 = (int)(tile % tiles_per_signal) * FR;
+  const unsigned tile = xcd_tile_remap32(blockIdx.x, gridDim.x);  // 32-bit: grids below 2^31 (launcher)
+  const unsigned b = tile / (unsigned)tiles_per_signal;
+  const int f0 = (int)(tile - b * (unsigned)tiles_per_signal) * FR;
   const int tid = threadIdx.x % T;
   const int pl = threadIdx.x / T;
   const int fa = f0 + 2 * pl;  // frames fa (real part) and fa + 1 (imaginary part)
@@ -159,6 +159,7 @@ static hipError_t launch_stft_n(const StftArgs& a) {
   using C = StftCfg<NFFT>;
   const int tiles = (a.n_frames + C::FR - 1) / C::FR;
   const long long blocks = a.batch * (long long)tiles;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
   // stft_lds_extra: unused dynamic LDS that holds the workgroups resident per CU to one where that
   // measured faster
   hipLaunchKernelGGL((stft_kernel<NFFT>), dim3((unsigned)blocks), dim3(C::THREADS), stft_lds_extra(NFFT), a.stream,

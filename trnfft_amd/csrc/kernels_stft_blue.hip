@@ -41,9 +41,9 @@ __global__ __launch_bounds__((StftBlueCfg<M, E, FR>::THREADS)) void stft_blue_ke
   using C = StftBlueCfg<M, E, FR>;
   constexpr int T = C::T, EIN = C::EIN, EH = E / 2, AREA = C::AREA, THREADS = C::THREADS;
   __shared__ __attribute__((aligned(16))) float lds[FR * AREA];
-  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
-  const long long b = tile / tiles_per_signal;
-  const int f0 = (int)(tile % tiles_per_signal) * FR;
+  const unsigned tile = xcd_tile_remap32(blockIdx.x, gridDim.x);  // 32-bit: grids below 2^31 (launcher)
+  const unsigned b = tile / (unsigned)tiles_per_signal;
+  const int f0 = (int)(tile - b * (unsigned)tiles_per_signal) * FR;
   const int tid = threadIdx.x % T;
   const int fl = threadIdx.x / T;
   const int f = f0 + fl;
@@ -94,13 +94,17 @@ __global__ __launch_bounds__((StftBlueCfg<M, E, FR>::THREADS)) void stft_blue_ke
   const int kb = threadIdx.x / FR;
   if (f0 + fr >= n_frames) return;
   const float2* pb = reinterpret_cast<const float2*>(lds + fr * AREA);
-  const size_t ob = (size_t)b * n_bins * n_frames + f0 + fr;
+  // 32-bit offsets from the signal's (uniform) base: the host keeps n_bins * n_frames below 2^30
+  const size_t ob = (size_t)b * n_bins * n_frames + f0;
   float* ore = out_re + ob;
   float* oim = out_im + ob;
+  unsigned off = (unsigned)(fr + kb * n_frames);
+  const unsigned step = (unsigned)(KS * n_frames);
   for (int k = kb; k < n_bins; k += KS) {
     const float2 q = pb[k];
-    ore[(size_t)k * n_frames] = q.x;
-    oim[(size_t)k * n_frames] = q.y;
+    ore[off] = q.x;
+    oim[off] = q.y;
+    off += step;
   }
 }
 
@@ -182,9 +186,9 @@ __global__ __launch_bounds__((IstftBlueCfg<M, E, FR, ADJ>::THREADS)) void istft_
   constexpr int T = C::T, EH = E / 2, EOUT = C::EOUT, AREA = C::AREA, THREADS = C::THREADS;
   __shared__ __attribute__((aligned(16))) float lds[FR * AREA];
   __shared__ float wl[C::NW];
-  const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
-  const long long b = tile / tiles_per_signal;
-  const int t0 = (int)(tile % tiles_per_signal) * owned;  // first owned frame
+  const unsigned tile = xcd_tile_remap32(blockIdx.x, gridDim.x);  // 32-bit: grids below 2^31 (launcher)
+  const unsigned b = tile / (unsigned)tiles_per_signal;
+  const int t0 = (int)(tile - b * (unsigned)tiles_per_signal) * owned;  // first owned frame
   const int ta = t0 - halo > 0 ? t0 - halo : 0;          // first frame of the tile
   const int nf = (t0 + owned < n_frames ? t0 + owned : n_frames) - ta;  // frames in the tile (<= FR)
   const int K = n / 2 + 1;  // onesided bins

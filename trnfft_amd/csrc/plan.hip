@@ -877,6 +877,8 @@ int tfa_stft_execute(const tfa_plan* plan, int64_t batch, int64_t num_samples, c
   int rc = tfa_stft_frames(plan, num_samples, &frames);
   if (rc) return rc;
   const int n_bins = (plan->d.flags & TFA_STFT_ONESIDED) ? (int)(n_fft / 2 + 1) : (int)n_fft;
+  // the kernels address a signal's output planes with 32-bit byte offsets
+  if ((int64_t)n_bins * frames > (int64_t)1 << 30) return fail(TFA_ERR_UNSUPPORTED, "signal too long");
   const float scale = (plan->d.flags & TFA_STFT_NORMALIZED) ? (float)(1.0 / std::sqrt((double)n_fft)) : 1.0f;
   // a hop beyond the padded signal leaves one frame, whatever its value: keep it within int
   const int64_t hop = std::min<int64_t>(plan->d.hop, num_samples + 2 * pad);
