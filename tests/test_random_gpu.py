@@ -8,7 +8,9 @@ stft.  Every case must meet 1e-6 * log2 N relative L2 against float64 (numpy.fft
 torch.stft), the same bound as the fixed-shape tests.  A second seeded sweep (48 cases) draws
 any length (mostly Bluestein) for c2c, rfft, strided axes and fft2 and checks it against the
 oracle's restatement of the reference operator at 1e-5 * log2 N: the reference's fp32 Bluestein
-chirp puts that operator itself up to ~3e-3 from the exact DFT at large n.
+chirp puts that operator itself up to ~3e-3 from the exact DFT at large n.  A third seeded
+sweep (24 cases) draws STFT and inverse STFT calls at any n_fft in [9, 2048] with random hop,
+centring, normalisation and sidedness against the oracle's restatement of trnfft/api.py:291-470.
 """
 
 from __future__ import annotations
@@ -171,3 +173,42 @@ def test_random_any_length_vs_oracle(case):
             y = trnfft_amd.fft2(ComplexTensor(re.cuda(), im.cuda()))
             ref = oracle.fft2((re, im))
         assert rel_l2(y.real, y.imag, *ref) <= 2 * tol_bluestein(max(h, w))
+
+
+def _cases_stft(count: int, seed: int):
+    rng = random.Random(seed)
+    out = []
+    for i in range(count):
+        n_fft = rng.randrange(9, 2049)
+        hop = max(1, int(n_fft * rng.choice([0.25, 0.4, 0.5, 0.75, 1.0, 1.3])))
+        out.append(("istft" if i % 3 == 2 else "stft", n_fft, hop, rng.randrange(1, 4), rng.randrange(n_fft + 1, 12000),
+                    rng.random() < 0.75, rng.random() < 0.25, rng.random() < 0.8))
+    return out
+
+
+# STFT / inverse STFT at any n_fft (the per-frame Bluestein kernels, or the composed paths where
+# the fused tiles do not apply) against the oracle's restatement of trnfft/api.py:291-470
+@pytest.mark.parametrize("case", _cases_stft(24, 11), ids=lambda c: "-".join(str(v) for v in c))
+def test_random_stft_any_n_fft_vs_oracle(case):
+    import oracle
+    from conftest import tol_bluestein
+
+    kind, n_fft, hop, batch, length, center, normalized, onesided = case
+    seed = zlib.crc32(repr(case).encode())
+    tol = tol_pow2(n_fft) * 4 if n_fft & (n_fft - 1) == 0 else tol_bluestein(n_fft)
+    if kind == "stft":
+        x = torch.from_numpy(_randn((batch, length), seed))
+        y = trnfft_amd.stft(x.cuda(), n_fft, hop_length=hop, center=center, normalized=normalized, onesided=onesided)
+        ref = oracle.stft(x, n_fft, hop_length=hop, center=center, normalized=normalized, onesided=onesided)
+        assert y.shape == ref[0].shape
+        assert rel_l2(y.real, y.imag, *ref) <= tol
+    else:
+        frames = max(1, (length - n_fft) // hop)
+        bins = n_fft // 2 + 1 if onesided else n_fft
+        re = torch.from_numpy(_randn((batch, bins, frames), seed))
+        im = torch.from_numpy(_randn((batch, bins, frames), seed + 1))
+        y = trnfft_amd.istft(ComplexTensor(re.cuda(), im.cuda()), n_fft, hop_length=hop, center=center,
+                             normalized=normalized, onesided=onesided)
+        ref = oracle.istft((re, im), n_fft, hop_length=hop, center=center, normalized=normalized, onesided=onesided)
+        assert y.shape == ref.shape
+        assert rel_l2(y, torch.zeros_like(y), ref, torch.zeros_like(ref)) <= tol
