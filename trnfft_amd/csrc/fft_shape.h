@@ -96,16 +96,24 @@ __host__ __device__ constexpr bool fft2_small_ok(long long h, long long w) {
 // power-of-two m = 16384 kernel: 29.0 us).  Timing probes of that kernel: the LDS exchanges cost
 // 3.5 us and the twiddle-table reads 1.4 us of the 18.9; the rest is VALU (1536 instructions per
 // wave, each 4 cycles on a 16-lane SIMD) and the load latencies.
+// Mixed-radix lengths 3 * 2^k below that, measured against the power-of-two length the reference
+// pads to (4M complex elements per launch; only the faster ones are used):
+// 768 (E = 12, 256 threads) n = 300: 45.3 against 59.8 us at 1024, n = 380: 39.2 against 50.3;
+// 1536 (E = 24, 256 threads) n = 600: 57.7 against 62.4 at 2048, n = 700: 46.1 against 55.3;
+// 3072 (E = 12, 256 threads) n = 1300: 57.6 against 62.6 at 4096, n = 1500: 52.0 against 55.2.
+// Slower or no better: 96, 192, 384 (within 3 %), 6144 (84 against 79 us at 8192), E = 12 with
+// 512 threads at 1536 and 3072 (70-79 us), E = 6 at 768 (65-89 us).  The plan takes these lengths
+// (blue_fused_length) only where they hold 2n - 1 points and are shorter than m.
 __host__ __device__ constexpr int blue_epth(int m) {
-  return m % 3 == 0 ? 12 : m >= 16384 ? 16 : m >= 128 ? 8 : lds_epth(m);
+  return m == 1536 ? 24 : m % 3 == 0 ? 12 : m >= 16384 ? 16 : m >= 128 ? 8 : lds_epth(m);
 }
 __host__ __device__ constexpr int blue_threads(int m) {
-  return m % 3 == 0 ? m / 12 : m == 2048 || m >= 8192 ? 512 : 256;
+  return m % 3 == 0 ? (m == 9216 ? m / 12 : 256) : m == 2048 || m >= 8192 ? 512 : 256;
 }
 __host__ __device__ constexpr bool blue_pf(int m) { return m >= 256; }
 // double-buffered LDS exchange in the fused kernel (one barrier per pass exchange) where two
 // buffers fit the CU's LDS: C3a (m = 2048) 12.8 -> 12.2 us; no change at m = 9216
-__host__ __device__ constexpr bool blue_db(int m) { return m % 3 == 0 || (m >= 1024 && m <= 8192); }
+__host__ __device__ constexpr bool blue_db(int m) { return (m % 3 == 0 && m <= 9216) || (m >= 1024 && m <= 8192); }
 // wrapped-convolution lengths of the fused kernel (power-of-two M = 2n - 1 - wrap, 1 <= wrap <= 15):
 // from 128 (16 threads per row, so the corrected outputs k < wrap are all in element 0)
 __host__ __device__ constexpr bool blue_wrap_ok(int m) { return m >= 128 && m <= 16384 && (m & (m - 1)) == 0; }

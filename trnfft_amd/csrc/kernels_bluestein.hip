@@ -269,6 +269,9 @@ hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a) {
     case 4096: return launch_blue_m<4096>(a);
     case 8192: return launch_blue_m<8192>(a);
     case 16384: return launch_blue_m<16384>(a);
+    case 768: return launch_blue_m<768>(a);
+    case 1536: return launch_blue_m<1536>(a);
+    case 3072: return launch_blue_m<3072>(a);
     case 9216: return launch_blue_m<9216>(a);
     default: return hipErrorInvalidValue;
   }

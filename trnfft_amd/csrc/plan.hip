@@ -217,9 +217,13 @@ namespace {
 // Otherwise the circular convolution needs L >= 2n - 1, and where m overshoots that by most, a
 // mixed-radix length (3^2 * 2^10 = 9216 for 4096 < n <= 4608, against m = 16384) halves the
 // transforms and the LDS (two workgroups per CU instead of one).
+// Internal length of the fused Bluestein kernel: the wrapped power of two m/2 where at most
+// kBlueWrapMax outputs need correcting, else the shortest measured-faster mixed-radix length that
+// holds the 2n - 1 point convolution, else the reference's m.
 int64_t blue_fused_length(int64_t n, int64_t m) {
   if (tfa::blue_wrap_ok((int)std::min<int64_t>(m / 2, 1 << 30)) && 2 * n - 1 - m / 2 <= tfa::kBlueWrapMax) return m / 2;
-  if (m == 16384 && 2 * n - 1 <= 9216) return 9216;
+  for (int64_t c : {768, 1536, 3072, 9216})
+    if (c >= 2 * n - 1 && c < m) return c;
   return m;
 }
 
