@@ -236,6 +236,8 @@ struct LdsFft {
   static constexpr LdsShape S = make_shape(N, E);
   static constexpr int T = N / E;
   static_assert(!DB || (IL && !SPLIT && !WAVE_LOCAL), "double buffering is for the interleaved workgroup exchange");
+  // consecutive T-thread transforms stay inside one wavefront only when T divides 64
+  static_assert(!WAVE_LOCAL || 64 % T == 0, "a wave-local transform must not straddle wavefronts");
   static constexpr int DBOFF = 2 * lds_pad(N);  // floats between the two buffers
   static constexpr int TQ = PF ? (E / 2 > 0 ? E / 2 : 1) : 1;  // float4 twiddles per thread per pass
 
