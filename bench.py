@@ -437,6 +437,21 @@ def bench_secondary():
                                               None, None, st)), S)
     rec("irfft_c2r_4096x1024", t, flops_fft(n, b) / 2, nbytes, sets=S, note="flops = 2.5 N log2 N per row")
     del xs, bins
+    # reference point for the headline: a plain device copy of the headline's traffic (two 16 MiB
+    # planes read, two written), same rotation and timing
+    plane = 4096 * 1024
+    S = _n_sets(4 * plane * 4)
+    srcs = [(torch.randn(plane, device=dev), torch.randn(plane, device=dev)) for _ in range(S)]
+    dsts = [(torch.empty(plane, device=dev), torch.empty(plane, device=dev)) for _ in range(S)]
+
+    def copy_pair(k, st):
+        dsts[k][0].copy_(srcs[k][0])
+        dsts[k][1].copy_(srcs[k][1])
+
+    t = _time_rot(copy_pair, S)
+    rec("copy_2x16MiB_planes", t, 0, 4 * plane * 4, sets=S,
+        note="torch copy_ of the headline's bytes (two launches): the c2c kernel's rate against a plain copy")
+    del srcs, dsts
     torch.cuda.empty_cache()
     return out
 
