@@ -313,18 +313,20 @@ def bench_secondary():
             r["note"] = note
         out[name] = r
 
-    # C2: STFT 64 x 160000, n_fft 512, hop 256 (center, reflect, periodic Hann, onesided)
+    # C2: STFT 64 x 160000, n_fft 512, hop 256 (center, reflect, periodic Hann, onesided); spectra
+    # in the API's memory order (frames-major: torch.stft's, and the reference's transposed frames)
+    fm = _lib.STFT_CENTER | _lib.STFT_ONESIDED | _lib.STFT_FRAMES_MAJOR
     nbytes = 64 * 160000 * 4 + 2 * 64 * 257 * 626 * 4
     S = _n_sets(nbytes)
     xs = rolled(make_stft_input(64, 160000), S)
     win = torch.hann_window(512).to(dev)
-    pl = native_plan(_lib.KIND_STFT, 512, False, dev.index, hop=256, flags=_lib.STFT_CENTER | _lib.STFT_ONESIDED)
-    os_ = [(torch.empty(64, 257, 626, device=dev), torch.empty(64, 257, 626, device=dev)) for _ in range(S)]
+    pl = native_plan(_lib.KIND_STFT, 512, False, dev.index, hop=256, flags=fm)
+    os_ = [(torch.empty(64, 626, 257, device=dev), torch.empty(64, 626, 257, device=dev)) for _ in range(S)]
     t = _time_rot(lambda k, st: chk(L.tfa_stft_execute(pl.handle, 64, 160000, P(xs[k]), P(win), P(os_[k][0]),
                                                    P(os_[k][1]), st)), S)
     rec("c2_stft_64x160000_nfft512", t, 40064 * 5 * 512 * 9, nbytes, sets=S)
     # inverse of C2 (fused istft: completion, inverse transform, window, overlap-add, envelope, trim)
-    ipl = native_plan(_lib.KIND_STFT, 512, True, dev.index, hop=256, flags=_lib.STFT_CENTER | _lib.STFT_ONESIDED)
+    ipl = native_plan(_lib.KIND_STFT, 512, True, dev.index, hop=256, flags=fm)
     ys = [torch.empty(64, 160000, device=dev) for _ in range(S)]
     t = _time_rot(lambda k, st: chk(L.tfa_istft_execute(ipl.handle, 64, 626, P(os_[k][0]), P(os_[k][1]), P(win),
                                                         P(ys[k]), 160000, st)), S)
@@ -333,16 +335,16 @@ def bench_secondary():
     del os_, ys
     # C2's signals at n_fft 400 (25 ms at 16 kHz), hop 160: one Bluestein chain per frame
     w400 = torch.hann_window(400).to(dev)
-    p400 = native_plan(_lib.KIND_STFT, 400, False, dev.index, hop=160, flags=_lib.STFT_CENTER | _lib.STFT_ONESIDED)
+    p400 = native_plan(_lib.KIND_STFT, 400, False, dev.index, hop=160, flags=fm)
     frames = 1 + 160000 // 160
     nbytes = 64 * 160000 * 4 + 2 * 64 * 201 * frames * 4
-    os_ = [(torch.empty(64, 201, frames, device=dev), torch.empty(64, 201, frames, device=dev)) for _ in range(S)]
+    os_ = [(torch.empty(64, frames, 201, device=dev), torch.empty(64, frames, 201, device=dev)) for _ in range(S)]
     t = _time_rot(lambda k, st: chk(L.tfa_stft_execute(p400.handle, 64, 160000, P(xs[k]), P(w400), P(os_[k][0]),
                                                    P(os_[k][1]), st)), S)
     rec("stft_64x160000_nfft400", t, 64 * frames * 2 * 5 * 768 * math.log2(768), nbytes, sets=S,
         note="non-power-of-two n_fft: two 768-point transforms per frame (gflops counts those), VALU-bound")
     # its inverse: one inverse Bluestein chain per frame (1024 points: every sample is kept)
-    ip400 = native_plan(_lib.KIND_STFT, 400, True, dev.index, hop=160, flags=_lib.STFT_CENTER | _lib.STFT_ONESIDED)
+    ip400 = native_plan(_lib.KIND_STFT, 400, True, dev.index, hop=160, flags=fm)
     ys = [torch.empty(64, 160000, device=dev) for _ in range(S)]
     t = _time_rot(lambda k, st: chk(L.tfa_istft_execute(ip400.handle, 64, frames, P(os_[k][0]), P(os_[k][1]),
                                                         P(w400), P(ys[k]), 160000, st)), S)

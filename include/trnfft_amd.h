@@ -43,6 +43,11 @@ typedef void* tfa_stream; /* hipStream_t; NULL = the null stream */
 #define TFA_STFT_CENTER 1     /* reflect-pad n_fft/2 on both sides (pad_mode="reflect") */
 #define TFA_STFT_NORMALIZED 2 /* scale by 1/sqrt(n_fft)                                 */
 #define TFA_STFT_ONESIDED 4   /* keep bins 0..n_fft/2                                   */
+/* Spectra stored (batch, n_frames, n_bins) row-major instead of (batch, n_bins, n_frames): the
+ * memory order of torch.stft's (..., freq, time) result and of trnfft's (trnfft/api.py:356-358
+ * returns the transpose of (..., time, freq) frames), whose shape is the same.  Applies to the
+ * forward output, the inverse input and the backward's gradient input. */
+#define TFA_STFT_FRAMES_MAJOR 8
 
 typedef struct tfa_plan_desc {
   int32_t kind;    /* TFA_KIND_* */
@@ -134,8 +139,8 @@ int tfa_execute_strided_ws(const tfa_plan* plan, int64_t outer, int64_t stride, 
  * Short-time Fourier transform of `batch` real signals of `num_samples` samples each.  Frames
  * of n_fft samples every hop, after reflect padding when TFA_STFT_CENTER; each frame is
  * multiplied by window (device pointer, n_fft floats, already centre-padded to n_fft) and
- * transformed; output planes are (batch, n_bins, n_frames) row-major with n_bins = n_fft/2+1
- * when TFA_STFT_ONESIDED else n_fft.  Replaces trnfft/api.py:291-365 (stft).  n_fft: a power
+ * transformed; output planes are (batch, n_bins, n_frames) row-major, or (batch, n_frames,
+ * n_bins) with TFA_STFT_FRAMES_MAJOR, with n_bins = n_fft/2+1 when TFA_STFT_ONESIDED else n_fft.  Replaces trnfft/api.py:291-365 (stft).  n_fft: a power
  * of two in [16, 4096], or any other n_fft from 9 up to 2731 (onesided) or 2048 (two-sided),
  * forward only: each frame then goes through the reference's Bluestein chain
  * (trnfft/fft_core.py:1285-1376), convolved at the shortest power of two or 3 * 2^k that holds
@@ -160,8 +165,8 @@ int tfa_complex_gemm(int64_t m, int64_t n, int64_t k, const float* a_re, const f
 
 /*
  * Inverse STFT of onesided spectra (TFA_KIND_STFT plan created with inverse = 1; n = n_fft,
- * hop, flags CENTER / NORMALIZED, ONESIDED required): spec_re/spec_im (batch, n/2+1, n_frames)
- * -> out (batch, out_len), out_len from tfa_istft_length (length < 0: the default length).
+ * hop, flags CENTER / NORMALIZED, ONESIDED required, FRAMES_MAJOR optional): spec_re/spec_im
+ * (batch, n/2+1, n_frames), or (batch, n_frames, n/2+1) with FRAMES_MAJOR, -> out (batch, out_len), out_len from tfa_istft_length (length < 0: the default length).
  * Hermitian completion, inverse transform, window, overlap-add, division by the window-square
  * envelope where it exceeds 1e-8 (the raw overlap-add elsewhere), centre trim and zero fill to
  * `length` in one kernel.  Replaces trnfft/api.py:368-470 (istft), whose per-frame loops
@@ -173,7 +178,8 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
 
 /*
  * Gradient of the onesided forward STFT with respect to its padded signal: grad_re/grad_im
- * (batch, n/2+1, n_frames), the gradient of tfa_stft_execute's output planes, -> grad_padded
+ * (batch, n/2+1, n_frames), or (batch, n_frames, n/2+1) when the plan has FRAMES_MAJOR, the
+ * gradient of tfa_stft_execute's output planes, -> grad_padded
  * (batch, padded_len), padded_len = num_samples + 2*(n/2) when CENTER else num_samples, n_frames
  * = 1 + (padded_len - n)/hop.  Per frame the adjoint of the r2c transform (interior bins halved,
  * Hermitian-completed inverse transform, unscaled; 1/sqrt(n) when NORMALIZED), times the window,

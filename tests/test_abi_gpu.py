@@ -112,3 +112,55 @@ def test_bluestein_split_needs_workspace():
     assert lib.tfa_execute(p, 2, P(x), P(x), P(y), P(y), None, st) == _lib.TFA_ERR_INVALID
     assert "workspace" in _err()
     lib.tfa_plan_destroy(p)
+
+
+@pytest.mark.parametrize("n_fft,hop,onesided", [(512, 256, True), (400, 160, True), (64, 16, False), (100, 40, False),
+                                                 (2048, 512, True)])
+def test_stft_frames_major_layout(n_fft, hop, onesided):
+    # TFA_STFT_FRAMES_MAJOR stores the same values as (batch, frames, bins): the forward output,
+    # the inverse input and the backward's gradient input, bit for bit
+    lib = _lib.lib()
+    st = VP(torch.cuda.current_stream().cuda_stream)
+    g = torch.Generator(device="cuda").manual_seed(n_fft)
+    length = 5000
+    x = torch.randn(3, length, device="cuda", generator=g)
+    w = torch.hann_window(n_fft, device="cuda")
+    base = _lib.STFT_CENTER | (_lib.STFT_ONESIDED if onesided else 0)
+    bins = n_fft // 2 + 1 if onesided else n_fft
+    frames = 1 + (length + 2 * (n_fft // 2) - n_fft) // hop
+    plans = []
+    for fl in (base, base | _lib.STFT_FRAMES_MAJOR):
+        rc, h = _plan(_lib.KIND_STFT, n_fft, hop=hop, flags=fl)
+        assert rc == 0, _err()
+        plans.append(h)
+    a_re, a_im = torch.empty(3, bins, frames, device="cuda"), torch.empty(3, bins, frames, device="cuda")
+    b_re, b_im = torch.empty(3, frames, bins, device="cuda"), torch.empty(3, frames, bins, device="cuda")
+    assert lib.tfa_stft_execute(plans[0], 3, length, P(x), P(w), P(a_re), P(a_im), st) == 0
+    assert lib.tfa_stft_execute(plans[1], 3, length, P(x), P(w), P(b_re), P(b_im), st) == 0
+    torch.testing.assert_close(a_re, b_re.transpose(1, 2), rtol=0, atol=0)
+    torch.testing.assert_close(a_im, b_im.transpose(1, 2), rtol=0, atol=0)
+    if onesided:
+        # the signal gradient on the forward plans: (gradient planes in each plan's layout)
+        outs = []
+        for h, (gr, gi) in zip(plans, [(a_re, a_im), (b_re, b_im)]):
+            d = torch.empty(3, length + 2 * (n_fft // 2), device="cuda")
+            rc = lib.tfa_stft_backward_execute(h, 3, frames, P(gr), P(gi), P(w), P(d), d.shape[1], st)
+            assert rc == 0, _err()
+            outs.append(d)
+        torch.testing.assert_close(outs[0], outs[1], rtol=0, atol=0)
+        # the inverse
+        inv = []
+        for fl in (base, base | _lib.STFT_FRAMES_MAJOR):
+            rc, h = _plan(_lib.KIND_STFT, n_fft, inverse=1, hop=hop, flags=fl)
+            assert rc == 0, _err()
+            inv.append(h)
+        ys = []
+        for h, (gr, gi) in zip(inv, [(a_re, a_im), (b_re, b_im)]):
+            y = torch.empty(3, length, device="cuda")
+            assert lib.tfa_istft_execute(h, 3, frames, P(gr), P(gi), P(w), P(y), length, st) == 0, _err()
+            ys.append(y)
+        torch.testing.assert_close(ys[0], ys[1], rtol=0, atol=0)
+        plans += inv
+    torch.cuda.synchronize()
+    for h in plans:
+        lib.tfa_plan_destroy(h)

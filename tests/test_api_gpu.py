@@ -200,6 +200,25 @@ def test_stft_fused_bluestein_matches_composed_path(n_fft, hop, pad_mode):
         <= tol_bluestein(n_fft) / 4
 
 
+@pytest.mark.parametrize("n_fft,hop", [(512, 256), (400, 160), (8192, 2048)])
+def test_stft_memory_order_is_frames_major_like_torch(n_fft, hop):
+    # the (..., freq, time) result is a transposed view of (..., time, freq) buffers, the memory
+    # order of torch.stft's result and of the reference's own transpose (trnfft/api.py:356-358);
+    # istft takes either order, and a bins-major copy gives the same signal
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 3, 20000, generator=g).cuda()
+    y = trnfft_amd.stft(x, n_fft=n_fft, hop_length=hop)
+    ref = torch.stft(x[0, 0].cpu(), n_fft, hop, window=torch.hann_window(n_fft), return_complex=True)
+    assert y.real.shape == (2, 3) + tuple(ref.shape)
+    assert y.real.transpose(-2, -1).is_contiguous() and y.imag.transpose(-2, -1).is_contiguous()
+    a = trnfft_amd.istft(y, n_fft=n_fft, hop_length=hop, length=20000)
+    b = trnfft_amd.istft(ComplexTensor(y.real.contiguous(), y.imag.contiguous()), n_fft=n_fft, hop_length=hop,
+                         length=20000)
+    tol = 1e-6 if n_fft & (n_fft - 1) == 0 else 1e-5
+    assert rel_l2(a, torch.zeros_like(a), b, torch.zeros_like(b)) <= tol
+    assert rel_l2(a, torch.zeros_like(a), x, torch.zeros_like(x)) <= (1e-5 if tol == 1e-6 else 1e-4)
+
+
 def test_stft_win_length_below_n_fft_and_custom_window_composed():
     g = torch.Generator().manual_seed(5)
     x = torch.randn(2, 6000, generator=g)

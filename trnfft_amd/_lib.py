@@ -30,6 +30,7 @@ OP_N, OP_T, OP_C, OP_R = 0, 1, 2, 3
 STFT_CENTER = 1
 STFT_NORMALIZED = 2
 STFT_ONESIDED = 4
+STFT_FRAMES_MAJOR = 8
 
 # every symbol include/trnfft_amd.h declares
 EXPORTS = (

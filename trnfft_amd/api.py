@@ -16,6 +16,7 @@ from . import _lib
 from .complex import ComplexTensor
 from .dispatch import _require_hip, target_device, to_device_f32
 from . import autograd as _ag
+from . import fft_core as _fc
 from .fft_core import fft2_ok, fft_core, real_ok, strided_ok
 from .plan import native_plan
 from .precision import _resolve
@@ -337,16 +338,17 @@ def stft(
         return out if out_dev == dev else out.to(out_dev)
     # trnfft/api.py:321-363 on the device: frame gather, window, transform of real frames,
     # onesided slice, (freq, time) transpose, normalisation
-    frame_idx = (torch.arange(n_fft, device=dev).unsqueeze(0)
-                 + torch.arange(num_frames, device=dev).unsqueeze(1) * hop_length)
-    frames = (x[..., frame_idx] * win).contiguous()  # (..., T, n_fft)
+    # (the frame gather as a strided view: the same elements as the reference's index tensor,
+    # and a cheap adjoint under autograd)
+    frames = (x.unfold(-1, n_fft, hop_length)[..., :num_frames, :] * win).contiguous()  # (..., T, n_fft)
     spec = rfft(frames) if onesided else _real_1d(frames, inverse=False)
-    out_re = spec.real.transpose(-2, -1)
-    out_im = spec.imag.transpose(-2, -1)
+    # (..., T, bins) buffers returned as (..., bins, T) views: the reference's own transpose
+    out_re = spec.real.contiguous()
+    out_im = spec.imag.contiguous()
     if normalized:
         scale = 1.0 / math.sqrt(n_fft)
         out_re, out_im = out_re * scale, out_im * scale
-    out = ComplexTensor._wrap(out_re.contiguous(), out_im.contiguous())
+    out = ComplexTensor._wrap(out_re.transpose(-2, -1), out_im.transpose(-2, -1))
     return out if out_dev == dev else out.to(out_dev)
 
 
@@ -444,17 +446,21 @@ def _istft_fused(spec, n_fft, hop, win_length, window, center, normalized, onesi
     dev = target_device(re, im)
     out_dev = re.device
     flags = _lib.STFT_ONESIDED | (_lib.STFT_CENTER if center else 0) | (_lib.STFT_NORMALIZED if normalized else 0)
+    re = to_device_f32(re, dev)
+    im = to_device_f32(im, dev)
+    frames = re.shape[-1]
+    lead = re.shape[:-2]
+    batch = re.numel() // (re.shape[-2] * frames)
+    # either memory order of the (..., bins, frames) planes, without a copy where possible
+    re, im, fm = _fc.stft_planes(re.reshape(batch, re.shape[-2], frames), im.reshape(batch, im.shape[-2], frames))
+    if fm:
+        flags |= _lib.STFT_FRAMES_MAJOR
     try:
         plan = native_plan(_lib.KIND_STFT, n_fft, True, dev.index, hop=hop, flags=flags)
     except NotImplementedError:
         return None  # hop too small for the kernel's frame tile
     win = _effective_window(window.to(dev) if window is not None else None, n_fft, win_length, torch.float32, dev)
     win = to_device_f32(win, dev)
-    re = to_device_f32(re, dev)
-    im = to_device_f32(im, dev)
-    frames = re.shape[-1]
-    lead = re.shape[:-2]
-    batch = re.numel() // (re.shape[-2] * frames)
     out_len = ctypes.c_int64()
     lib = _lib.lib()
     req = -1 if length is None else int(length)

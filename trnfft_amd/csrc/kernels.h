@@ -247,6 +247,8 @@ struct StftArgs {
   const float2* chirp = nullptr;
   const float2* hs = nullptr;
   int m = 0;
+  // output planes (batch, n_frames, n_bins) instead of (batch, n_bins, n_frames)
+  bool frames_major = false;
 };
 hipError_t launch_stft(int n_fft, const StftArgs& a);
 hipError_t launch_stft_blue(int n_fft, const StftArgs& a);  // a.m != 0
@@ -286,6 +288,8 @@ struct IstftArgs {
   // hop, start, out_pitch and write_len multiples of 4 and out 16-byte aligned: interior tiles
   // write four consecutive samples per thread (host-checked)
   bool vec4 = false;
+  // input planes (batch, n_frames, n_fft/2+1) instead of (batch, n_fft/2+1, n_frames)
+  bool frames_major = false;
   // n_fft that is not a power of two (one inverse Bluestein chain per frame, length m): forward
   // and inverse m-point tables, the inverse chirp (n_fft) and its filter spectrum H/m (m)
   const float2* blue_tw_f = nullptr;

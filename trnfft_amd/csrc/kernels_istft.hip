@@ -41,7 +41,8 @@ struct IstftCfg {
   static_assert(PAIRS >= 1 && RP >= 4 * F && RP >= 2 * NFFT, "istft tile");
 };
 
-template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = istft_threads(NFFT) / (NFFT / E_), bool ADJ = false>
+template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = istft_threads(NFFT) / (NFFT / E_), bool ADJ = false,
+          bool FM = false>
 __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_kernel(
     const float* __restrict__ sre, const float* __restrict__ sim, const float* __restrict__ win,
     float* __restrict__ out, const float2* __restrict__ tw, int n_frames, int hop, int halo, int owned,
@@ -63,43 +64,73 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
   const int nf = (t0 + owned < n_frames ? t0 + owned : n_frames) - ta;  // frames in the tile (<= FR)
 
   for (int i = threadIdx.x; i < NFFT; i += THREADS) wl[i] = win[i];
-  // 1. stage bins: region of pair p = [re_a | im_a | re_b | im_b], F floats each.  Lane fs of
-  //    every KS-lane group reads frame fs of bin rows k0, k0 + KS, ... (THREADS is a multiple
-  //    of FR, so a lane keeps its frame): one 32-bit offset step per load from the signal's base
-  //    (the former per-load 64-bit index arithmetic was a quarter of the kernel's VALU work)
-  constexpr int KS = THREADS / FR;
-  static_assert(THREADS % FR == 0, "lanes keep their frame across the staging steps");
-  const int fs = (int)threadIdx.x % FR, k0 = (int)threadIdx.x / FR;
-  const float* bre = sre + (size_t)b * F * n_frames + ta;
-  const float* bim = sim + (size_t)b * F * n_frames + ta;
-  // every load of the tile is issued before the first LDS write (a load-then-store loop would
-  // wait out the full memory latency once per iteration)
-  constexpr int SI = (F + KS - 1) / KS;
-  float sr[SI], si[SI];
-  {
-    unsigned off = (unsigned)(fs + k0 * n_frames);
-    const unsigned step = (unsigned)(KS * n_frames);
-    const bool fok = fs < nf;
+  // 1. stage bins: region of pair p = [re_a | im_a | re_b | im_b], F floats each.  Every load of
+  //    the tile is issued before the first LDS write (a load-then-store loop would wait out the
+  //    full memory latency once per iteration).
+  if constexpr (FM) {
+    // frames-major input (batch, n_frames, F): the tile's frames are consecutive rows, one
+    // contiguous run of nf * F floats per plane read by consecutive lanes
+    const float* bre = sre + ((size_t)b * n_frames + ta) * F;
+    const float* bim = sim + ((size_t)b * n_frames + ta) * F;
+    constexpr int SJ = (FR * F + THREADS - 1) / THREADS;
+    float sr[SJ], si[SJ];
 #pragma unroll
-    for (int it = 0; it < SI; ++it) {
+    for (int it = 0; it < SJ; ++it) {
+      const int i = (int)threadIdx.x + THREADS * it;
       sr[it] = 0.0f;
       si[it] = 0.0f;
-      if (k0 + KS * it < F && fok) {
-        // plain loads: a bin row segment is FR frames (64 bytes at n_fft 512), so a cache line is
-        // shared with the neighbouring tile, which then finds it in L2 (measured 4 % faster)
-        sr[it] = bre[off];
-        si[it] = bim[off];
+      if (i < nf * F) {
+        sr[it] = bre[i];
+        si[it] = bim[i];
       }
-      off += step;
     }
-  }
-  float* sreg = lds + (fs >> 1) * RP + (fs & 1) * 2 * F + k0;
 #pragma unroll
-  for (int it = 0; it < SI; ++it) {
-    const int k = k0 + KS * it;
-    if (k < F) {
-      sreg[KS * it] = (ADJ && (k == 0 || k == NFFT / 2)) ? 2.0f * sr[it] : sr[it];
-      sreg[F + KS * it] = (k == 0 || k == NFFT / 2) ? 0.0f : si[it];
+    for (int it = 0; it < SJ; ++it) {
+      const int i = (int)threadIdx.x + THREADS * it;
+      if (i < FR * F) {
+        const int f = i / F, k = i - f * F;
+        float* r = lds + (f >> 1) * RP + (f & 1) * 2 * F;
+        r[k] = (ADJ && (k == 0 || k == NFFT / 2)) ? 2.0f * sr[it] : sr[it];
+        r[F + k] = (k == 0 || k == NFFT / 2) ? 0.0f : si[it];
+      }
+    }
+  } else {
+    // (batch, F, n_frames): lane fs of every KS-lane group reads frame fs of bin rows k0,
+    // k0 + KS, ... (THREADS is a multiple of FR, so a lane keeps its frame): one 32-bit offset
+    // step per load from the signal's base (the former per-load 64-bit index arithmetic was a
+    // quarter of the kernel's VALU work)
+    constexpr int KS = THREADS / FR;
+    static_assert(THREADS % FR == 0, "lanes keep their frame across the staging steps");
+    const int fs = (int)threadIdx.x % FR, k0 = (int)threadIdx.x / FR;
+    const float* bre = sre + (size_t)b * F * n_frames + ta;
+    const float* bim = sim + (size_t)b * F * n_frames + ta;
+    constexpr int SI = (F + KS - 1) / KS;
+    float sr[SI], si[SI];
+    {
+      unsigned off = (unsigned)(fs + k0 * n_frames);
+      const unsigned step = (unsigned)(KS * n_frames);
+      const bool fok = fs < nf;
+#pragma unroll
+      for (int it = 0; it < SI; ++it) {
+        sr[it] = 0.0f;
+        si[it] = 0.0f;
+        if (k0 + KS * it < F && fok) {
+          // plain loads: a bin row segment is FR frames (64 bytes at n_fft 512), so a cache line
+          // is shared with the neighbouring tile, which then finds it in L2 (measured 4 % faster)
+          sr[it] = bre[off];
+          si[it] = bim[off];
+        }
+        off += step;
+      }
+    }
+    float* sreg = lds + (fs >> 1) * RP + (fs & 1) * 2 * F + k0;
+#pragma unroll
+    for (int it = 0; it < SI; ++it) {
+      const int k = k0 + KS * it;
+      if (k < F) {
+        sreg[KS * it] = (ADJ && (k == 0 || k == NFFT / 2)) ? 2.0f * sr[it] : sr[it];
+        sreg[F + KS * it] = (k == 0 || k == NFFT / 2) ? 0.0f : si[it];
+      }
     }
   }
   __syncthreads();
@@ -250,15 +281,19 @@ static hipError_t launch_istft_cfg(const IstftArgs& a) {
   const int tiles = (a.n_frames + owned - 1) / owned;
   const long long blocks = a.batch * (long long)tiles;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-  if (a.adjoint)
-    hipLaunchKernelGGL((istft_kernel<NFFT, istft_epth(NFFT), MAXP, true>), dim3((unsigned)blocks), dim3(C::THREADS),
-                       0, a.stream, a.spec_re, a.spec_im, a.window, a.out, a.tw, a.n_frames, a.hop, a.halo, owned,
-                       tiles, (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale,
-                       (int)a.vec4);
-  else
-    hipLaunchKernelGGL((istft_kernel<NFFT, istft_epth(NFFT), MAXP>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
-                       a.stream, a.spec_re, a.spec_im, a.window, a.out, a.tw, a.n_frames, a.hop, a.halo, owned, tiles,
-                       (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale, (int)a.vec4);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream, a.spec_re, a.spec_im, a.window,
+                       a.out, a.tw, a.n_frames, a.hop, a.halo, owned, tiles, (int)a.expected_len, (int)a.start,
+                       (int)a.write_len, (int)a.out_pitch, a.scale, (int)a.vec4);
+  };
+  constexpr int E = istft_epth(NFFT);
+  if (a.adjoint) {
+    if (a.frames_major) go(istft_kernel<NFFT, E, MAXP, true, true>);
+    else go(istft_kernel<NFFT, E, MAXP, true, false>);
+  } else {
+    if (a.frames_major) go(istft_kernel<NFFT, E, MAXP, false, true>);
+    else go(istft_kernel<NFFT, E, MAXP, false, false>);
+  }
   return hipGetLastError();
 }
 

@@ -10,8 +10,10 @@
 //      the half-hop overlap between neighbouring frames is served by L2;
 //   2. each pair is transformed (LDS Stockham; one wavefront per pair at n_fft = 512);
 //   3. each pair stores its spectrum as packed entries (Z[k], Z[n-k]), k <= n/2, one float4 each;
-//      lanes then run over consecutive frames and read one entry per output bin, so every store
-//      instruction writes FR contiguous floats of bin rows of the (batch, bins, frames) output.
+//      frames-major output (batch, frames, bins) -- the memory order of torch.stft's result and
+//      of trnfft's transposed view -- is then one contiguous run per plane for the whole tile;
+//      for (batch, bins, frames) lanes run over consecutive frames and read one entry per output
+//      bin, so every store instruction writes FR contiguous floats of bin rows.
 // The window is pre-scaled by scale/2 (the 1/2 of the pair separation, and the normalisation), so
 // the separation is two additions per output value.
 #include "kernels.h"
@@ -33,11 +35,11 @@ constexpr int stft_area(int n) {
   return a;
 }
 
-template <int NFFT>
+template <int NFFT, int PAIRS_ = stft_pairs<NFFT>(), int E_ = stft_epth(NFFT)>
 struct StftCfg {
-  static constexpr int E = stft_epth(NFFT);
+  static constexpr int E = E_;
   static constexpr int T = NFFT / E;  // threads per frame pair
-  static constexpr int PAIRS = stft_pairs<NFFT>();
+  static constexpr int PAIRS = PAIRS_;
   static constexpr int FR = 2 * PAIRS;  // frames per workgroup
   static constexpr int THREADS = PAIRS * T;
   static constexpr int AREA = stft_area(NFFT);
@@ -46,12 +48,17 @@ struct StftCfg {
   static_assert(THREADS % FR == 0, "the output stage maps lanes to (bin, frame)");
 };
 
-template <int NFFT>
-__global__ __launch_bounds__((StftCfg<NFFT>::THREADS)) void stft_kernel(
+// FM: frames-major output, (batch, n_frames, n_bins): the tile's frames are consecutive rows, so
+// every plane receives one contiguous run of (frames in the tile) * n_bins floats, written by
+// consecutive lanes; otherwise (batch, n_bins, n_frames), FR floats per bin row.  LDNT / STNT:
+// non-temporal waveform loads / frames-major stores.
+template <int NFFT, bool FM = false, int PAIRS_ = stft_pairs<NFFT>(), int E_ = stft_epth(NFFT), bool LDNT = true,
+          bool STNT = true>
+__global__ __launch_bounds__((StftCfg<NFFT, PAIRS_, E_>::THREADS)) void stft_kernel(
     const float* __restrict__ sig, const float* __restrict__ win, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ tw, int length, int hop, int pad,
     int n_frames, int n_bins, int tiles_per_signal, float hs) {
-  using C = StftCfg<NFFT>;
+  using C = StftCfg<NFFT, PAIRS_, E_>;
   constexpr int E = C::E, T = C::T, FR = C::FR, AREA = C::AREA, THREADS = C::THREADS, NB1 = C::NB1;
   __shared__ __attribute__((aligned(16))) float lds[C::PAIRS * AREA];
   const unsigned tile = xcd_tile_remap32(blockIdx.x, gridDim.x);  // 32-bit: grids below 2^31 (launcher)
@@ -72,9 +79,9 @@ __global__ __launch_bounds__((StftCfg<NFFT>::THREADS)) void stft_kernel(
     const float* p1 = p0 + hop;
     float a[E], c[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) a[e] = ld_stream(p0 + T * e);
+    for (int e = 0; e < E; ++e) a[e] = LDNT ? ld_stream(p0 + T * e) : p0[T * e];
 #pragma unroll
-    for (int e = 0; e < E; ++e) c[e] = ld_stream(p1 + T * e);
+    for (int e = 0; e < E; ++e) c[e] = LDNT ? ld_stream(p1 + T * e) : p1[T * e];
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = make_float2(a[e] * wv[e], c[e] * wv[e]);
   } else {
@@ -113,6 +120,39 @@ __global__ __launch_bounds__((StftCfg<NFFT>::THREADS)) void stft_kernel(
     sp[2 * (NFFT / 2)] = v[E / 2]; // entry n/2: Z[n/2] in both halves
   }
   __syncthreads();
+  if constexpr (FM) {
+    const int nfr = n_frames - f0 < FR ? n_frames - f0 : FR;
+    const size_t ob = ((size_t)b * n_frames + f0) * n_bins;
+    float* cre = out_re + ob;
+    float* cim = out_im + ob;
+    if (n_bins == NB1) {
+      for (int i = threadIdx.x; i < nfr * NB1; i += THREADS) {
+        const int fl = i / NB1, k = i - fl * NB1;
+        const float4 q = reinterpret_cast<const float4*>(lds + (fl >> 1) * AREA)[k];  // (Z[k], Z[n-k])
+        const bool odd = fl & 1;
+        const float re = odd ? (q.y + q.w) : (q.x + q.z), im = odd ? (q.z - q.x) : (q.y - q.w);
+        if constexpr (STNT) {
+          st_stream(cre + i, re);
+          st_stream(cim + i, im);
+        } else {
+          cre[i] = re;
+          cim[i] = im;
+        }
+      }
+    } else {
+      // two-sided: bins above n/2 read entry n - k with its halves swapped
+      for (int i = threadIdx.x; i < nfr * NFFT; i += THREADS) {
+        const int fl = i / NFFT, k = i % NFFT;
+        const bool hi = k > NFFT / 2;
+        const float4 q = reinterpret_cast<const float4*>(lds + (fl >> 1) * AREA)[hi ? NFFT - k : k];
+        const float zr = hi ? q.z : q.x, zi = hi ? q.w : q.y, yr = hi ? q.x : q.z, yi = hi ? q.y : q.w;
+        const bool odd = fl & 1;
+        st_stream(cre + i, odd ? (zi + yi) : (zr + yr));
+        st_stream(cim + i, odd ? (yr - zr) : (zi - yi));
+      }
+    }
+    return;
+  }
   // lanes over consecutive frames fr: frame fr = 2p (+1) is the real (imaginary) part of pair p
   constexpr int KS = THREADS / FR;  // bins per step
   const int fr = threadIdx.x % FR;
@@ -154,8 +194,30 @@ __global__ __launch_bounds__((StftCfg<NFFT>::THREADS)) void stft_kernel(
   }
 }
 
+// Frame pairs per workgroup of the frames-major kernel, from a sweep on MI355X (64 x 160000
+// samples, hop n/2, 1..32 pairs): 256 threads up to n_fft = 512, 512 above (64: 30.5 us, 128:
+// 31.3, 256: 32.0, 512: 32.8 against 36.8 with the bins-major tile shape, 1024: 36.2, 2048: 36.9,
+// 4096: 38.9), with temporal waveform loads (the half-hop overlap of neighbouring frames then hits
+// in the cache: 512 with 4 pairs 34.3 -> 32.7 us).
+template <int NFFT>
+constexpr int stft_fm_pairs() {
+  constexpr int p = (NFFT <= 512 ? 256 : 512) / (NFFT / stft_epth(NFFT));
+  return p < 1 ? 1 : p > 32 ? 32 : p;
+}
+
 template <int NFFT>
 static hipError_t launch_stft_n(const StftArgs& a) {
+  if (a.frames_major) {
+    constexpr int P = stft_fm_pairs<NFFT>();
+    using C = StftCfg<NFFT, P>;
+    const int tiles = (a.n_frames + C::FR - 1) / C::FR;
+    const long long blocks = a.batch * (long long)tiles;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((stft_kernel<NFFT, true, P, stft_epth(NFFT), false, true>), dim3((unsigned)blocks),
+                       dim3(C::THREADS), 0, a.stream, a.signal, a.window, a.out_re, a.out_im, a.tw, a.length, a.hop,
+                       a.pad, a.n_frames, a.n_bins, tiles, 0.5f * a.scale);
+    return hipGetLastError();
+  }
   using C = StftCfg<NFFT>;
   const int tiles = (a.n_frames + C::FR - 1) / C::FR;
   const long long blocks = a.batch * (long long)tiles;
@@ -163,8 +225,8 @@ static hipError_t launch_stft_n(const StftArgs& a) {
   // stft_lds_extra: unused dynamic LDS that holds the workgroups resident per CU to one where that
   // measured faster
   hipLaunchKernelGGL((stft_kernel<NFFT>), dim3((unsigned)blocks), dim3(C::THREADS), stft_lds_extra(NFFT), a.stream,
-                     a.signal, a.window, a.out_re, a.out_im, a.tw, a.length, a.hop, a.pad, a.n_frames, a.n_bins, tiles,
-                     0.5f * a.scale);
+                     a.signal, a.window, a.out_re, a.out_im, a.tw, a.length, a.hop, a.pad, a.n_frames, a.n_bins,
+                     tiles, 0.5f * a.scale);
   return hipGetLastError();
 }
 

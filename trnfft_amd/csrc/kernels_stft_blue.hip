@@ -32,7 +32,7 @@ struct StftBlueCfg {
   static_assert(AREA % 4 == 0, "frame areas start 16-byte aligned");
 };
 
-template <int M, int E, int FR>
+template <int M, int E, int FR, bool FM = false>
 __global__ __launch_bounds__((StftBlueCfg<M, E, FR>::THREADS)) void stft_blue_kernel(
     const float* __restrict__ sig, const float* __restrict__ win, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ chirp, const float2* __restrict__ hs,
@@ -89,6 +89,23 @@ __global__ __launch_bounds__((StftBlueCfg<M, E, FR>::THREADS)) void stft_blue_ke
     }
   }
   __syncthreads();
+  if constexpr (FM) {
+    // frames-major output (batch, n_frames, n_bins): the tile's frames are consecutive rows, one
+    // contiguous run of nfr * n_bins floats per plane written by consecutive lanes
+    const int nfr = n_frames - f0 < FR ? n_frames - f0 : FR;
+    const size_t ob = ((size_t)b * n_frames + f0) * n_bins;
+    float* cre = out_re + ob;
+    float* cim = out_im + ob;
+    const float rb = 1.0f / (float)n_bins;
+    for (int i = threadIdx.x; i < nfr * n_bins; i += THREADS) {
+      int k;
+      const int fl = divmod_small(i, n_bins, rb, k);
+      const float2 q = reinterpret_cast<const float2*>(lds + fl * AREA)[k];
+      st_stream(cre + i, q.x);
+      st_stream(cim + i, q.y);
+    }
+    return;
+  }
   constexpr int KS = THREADS / FR;  // bins per step
   const int fr = threadIdx.x % FR;
   const int kb = threadIdx.x / FR;
@@ -118,9 +135,14 @@ static hipError_t launch_stft_blue_m(int n_fft, const StftArgs& a) {
   const int tiles = (a.n_frames + FR - 1) / FR;
   const long long blocks = a.batch * (long long)tiles;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((stft_blue_kernel<M, E, FR>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream,
-                     a.signal, a.window, a.out_re, a.out_im, a.chirp, a.hs, a.tw, a.tw_i, n_fft, a.length, a.hop,
-                     a.pad, a.n_frames, a.n_bins, tiles, a.scale);
+  if (a.frames_major)
+    hipLaunchKernelGGL((stft_blue_kernel<M, E, FR, true>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream,
+                       a.signal, a.window, a.out_re, a.out_im, a.chirp, a.hs, a.tw, a.tw_i, n_fft, a.length, a.hop,
+                       a.pad, a.n_frames, a.n_bins, tiles, a.scale);
+  else
+    hipLaunchKernelGGL((stft_blue_kernel<M, E, FR>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream,
+                       a.signal, a.window, a.out_re, a.out_im, a.chirp, a.hs, a.tw, a.tw_i, n_fft, a.length, a.hop,
+                       a.pad, a.n_frames, a.n_bins, tiles, a.scale);
   return hipGetLastError();
 }
 
@@ -176,7 +198,7 @@ struct IstftBlueCfg {
   static_assert(FR * AREA * 4 + NW * 4 <= kLdsBytes, "inverse STFT frame tile exceeds LDS");
 };
 
-template <int M, int E, int FR, bool ADJ = false>
+template <int M, int E, int FR, bool ADJ = false, bool FM = false>
 __global__ __launch_bounds__((IstftBlueCfg<M, E, FR, ADJ>::THREADS)) void istft_blue_kernel(
     const float* __restrict__ sre, const float* __restrict__ sim, const float* __restrict__ win,
     float* __restrict__ out, const float2* __restrict__ chirp, const float2* __restrict__ hs,
@@ -195,25 +217,56 @@ __global__ __launch_bounds__((IstftBlueCfg<M, E, FR, ADJ>::THREADS)) void istft_
 
   for (int i = threadIdx.x; i < n; i += THREADS) wl[i] = win[i];
   // 1. stage bins: frame f's area = [re (K) | im (K)]; four loads in flight per thread
-  const size_t sbase = (size_t)b * K * n_frames + ta;
-  for (int i0 = threadIdx.x; i0 < K * FR; i0 += 4 * THREADS) {
-    float sr[4], si[4];
+  if constexpr (FM) {
+    // frames-major input (batch, n_frames, K): the tile's frames are consecutive rows, one
+    // contiguous run of nf * K floats per plane (frames past nf stage zeros)
+    const float* bre = sre + ((size_t)b * n_frames + ta) * K;
+    const float* bim = sim + ((size_t)b * n_frames + ta) * K;
+    const float rk = 1.0f / (float)K;
+    for (int i0 = threadIdx.x; i0 < K * FR; i0 += 4 * THREADS) {
+      float sr[4], si[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = i0 + u * THREADS, f = i % FR, k = i / FR;
-      sr[u] = 0.0f;
-      si[u] = 0.0f;
-      if (i < K * FR && f < nf) {
-        sr[u] = sre[sbase + (size_t)k * n_frames + f];
-        si[u] = sim[sbase + (size_t)k * n_frames + f];
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * THREADS;
+        sr[u] = 0.0f;
+        si[u] = 0.0f;
+        if (i < K * nf) {
+          sr[u] = bre[i];
+          si[u] = bim[i];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * THREADS;
+        if (i < K * FR) {
+          int k;
+          const int f = divmod_small(i, K, rk, k);
+          lds[f * AREA + k] = sr[u];
+          lds[f * AREA + K + k] = si[u];
+        }
       }
     }
+  } else {
+    const size_t sbase = (size_t)b * K * n_frames + ta;
+    for (int i0 = threadIdx.x; i0 < K * FR; i0 += 4 * THREADS) {
+      float sr[4], si[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = i0 + u * THREADS, f = i % FR, k = i / FR;
-      if (i < K * FR) {
-        lds[f * AREA + k] = sr[u];
-        lds[f * AREA + K + k] = si[u];
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * THREADS, f = i % FR, k = i / FR;
+        sr[u] = 0.0f;
+        si[u] = 0.0f;
+        if (i < K * FR && f < nf) {
+          sr[u] = sre[sbase + (size_t)k * n_frames + f];
+          si[u] = sim[sbase + (size_t)k * n_frames + f];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * THREADS, f = i % FR, k = i / FR;
+        if (i < K * FR) {
+          lds[f * AREA + k] = sr[u];
+          lds[f * AREA + K + k] = si[u];
+        }
       }
     }
   }
@@ -294,10 +347,13 @@ static hipError_t launch_istft_blue_cfg(int n_fft, const IstftArgs& a) {
   const int tiles = (a.n_frames + owned - 1) / owned;
   const long long blocks = a.batch * (long long)tiles;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((istft_blue_kernel<M, E, FR, ADJ>), dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream,
-                     a.spec_re, a.spec_im, a.window, a.out, a.chirp, a.hs, a.blue_tw_f, a.blue_tw_i, n_fft,
-                     a.n_frames, a.hop, a.halo, owned, tiles, (int)a.expected_len, (int)a.start, (int)a.write_len,
-                     (int)a.out_pitch, a.scale);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(C::THREADS), 0, a.stream, a.spec_re, a.spec_im, a.window,
+                       a.out, a.chirp, a.hs, a.blue_tw_f, a.blue_tw_i, n_fft, a.n_frames, a.hop, a.halo, owned, tiles,
+                       (int)a.expected_len, (int)a.start, (int)a.write_len, (int)a.out_pitch, a.scale);
+  };
+  if (a.frames_major) go(istft_blue_kernel<M, E, FR, ADJ, true>);
+  else go(istft_blue_kernel<M, E, FR, ADJ, false>);
   return hipGetLastError();
 }
 

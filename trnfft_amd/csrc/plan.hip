@@ -888,6 +888,7 @@ int tfa_stft_execute(const tfa_plan* plan, int64_t batch, int64_t num_samples, c
   const int64_t hop = std::min<int64_t>(plan->d.hop, num_samples + 2 * pad);
   tfa::StftArgs a{signal, window, out_re, out_im, plan->fwd.tw, (int)num_samples, (int)hop,
                   (int)pad, (int)frames, n_bins, batch, scale, static_cast<hipStream_t>(stream)};
+  a.frames_major = (plan->d.flags & TFA_STFT_FRAMES_MAJOR) != 0;
   if (!is_pow2(n_fft)) {
     a.tw_i = plan->inv.tw;
     a.chirp = plan->chirp;
@@ -942,6 +943,7 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
                    batch, expected, start, cur < out_len ? cur : out_len, out_len, (float)sc,
                    static_cast<hipStream_t>(stream)};
   a.vec4 = vec4_ok(a, out);
+  a.frames_major = (plan->d.flags & TFA_STFT_FRAMES_MAJOR) != 0;
   hipError_t e;
   if (!is_pow2(n_fft)) {
     a.blue_tw_f = plan->fwd.tw;
@@ -989,6 +991,7 @@ int tfa_stft_backward_execute(const tfa_plan* plan, int64_t batch, int64_t n_fra
                    static_cast<hipStream_t>(stream)};
   a.adjoint = true;
   a.vec4 = vec4_ok(a, grad_padded);
+  a.frames_major = (plan->d.flags & TFA_STFT_FRAMES_MAJOR) != 0;
   hipError_t e;
   if (pow2) {
     e = tfa::launch_istft((int)n_fft, a);

@@ -250,12 +250,29 @@ def execute_fft2_any(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -
     return execute_1d(y.real, y.imag, inverse)
 
 
+def stft_planes(re: torch.Tensor, im: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, bool]:
+    """(..., bins, frames) spectrum planes as contiguous buffers for the STFT kernels, without a
+    copy where possible: (..., frames, bins) buffers (frames_major True) when both planes are
+    transposed views of such tensors -- the layout of torch.stft's result, of trnfft's
+    (trnfft/api.py:356-358) and of this backend's -- the planes themselves when both are
+    contiguous, else frames-major copies."""
+    rt, it = re.transpose(-2, -1), im.transpose(-2, -1)
+    if rt.is_contiguous() and it.is_contiguous():
+        return rt, it, True
+    if re.is_contiguous() and im.is_contiguous():
+        return re, im, False
+    return rt.contiguous(), it.contiguous(), True
+
+
 def execute_stft(x: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int, center: bool, normalized: bool,
                  onesided: bool, num_frames: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Fused STFT kernel on device-resident fp32 x (..., L) and window (n_fft): (re, im) planes of
-    shape (..., bins, frames) (replaces trnfft/api.py:291-365 after its argument handling)."""
+    shape (..., bins, frames) (replaces trnfft/api.py:291-365 after its argument handling).  The
+    planes are transposed views of (..., frames, bins) buffers, the memory order of torch.stft's
+    result and of the reference's own transposed frames, which the kernel writes as one
+    contiguous run per tile."""
     flags = (_lib.STFT_CENTER if center else 0) | (_lib.STFT_NORMALIZED if normalized else 0)
-    flags |= _lib.STFT_ONESIDED if onesided else 0
+    flags |= (_lib.STFT_ONESIDED if onesided else 0) | _lib.STFT_FRAMES_MAJOR
     dev = x.device
     x = x.contiguous()
     win = win.contiguous()
@@ -265,14 +282,14 @@ def execute_stft(x: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int, cente
     batch = 1
     for d in lead:
         batch *= d
-    out_re = torch.empty(*lead, bins, num_frames, dtype=torch.float32, device=dev)
+    out_re = torch.empty(*lead, num_frames, bins, dtype=torch.float32, device=dev)
     out_im = torch.empty_like(out_re)
     with torch.cuda.device(dev):
         rc = _lib.lib().tfa_stft_execute(
             plan.handle, batch, x.shape[-1], ptr(x), ptr(win), ptr(out_re), ptr(out_im), stream_handle(dev)
         )
     _lib.check(rc, "tfa_stft_execute")
-    return out_re, out_im
+    return out_re.transpose(-2, -1), out_im.transpose(-2, -1)
 
 
 def execute_stft_backward(g_re: torch.Tensor, g_im: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int,
@@ -282,12 +299,15 @@ def execute_stft_backward(g_re: torch.Tensor, g_im: torch.Tensor, win: torch.Ten
     frame the adjoint of the transform -- the r2c adjoint, or the adjoint Bluestein chain for
     n_fft that is not a power of two -- window, overlap-add; replaces the autograd of
     trnfft/api.py:310-349's frame gather, window and per-frame transform).  None when the kernel's
-    frame tile refuses the hop (the caller composes)."""
+    frame tile refuses the hop (the caller composes).  The gradient planes may be in either
+    layout (stft_planes)."""
+    g_re, g_im, fm = stft_planes(g_re, g_im)
     flags = _lib.STFT_ONESIDED | (_lib.STFT_CENTER if center else 0) | (_lib.STFT_NORMALIZED if normalized else 0)
+    flags |= _lib.STFT_FRAMES_MAJOR if fm else 0
     dev = g_re.device
     plan = native_plan(_lib.KIND_STFT, n_fft, False, dev.index, hop=hop, flags=flags)
-    g_re, g_im, win = g_re.contiguous(), g_im.contiguous(), win.contiguous()
-    b, frames = g_re.shape[0], g_re.shape[-1]
+    win = win.contiguous()
+    b, frames = g_re.shape[0], (g_re.shape[-2] if fm else g_re.shape[-1])
     out = torch.empty(b, padded_len, dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         rc = _lib.lib().tfa_stft_backward_execute(plan.handle, b, frames, ptr(g_re), ptr(g_im), ptr(win), ptr(out),
