@@ -53,7 +53,7 @@ struct StftCfg {
 // consecutive lanes; otherwise (batch, n_bins, n_frames), FR floats per bin row.  LDNT / STNT:
 // non-temporal waveform loads / frames-major stores.
 template <int NFFT, bool FM = false, int PAIRS_ = stft_pairs<NFFT>(), int E_ = stft_epth(NFFT), bool LDNT = true,
-          bool STNT = true>
+          bool STNT = true, bool ALIGN = false>
 __global__ __launch_bounds__((StftCfg<NFFT, PAIRS_, E_>::THREADS)) void stft_kernel(
     const float* __restrict__ sig, const float* __restrict__ win, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ tw, int length, int hop, int pad,
@@ -125,8 +125,12 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS_, E_>::THREADS)) void stft_ker
     const size_t ob = ((size_t)b * n_frames + f0) * n_bins;
     float* cre = out_re + ob;
     float* cim = out_im + ob;
+    // lanes start one cache line early by the run's misalignment, so every store instruction of a
+    // full wave covers whole 128-byte lines (non-temporal stores of partial lines each reach HBM)
+    const int sh = ALIGN ? (int)((reinterpret_cast<uintptr_t>(cre) >> 2) & 31) : 0;
     if (n_bins == NB1) {
-      for (int i = threadIdx.x; i < nfr * NB1; i += THREADS) {
+      for (int i = (int)threadIdx.x - sh; i < nfr * NB1; i += THREADS) {
+        if (i < 0) continue;
         const int fl = i / NB1, k = i - fl * NB1;
         const float4 q = reinterpret_cast<const float4*>(lds + (fl >> 1) * AREA)[k];  // (Z[k], Z[n-k])
         const bool odd = fl & 1;
@@ -141,7 +145,8 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS_, E_>::THREADS)) void stft_ker
       }
     } else {
       // two-sided: bins above n/2 read entry n - k with its halves swapped
-      for (int i = threadIdx.x; i < nfr * NFFT; i += THREADS) {
+      for (int i = (int)threadIdx.x - sh; i < nfr * NFFT; i += THREADS) {
+        if (i < 0) continue;
         const int fl = i / NFFT, k = i % NFFT;
         const bool hi = k > NFFT / 2;
         const float4 q = reinterpret_cast<const float4*>(lds + (fl >> 1) * AREA)[hi ? NFFT - k : k];
@@ -198,7 +203,9 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS_, E_>::THREADS)) void stft_ker
 // samples, hop n/2, 1..32 pairs): 256 threads up to n_fft = 512, 512 above (64: 30.5 us, 128:
 // 31.3, 256: 32.0, 512: 32.8 against 36.8 with the bins-major tile shape, 1024: 36.2, 2048: 36.9,
 // 4096: 38.9), with temporal waveform loads (the half-hop overlap of neighbouring frames then hits
-// in the cache: 512 with 4 pairs 34.3 -> 32.7 us).
+// in the cache: 512 with 4 pairs 34.3 -> 32.7 us) and line-aligned non-temporal stores (256:
+// 32.1 -> 29.6 us, 512: 33.0 -> 30.7-31.0, 1024: 36.2 -> 34.5; the unaligned runs wrote 1.10x
+// their bytes).
 template <int NFFT>
 constexpr int stft_fm_pairs() {
   constexpr int p = (NFFT <= 512 ? 256 : 512) / (NFFT / stft_epth(NFFT));
@@ -213,7 +220,7 @@ static hipError_t launch_stft_n(const StftArgs& a) {
     const int tiles = (a.n_frames + C::FR - 1) / C::FR;
     const long long blocks = a.batch * (long long)tiles;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((stft_kernel<NFFT, true, P, stft_epth(NFFT), false, true>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((stft_kernel<NFFT, true, P, stft_epth(NFFT), false, true, true>), dim3((unsigned)blocks),
                        dim3(C::THREADS), 0, a.stream, a.signal, a.window, a.out_re, a.out_im, a.tw, a.length, a.hop,
                        a.pad, a.n_frames, a.n_bins, tiles, 0.5f * a.scale);
     return hipGetLastError();

@@ -97,7 +97,11 @@ __global__ __launch_bounds__((StftBlueCfg<M, E, FR>::THREADS)) void stft_blue_ke
     float* cre = out_re + ob;
     float* cim = out_im + ob;
     const float rb = 1.0f / (float)n_bins;
-    for (int i = threadIdx.x; i < nfr * n_bins; i += THREADS) {
+    // lanes start early by the run's misalignment to a 128-byte line, so full-wave stores cover
+    // whole lines (non-temporal stores of partial lines each reach HBM)
+    const int sh = (int)((reinterpret_cast<uintptr_t>(cre) >> 2) & 31);
+    for (int i = (int)threadIdx.x - sh; i < nfr * n_bins; i += THREADS) {
+      if (i < 0) continue;
       int k;
       const int fl = divmod_small(i, n_bins, rb, k);
       const float2 q = reinterpret_cast<const float2*>(lds + fl * AREA)[k];
