@@ -53,7 +53,7 @@ struct StftCfg {
 // consecutive lanes; otherwise (batch, n_bins, n_frames), FR floats per bin row.  LDNT / STNT:
 // non-temporal waveform loads / frames-major stores.
 template <int NFFT, bool FM = false, int PAIRS_ = stft_pairs<NFFT>(), int E_ = stft_epth(NFFT), bool LDNT = true,
-          bool STNT = true, bool ALIGN = false>
+          bool STNT = true, bool ALIGN = false, int OU = 0>
 __global__ __launch_bounds__((StftCfg<NFFT, PAIRS_, E_>::THREADS)) void stft_kernel(
     const float* __restrict__ sig, const float* __restrict__ win, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ tw, int length, int hop, int pad,
@@ -128,7 +128,37 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS_, E_>::THREADS)) void stft_ker
     // lanes start one cache line early by the run's misalignment, so every store instruction of a
     // full wave covers whole 128-byte lines (non-temporal stores of partial lines each reach HBM)
     const int sh = ALIGN ? (int)((reinterpret_cast<uintptr_t>(cre) >> 2) & 31) : 0;
-    if (n_bins == NB1) {
+    if (OU > 0 && n_bins == NB1) {
+      // OU store steps at a time: their LDS entries are read together (indices clamped into the
+      // tile, so the reads need no branch), then the in-range lanes store; 32-bit byte offsets
+      // from the tile's (wave-uniform) run bases
+      const int cnt = nfr * NB1;
+      char* bre = reinterpret_cast<char*>(cre);
+      char* bim = reinterpret_cast<char*>(cim);
+      for (int i0 = (int)threadIdx.x - sh; i0 < cnt; i0 += OU * THREADS) {
+        float4 q[OU > 0 ? OU : 1];
+        bool odd[OU > 0 ? OU : 1];
+#pragma unroll
+        for (int u = 0; u < OU; ++u) {
+          const int i = i0 + u * THREADS;
+          const int ic = i < 0 ? 0 : (i < FR * NB1 ? i : FR * NB1 - 1);
+          const int fl = ic / NB1, k = ic - fl * NB1;
+          q[u] = reinterpret_cast<const float4*>(lds + (fl >> 1) * AREA)[k];  // (Z[k], Z[n-k])
+          odd[u] = fl & 1;
+        }
+#pragma unroll
+        for (int u = 0; u < OU; ++u) {
+          const int i = i0 + u * THREADS;
+          if (i >= 0 && i < cnt) {
+            const float re = odd[u] ? (q[u].y + q[u].w) : (q[u].x + q[u].z);
+            const float im = odd[u] ? (q[u].z - q[u].x) : (q[u].y - q[u].w);
+            const unsigned o = (unsigned)i * 4u;
+            st_stream(reinterpret_cast<float*>(bre + o), re);
+            st_stream(reinterpret_cast<float*>(bim + o), im);
+          }
+        }
+      }
+    } else if (n_bins == NB1) {
       for (int i = (int)threadIdx.x - sh; i < nfr * NB1; i += THREADS) {
         if (i < 0) continue;
         const int fl = i / NB1, k = i - fl * NB1;
@@ -205,7 +235,9 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS_, E_>::THREADS)) void stft_ker
 // 4096: 38.9), with temporal waveform loads (the half-hop overlap of neighbouring frames then hits
 // in the cache: 512 with 4 pairs 34.3 -> 32.7 us) and line-aligned non-temporal stores (256:
 // 32.1 -> 29.6 us, 512: 33.0 -> 30.7-31.0, 1024: 36.2 -> 34.5; the unaligned runs wrote 1.10x
-// their bytes).
+// their bytes); the onesided store loop takes three steps at a time (128: 28.5 -> 28.2 us, 512:
+// 30.8 -> 30.3-30.5, 2048: 36.6 -> 36.0, 4096: 40.0 -> 38.1).  Four elements per thread (512:
+// 40.5 us) or sixteen (35.5; 1024: 33.9 against 34.9, the only size where it won) were slower.
 template <int NFFT>
 constexpr int stft_fm_pairs() {
   constexpr int p = (NFFT <= 512 ? 256 : 512) / (NFFT / stft_epth(NFFT));
@@ -220,7 +252,7 @@ static hipError_t launch_stft_n(const StftArgs& a) {
     const int tiles = (a.n_frames + C::FR - 1) / C::FR;
     const long long blocks = a.batch * (long long)tiles;
     if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((stft_kernel<NFFT, true, P, stft_epth(NFFT), false, true, true>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((stft_kernel<NFFT, true, P, stft_epth(NFFT), false, true, true, 3>), dim3((unsigned)blocks),
                        dim3(C::THREADS), 0, a.stream, a.signal, a.window, a.out_re, a.out_im, a.tw, a.length, a.hop,
                        a.pad, a.n_frames, a.n_bins, tiles, 0.5f * a.scale);
     return hipGetLastError();
