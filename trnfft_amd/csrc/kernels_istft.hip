@@ -70,28 +70,38 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
   if constexpr (FM) {
     // frames-major input (batch, n_frames, F): the tile's frames are consecutive rows, one
     // contiguous run of nf * F floats per plane read by consecutive lanes
-    const float* bre = sre + ((size_t)b * n_frames + ta) * F;
-    const float* bim = sim + ((size_t)b * n_frames + ta) * F;
+    // (32-bit byte offsets from the run's wave-uniform bases; the lane's (frame, bin) advances by
+    // THREADS entries per step without a division)
+    const char* bre = reinterpret_cast<const char*>(sre + ((size_t)b * n_frames + ta) * F);
+    const char* bim = reinterpret_cast<const char*>(sim + ((size_t)b * n_frames + ta) * F);
     constexpr int SJ = (FR * F + THREADS - 1) / THREADS;
+    const int cnt = nf * F;
     float sr[SJ], si[SJ];
 #pragma unroll
     for (int it = 0; it < SJ; ++it) {
       const int i = (int)threadIdx.x + THREADS * it;
       sr[it] = 0.0f;
       si[it] = 0.0f;
-      if (i < nf * F) {
-        sr[it] = bre[i];
-        si[it] = bim[i];
+      if (i < cnt) {
+        const unsigned o = (unsigned)i * 4u;
+        sr[it] = *reinterpret_cast<const float*>(bre + o);
+        si[it] = *reinterpret_cast<const float*>(bim + o);
       }
     }
+    constexpr int DF = THREADS / F, DK = THREADS % F;
+    int f = (int)threadIdx.x / F, k = (int)threadIdx.x - f * F;
 #pragma unroll
     for (int it = 0; it < SJ; ++it) {
-      const int i = (int)threadIdx.x + THREADS * it;
-      if (i < FR * F) {
-        const int f = i / F, k = i - f * F;
+      if ((int)threadIdx.x + THREADS * it < FR * F) {
         float* r = lds + (f >> 1) * RP + (f & 1) * 2 * F;
-        r[k] = (ADJ && (k == 0 || k == NFFT / 2)) ? 2.0f * sr[it] : sr[it];
-        r[F + k] = (k == 0 || k == NFFT / 2) ? 0.0f : si[it];
+        r[k] = sr[it];
+        r[F + k] = si[it];
+      }
+      k += DK;
+      f += DF;
+      if (k >= F) {
+        k -= F;
+        ++f;
       }
     }
   } else {
@@ -126,10 +136,9 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
     float* sreg = lds + (fs >> 1) * RP + (fs & 1) * 2 * F + k0;
 #pragma unroll
     for (int it = 0; it < SI; ++it) {
-      const int k = k0 + KS * it;
-      if (k < F) {
-        sreg[KS * it] = (ADJ && (k == 0 || k == NFFT / 2)) ? 2.0f * sr[it] : sr[it];
-        sreg[F + KS * it] = (k == 0 || k == NFFT / 2) ? 0.0f : si[it];
+      if (k0 + KS * it < F) {
+        sreg[KS * it] = sr[it];
+        sreg[F + KS * it] = si[it];
       }
     }
   }
@@ -142,7 +151,18 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
   for (int e = 0; e < E; ++e) {
     const int k = tid + T * e;
     if (k <= NFFT / 2) {  // Z = X_a + i X_b
-      v[e] = make_float2((reg[k] - reg[3 * F + k]) * scale, (reg[F + k] + reg[2 * F + k]) * scale);
+      float ra = reg[k], ia = reg[F + k], rb = reg[2 * F + k], ib = reg[3 * F + k];
+      if ((e == 0 || e == E / 2) && tid == 0) {
+        // bins 0 and n/2 (k = 0 and T * E / 2): their imaginary parts are dropped; the adjoint
+        // counts them once against twice for the interior bins
+        ia = 0.0f;
+        ib = 0.0f;
+        if constexpr (ADJ) {
+          ra *= 2.0f;
+          rb *= 2.0f;
+        }
+      }
+      v[e] = make_float2((ra - ib) * scale, (ia + rb) * scale);
     } else {              // X[k] = conj X[n-k]:  Z = (ra + ib) + i (rb - ia) at n-k
       const int q = NFFT - k;
       v[e] = make_float2((reg[q] + reg[3 * F + q]) * scale, (reg[2 * F + q] - reg[F + q]) * scale);
