@@ -157,14 +157,6 @@ def bench_headline(steps: int, warmup: int):
         torch.cuda.synchronize()
         return ev0.elapsed_time(ev1) * 1e-3, time.perf_counter() - t0
 
-    for k in range(warmup):
-        step(k)
-    torch.cuda.synchronize()
-
-    # the timed region reported as `value`: exactly K steps, three times, median
-    regions = sorted(eager_region(steps) for _ in range(3))
-    t_region, wall = regions[1]
-
     # roofline.t_launch: a fixed region of ROOFLINE_STEPS steps (2 x ROOFLINE_STEPS back-to-back
     # launches, alternating directions over the rotated sets), independent of --steps, captured
     # once into a HIP graph (no host work between launches); 3 warm-up replays, then 3 timed
@@ -192,6 +184,17 @@ def bench_headline(steps: int, warmup: int):
     # the same fixed region launched eagerly, for comparison
     t_launch_eager = _median([eager_region(ROOFLINE_STEPS)[0] for _ in range(3)]) / (2 * ROOFLINE_STEPS)
 
+    # the timed region reported as `value`: W warm-up steps, then exactly K steps, three times,
+    # median.  It follows the fixed regions above without a pause, so the GPU has been running
+    # this kernel for some 45 ms when it starts: back-to-back regions of 400 launches read 14.8,
+    # 13.9, 13.2, 12.9 and then 12.7 us per launch from the process's first launches on, and the
+    # same after a stretch of isolated launches.
+    for k in range(warmup):
+        step(k)
+    torch.cuda.synchronize()
+    regions = sorted(eager_region(steps) for _ in range(3))
+    t_region, wall = regions[1]
+
     # per-launch kernel durations (separate pass, event pairs around each launch)
     timer = EventTimer()
     for k in range(100):
@@ -209,6 +212,7 @@ def bench_headline(steps: int, warmup: int):
     assert torch.equal(chk.real, outs[kf][0]) and torch.equal(chk.imag, outs[kf][1])
     assert torch.equal(chk_i.real, outs[ki][0]) and torch.equal(chk_i.imag, outs[ki][1])
     del graph
+
 
     # plain device copy of the same bytes (32 MiB in, 32 MiB out per launch, same rotation): the
     # achievable-bandwidth reference, and the known-size kernel that calibrates rocprof counters
