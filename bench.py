@@ -261,16 +261,22 @@ def _n_sets(set_bytes: int) -> int:
     return max(1, math.ceil(ROTATE_BYTES / set_bytes))
 
 
-def _time_rot(fn, n_sets: int, reps: int = 100, warm: int = 3) -> float:
+def _time_rot(fn, n_sets: int, reps: int = 100, warm: int = 3, warm_s: float = 0.03) -> float:
     """Average launch duration of fn(k, stream) over `reps` back-to-back launches (k = buffer set
     k % n_sets) on the current stream, HIP events around the region, synchronize on both sides;
     median of three regions.  Eager launches: the host enqueues faster than these kernels run,
-    so the region is the kernels' own time (a captured graph adds ~100 us per replay)."""
+    so the region is the kernels' own time (a captured graph adds ~100 us per replay).  The
+    untimed warm-up runs the same launches for at least `warm_s` seconds first: the GPU runs the
+    first ~20 ms of work after a pause measurably slower."""
     cur = torch.cuda.current_stream()
     h = ctypes.c_void_p(cur.cuda_stream)
-    for k in range(warm):
-        fn(k % n_sets, h)
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    k = 0
+    while k < warm or time.perf_counter() - t0 < warm_s:
+        for _ in range(8):
+            fn(k % n_sets, h)
+            k += 1
+        torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     regions = []
