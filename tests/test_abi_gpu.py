@@ -114,6 +114,37 @@ def test_bluestein_split_needs_workspace():
     lib.tfa_plan_destroy(p)
 
 
+@pytest.mark.parametrize("n_fft,hop,onesided", [(512, 256, True), (400, 160, True), (64, 16, False), (100, 40, False)])
+def test_stft_frames_major_planes_off_the_line_grid(n_fft, hop, onesided):
+    # output planes that start 1 and 7 floats past a 128-byte line (the stores of each tile start
+    # their lanes on a line, whatever the plane's alignment): the same values as aligned planes
+    lib = _lib.lib()
+    st = VP(torch.cuda.current_stream().cuda_stream)
+    g = torch.Generator(device="cuda").manual_seed(n_fft + 1)
+    length = 7001
+    x = torch.randn(2, length, device="cuda", generator=g)
+    w = torch.hann_window(n_fft, device="cuda")
+    bins = n_fft // 2 + 1 if onesided else n_fft
+    frames = 1 + (length + 2 * (n_fft // 2) - n_fft) // hop
+    fl = _lib.STFT_CENTER | _lib.STFT_FRAMES_MAJOR | (_lib.STFT_ONESIDED if onesided else 0)
+    rc, h = _plan(_lib.KIND_STFT, n_fft, hop=hop, flags=fl)
+    assert rc == 0, _err()
+    cnt = 2 * frames * bins
+    a_re, a_im = torch.empty(cnt, device="cuda"), torch.empty(cnt, device="cuda")
+    flat_re = torch.full((cnt + 64,), float("nan"), device="cuda")
+    flat_im = torch.full((cnt + 64,), float("nan"), device="cuda")
+    b_re, b_im = flat_re[1:1 + cnt], flat_im[7:7 + cnt]
+    assert lib.tfa_stft_execute(h, 2, length, P(x), P(w), P(a_re), P(a_im), st) == 0, _err()
+    assert lib.tfa_stft_execute(h, 2, length, P(x), P(w), P(b_re), P(b_im), st) == 0, _err()
+    torch.testing.assert_close(a_re, b_re, rtol=0, atol=0)
+    torch.testing.assert_close(a_im, b_im, rtol=0, atol=0)
+    # nothing written outside the planes
+    assert torch.isnan(flat_re[:1]).all() and torch.isnan(flat_re[1 + cnt:]).all()
+    assert torch.isnan(flat_im[:7]).all() and torch.isnan(flat_im[7 + cnt:]).all()
+    torch.cuda.synchronize()
+    lib.tfa_plan_destroy(h)
+
+
 @pytest.mark.parametrize("n_fft,hop,onesided", [(512, 256, True), (400, 160, True), (64, 16, False), (100, 40, False),
                                                  (2048, 512, True)])
 def test_stft_frames_major_layout(n_fft, hop, onesided):
