@@ -548,14 +548,14 @@ static hipError_t launch_fourstep_t(const FourStepArgs& a) {
   return launch_fourstep_tiles<N1, N2, DIR, 0>(a);
 }
 
-// n = n1 * n2 with n1 = 2^floor(lg/2) <= n2 (the plan's split)
+// n = n1 * n2 (the plan's split: n1 = 2^floor(lg/2) <= n2, or n1 = 2 n2 at 2^15 and 2^17)
 template <int DIR>
 static hipError_t launch_fourstep_dir(const FourStepArgs& a) {
   const long long key = (long long)a.n1 * 8192 + a.n2;
   switch (key) {
-    case 128LL * 8192 + 256: return launch_fourstep_t<128, 256, DIR>(a);
+    case 256LL * 8192 + 128: return launch_fourstep_t<256, 128, DIR>(a);
+    case 512LL * 8192 + 256: return launch_fourstep_t<512, 256, DIR>(a);
     case 256LL * 8192 + 256: return launch_fourstep_t<256, 256, DIR>(a);
-    case 256LL * 8192 + 512: return launch_fourstep_t<256, 512, DIR>(a);
     case 512LL * 8192 + 512: return launch_fourstep_t<512, 512, DIR>(a);
     case 512LL * 8192 + 1024: return launch_fourstep_t<512, 1024, DIR>(a);
     case 1024LL * 8192 + 1024: return launch_fourstep_t<1024, 1024, DIR>(a);

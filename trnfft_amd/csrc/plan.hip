@@ -190,12 +190,14 @@ struct tfa_plan {
     return TFA_OK;
   }
 
-  // n = n1 * n2 (n1 = 2^floor(lg/2) <= n2): LDS-FFT tables of both lengths (tfa::fourstep_epth
-  // layout) and the two-level W_n^j tables of the twiddle between the passes
+  // n = n1 * n2 (n1 = 2^floor(lg/2) <= n2, except 2^15 and 2^17, whose longer column transform
+  // measured faster: 128 x 2^15 35.2 -> 32.8 us as 256 x 128, 32 x 2^17 32.7 -> 31.1 as
+  // 512 x 256, while 2^19, 2^21 and 2^23 lost 3-10 % that way): LDS-FFT tables of both lengths
+  // (tfa::fourstep_epth layout) and the two-level W_n^j tables of the twiddle between the passes
   int build_split(int64_t n, int dir, C2cTables* t) {
     const int lg = tfa::ilog2(n);
-    t->n1 = 1 << (lg / 2);      // column transform length (strided)
-    t->n2 = (int)(n / t->n1);   // row transform length (contiguous), n2 >= n1
+    t->n1 = 1 << ((lg == 15 || lg == 17) ? lg - lg / 2 : lg / 2);  // column transform length (strided)
+    t->n2 = (int)(n / t->n1);                                      // row transform length (contiguous)
     t->lo_bits = (lg + 1) / 2;
     int rc;
     if ((rc = upload(lds_table(t->n1, dir, tfa::fourstep_epth(t->n1)), &t->tw1))) return rc;
