@@ -129,7 +129,7 @@ __host__ __device__ constexpr bool blue_split_pf(int) { return true; }
 // 256 threads per workgroup up to n = 64, 512 up to 1024, 1024 above (n = 16: 64 -> 45 us,
 // 256: 65 -> 48, 1024: 73 -> 63, 4096: 122 -> 100 against the former shapes).  With frames-major
 // spectra (in-run A/B, hop n/2): n = 256 at 256 threads 30.2 -> 29.2 us; n = 1024 at 1024 threads
-// 36.7 -> 42.8 (kept at 512).
+// 36.7 -> 42.8 (kept at 512); E = 16 at 1024 / 2048 38.2 -> 43.8 / 42.2 -> 55.9 us (kept at 8).
 __host__ __device__ constexpr int istft_epth(int n) { return n <= 2048 ? 8 : 16; }
 __host__ __device__ constexpr int istft_threads(int n) { return n <= 64 || n == 256 ? 256 : n <= 1024 ? 512 : 1024; }
 // next-pass twiddle prefetch in the inverse STFT from n_fft = 512 (C2's inverse 53.4 -> 52.6 us,
