@@ -1,8 +1,9 @@
 """Batches past 2^31 elements per plane (64-bit element offsets) through every kernel family: the
 batched c2c kernel on a ragged batch, r2c / c2r, the fused Bluestein kernel, the four-step passes,
-the two-pass real fft2, the frames-major STFT and its inverse.  First and last rows (signals,
-images) against float64 numpy / torch.stft, the oracle for Bluestein, or the round trip, at the
-bounds of the fixed-shape tests.  Up to ~50 GB of device memory per test, freed after each."""
+the two-pass real fft2, a strided axis, the frames-major STFT (power-of-two and Bluestein n_fft),
+the inverse STFT and the complex GEMM.  First and last rows (signals, images) against float64
+numpy / torch.stft, the oracle for Bluestein and the GEMM, or the round trip, at the bounds of the
+fixed-shape tests.  Up to ~50 GB of device memory per test, freed after each."""
 
 from __future__ import annotations
 
@@ -146,4 +147,60 @@ def test_istft_output_past_2_31_samples():
         xs = x[b].double().cpu().numpy()
         assert rel_l2(y[b], np.zeros_like(xs), xs, np.zeros_like(xs)) < 4 * tol_pow2(n_fft)
     del x, s, y
+    torch.cuda.empty_cache()
+
+
+def test_strided_axis_past_2_31_elements():
+    _need(48)
+    b, n, stride = 2049, 1024, 1024  # transform along dim 1: 2^31 + 2^20 elements
+    g = torch.Generator(device="cuda").manual_seed(38)
+    re = torch.randn(b, n, stride, device="cuda", generator=g)
+    im = torch.randn(b, n, stride, device="cuda", generator=g)
+    assert re.numel() > 2**31
+    out = trnfft_amd.fftn(ComplexTensor(re, im), dim=(1,))
+    torch.cuda.synchronize()
+    for i, cols in ((0, slice(0, 5)), (b - 1, slice(stride - 5, stride))):
+        x = re[i, :, cols].double().cpu().numpy() + 1j * im[i, :, cols].double().cpu().numpy()
+        ref = np.fft.fft(x, axis=0)
+        assert rel_l2(out.real[i, :, cols], out.imag[i, :, cols], ref.real, ref.imag) < tol_pow2(n)
+    del re, im, out
+    torch.cuda.empty_cache()
+
+
+def test_stft_bluestein_past_2_31_output_elements():
+    import oracle
+
+    _need(40)
+    n_fft, hop, length = 400, 160, 160000
+    batch = 13500  # 13500 * 1001 * 201 > 2^31 bins per plane
+    g = torch.Generator(device="cuda").manual_seed(39)
+    x = torch.randn(batch, length, device="cuda", generator=g)
+    s = trnfft_amd.stft(x, n_fft, hop_length=hop)
+    torch.cuda.synchronize()
+    assert s.real.numel() > 2**31
+    for i in (0, batch - 1):
+        rr, ri = oracle.stft(x[i:i + 1].cpu(), n_fft=n_fft, hop_length=hop)
+        assert rel_l2(s.real[i:i + 1], s.imag[i:i + 1], rr, ri) < tol_bluestein(n_fft)
+    del x, s
+    torch.cuda.empty_cache()
+
+
+def test_complex_matmul_rows_past_2_31_elements():
+    import oracle
+
+    _need(40)
+    m, k, n = (1 << 21) + 5, 1024, 64  # A has 2^31 + 5120 elements per plane
+    g = torch.Generator(device="cuda").manual_seed(40)
+    ar = torch.randn(m, k, device="cuda", generator=g)
+    ai = torch.randn(m, k, device="cuda", generator=g)
+    br = torch.randn(k, n, device="cuda", generator=g)
+    bi = torch.randn(k, n, device="cuda", generator=g)
+    assert ar.numel() > 2**31
+    out = trnfft_amd.complex_matmul(ComplexTensor(ar, ai), ComplexTensor(br, bi))
+    torch.cuda.synchronize()
+    for sl in (slice(0, 4), slice(m - 4, m)):
+        rr, ri = oracle.complex_matmul((ar[sl].double().cpu(), ai[sl].double().cpu()),
+                                       (br.double().cpu(), bi.double().cpu()))
+        assert rel_l2(out.real[sl], out.imag[sl], rr, ri) < 1e-5
+    del ar, ai, br, bi, out
     torch.cuda.empty_cache()
