@@ -35,6 +35,8 @@ __host__ __device__ constexpr int c2c_epth(int n) {
 }
 // Interleaved (re, im) LDS exchange (one 64-bit access per element) in the batched c2c kernel:
 // measured 1-4 % faster at most lengths (identical results), 2-4 % slower at 512 and 8192.
+// (The exchange one plane at a time, half the LDS per row, measured slower from 2048 up: 8192
+// 15.4 -> 16.6 us, 16384 18.5 -> 20.5 at 4M points.)
 __host__ __device__ constexpr bool c2c_il(int n) { return n != 512 && n != 8192; }
 // Next-pass twiddle prefetch (LdsFft PF) where one or two transforms fill a workgroup and the
 // table latency after each exchange is exposed: N = 16384 21.2 -> 18.8 us; at high occupancy it
