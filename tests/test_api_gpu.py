@@ -200,23 +200,84 @@ def test_stft_fused_bluestein_matches_composed_path(n_fft, hop, pad_mode):
         <= tol_bluestein(n_fft) / 4
 
 
-@pytest.mark.parametrize("n_fft,hop", [(512, 256), (400, 160), (8192, 2048)])
-def test_stft_memory_order_is_frames_major_like_torch(n_fft, hop):
-    # the (..., freq, time) result is a transposed view of (..., time, freq) buffers, the memory
-    # order of torch.stft's result and of the reference's own transpose (trnfft/api.py:356-358);
-    # istft takes either order, and a bins-major copy gives the same signal
+@pytest.mark.parametrize("n_fft,hop", [(512, 256), (256, 64), (400, 160), (8192, 2048), (8, 2)])
+def test_stft_result_layout_is_the_references(n_fft, hop):
+    # the reference returns ComplexTensor(result_re, result_im) of its transposed frame spectra,
+    # and its constructor makes both planes contiguous (trnfft/api.py:357-365,
+    # trnfft/complex.py:29-33): dense (..., freq, time) planes, the oracle's strides
     g = torch.Generator().manual_seed(9)
-    x = torch.randn(2, 3, 20000, generator=g).cuda()
-    y = trnfft_amd.stft(x, n_fft=n_fft, hop_length=hop)
-    ref = torch.stft(x[0, 0].cpu(), n_fft, hop, window=torch.hann_window(n_fft), return_complex=True)
-    assert y.real.shape == (2, 3) + tuple(ref.shape)
-    assert y.real.transpose(-2, -1).is_contiguous() and y.imag.transpose(-2, -1).is_contiguous()
+    x = torch.randn(2, 3, 20000, generator=g)
+    y = trnfft_amd.stft(x.cuda(), n_fft=n_fft, hop_length=hop)
+    ref = oracle.stft(x, n_fft=n_fft, hop_length=hop)
+    assert y.real.shape == ref[0].shape
+    assert y.real.is_contiguous() and y.imag.is_contiguous()
+    assert y.real.stride() == ref[0].stride() and y.imag.stride() == ref[1].stride()
+    tol = tol_pow2(n_fft) if n_fft & (n_fft - 1) == 0 else tol_bluestein(n_fft)
+    assert rel_l2(y.real, y.imag, *ref) <= tol
+    # the opt-in frames-major result: the same values as views of (..., time, freq) buffers (the
+    # memory order of torch.stft's result); istft takes either order
+    fm = trnfft_amd.stft(x.cuda(), n_fft=n_fft, hop_length=hop, frames_major=True)
+    assert fm.real.transpose(-2, -1).is_contiguous() and fm.imag.transpose(-2, -1).is_contiguous()
+    assert rel_l2(fm.real, fm.imag, y.real, y.imag) <= tol
     a = trnfft_amd.istft(y, n_fft=n_fft, hop_length=hop, length=20000)
-    b = trnfft_amd.istft(ComplexTensor(y.real.contiguous(), y.imag.contiguous()), n_fft=n_fft, hop_length=hop,
-                         length=20000)
-    tol = 1e-6 if n_fft & (n_fft - 1) == 0 else 1e-5
+    b = trnfft_amd.istft(fm, n_fft=n_fft, hop_length=hop, length=20000)
     assert rel_l2(a, torch.zeros_like(a), b, torch.zeros_like(b)) <= tol
-    assert rel_l2(a, torch.zeros_like(a), x, torch.zeros_like(x)) <= (1e-5 if tol == 1e-6 else 1e-4)
+    assert rel_l2(a, torch.zeros_like(a), x.cuda(), torch.zeros_like(a)) <= 100 * tol
+
+
+@pytest.mark.parametrize("n_fft,hop,shape,center", [
+    (512, 256, (64, 160000), True),    # 626 frames, 4 ranges per signal, 256 workgroups
+    (512, 256, (1, 40192), True),      # one signal (158 frames): ranges of one sub-tile and a half
+    (512, 128, (3, 9100), True),       # 72 frames: two ranges of 36
+    (512, 300, (5, 50100), False),     # no padding; hop not a divisor of n_fft (166 frames)
+    (512, 256, (300, 16640), True),    # more signals than CUs (66 frames, two ranges each)
+    (512, 512, (7, 33536), True),      # hop = n_fft (66 frames)
+    (512, 100, (2, 12445), True),      # odd frame count (125): the fixed-tile kernel
+    (256, 64, (16, 30016), True),      # n_fft 256: two pair transforms per wavefront (470 frames)
+    (256, 128, (130, 8320), True),
+    (256, 32, (1, 4000), False),       # 118 frames
+])
+def test_stft_bins_major_whole_line_kernel_vs_oracle(n_fft, hop, shape, center):
+    # the whole-line bins-major kernel (frame ranges per workgroup, forward and backward walks,
+    # carried line parts, reflected edge frames) against the reference's composition
+    g = torch.Generator().manual_seed(n_fft + hop + shape[0])
+    x = torch.randn(*shape, generator=g)
+    got = trnfft_amd.stft(x.cuda(), n_fft=n_fft, hop_length=hop, center=center)
+    ref = oracle.stft(x, n_fft=n_fft, hop_length=hop, center=center)
+    assert got.shape == ref[0].shape and got.real.is_contiguous()
+    assert rel_l2(got.real, got.imag, *ref) <= tol_pow2(n_fft)
+    # every element written: the frames-major kernel gives the same spectra (to rounding)
+    fm = trnfft_amd.stft(x.cuda(), n_fft=n_fft, hop_length=hop, center=center, frames_major=True)
+    assert torch.allclose(got.real, fm.real, rtol=1e-5, atol=1e-4 * float(fm.real.abs().max()))
+    assert torch.allclose(got.imag, fm.imag, rtol=1e-5, atol=1e-4 * float(fm.imag.abs().max()))
+
+
+def test_stft_bins_major_into_planes_at_any_line_offset():
+    # through the C ABI: output planes that start anywhere on the 8-byte grid (the kernel writes
+    # whole 128-byte lines from each row's offset; other alignments take the fixed-tile kernel),
+    # with sentinels around each plane: nothing is written outside the (64, 257, 626) planes
+    from trnfft_amd import _lib
+    from trnfft_amd.dispatch import ptr, stream_handle
+    from trnfft_amd.plan import native_plan
+
+    x = torch.randn(8, 40000, generator=torch.Generator().manual_seed(3)).cuda()
+    win = torch.hann_window(512, device="cuda")
+    frames = 1 + 40000 // 256
+    n = 8 * 257 * frames
+    plan = native_plan(_lib.KIND_STFT, 512, False, 0, hop=256, flags=_lib.STFT_CENTER | _lib.STFT_ONESIDED)
+    ref = trnfft_amd.stft(x, n_fft=512, hop_length=256)
+    for off_re, off_im in [(0, 0), (2, 2), (18, 18), (30, 30), (6, 22), (1, 1)]:
+        bre = torch.full((n + 64,), 7.0, device="cuda")
+        bim = torch.full((n + 64,), 7.0, device="cuda")
+        o_re, o_im = bre[off_re:off_re + n], bim[off_im:off_im + n]
+        rc = _lib.lib().tfa_stft_execute(plan.handle, 8, 40000, ptr(x), ptr(win), ptr(o_re), ptr(o_im),
+                                         stream_handle(x.device))
+        _lib.check(rc, "tfa_stft_execute")
+        torch.cuda.synchronize()
+        assert torch.allclose(o_re.view(8, 257, frames), ref.real, rtol=1e-5, atol=1e-3), (off_re, off_im)
+        assert torch.allclose(o_im.view(8, 257, frames), ref.imag, rtol=1e-5, atol=1e-3), (off_re, off_im)
+        assert bool((bre[:off_re] == 7.0).all()) and bool((bre[off_re + n:] == 7.0).all())
+        assert bool((bim[:off_im] == 7.0).all()) and bool((bim[off_im + n:] == 7.0).all())
 
 
 def test_stft_win_length_below_n_fft_and_custom_window_composed():

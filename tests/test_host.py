@@ -125,6 +125,73 @@ def test_precision_modes():
     trnfft_amd.set_ozaki_product_precision_verified(False)
 
 
+def test_hip_accepts_only_fp32_under_fast_precision(monkeypatch):
+    # the integration hooks route a call here only when this predicate holds; everything else
+    # stays on trnfft's own path (the reference computes in the input's dtype, fft_core.py:84-88,
+    # and runs "kahan"/"double" itself)
+    from trnfft_amd import dispatch
+
+    monkeypatch.setattr(dispatch, "_use_hip", lambda: True)
+    x32, x64 = torch.randn(4, 8), torch.randn(4, 8, dtype=torch.float64)
+    assert trnfft_amd.hip_accepts(x32, x32, precision="fast")
+    assert trnfft_amd.hip_accepts(x32, None)
+    assert not trnfft_amd.hip_accepts(x64, x64, precision="fast")
+    assert not trnfft_amd.hip_accepts(x32, x64)
+    assert not trnfft_amd.hip_accepts(x32.half())
+    assert not trnfft_amd.hip_accepts(x32.to(torch.bfloat16))
+    assert not trnfft_amd.hip_accepts(torch.complex(x32, x32))
+    assert not trnfft_amd.hip_accepts(torch.arange(8))
+    for mode in ("kahan", "double", "bf16", "bf16_refined", "ozaki", "ozaki_hq", "bogus"):
+        assert not trnfft_amd.hip_accepts(x32, precision=mode), mode
+    # the backend's own switch still decides for fp32 / "fast"
+    monkeypatch.setattr(dispatch, "_use_hip", lambda: False)
+    assert not trnfft_amd.hip_accepts(x32, x32, precision="fast")
+
+
+def test_hook_keeps_other_precisions_and_dtypes_off_the_hip_path(monkeypatch):
+    # the fft_core hook of the integration guide: resolve trnfft's precision first, then route by
+    # the predicate; a stand-in for trnfft's own path records what it was given
+    from trnfft_amd import dispatch
+
+    monkeypatch.setattr(dispatch, "_use_hip", lambda: True)
+    routed = []
+
+    def hook(x_re, x_im, precision, global_mode):
+        prec = global_mode if precision is None else precision  # trnfft/precision.py:88-94
+        if trnfft_amd.hip_accepts(x_re, x_im, precision=prec):
+            routed.append(("hip", prec))
+        else:
+            routed.append(("trnfft", prec))
+
+    x = torch.randn(2, 16)
+    hook(x, x, None, "fast")
+    hook(x, x, None, "double")
+    hook(x, x, "kahan", "fast")
+    hook(x.double(), x.double(), None, "fast")
+    assert routed == [("hip", "fast"), ("trnfft", "double"), ("trnfft", "kahan"), ("trnfft", "fast")]
+
+
+def test_backend_refuses_rather_than_computing_fp32():
+    # asked directly, the backend raises for what it does not compute: another precision mode
+    # (NotImplementedError, before any device work) or non-fp32 data (TypeError)
+    x = ComplexTensor(torch.randn(2, 16), torch.randn(2, 16))
+    for mode in ("double", "kahan"):
+        with pytest.raises(NotImplementedError):
+            trnfft_amd.fft_core.fft_core(x, precision=mode)
+    trnfft_amd.set_precision("double")
+    try:
+        for call in (lambda: trnfft_amd.fft(x), lambda: trnfft_amd.stft(torch.randn(2, 600), 64),
+                     lambda: trnfft_amd.fft2(torch.randn(2, 8, 8)), lambda: trnfft_amd.rfft(torch.randn(2, 16))):
+            with pytest.raises(NotImplementedError):
+                call()
+    finally:
+        trnfft_amd.set_precision("fast")
+    from trnfft_amd.dispatch import to_device_f32
+
+    with pytest.raises(TypeError):
+        to_device_f32(torch.randn(4, dtype=torch.float64), torch.device("cpu"))
+
+
 class TestComplexTensor:
     def test_from_real_and_complex(self):
         x = ComplexTensor(torch.tensor([1.0, 2.0, 3.0]))

@@ -26,7 +26,7 @@ from .api import (
     stft,
 )
 from .complex import ComplexTensor, complex_matmul
-from .dispatch import HAS_HIP, HAS_NKI, complex_gemm, complex_linear, get_backend, set_backend
+from .dispatch import HAS_HIP, HAS_NKI, complex_gemm, complex_linear, get_backend, hip_accepts, set_backend
 from .plan import FFTAlgorithm, FFTPlan, clear_plan_cache, create_plan
 from .precision import get_precision, set_ozaki_product_precision_verified, set_precision
 
@@ -58,6 +58,7 @@ __all__ = [
     "HAS_NKI",
     "set_backend",
     "get_backend",
+    "hip_accepts",
     "set_precision",
     "set_ozaki_product_precision_verified",
     "get_precision",

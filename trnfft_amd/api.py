@@ -281,8 +281,16 @@ def stft(
     pad_mode: str = "reflect",
     normalized: bool = False,
     onesided: bool = True,
+    *,
+    frames_major: bool = False,
 ) -> ComplexTensor:
     """Short-time Fourier transform, output (..., freq, time) (trnfft/api.py:291-365).
+
+    The result planes are contiguous (..., freq, time) tensors, as the reference returns them (its
+    ComplexTensor makes the transposed planes contiguous, trnfft/complex.py:29-33).
+    ``frames_major=True`` (not in the reference) returns transposed views of (..., time, freq)
+    buffers instead -- torch.stft's memory order, which the fused kernel writes as one contiguous
+    run per frame tile -- for callers that accept strided planes; ``istft`` reads either.
 
     Power-of-two n_fft in [16, 4096], and other n_fft from 9 to 2731 (2048 two-sided), run as
     one fused kernel that reads the raw waveform (framing, padding, window, transform -- one
@@ -309,7 +317,7 @@ def stft(
         if length <= n_fft // 2:
             raise ValueError(f"reflect padding of {n_fft // 2} needs more than {n_fft // 2} samples; got {length}")
         num_frames = stft_num_frames(length, n_fft, hop_length, center)
-        out = _ag.stft(x, win, n_fft, hop_length, True, normalized, onesided, num_frames)
+        out = _ag.stft(x, win, n_fft, hop_length, True, normalized, onesided, num_frames, frames_major)
         out_re, out_im = out.real, out.imag
         if x.dim() == 2 and x.shape[0] == 1:
             # the reference squeezes a (1, L) signal to 1-D after padding (trnfft/api.py:313-315),
@@ -334,7 +342,8 @@ def stft(
         return out if out_dev == dev else out.to(out_dev)
     if fused:
         # the padded signal through the fused kernel (no centre padding of its own)
-        out = _ag.stft(x.contiguous(), win, n_fft, hop_length, False, normalized, onesided, num_frames)
+        out = _ag.stft(x.contiguous(), win, n_fft, hop_length, False, normalized, onesided, num_frames,
+                       frames_major)
         return out if out_dev == dev else out.to(out_dev)
     # trnfft/api.py:321-363 on the device: frame gather, window, transform of real frames,
     # onesided slice, (freq, time) transpose, normalisation
@@ -342,13 +351,15 @@ def stft(
     # and a cheap adjoint under autograd)
     frames = (x.unfold(-1, n_fft, hop_length)[..., :num_frames, :] * win).contiguous()  # (..., T, n_fft)
     spec = rfft(frames) if onesided else _real_1d(frames, inverse=False)
-    # (..., T, bins) buffers returned as (..., bins, T) views: the reference's own transpose
-    out_re = spec.real.contiguous()
-    out_im = spec.imag.contiguous()
+    # (..., T, bins) -> (..., bins, T): the reference's transpose, made contiguous by its
+    # ComplexTensor (views of the (..., T, bins) buffers with frames_major)
+    out_re, out_im = spec.real.transpose(-2, -1), spec.imag.transpose(-2, -1)
     if normalized:
         scale = 1.0 / math.sqrt(n_fft)
         out_re, out_im = out_re * scale, out_im * scale
-    out = ComplexTensor._wrap(out_re.transpose(-2, -1), out_im.transpose(-2, -1))
+    if not frames_major:
+        out_re, out_im = out_re.contiguous(), out_im.contiguous()
+    out = ComplexTensor._wrap(out_re, out_im)
     return out if out_dev == dev else out.to(out_dev)
 
 

@@ -179,10 +179,10 @@ def c2r(re: torch.Tensor, im: torch.Tensor, n: int) -> torch.Tensor:
 
 class _StftFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, win, n_fft, hop, center, normalized, onesided, num_frames):
+    def forward(ctx, x, win, n_fft, hop, center, normalized, onesided, num_frames, frames_major):
         ctx.save_for_backward(x, win)
         ctx.cfg = (n_fft, hop, center, normalized, onesided, num_frames)
-        return _fc.execute_stft(x, win, n_fft, hop, center, normalized, onesided, num_frames)
+        return _fc.execute_stft(x, win, n_fft, hop, center, normalized, onesided, num_frames, frames_major)
 
     @staticmethod
     @once_differentiable
@@ -199,7 +199,8 @@ class _StftFn(torch.autograd.Function):
             d_xp = _fc.execute_stft_backward(g_re.reshape(b, bins, frames), g_im.reshape(b, bins, frames), win,
                                              n_fft, hop, center, normalized, length + 2 * pad)
             if d_xp is not None:
-                return _unpad_reflect(d_xp, pad, length).reshape(*lead, length), None, None, None, None, None, None, None
+                return (_unpad_reflect(d_xp, pad, length).reshape(*lead, length), None, None, None, None, None, None, None,
+                        None)
         # (..., bins, frames) -> (b, frames, bins): one spectrum per row
         gr = g_re.reshape(b, bins, frames).transpose(1, 2).contiguous()
         gi = g_im.reshape(b, bins, frames).transpose(1, 2).contiguous()
@@ -229,7 +230,7 @@ class _StftFn(torch.autograd.Function):
             d_xp = F.fold(fg.transpose(1, 2), output_size=(1, lp), kernel_size=(1, n_fft), stride=(1, hop))
             d_xp = d_xp.reshape(b, lp)
             d_x = _unpad_reflect(d_xp, pad, length).reshape(*lead, length)
-        return d_x, d_win, None, None, None, None, None, None
+        return d_x, d_win, None, None, None, None, None, None, None
 
 
 def _unpad_reflect(d_xp: torch.Tensor, pad: int, length: int) -> torch.Tensor:
@@ -243,12 +244,14 @@ def _unpad_reflect(d_xp: torch.Tensor, pad: int, length: int) -> torch.Tensor:
     return d_x
 
 
-def stft(x, win, n_fft, hop, center, normalized, onesided, num_frames) -> ComplexTensor:
-    """Fused STFT kernel on device fp32 x (..., L), window (n_fft); differentiable in x and window."""
+def stft(x, win, n_fft, hop, center, normalized, onesided, num_frames, frames_major=False) -> ComplexTensor:
+    """Fused STFT kernel on device fp32 x (..., L), window (n_fft); differentiable in x and window.
+    Contiguous (..., bins, frames) planes, or with ``frames_major`` transposed views of
+    (..., frames, bins) buffers."""
     if _grad_on(x, win):
-        y_re, y_im = _StftFn.apply(x, win, n_fft, hop, center, normalized, onesided, num_frames)
+        y_re, y_im = _StftFn.apply(x, win, n_fft, hop, center, normalized, onesided, num_frames, frames_major)
     else:
-        y_re, y_im = _fc.execute_stft(x, win, n_fft, hop, center, normalized, onesided, num_frames)
+        y_re, y_im = _fc.execute_stft(x, win, n_fft, hop, center, normalized, onesided, num_frames, frames_major)
     return ComplexTensor._wrap(y_re, y_im)
 
 

@@ -31,7 +31,9 @@ class ComplexTensor:
 
     @classmethod
     def _wrap(cls, real: torch.Tensor, imag: torch.Tensor) -> ComplexTensor:
-        """Wrap two planes that are already contiguous (no copy, no checks)."""
+        """Wrap two planes as they are (no copy, no checks): contiguous planes -- every result of
+        this package -- or the transposed views that ``stft(..., frames_major=True)`` returns on
+        request."""
         obj = cls.__new__(cls)
         obj.real = real
         obj.imag = imag

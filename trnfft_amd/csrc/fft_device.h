@@ -381,4 +381,66 @@ struct LdsFft {
   }
 };
 
+// M independent wave-local transforms of length N per thread group (interleaved LDS exchange),
+// advanced pass by pass together: one exchange synchronisation per pass for all of them, so a
+// wavefront has M times the independent work between exchanges.  area[m] is transform m's LDS
+// scratch (lds_pad(N) float2 entries); v[m] as LdsFft's v.
+template <int N, int E, int DIR, int M>
+struct LdsFftMulti {
+  using F = LdsFft<N, E, DIR, true, false, true, false>;
+  static constexpr LdsShape S = F::S;
+  static constexpr int T = F::T;
+
+  template <int P>
+  __device__ __forceinline__ static void pass(float2 (&v)[M][E], float* const (&area)[M],
+                                              const float2* __restrict__ tw, int tid) {
+    if constexpr (P < S.npass) {
+      constexpr int R = S.radix[P];
+      constexpr int NB = E / R;
+      constexpr int LS = S.ls[P];
+      constexpr bool LAST = (P == S.npass - 1);
+      constexpr bool LIN_W = (LS == 1) ? (R % 16 == 0) : (LS % 16 == 0);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int j = tid + b * T;
+          const int k = (int)((unsigned)j % (unsigned)LS);
+          float2 w[R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) w[r] = v[m][b + r * NB];
+          if constexpr (P > 0) {
+            const float4* t4 = reinterpret_cast<const float4*>(tw + S.twoff[P] + k * R);
+#pragma unroll
+            for (int r2 = 0; r2 < R / 2; ++r2) {
+              const float4 q = t4[r2];
+              if (r2 > 0) w[2 * r2] = cmul(w[2 * r2], make_float2(q.x, q.y));
+              w[2 * r2 + 1] = cmul(w[2 * r2 + 1], make_float2(q.z, q.w));
+            }
+          }
+          Dft<R, DIR>::run(w);
+          if constexpr (LAST) {
+#pragma unroll
+            for (int u = 0; u < R; ++u) v[m][b + u * NB] = w[u];
+          } else {
+            F::template store_pass<R, LS, LIN_W>(w, area[m], nullptr, j, k, 3);
+          }
+        }
+      }
+      if constexpr (!LAST) {
+        exchange_sync<true>();
+#pragma unroll
+        for (int m = 0; m < M; ++m) F::load_pass(v[m], area[m], nullptr, tid, 3);
+        exchange_sync<true>();
+        pass<P + 1>(v, area, tw, tid);
+      }
+    }
+  }
+
+  __device__ __forceinline__ static void run(float2 (&v)[M][E], float* const (&area)[M],
+                                             const float2* __restrict__ tw, int tid) {
+    pass<0>(v, area, tw, tid);
+  }
+};
+
 }  // namespace tfa

@@ -252,27 +252,28 @@ def execute_fft2_any(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -
 
 def stft_planes(re: torch.Tensor, im: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, bool]:
     """(..., bins, frames) spectrum planes as contiguous buffers for the STFT kernels, without a
-    copy where possible: (..., frames, bins) buffers (frames_major True) when both planes are
-    transposed views of such tensors -- the layout of torch.stft's result, of trnfft's
-    (trnfft/api.py:356-358) and of this backend's -- the planes themselves when both are
-    contiguous, else frames-major copies."""
+    copy where possible: the planes themselves when both are contiguous (the reference's layout,
+    trnfft/complex.py:29-33), (..., frames, bins) buffers (frames_major True) when both planes are
+    transposed views of such tensors (torch.stft's memory order, and ``stft(...,
+    frames_major=True)``), else contiguous copies."""
+    if re.is_contiguous() and im.is_contiguous():
+        return re, im, False
     rt, it = re.transpose(-2, -1), im.transpose(-2, -1)
     if rt.is_contiguous() and it.is_contiguous():
         return rt, it, True
-    if re.is_contiguous() and im.is_contiguous():
-        return re, im, False
-    return rt.contiguous(), it.contiguous(), True
+    return re.contiguous(), im.contiguous(), False
 
 
 def execute_stft(x: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int, center: bool, normalized: bool,
-                 onesided: bool, num_frames: int) -> tuple[torch.Tensor, torch.Tensor]:
+                 onesided: bool, num_frames: int, frames_major: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
     """Fused STFT kernel on device-resident fp32 x (..., L) and window (n_fft): (re, im) planes of
-    shape (..., bins, frames) (replaces trnfft/api.py:291-365 after its argument handling).  The
-    planes are transposed views of (..., frames, bins) buffers, the memory order of torch.stft's
-    result and of the reference's own transposed frames, which the kernel writes as one
-    contiguous run per tile."""
+    shape (..., bins, frames) (replaces trnfft/api.py:291-365 after its argument handling).  By
+    default the planes are contiguous, the reference's layout (its ComplexTensor makes the
+    transposed planes contiguous, trnfft/complex.py:29-33); with ``frames_major`` they are
+    transposed views of (..., frames, bins) buffers (torch.stft's memory order), which the kernel
+    writes as one contiguous run per tile."""
     flags = (_lib.STFT_CENTER if center else 0) | (_lib.STFT_NORMALIZED if normalized else 0)
-    flags |= (_lib.STFT_ONESIDED if onesided else 0) | _lib.STFT_FRAMES_MAJOR
+    flags |= (_lib.STFT_ONESIDED if onesided else 0) | (_lib.STFT_FRAMES_MAJOR if frames_major else 0)
     dev = x.device
     x = x.contiguous()
     win = win.contiguous()
@@ -282,14 +283,17 @@ def execute_stft(x: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int, cente
     batch = 1
     for d in lead:
         batch *= d
-    out_re = torch.empty(*lead, num_frames, bins, dtype=torch.float32, device=dev)
+    shape = (*lead, num_frames, bins) if frames_major else (*lead, bins, num_frames)
+    out_re = torch.empty(*shape, dtype=torch.float32, device=dev)
     out_im = torch.empty_like(out_re)
     with torch.cuda.device(dev):
         rc = _lib.lib().tfa_stft_execute(
             plan.handle, batch, x.shape[-1], ptr(x), ptr(win), ptr(out_re), ptr(out_im), stream_handle(dev)
         )
     _lib.check(rc, "tfa_stft_execute")
-    return out_re.transpose(-2, -1), out_im.transpose(-2, -1)
+    if frames_major:
+        return out_re.transpose(-2, -1), out_im.transpose(-2, -1)
+    return out_re, out_im
 
 
 def execute_stft_backward(g_re: torch.Tensor, g_im: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int,
