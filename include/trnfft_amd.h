@@ -105,8 +105,10 @@ int tfa_execute(const tfa_plan* plan, int64_t batch, const float* in_re, const f
  * counterpart in the reference; it is for callers that cannot allocate device memory (code under
  * HIP-graph capture, serving loops, harnesses that forbid hipMalloc).  A call whose scratch
  * (tfa_plan_workspace_size) exceeds 64 MiB fails with TFA_ERR_INVALID; plans that need no scratch
- * run exactly as tfa_execute.  Every call on one GPU shares that GPU's scratch: calls that
- * overlap on one GPU (concurrent streams) race and must be serialised by the caller.
+ * run exactly as tfa_execute.  Every call on one GPU shares that GPU's scratch: eager calls are
+ * ordered on the device by the library (each waits, on its stream, for an event the previous
+ * eager call recorded), but calls made while the stream is capturing a HIP graph are not, so
+ * graph replays that overlap other noalloc calls on the same GPU race.
  */
 int tfa_execute_noalloc(const tfa_plan* plan, int64_t batch, const float* in_re, const float* in_im,
                         float* out_re, float* out_im, tfa_stream stream);

@@ -71,3 +71,34 @@ def test_noalloc_rejects_oversized_scratch_with_a_clear_error():
     rc = lib.tfa_execute_noalloc(plan.handle, batch, _P(x), _P(x), _P(x), _P(x), None)
     assert rc == _lib.TFA_ERR_INVALID
     assert b"64" in lib.tfa_last_error() or b"67108864" in lib.tfa_last_error()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered():
+    # eager calls on two streams share the GPU's scratch; the library orders them on the device
+    # (each waits for the previous call's event), so every output equals tfa_execute's with a
+    # workspace of its own, bit for bit, though the host enqueues the calls back to back
+    lib = _lib.lib()
+    dev = torch.cuda.current_device()
+    plan = native_plan(_lib.KIND_C2C, 1 << 20, False, dev)
+    blue = native_plan(_lib.KIND_BLUESTEIN, 20000, True, dev)  # split Bluestein, m = 65536
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]  # default priority
+    cases = []
+    for i in range(6):
+        p, n, batch = (plan, 1 << 20, 4) if i % 2 == 0 else (blue, 20000, 3)
+        re, im = seeded_complex(batch, n, seed=70 + i)
+        re, im = re.cuda(), im.cuda()
+        ws = torch.empty(p.workspace_bytes(batch) // 4, device="cuda")
+        ref = (torch.empty(batch, n, device="cuda"), torch.empty(batch, n, device="cuda"))
+        _lib.check(lib.tfa_execute(p.handle, batch, _P(re), _P(im), _P(ref[0]), _P(ref[1]), _P(ws),
+                                   ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "tfa_execute")
+        got = (torch.full((batch, n), float("nan"), device="cuda"), torch.full((batch, n), float("nan"), device="cuda"))
+        cases.append((p, batch, re, im, ref, got))
+    torch.cuda.synchronize()
+    for i, (p, batch, re, im, ref, got) in enumerate(cases):
+        s = streams[i % 2]
+        rc = lib.tfa_execute_noalloc(p.handle, batch, _P(re), _P(im), _P(got[0]), _P(got[1]),
+                                     ctypes.c_void_p(s.cuda_stream))
+        _lib.check(rc, "tfa_execute_noalloc")
+    torch.cuda.synchronize()
+    for i, (p, batch, re, im, ref, got) in enumerate(cases):
+        assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1]), i

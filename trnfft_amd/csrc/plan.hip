@@ -18,7 +18,7 @@ using tfa::LdsShape;
 // Scratch of the allocation-free entry point (tfa_execute_noalloc): device memory of the loaded
 // code object, one copy per GPU, held until the process ends.  Host code must never pass this
 // name to a kernel (it is a host-side stand-in); it uses the per-device address from
-// hipGetSymbolAddress (scratch_for_device below).
+// hipGetSymbolAddress (scratch_setup below).
 constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
@@ -390,22 +390,26 @@ void note_capture(const tfa_plan* plan, tfa_stream stream) {
 }
 
 constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
+std::mutex g_scratch_mu;  // held across a noalloc call's wait, launch and record (per process)
 void* g_scratch_ptr[kMaxScratchDevices] = {};
+hipEvent_t g_scratch_done[kMaxScratchDevices] = {};  // recorded after each eager noalloc call
+bool g_scratch_used[kMaxScratchDevices] = {};
 
-// Device address of `scratch` on `dev`, which must be the current device; resolved on the first
-// call on each device and kept.
-int scratch_for_device(int dev, void** out) {
-  if (dev < 0 || dev >= kMaxScratchDevices) return fail(TFA_ERR_UNSUPPORTED, "device index beyond the scratch table");
-  std::lock_guard<std::mutex> g(g_scratch_mu);
+// Set-up of the noalloc scratch on `dev`, which must be the current device (first call on each
+// device, g_scratch_mu held): the device address of `scratch` and the event that orders the
+// calls sharing it.
+int scratch_setup(int dev) {
   if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
     hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
     if (!p) return fail(TFA_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(e, "hipEventCreateWithFlags(noalloc order)");
+    g_scratch_done[dev] = ev;
     g_scratch_ptr[dev] = p;
   }
-  *out = g_scratch_ptr[dev];
   return TFA_OK;
 }
 
@@ -785,16 +789,37 @@ int tfa_execute_noalloc(const tfa_plan* plan, int64_t batch, const float* in_re,
     return fail(TFA_ERR_INVALID, "tfa_execute_noalloc: this transform needs " + std::to_string(need) +
                                      " bytes of scratch, above the static scratch of " +
                                      std::to_string(kNoAllocScratchBytes) + " bytes (use tfa_execute with a workspace)");
-  void* ws = nullptr;
-  if (need > 0) {
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
-      return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
-    if ((rc = scratch_for_device(dev, &ws))) return rc;
+  if (need == 0) return tfa_execute(plan, batch, in_re, in_im, out_re, out_im, nullptr, stream);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
+    return fail(TFA_ERR_INVALID, "plan was created on another device than the current one");
+  if (dev < 0 || dev >= kMaxScratchDevices) return fail(TFA_ERR_UNSUPPORTED, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if ((rc = scratch_setup(dev))) return rc;
+  // every call on this GPU shares the scratch: an eager call waits on the device for the previous
+  // eager call's kernels (on whatever stream) before its own use it.  Calls captured into a graph
+  // are not ordered (a captured wait on an event recorded outside the capture is not allowed):
+  // replays that overlap other noalloc calls on this GPU race.
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    st = hipStreamCaptureStatusNone;
+  }
+  const bool eager = st == hipStreamCaptureStatusNone;
+  if (eager && g_scratch_used[dev]) {
+    const hipError_t e = hipStreamWaitEvent(s, g_scratch_done[dev], 0);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent(noalloc order)");
   }
   // the same kernels as tfa_execute; every kernel writes the scratch it later reads, so nothing
   // needs clearing between calls
-  return tfa_execute(plan, batch, in_re, in_im, out_re, out_im, ws, stream);
+  rc = tfa_execute(plan, batch, in_re, in_im, out_re, out_im, g_scratch_ptr[dev], stream);
+  if (rc == TFA_OK && eager) {
+    const hipError_t e = hipEventRecord(g_scratch_done[dev], s);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord(noalloc order)");
+    g_scratch_used[dev] = true;
+  }
+  return rc;
 }
 
 int tfa_execute_strided_ws(const tfa_plan* plan, int64_t outer, int64_t stride, const float* in_re,

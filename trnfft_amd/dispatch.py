@@ -21,6 +21,7 @@ import torch
 
 from . import _lib
 from .complex import ComplexTensor
+from .precision import _SUPPORTED as _SUPPORTED_PRECISION
 
 HAS_HIP = _lib.library_present()
 # the reference's flag (trnfft/nki/dispatch.py:17-24): this backend has no NKI path
@@ -67,6 +68,28 @@ def _use_hip() -> bool:
     if _backend == "pytorch":
         return False
     return _hip_ready()
+
+
+def hip_accepts(*tensors: torch.Tensor | None, precision: str = "fast") -> bool:
+    """Whether a call should be routed to this backend at all.
+
+    True only when the backend is selected and usable (``_use_hip()``), the caller's *resolved*
+    precision mode is ``"fast"`` -- the caller resolves its per-call override against its own
+    global first, as trnfft/precision.py:88-94 does for trnfft/fft_core.py:37-39 -- and every
+    tensor given (signal planes, window, weights; None is skipped) is a real float32 tensor.
+    The reference computes in its input's dtype (twiddles in ``re.dtype``, fft_core.py:84-88; the
+    chirp in ``x.dtype``, :1317; the window in ``input.dtype``, api.py:307-308) and runs its
+    "kahan"/"double" modes on its own path, so for anything else the caller keeps that path.
+    Asked directly, this package raises for such calls (TypeError for other dtypes,
+    NotImplementedError for other modes); it never computes them in fp32."""
+    if precision not in _SUPPORTED_PRECISION:
+        return False
+    for t in tensors:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.float32:
+            return False
+    return _use_hip()
 
 
 def _require_hip(what: str) -> None:
