@@ -80,6 +80,40 @@ def _median(v):
     return v[len(v) // 2]
 
 
+def _copy_lib():
+    """libtfa_copy.so (built with the library): plain split-plane copy kernels, the measured
+    ceiling for a transform's traffic."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "trnfft_amd", "libtfa_copy.so"))
+    lib.tfa_bench_copy2.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_longlong, ctypes.c_int, ctypes.c_void_p]
+    lib.tfa_bench_copy2.restype = ctypes.c_int
+    lib.tfa_bench_copy2_variants.restype = ctypes.c_int
+    return lib
+
+
+def bench_copy_ceiling(plane_floats: int, warm_s: float = 0.03):
+    """Best time of the native split-plane copy variants (two planes of plane_floats fp32 read,
+    two written: a transform's algorithmic traffic) over buffer sets rotated past the Infinity
+    Cache, each variant timed like the secondary configs; returns (seconds, per-variant seconds)."""
+    lib = _copy_lib()
+    dev = torch.device("cuda", torch.cuda.current_device())
+    S = _n_sets(4 * plane_floats * 4)
+    srcs = [(torch.randn(plane_floats, device=dev), torch.randn(plane_floats, device=dev)) for _ in range(S)]
+    dsts = [(torch.empty(plane_floats, device=dev), torch.empty(plane_floats, device=dev)) for _ in range(S)]
+    times = []
+    for v in range(lib.tfa_bench_copy2_variants()):
+        def fn(k, st, v=v):
+            a, b = srcs[k]
+            c, d = dsts[(k + 1) % S]
+            rc = lib.tfa_bench_copy2(a.data_ptr(), b.data_ptr(), c.data_ptr(), d.data_ptr(), plane_floats, v, st)
+            if rc:
+                raise RuntimeError(f"tfa_bench_copy2 variant {v}: hip error {rc}")
+        times.append(_time_rot(fn, S, warm_s=warm_s))
+    for a, b in zip(srcs, dsts[1:] + dsts[:1]):
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    del srcs, dsts
+    return min(times), times
+
+
 def _traffic_from_profiles(kernel_tag: str):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/*.md), or None."""
     path = os.path.join(ROOT, "profiles", f"{kernel_tag}_pmc.md")
@@ -214,26 +248,17 @@ def bench_headline(steps: int, warmup: int):
     del graph
 
 
-    # plain device copy of the same bytes (32 MiB in, 32 MiB out per launch, same rotation): the
-    # achievable-bandwidth reference, and the known-size kernel that calibrates rocprof counters
-    csrc = [torch.cat([a.reshape(-1), b.reshape(-1)]) for a, b in ins]
-    cdst = [torch.empty_like(csrc[0]) for _ in range(sets)]
-    for k in range(warmup):
-        cdst[k % sets].copy_(csrc[k % sets])
-    torch.cuda.synchronize()
-    reps = 2 * ROOFLINE_STEPS
-    ev0.record()
-    for k in range(reps):
-        cdst[k % sets].copy_(csrc[(k + 3) % sets])
-    ev1.record()
-    torch.cuda.synchronize()
-    t_copy = ev0.elapsed_time(ev1) * 1e-3 / reps
-    del csrc, cdst
+    # the achievable rate for these bytes: native split-plane copies (two 16 MiB planes read, two
+    # written per launch, rotated like the transform), best of four access styles
+    del ins, outs, args_f, args_i
+    torch.cuda.empty_cache()
+    t_copy, copy_times = bench_copy_ceiling(batch * n)
 
     flops_step = 2 * flops_fft(n, batch)
     bytes_launch = 2 * 2 * plane  # read re+im, write re+im
     return {
         "t_copy_s": t_copy,
+        "copy_variants_us": [round(t * 1e6, 3) for t in copy_times],
         "t_region_s": t_region,
         "wall_s": wall,
         "ms_per_step": t_region / steps * 1e3,
@@ -323,38 +348,50 @@ def bench_secondary():
             r["note"] = note
         out[name] = r
 
-    # C2: STFT 64 x 160000, n_fft 512, hop 256 (center, reflect, periodic Hann, onesided); spectra
-    # in the API's memory order (frames-major: torch.stft's, and the reference's transposed frames)
-    fm = _lib.STFT_CENTER | _lib.STFT_ONESIDED | _lib.STFT_FRAMES_MAJOR
+    # C2: STFT 64 x 160000, n_fft 512, hop 256 (center, reflect, periodic Hann, onesided).  The
+    # reference's result layout: contiguous (64, 257, 626) planes (its ComplexTensor makes the
+    # transposed spectra contiguous, trnfft/complex.py:29-33); frames-major spectra (torch.stft's
+    # memory order, an opt-in here) as a separate line
+    bm = _lib.STFT_CENTER | _lib.STFT_ONESIDED
+    fm = bm | _lib.STFT_FRAMES_MAJOR
     nbytes = 64 * 160000 * 4 + 2 * 64 * 257 * 626 * 4
     S = _n_sets(nbytes)
     xs = rolled(make_stft_input(64, 160000), S)
     win = torch.hann_window(512).to(dev)
-    pl = native_plan(_lib.KIND_STFT, 512, False, dev.index, hop=256, flags=fm)
-    os_ = [(torch.empty(64, 626, 257, device=dev), torch.empty(64, 626, 257, device=dev)) for _ in range(S)]
-    t = _time_rot(lambda k, st: chk(L.tfa_stft_execute(pl.handle, 64, 160000, P(xs[k]), P(win), P(os_[k][0]),
-                                                   P(os_[k][1]), st)), S)
-    rec("c2_stft_64x160000_nfft512", t, 40064 * 5 * 512 * 9, nbytes, sets=S)
+    specs = {}
+    for tag, flags, shape in [("", bm, (64, 257, 626)), ("_frames_major", fm, (64, 626, 257))]:
+        pl = native_plan(_lib.KIND_STFT, 512, False, dev.index, hop=256, flags=flags)
+        os_ = [(torch.empty(*shape, device=dev), torch.empty(*shape, device=dev)) for _ in range(S)]
+        t = _time_rot(lambda k, st: chk(L.tfa_stft_execute(pl.handle, 64, 160000, P(xs[k]), P(win), P(os_[k][0]),
+                                                           P(os_[k][1]), st)), S)
+        rec("c2_stft_64x160000_nfft512" + tag, t, 40064 * 5 * 512 * 9, nbytes, sets=S,
+            note="spectra (64, 257, 626) contiguous: the reference's layout" if not tag else
+            "spectra (64, 626, 257): torch.stft's memory order (opt-in)")
+        specs[tag] = (flags, os_)
     # inverse of C2 (fused istft: completion, inverse transform, window, overlap-add, envelope, trim)
-    ipl = native_plan(_lib.KIND_STFT, 512, True, dev.index, hop=256, flags=fm)
+    # from each layout
     ys = [torch.empty(64, 160000, device=dev) for _ in range(S)]
-    t = _time_rot(lambda k, st: chk(L.tfa_istft_execute(ipl.handle, 64, 626, P(os_[k][0]), P(os_[k][1]), P(win),
-                                                        P(ys[k]), 160000, st)), S)
-    rec("c2_istft_64x257x626_nfft512", t, 40064 * 5 * 512 * 9, nbytes, sets=S,
-        note="inverse of c2: spectra in, 64 x 160000 samples out")
-    del os_, ys
-    # C2's signals at n_fft 400 (25 ms at 16 kHz), hop 160: one Bluestein chain per frame
+    for tag, (flags, os_) in specs.items():
+        ipl = native_plan(_lib.KIND_STFT, 512, True, dev.index, hop=256, flags=flags)
+        t = _time_rot(lambda k, st: chk(L.tfa_istft_execute(ipl.handle, 64, 626, P(os_[k][0]), P(os_[k][1]), P(win),
+                                                            P(ys[k]), 160000, st)), S)
+        rec("c2_istft_64x257x626_nfft512" + tag, t, 40064 * 5 * 512 * 9, nbytes, sets=S,
+            note="inverse of c2: spectra " + ("(64, 257, 626), the reference's layout" if not tag else
+                                              "(64, 626, 257)") + " in, 64 x 160000 samples out")
+    del specs, ys
+    # C2's signals at n_fft 400 (25 ms at 16 kHz), hop 160: one Bluestein chain per frame (the
+    # reference's layout)
     w400 = torch.hann_window(400).to(dev)
-    p400 = native_plan(_lib.KIND_STFT, 400, False, dev.index, hop=160, flags=fm)
+    p400 = native_plan(_lib.KIND_STFT, 400, False, dev.index, hop=160, flags=bm)
     frames = 1 + 160000 // 160
     nbytes = 64 * 160000 * 4 + 2 * 64 * 201 * frames * 4
-    os_ = [(torch.empty(64, frames, 201, device=dev), torch.empty(64, frames, 201, device=dev)) for _ in range(S)]
+    os_ = [(torch.empty(64, 201, frames, device=dev), torch.empty(64, 201, frames, device=dev)) for _ in range(S)]
     t = _time_rot(lambda k, st: chk(L.tfa_stft_execute(p400.handle, 64, 160000, P(xs[k]), P(w400), P(os_[k][0]),
                                                    P(os_[k][1]), st)), S)
     rec("stft_64x160000_nfft400", t, 64 * frames * 2 * 5 * 768 * math.log2(768), nbytes, sets=S,
         note="non-power-of-two n_fft: two 768-point transforms per frame (gflops counts those), VALU-bound")
     # its inverse: one inverse Bluestein chain per frame (1024 points: every sample is kept)
-    ip400 = native_plan(_lib.KIND_STFT, 400, True, dev.index, hop=160, flags=fm)
+    ip400 = native_plan(_lib.KIND_STFT, 400, True, dev.index, hop=160, flags=bm)
     ys = [torch.empty(64, 160000, device=dev) for _ in range(S)]
     t = _time_rot(lambda k, st: chk(L.tfa_istft_execute(ip400.handle, 64, frames, P(os_[k][0]), P(os_[k][1]),
                                                         P(w400), P(ys[k]), 160000, st)), S)
@@ -449,21 +486,13 @@ def bench_secondary():
                                               None, None, st)), S)
     rec("irfft_c2r_4096x1024", t, flops_fft(n, b) / 2, nbytes, sets=S, note="flops = 2.5 N log2 N per row")
     del xs, bins
-    # reference point for the headline: a plain device copy of the headline's traffic (two 16 MiB
-    # planes read, two written), same rotation and timing
-    plane = 4096 * 1024
-    S = _n_sets(4 * plane * 4)
-    srcs = [(torch.randn(plane, device=dev), torch.randn(plane, device=dev)) for _ in range(S)]
-    dsts = [(torch.empty(plane, device=dev), torch.empty(plane, device=dev)) for _ in range(S)]
-
-    def copy_pair(k, st):
-        dsts[k][0].copy_(srcs[k][0])
-        dsts[k][1].copy_(srcs[k][1])
-
-    t = _time_rot(copy_pair, S)
-    rec("copy_2x16MiB_planes", t, 0, 4 * plane * 4, sets=S,
-        note="torch copy_ of the headline's bytes (two launches): the c2c kernel's rate against a plain copy")
-    del srcs, dsts
+    # achievable-rate references: native split-plane copies of the headline's and C3b's traffic
+    # (best of four access styles, same rotation and timing)
+    for name, planef, what in [("copy_2x16MiB_planes", 4096 * 1024, "the headline's bytes (C1)"),
+                               ("copy_2x4MiB_planes", 256 * 4099, "C3b's bytes (256 x 4099)")]:
+        t, _ = bench_copy_ceiling(planef)
+        rec(name, t, 0, 4 * planef * 4, sets=_n_sets(4 * planef * 4),
+            note=f"native split-plane copy of {what}: the achievable rate for that traffic")
     torch.cuda.empty_cache()
     return out
 
@@ -495,24 +524,29 @@ def bench_cpu_baseline():
         model = ""
 
     def timed(fn, k_limit=None, reps=1):
-        """Median over reps of the (extrapolated) seconds of fn() under the literal loop."""
+        """Median over reps of the (extrapolated) seconds of fn() under the literal loop, the
+        wall seconds actually run for it, and the fraction of butterfly positions run."""
         secs, frac = [], 1.0
         for _ in range(reps):
             with oracle.LiteralLoopTiming(k_limit) as t:
                 fn()
-            secs.append(t.seconds)
+            secs.append((t.seconds, t.seconds - t.skipped_s))
             frac = t.positions_run / max(1, t.positions_total)
-        return _median(secs), frac
+        sec, ran = sorted(secs)[len(secs) // 2]
+        return sec, ran, frac
 
     configs = {}
 
     def rec(name, fn, flops, sample, k_limit=None, reps=1, scale=1.0):
-        sec, frac = timed(fn, k_limit, reps)
+        sec, ran, frac = timed(fn, k_limit, reps)
         sec *= scale
         configs[name] = {
             "seconds": round(sec, 4),
             "gflops": round(flops / sec / 1e9, 4),
             "reps": reps,
+            # wall seconds actually measured for the sample (before extrapolation / scaling)
+            "measured_seconds": round(ran, 4),
+            "extrapolated": bool(k_limit) or scale != 1.0,
             "sample": sample + (f"; literal loop capped at {k_limit} positions per stage "
                                 f"({100 * frac:.1f} % of positions run, rest extrapolated)" if k_limit else ""),
         }
@@ -630,6 +664,9 @@ def main(argv=None):
             "t_launch_isolated_median_us": round(head["t_launch_median_s"] * 1e6, 3),
             "bytes_per_launch": head["bytes_launch"],
             "copy_gbps": round(head["bytes_launch"] / head["t_copy_s"] / 1e9, 1),
+            "copy_from": "native split-plane copy of the same bytes (libtfa_copy.so), best of 4 access styles, "
+            "same buffer rotation",
+            "copy_variants_us": head["copy_variants_us"],
             "frac_of_copy": round(head["t_copy_s"] / head["t_launch_s"], 4),
         },
     }

@@ -1,4 +1,5 @@
-"""Build libtrnfft_amd.so (all HIP kernels + the C ABI) for gfx950 with hipcc, in-tree.
+"""Build libtrnfft_amd.so (all HIP kernels + the C ABI) for gfx950 with hipcc, in-tree, and
+libtfa_copy.so, the plain-copy kernels bench.py measures the achievable memory rate with.
 
 Usage: python -m trnfft_amd.csrc.build   (or trnfft_amd.csrc.build.build()).
 """
@@ -14,6 +15,8 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 LIB = os.path.join(PKG, "libtrnfft_amd.so")
+COPY_LIB = os.path.join(PKG, "libtfa_copy.so")
+COPY_SOURCE = "bench_copy.hip"
 SOURCES = [
     "plan.hip",
     "kernels_c2c.hip",
@@ -56,23 +59,29 @@ def _compile(src: str, obj: str) -> None:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")
 
 
+def _link(objs: list[str], out: str) -> None:
+    tmp = out + ".tmp"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed for {os.path.basename(out)}:\n{res.stderr}")
+    os.replace(tmp, out)
+
+
 def build(verbose: bool = False) -> str:
-    """Compile every source and link the shared library; returns its path."""
+    """Compile every source and link the shared libraries; returns the main library's path."""
     if not shutil.which(HIPCC) and not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found ({HIPCC})")
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs = [os.path.join(objdir, s.rsplit(".", 1)[0] + ".o") for s in SOURCES]
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
-        list(ex.map(lambda so: _compile(*so), zip(SOURCES, objs)))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB)
+    srcs = SOURCES + [COPY_SOURCE]
+    objs = [os.path.join(objdir, s.rsplit(".", 1)[0] + ".o") for s in srcs]
+    with ThreadPoolExecutor(max_workers=min(len(srcs), os.cpu_count() or 1)) as ex:
+        list(ex.map(lambda so: _compile(*so), zip(srcs, objs)))
+    _link(objs[:-1], LIB)
+    _link(objs[-1:], COPY_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {COPY_LIB}")
     return LIB
 
 
