@@ -168,6 +168,43 @@ def test_stft_vs_torch_stft(n_fft, hop, center):
     assert rel_l2(r, i, e.real, e.imag) < 1e-5
 
 
+@pytest.mark.parametrize("n_fft,hop,center,pad_mode,onesided,normalized", [
+    (512, 256, True, "constant", True, False),
+    (512, 128, True, "replicate", True, False),
+    (256, 100, True, "circular", True, True),
+    (256, 64, True, "constant", False, False),    # two-sided spectrum
+    (400, 160, True, "reflect", True, False),     # non-power-of-two n_fft: Bluestein per frame
+    (400, 160, False, "reflect", True, False),
+    (400, 100, True, "constant", True, True),
+    (400, 133, True, "replicate", False, False),
+    (12, 3, True, "reflect", True, False),
+    (12, 5, False, "constant", True, False),
+    (12, 4, True, "circular", False, True),
+])
+def test_stft_pad_modes_and_other_lengths_vs_torch_stft(n_fft, hop, center, pad_mode, onesided, normalized):
+    # the oracle's F.pad modes, framing, window, non-power-of-two per-frame transform, onesided
+    # slice and normalisation against torch.stft in float64.  Power-of-two n_fft within fp32
+    # rounding; non-power-of-two n_fft carry the reference's fp32 Bluestein chirp (angle rounded
+    # in fp32, trnfft/fft_core.py:1317-1320; pinned bit-exact by the golden vectors above), whose
+    # distance from the exact DFT is 2e-5 to 4e-5 at n_fft 400 (5e-7 at 12)
+    g = torch.Generator().manual_seed(n_fft * 3 + hop)
+    x = torch.randn(2, 3001, generator=g)
+    r, i = oracle.stft(x, n_fft=n_fft, hop_length=hop, center=center, pad_mode=pad_mode, onesided=onesided,
+                       normalized=normalized)
+    e = torch.stft(x.double(), n_fft, hop_length=hop, window=torch.hann_window(n_fft, dtype=torch.float64),
+                   center=center, pad_mode=pad_mode, normalized=normalized, onesided=onesided,
+                   return_complex=True)
+    assert r.shape == e.shape
+    tol = 1e-5 if n_fft & (n_fft - 1) == 0 else 1e-4
+    assert rel_l2(r, i, e.real, e.imag) < tol
+    # a plausible mistake fails: the padded signal reflected with its edge sample repeated
+    # (mode "symmetric") instead of torch's reflect
+    if center and pad_mode == "reflect":
+        xs = torch.cat([x[:, : n_fft // 2].flip(-1), x, x[:, -(n_fft // 2):].flip(-1)], dim=-1)
+        rs, is_ = oracle.stft(xs, n_fft=n_fft, hop_length=hop, center=False, onesided=onesided, normalized=normalized)
+        assert rel_l2(rs, is_, e.real, e.imag) > 10 * tol
+
+
 def test_istft_roundtrip():
     g = torch.Generator().manual_seed(42)
     x = torch.randn(2, 1024, generator=g)
