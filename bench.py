@@ -605,6 +605,47 @@ def bench_cpu_baseline():
     }
 
 
+HEADLINE_KERNEL = "c2c_lds_kernel<1024, "
+
+
+def trace_summary(csv_path: str, warmup: int, steps: int) -> dict:
+    """Per-region average duration of the headline kernel's dispatches in a rocprofv3 kernel trace
+    of `bench.py --steps K --warmup W` (the *_kernel_trace.csv of --kernel-trace), from the
+    order bench_headline launches them in (both directions counted together):
+      graph warm-up replays   3 x 2*ROOFLINE_STEPS
+      graph timed replays     3 x 2*ROOFLINE_STEPS   <- roofline.t_launch
+      eager fixed region      3 x 2*ROOFLINE_STEPS   <- roofline.t_launch_eager
+      warm-up steps           2*W
+      timed K-step regions    3 x 2*K                 <- value
+      isolated event pairs    200                     <- roofline.t_launch_isolated_median
+    For the graph regions it also reports the span from the first dispatch's start to the last's
+    end divided by the dispatch count (what the events around a replay measure)."""
+    import csv
+
+    rows = []
+    with open(csv_path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r.get("Kernel_Name", "").startswith(HEADLINE_KERNEL):
+                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    rows.sort()
+    R = 2 * ROOFLINE_STEPS
+    bounds = [("graph_warmup", 3 * R), ("graph_timed", 3 * R), ("eager_fixed", 3 * R), ("warmup_steps", 2 * warmup),
+              ("timed_steps", 3 * 2 * steps), ("isolated_pairs", 200)]
+    out, i = {"dispatches": len(rows)}, 0
+    for name, cnt in bounds:
+        seg = rows[i:i + cnt]
+        i += cnt
+        if len(seg) < cnt:
+            break
+        durs = [(e - b) * 1e-3 for b, e in seg]
+        reg = {"dispatches": cnt, "avg_us": round(sum(durs) / cnt, 3), "median_us": round(_median(durs), 3)}
+        if name.startswith("graph") or name == "eager_fixed":
+            spans = [(seg[j + R - 1][1] - seg[j][0]) * 1e-3 / R for j in range(0, cnt, R)]
+            reg["span_per_dispatch_us"] = [round(x, 3) for x in spans]
+        out[name] = reg
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -612,7 +653,13 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="summarise a rocprofv3 kernel trace of a bench run made with the same --steps/--warmup "
+                    "by region (no GPU needed) and exit")
     args = ap.parse_args(argv)
+    if args.trace_summary:
+        print(json.dumps(trace_summary(args.trace_summary, args.warmup, args.steps), indent=1))
+        return 0
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU only (requested --gpus {args.gpus}): every config here is a batch "

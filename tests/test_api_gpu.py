@@ -404,7 +404,9 @@ def test_fft2_complex_and_inverse(shape):
 
 
 @pytest.mark.parametrize("shape", [(2, 16, 16), (1, 4096, 16), (3, 16, 2048), (2, 512, 1024), (1, 128, 64), (2, 64, 32),
-                                   (2, 64, 4096), (1, 256, 4096)])
+                                   (2, 64, 4096), (1, 256, 4096),
+                                   # 16 row groups (H = 16 x HR): HR = 64, 256 and 128
+                                   (2, 1024, 1024), (1, 4096, 2048), (1, 2048, 1024), (1, 1024, 2048)])
 def test_fft2_real_input(shape):
     # real input.  Two-pass shapes: pass 1 writes columns 0..W/2, pass 2 completes W/2+1..W-1
     # from the 2-D Hermitian symmetry; small images are transformed whole.  Forward and inverse
