@@ -50,6 +50,40 @@ CASES = [
 ]
 
 
+# bins-major spectra (the reference's layout, what stft returns) against the frames-major input
+# path on the same spectra and against the oracle: batch, frame counts, halo 0..3, zero fill,
+# leading dims
+RANGE_CASES = [
+    # lead, n_fft, hop, frames, center, normalized, length
+    ((64,), 512, 256, 626, True, False, None),    # BASELINE config 2's inverse
+    ((1,), 512, 256, 2000, True, False, None),    # one signal
+    ((2,), 512, 256, 627, True, False, None),     # odd frame count
+    ((300,), 512, 256, 70, True, False, None),    # more signals than CUs
+    ((3,), 512, 512, 90, True, False, None),      # halo 0
+    ((4,), 512, 200, 150, False, True, None),     # halo 2, hop not dividing n_fft, no centring
+    ((2,), 512, 256, 300, True, False, 40000),    # length beyond the signal: zero fill
+    ((2,), 512, 256, 300, True, False, 50001),    # one-sample path (length not a multiple of 4)
+    ((5, 2), 256, 128, 400, True, False, None),   # leading dims; n_fft 256 (two pairs per wavefront)
+    ((3,), 256, 64, 200, True, True, 12000),      # halo 3, truncation
+    ((1,), 256, 100, 64, False, False, None),     # hop not a multiple of 4
+]
+
+
+@pytest.mark.parametrize("lead,n_fft,hop,frames,center,normalized,length", RANGE_CASES)
+def test_istft_bins_major_against_frames_major(lead, n_fft, hop, frames, center, normalized, length):
+    re, im = _spec(lead, n_fft, frames, seed=frames + hop)
+    got = trnfft_amd.istft(ComplexTensor(re.cuda(), im.cuda()), n_fft, hop_length=hop, center=center,
+                           normalized=normalized, length=length)
+    ref = oracle.istft((re, im), n_fft, hop_length=hop, center=center, normalized=normalized, length=length)
+    assert got.shape == ref.shape
+    assert _rel(got, ref) <= 1e-6 * math.log2(n_fft) * 4
+    # the frames-major kernel on the same spectra: the same samples to rounding
+    fm = trnfft_amd.istft(ComplexTensor._wrap(re.transpose(-2, -1).contiguous().cuda().transpose(-2, -1),
+                                              im.transpose(-2, -1).contiguous().cuda().transpose(-2, -1)),
+                          n_fft, hop_length=hop, center=center, normalized=normalized, length=length)
+    assert _rel(got, fm) <= 1e-6 * math.log2(n_fft)
+
+
 @pytest.mark.parametrize("n_fft,hop,frames,center,normalized,length", CASES)
 def test_istft_matches_reference(n_fft, hop, frames, center, normalized, length):
     re, im = _spec((3,), n_fft, frames, seed=n_fft + hop)
