@@ -43,10 +43,12 @@ typedef void* tfa_stream; /* hipStream_t; NULL = the null stream */
 #define TFA_STFT_CENTER 1     /* reflect-pad n_fft/2 on both sides (pad_mode="reflect") */
 #define TFA_STFT_NORMALIZED 2 /* scale by 1/sqrt(n_fft)                                 */
 #define TFA_STFT_ONESIDED 4   /* keep bins 0..n_fft/2                                   */
-/* Spectra stored (batch, n_frames, n_bins) row-major instead of (batch, n_bins, n_frames): the
- * memory order of torch.stft's (..., freq, time) result and of trnfft's (trnfft/api.py:356-358
- * returns the transpose of (..., time, freq) frames), whose shape is the same.  Applies to the
- * forward output, the inverse input and the backward's gradient input. */
+/* Spectra stored (batch, n_frames, n_bins) row-major instead of (batch, n_bins, n_frames).  Without
+ * it the planes are trnfft's result layout: its stft wraps the transposed frame spectra in a
+ * ComplexTensor, whose constructor makes them contiguous (trnfft/api.py:357-365,
+ * trnfft/complex.py:29-33).  With it they are in the memory order of torch.stft's
+ * (..., freq, time) result (no reference counterpart).  Applies to the forward output, the
+ * inverse input and the backward's gradient input. */
 #define TFA_STFT_FRAMES_MAJOR 8
 
 typedef struct tfa_plan_desc {

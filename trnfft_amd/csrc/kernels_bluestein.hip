@@ -40,7 +40,9 @@ struct BlueCfg {
 // L = n - wrap) to the outputs k >= L and y[j] conj(chirp[k - j + M]) (j >= k + L) to the outputs
 // k < wrap; both are subtracted after the inverse transform from the chirped input ends y[0, wrap),
 // y[L, n) and chirp[L, n), kept in LDS.  n then exceeds M/2 by at most 8, so one more element per
-// thread can hold a sample.
+// thread can hold a sample.  The corrected outputs i < wrap sit in element 0 of their threads and
+// L <= i < n in elements E/2 - 1 and E/2 (L is up to 7 below M/2); the correction runs over every
+// element e < E/2 + 1.
 template <int M, bool REAL_IN, bool WRAP = false, int E_ = blue_epth(M), int THR = blue_threads(M)>
 __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fused_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re,
@@ -49,7 +51,8 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
     float scale, int wrap) {
   using C = BlueCfg<M, E_, THR>;
   constexpr int E = C::E, T = C::T;
-  static_assert(!WRAP || (T > kBlueWrapMax && E >= 2), "wrapped lengths: the corrected outputs are elements 0 and E/2");
+  static_assert(!WRAP || (T > kBlueWrapMax && E >= 2),
+                "wrapped lengths: the corrected outputs (i < wrap, L <= i < n) lie in elements 0, E/2 - 1 and E/2");
   __shared__ float2 lds[C::XF * C::PADN * C::NBUF];  // interleaved (re, im) exchange
   __shared__ float2 ends_all[WRAP ? C::XF * 3 * kBlueWrapMax : 1];  // per row: y[0, wrap), y[L, n), chirp[L, n)
   const int tid = threadIdx.x % T;
