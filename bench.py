@@ -625,7 +625,7 @@ def trace_summary(csv_path: str, warmup: int, steps: int) -> dict:
     rows = []
     with open(csv_path, newline="") as f:
         for r in csv.DictReader(f):
-            if r.get("Kernel_Name", "").startswith(HEADLINE_KERNEL):
+            if HEADLINE_KERNEL in r.get("Kernel_Name", ""):
                 rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
     rows.sort()
     R = 2 * ROOFLINE_STEPS
