@@ -87,6 +87,8 @@ def _copy_lib():
     lib.tfa_bench_copy2.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_longlong, ctypes.c_int, ctypes.c_void_p]
     lib.tfa_bench_copy2.restype = ctypes.c_int
     lib.tfa_bench_copy2_variants.restype = ctypes.c_int
+    lib.tfa_bench_copy1.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+    lib.tfa_bench_copy1.restype = ctypes.c_int
     return lib
 
 
@@ -112,6 +114,28 @@ def bench_copy_ceiling(plane_floats: int, warm_s: float = 0.03):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
     del srcs, dsts
     return min(times), times
+
+
+def bench_copy_1stream(floats: int, warm_s: float = 0.03):
+    """The same bytes as one contiguous stream (floats fp32 read from one buffer, written to
+    another; non-temporal float4), buffer sets rotated like bench_copy_ceiling: the fastest plain
+    copy of a transform's traffic on this part.  Returns seconds per copy."""
+    lib = _copy_lib()
+    dev = torch.device("cuda", torch.cuda.current_device())
+    S = _n_sets(2 * floats * 4)
+    srcs = [torch.randn(floats, device=dev) for _ in range(S)]
+    dsts = [torch.empty(floats, device=dev) for _ in range(S)]
+
+    def fn(k, st):
+        rc = lib.tfa_bench_copy1(srcs[k].data_ptr(), dsts[(k + 1) % S].data_ptr(), floats, st)
+        if rc:
+            raise RuntimeError(f"tfa_bench_copy1: hip error {rc}")
+
+    t = _time_rot(fn, S, warm_s=warm_s)
+    for a, b in zip(srcs, dsts[1:] + dsts[:1]):
+        assert torch.equal(a, b)
+    del srcs, dsts
+    return t
 
 
 def _traffic_from_profiles(kernel_tag: str):
@@ -253,11 +277,14 @@ def bench_headline(steps: int, warmup: int):
     del ins, outs, args_f, args_i
     torch.cuda.empty_cache()
     t_copy, copy_times = bench_copy_ceiling(batch * n)
+    # and the same bytes as one contiguous stream (the fastest plain copy of them)
+    t_copy1 = bench_copy_1stream(2 * batch * n)
 
     flops_step = 2 * flops_fft(n, batch)
     bytes_launch = 2 * 2 * plane  # read re+im, write re+im
     return {
         "t_copy_s": t_copy,
+        "t_copy1_s": t_copy1,
         "copy_variants_us": [round(t * 1e6, 3) for t in copy_times],
         "t_region_s": t_region,
         "wall_s": wall,
@@ -715,6 +742,10 @@ def main(argv=None):
             "same buffer rotation",
             "copy_variants_us": head["copy_variants_us"],
             "frac_of_copy": round(head["t_copy_s"] / head["t_launch_s"], 4),
+            "copy_1stream_gbps": round(head["bytes_launch"] / head["t_copy1_s"] / 1e9, 1),
+            "copy_1stream_from": "the same bytes as one contiguous 32 MiB stream (libtfa_copy.so, non-temporal "
+            "float4), same rotation: the fastest plain copy of them",
+            "frac_of_1stream_copy": round(head["t_copy1_s"] / head["t_launch_s"], 4),
         },
     }
     if not args.no_secondary:

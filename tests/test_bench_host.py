@@ -31,3 +31,18 @@ def test_synthetic_inputs_are_seeded_and_shaped():
     assert torch.equal(x, bench.make_stft_input(3, 16000))
     # three sinusoids of amplitude < 1 plus N(0, 0.1) noise
     assert 0.05 < float(x.std()) < 2.0
+
+
+def test_copy_ceiling_library_exports_its_entry_points():
+    # the bench's measured copy ceilings come from libtfa_copy.so (built with the library): it
+    # loads without a GPU and exports the split-plane and one-stream copies bench.py binds
+    import os
+    import pytest
+
+    path = os.path.join(bench.ROOT, "trnfft_amd", "libtfa_copy.so")
+    if not os.path.exists(path):
+        pytest.skip("libtfa_copy.so not built")
+    lib = bench._copy_lib()
+    for name in ("tfa_bench_copy2", "tfa_bench_copy2_variants", "tfa_bench_copy1"):
+        assert hasattr(lib, name)
+    assert lib.tfa_bench_copy2_variants() == 4

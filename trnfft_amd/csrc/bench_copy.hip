@@ -40,6 +40,13 @@ __global__ __launch_bounds__(256) void copy2_kernel(const f4* __restrict__ a, co
   }
 }
 
+// One contiguous stream: the same bytes as one plane pair, read from one buffer and written to
+// another (the fastest plain copy of a transform's traffic on this part).
+__global__ __launch_bounds__(256) void copy1_kernel(const f4* __restrict__ a, f4* __restrict__ c, long long n4) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n4) __builtin_nontemporal_store(__builtin_nontemporal_load(a + i), c + i);
+}
+
 template <int UNR, bool NTL, bool NTS>
 hipError_t launch(const float* a, const float* b, float* c, float* d, long long n, hipStream_t s) {
   const long long n4 = n / 4;
@@ -76,6 +83,20 @@ int tfa_bench_copy2(const float* a, const float* b, float* c, float* d, long lon
     case 3: return (int)launch<4, true, true>(a, b, c, d, n, s);
     default: return (int)hipErrorInvalidValue;
   }
+}
+
+// c[i] = a[i] for i < n as one stream (n a multiple of 4, both 16-byte aligned) on `stream`,
+// non-temporal float4 loads and stores.  Returns a hipError_t.
+int tfa_bench_copy1(const float* a, float* c, long long n, void* stream) {
+  if (n < 0 || (n & 3) != 0) return (int)hipErrorInvalidValue;
+  if (((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(c)) & 15) != 0) return (int)hipErrorInvalidValue;
+  if (n == 0) return (int)hipSuccess;
+  const long long n4 = n / 4;
+  const long long blocks = (n4 + 255) / 256;
+  if (blocks > 0x7fffffffLL) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(copy1_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     reinterpret_cast<const f4*>(a), reinterpret_cast<f4*>(c), n4);
+  return (int)hipGetLastError();
 }
 
 }  // extern "C"
