@@ -22,7 +22,12 @@ the same native kernels:
   complex linear Y = X W^T + b:    dX = dY conj(W),  dW = dY^T conj(X),  db = sum over rows of dY
   each product one tfa_complex_gemm_ex launch (the reference runs eight real matmuls).
 
-Second derivatives are not provided (the backward passes are themselves not differentiable).
+Second derivatives: every transform and product here is linear in each operand, so its adjoint
+is again one of these operations.  Under ``create_graph=True`` (grad mode on inside backward) each
+backward builds its adjoint from the differentiable wrappers of this module (c2c of the opposite
+direction, c2r for r2c and r2c for c2r with the same bin weights, complex products of conjugated /
+transposed operands, and torch ops for the STFT's framing, window and padding adjoints), so the
+gradient can be differentiated again; an ordinary backward keeps the direct kernel calls.
 """
 
 from __future__ import annotations
@@ -31,7 +36,6 @@ import math
 
 import torch
 import torch.nn.functional as F
-from torch.autograd.function import once_differentiable
 
 from . import _lib
 from . import fft_core as _fc
@@ -67,9 +71,15 @@ class _C2CFn(torch.autograd.Function):
         return y.real, y.imag
 
     @staticmethod
-    @once_differentiable
     def backward(ctx, g_re, g_im):
         adj = not ctx.inverse
+        if torch.is_grad_enabled():  # create_graph: the adjoint transform is recorded too
+            s = 1.0 / ctx.size if ctx.inverse else float(ctx.size)
+            if ctx.mode == "fft2":
+                y = _fft2_any(g_re, g_im, adj)
+            else:
+                y = _c2c(g_re, g_im, adj, ctx.mode, ctx.dim)
+            return y.real * s, None if ctx.real_in else y.imag * s, None, None, None
         g_re, g_im = _c(g_re), _c(g_im)
         if ctx.mode == "last":
             g = _fc.execute_1d(g_re, g_im, adj)
@@ -94,6 +104,14 @@ def _c2c(re, im, inverse, mode, dim=-1) -> ComplexTensor:
     return _fc.execute_fft2(re, im, inverse)
 
 
+def _fft2_any(re, im, inverse) -> ComplexTensor:
+    """Differentiable transform over the two trailing axes by the route execute_fft2_any takes."""
+    if _fc.fft2_ok(re.shape[-2], re.shape[-1], im is None):
+        return _c2c(re, im, inverse, "fft2")
+    y = _c2c(re, im, inverse, "strided", re.dim() - 2)
+    return _c2c(y.real, y.imag, inverse, "last")
+
+
 def c2c(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> ComplexTensor:
     """Last-axis transform (im None: real input), differentiable."""
     return _c2c(re, im, inverse, "last")
@@ -112,6 +130,14 @@ def fft2(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -> ComplexTen
 # ---------------------------------------------------------------------------------------------
 # real rows: r2c / c2r
 # ---------------------------------------------------------------------------------------------
+
+
+def _bin_weights(g: torch.Tensor, n: int, inner: float, edge: float) -> torch.Tensor:
+    """(n/2 + 1) weights: `inner` for bins 1..n/2-1, `edge` for bins 0 and n/2."""
+    w = torch.full((g.shape[-1],), inner, dtype=g.dtype, device=g.device)
+    w[0] = edge
+    w[n // 2] = edge
+    return w
 
 
 def _r2c_adjoint(g_re: torch.Tensor, g_im: torch.Tensor, n: int) -> torch.Tensor:
@@ -141,8 +167,10 @@ class _R2CFn(torch.autograd.Function):
         return y.real, y.imag
 
     @staticmethod
-    @once_differentiable
     def backward(ctx, g_re, g_im):
+        if torch.is_grad_enabled():  # create_graph: the same adjoint through the differentiable c2r
+            w = _bin_weights(g_re, ctx.n, 0.5, 1.0)
+            return c2r(g_re * w, g_im * w, ctx.n) * float(ctx.n)
         return _r2c_adjoint(g_re, g_im, ctx.n)
 
 
@@ -153,8 +181,11 @@ class _C2RFn(torch.autograd.Function):
         return _fc.execute_c2r(re, im, n)
 
     @staticmethod
-    @once_differentiable
     def backward(ctx, g):
+        if torch.is_grad_enabled():  # create_graph: the same adjoint through the differentiable r2c
+            y = r2c(g)
+            return (y.real * _bin_weights(y.real, ctx.n, 2.0 / ctx.n, 1.0 / ctx.n),
+                    y.imag * _bin_weights(y.imag, ctx.n, 2.0 / ctx.n, 0.0), None)
         d_re, d_im = _c2r_adjoint(g, ctx.n)
         return d_re, d_im, None
 
@@ -185,7 +216,6 @@ class _StftFn(torch.autograd.Function):
         return _fc.execute_stft(x, win, n_fft, hop, center, normalized, onesided, num_frames, frames_major)
 
     @staticmethod
-    @once_differentiable
     def backward(ctx, g_re, g_im):
         x, win = ctx.saved_tensors
         n_fft, hop, center, normalized, onesided, frames = ctx.cfg
@@ -194,6 +224,8 @@ class _StftFn(torch.autograd.Function):
         b = x.numel() // length
         bins = g_re.shape[-2]
         pad = n_fft // 2 if center else 0
+        if torch.is_grad_enabled():  # create_graph: the composed adjoint, recorded
+            return _stft_adjoint_recorded(ctx, x, win, g_re, g_im)
         if onesided and ctx.needs_input_grad[0] and not ctx.needs_input_grad[1] and g_re.is_cuda:
             # no window gradient: one fused kernel (per-frame transform adjoint, window, overlap-add)
             d_xp = _fc.execute_stft_backward(g_re.reshape(b, bins, frames), g_im.reshape(b, bins, frames), win,
@@ -231,6 +263,46 @@ class _StftFn(torch.autograd.Function):
             d_xp = d_xp.reshape(b, lp)
             d_x = _unpad_reflect(d_xp, pad, length).reshape(*lead, length)
         return d_x, d_win, None, None, None, None, None, None, None
+
+
+def _stft_adjoint_recorded(ctx, x, win, g_re, g_im):
+    """The STFT backward's composed adjoint (the same steps as the direct path) from differentiable
+    operations only, so that the gradients it returns can be differentiated again."""
+    n_fft, hop, center, normalized, onesided, frames = ctx.cfg
+    length = x.shape[-1]
+    lead = x.shape[:-1]
+    b = x.numel() // length
+    bins = g_re.shape[-2]
+    pad = n_fft // 2 if center else 0
+    gr = g_re.reshape(b, bins, frames).transpose(1, 2).contiguous()
+    gi = g_im.reshape(b, bins, frames).transpose(1, 2).contiguous()
+    if onesided and n_fft & (n_fft - 1) == 0:
+        w = _bin_weights(gr, n_fft, 0.5, 1.0)
+        fg = c2r(gr * w, gi * w, n_fft) * float(n_fft)
+    else:
+        if bins < n_fft:
+            gr = F.pad(gr, (0, n_fft - bins))
+            gi = F.pad(gi, (0, n_fft - bins))
+        fg = c2c(gr, gi, True).real * float(n_fft)
+    if normalized:
+        fg = fg * (1.0 / math.sqrt(n_fft))
+    if center:
+        xp = F.pad(x.reshape(b, 1, length), (pad, pad), mode="reflect").reshape(b, -1)
+    else:
+        xp = x.reshape(b, length)
+    lp = xp.shape[-1]
+    d_win = d_x = None
+    if ctx.needs_input_grad[1]:
+        d_win = (xp.unfold(-1, n_fft, hop)[:, :frames] * fg).sum(dim=(0, 1))
+    if ctx.needs_input_grad[0]:
+        d_xp = F.fold((fg * win).transpose(1, 2), output_size=(1, lp), kernel_size=(1, n_fft), stride=(1, hop))
+        d_xp = d_xp.reshape(b, lp)
+        d_x = d_xp[:, pad : pad + length]
+        if pad:  # the reflected edges folded back, out of place
+            d_x = (d_x + F.pad(d_xp[:, :pad].flip(-1), (1, length - 1 - pad))
+                   + F.pad(d_xp[:, pad + length :].flip(-1), (length - 1 - pad, 1)))
+        d_x = d_x.reshape(*lead, length)
+    return d_x, d_win, None, None, None, None, None, None, None
 
 
 def _unpad_reflect(d_xp: torch.Tensor, pad: int, length: int) -> torch.Tensor:
@@ -273,14 +345,24 @@ class _ComplexGEMMFn(torch.autograd.Function):
                        bias_re, bias_im, what=what)
 
     @staticmethod
-    @once_differentiable
     def backward(ctx, g_re, g_im):
         from .dispatch import gemm_ex
 
         a_re, a_im, b_re, b_im = ctx.saved_tensors
-        g_re, g_im = _c(g_re), _c(g_im)
         need = ctx.needs_input_grad
         da_re = da_im = db_re = db_im = dbias_re = dbias_im = None
+        if torch.is_grad_enabled():  # create_graph: the adjoint products through the differentiable gemm
+            if need[0] or need[1]:  # dA = dC op(B)^H
+                da_re, da_im = gemm(g_re, g_im, b_re, -b_im, not ctx.b_trans)
+            if need[2] or need[3]:
+                if ctx.b_trans:  # B = dC^T conj(A)
+                    db_re, db_im = gemm(g_re.t().contiguous(), g_im.t().contiguous(), a_re, -a_im, False)
+                else:  # B = A^H dC
+                    db_re, db_im = gemm(a_re.t().contiguous(), (-a_im).t().contiguous(), g_re, g_im, False)
+            if ctx.has_bias and (need[4] or need[5]):
+                dbias_re, dbias_im = g_re.sum(0), g_im.sum(0)
+            return da_re, da_im, db_re, db_im, dbias_re, dbias_im, None, None
+        g_re, g_im = _c(g_re), _c(g_im)
         if need[0] or need[1]:
             # dA = dC op(B)^H: op(B) = B -> B^H (OP_C of B); op(B) = B^T (linear) -> conj(B) (OP_R)
             da_re, da_im = gemm_ex(g_re, g_im, _lib.OP_N, b_re, b_im, _lib.OP_R if ctx.b_trans else _lib.OP_C,
@@ -318,15 +400,26 @@ class _ComplexBMMFn(torch.autograd.Function):
         return gemm_batched(a_re, a_im, _lib.OP_N, b_re, b_im, _lib.OP_N, batch)
 
     @staticmethod
-    @once_differentiable
     def backward(ctx, g_re, g_im):
         from .dispatch import gemm_batched, gemm_ex
 
         a_re, a_im, b_re, b_im = ctx.saved_tensors
-        g_re, g_im = _c(g_re), _c(g_im)
         batch = ctx.batch
         need = ctx.needs_input_grad
         da_re = da_im = db_re = db_im = None
+        if torch.is_grad_enabled():  # create_graph: the adjoint products through the differentiable bmm
+            if need[0] or need[1]:  # dA_b = dC_b B_b^H
+                da_re, da_im = bmm(g_re, g_im, b_re.transpose(1, 2).contiguous(), (-b_im).transpose(1, 2).contiguous(),
+                                   batch)
+                if a_re.shape[0] == 1 and batch > 1:
+                    da_re, da_im = da_re.sum(0, keepdim=True), da_im.sum(0, keepdim=True)
+            if need[2] or need[3]:  # dB_b = A_b^H dC_b
+                db_re, db_im = bmm(a_re.transpose(1, 2).contiguous(), (-a_im).transpose(1, 2).contiguous(), g_re, g_im,
+                                   batch)
+                if b_re.shape[0] == 1 and batch > 1:
+                    db_re, db_im = db_re.sum(0, keepdim=True), db_im.sum(0, keepdim=True)
+            return da_re, da_im, db_re, db_im, None
+        g_re, g_im = _c(g_re), _c(g_im)
         if need[0] or need[1]:
             # dA_b = dC_b B_b^H, summed over the batch when A is shared
             da_re, da_im = gemm_batched(g_re, g_im, _lib.OP_N, b_re, b_im, _lib.OP_C, batch,
