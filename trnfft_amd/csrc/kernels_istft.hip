@@ -112,25 +112,27 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
     constexpr int KS = THREADS / FR;
     static_assert(THREADS % FR == 0, "lanes keep their frame across the staging steps");
     const int fs = (int)threadIdx.x % FR, k0 = (int)threadIdx.x / FR;
-    const float* bre = sre + (size_t)b * F * n_frames + ta;
-    const float* bim = sim + (size_t)b * F * n_frames + ta;
+    // 32-bit byte offsets from the signal's wave-uniform bases (one offset add per load, the base
+    // in scalar registers), and no conditional loads: a lane past the tile's last frame (last tile
+    // of a signal) reads that last frame, a lane past the last bin row reads the last row; those
+    // values are never gathered or never written to LDS
+    const char* bre = reinterpret_cast<const char*>(sre + (size_t)b * F * n_frames + ta);
+    const char* bim = reinterpret_cast<const char*>(sim + (size_t)b * F * n_frames + ta);
     constexpr int SI = (F + KS - 1) / KS;
     float sr[SI], si[SI];
     {
-      unsigned off = (unsigned)(fs + k0 * n_frames);
-      const unsigned step = (unsigned)(KS * n_frames);
-      const bool fok = fs < nf;
+      const int fsc = fs < nf ? fs : nf - 1;
+      unsigned ob = (unsigned)(fsc + k0 * n_frames) * 4u;
+      const unsigned stepb = (unsigned)(KS * n_frames) * 4u;
+      const unsigned lastb = (unsigned)(fsc + (F - 1) * n_frames) * 4u;
 #pragma unroll
       for (int it = 0; it < SI; ++it) {
-        sr[it] = 0.0f;
-        si[it] = 0.0f;
-        if (k0 + KS * it < F && fok) {
-          // plain loads: a bin row segment is FR frames (64 bytes at n_fft 512), so a cache line
-          // is shared with the neighbouring tile, which then finds it in L2 (measured 4 % faster)
-          sr[it] = bre[off];
-          si[it] = bim[off];
-        }
-        off += step;
+        // plain loads: a bin row segment is FR frames (64 bytes at n_fft 512), so a cache line
+        // is shared with the neighbouring tile, which then finds it in L2 (measured 4 % faster)
+        const unsigned o = k0 + KS * it < F ? ob : lastb;
+        sr[it] = *reinterpret_cast<const float*>(bre + o);
+        si[it] = *reinterpret_cast<const float*>(bim + o);
+        ob += stepb;
       }
     }
     float* sreg = lds + (fs >> 1) * RP + (fs & 1) * 2 * F + k0;
