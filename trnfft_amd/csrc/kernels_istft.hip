@@ -114,14 +114,16 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
     const int fs = (int)threadIdx.x % FR, k0 = (int)threadIdx.x / FR;
     // 32-bit byte offsets from the signal's wave-uniform bases (one offset add per load, the base
     // in scalar registers), and no conditional loads: a lane past the tile's last frame (last tile
-    // of a signal) reads that last frame, a lane past the last bin row reads the last row; those
-    // values are never gathered or never written to LDS
+    // of a signal) reads that last frame and keeps zero (a frame shares its complex transform with
+    // its pair partner, whose rounding a nonzero partner would change), a lane past the last bin
+    // row reads the last row and writes nothing to LDS
     const char* bre = reinterpret_cast<const char*>(sre + (size_t)b * F * n_frames + ta);
     const char* bim = reinterpret_cast<const char*>(sim + (size_t)b * F * n_frames + ta);
     constexpr int SI = (F + KS - 1) / KS;
     float sr[SI], si[SI];
     {
-      const int fsc = fs < nf ? fs : nf - 1;
+      const bool fok = fs < nf;
+      const int fsc = fok ? fs : nf - 1;
       unsigned ob = (unsigned)(fsc + k0 * n_frames) * 4u;
       const unsigned stepb = (unsigned)(KS * n_frames) * 4u;
       const unsigned lastb = (unsigned)(fsc + (F - 1) * n_frames) * 4u;
@@ -130,8 +132,10 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
         // plain loads: a bin row segment is FR frames (64 bytes at n_fft 512), so a cache line
         // is shared with the neighbouring tile, which then finds it in L2 (measured 4 % faster)
         const unsigned o = k0 + KS * it < F ? ob : lastb;
-        sr[it] = *reinterpret_cast<const float*>(bre + o);
-        si[it] = *reinterpret_cast<const float*>(bim + o);
+        const float vr = *reinterpret_cast<const float*>(bre + o);
+        const float vi = *reinterpret_cast<const float*>(bim + o);
+        sr[it] = fok ? vr : 0.0f;
+        si[it] = fok ? vi : 0.0f;
         ob += stepb;
       }
     }
