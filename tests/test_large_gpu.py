@@ -42,16 +42,19 @@ def test_c2c_batch_past_2_31_elements():
     torch.cuda.empty_cache()
 
 
-def test_stft_frames_major_past_2_31_output_elements():
+@pytest.mark.parametrize("frames_major", [False, True])
+def test_stft_past_2_31_output_elements(frames_major):
+    # the reference's bins-major layout (whole-line kernel) and the frames-major opt-in
     _need(40)
     n_fft, hop, length = 512, 256, 160000
     batch = 13500  # 13500 * 626 * 257 > 2^31 bins per plane
     g = torch.Generator(device="cuda").manual_seed(32)
     x = torch.randn(batch, length, device="cuda", generator=g)
     w = torch.hann_window(n_fft, device="cuda")
-    s = trnfft_amd.stft(x, n_fft, hop_length=hop, window=w)
+    s = trnfft_amd.stft(x, n_fft, hop_length=hop, window=w, frames_major=frames_major)
     torch.cuda.synchronize()
     assert s.real.numel() > 2**31
+    assert s.real.is_contiguous() != frames_major
     for b in (0, batch - 1):
         ref = torch.stft(x[b].double().cpu(), n_fft, hop_length=hop, window=w.double().cpu(), center=True,
                          pad_mode="reflect", onesided=True, return_complex=True)
