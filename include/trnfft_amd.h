@@ -168,10 +168,12 @@ int tfa_complex_gemm(int64_t m, int64_t n, int64_t k, const float* a_re, const f
                      int64_t ldc, tfa_stream stream);
 
 /*
- * Inverse STFT of onesided spectra (TFA_KIND_STFT plan created with inverse = 1; n = n_fft,
- * hop, flags CENTER / NORMALIZED, ONESIDED required, FRAMES_MAJOR optional): spec_re/spec_im
- * (batch, n/2+1, n_frames), or (batch, n_frames, n/2+1) with FRAMES_MAJOR, -> out (batch, out_len), out_len from tfa_istft_length (length < 0: the default length).
- * Hermitian completion, inverse transform, window, overlap-add, division by the window-square
+ * Inverse STFT (TFA_KIND_STFT plan created with inverse = 1; n = n_fft, hop, flags CENTER /
+ * NORMALIZED / ONESIDED, FRAMES_MAJOR optional): spec_re/spec_im (batch, n_bins, n_frames), or
+ * (batch, n_frames, n_bins) with FRAMES_MAJOR, with n_bins = n/2+1 when ONESIDED else n, -> out
+ * (batch, out_len), out_len from tfa_istft_length (length < 0: the default length).
+ * Hermitian completion (onesided) or the real part of each frame's inverse transform (two-sided,
+ * power-of-two n only), inverse transform, window, overlap-add, division by the window-square
  * envelope where it exceeds 1e-8 (the raw overlap-add elsewhere), centre trim and zero fill to
  * `length` in one kernel.  Replaces trnfft/api.py:368-470 (istft), whose per-frame loops
  * (:438-452) and window-sum masking (:450-452) it fuses.

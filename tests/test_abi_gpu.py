@@ -43,10 +43,20 @@ def test_plan_kind_limits():
         rc, h = _plan(kind, n, **extra)
         assert rc in (_lib.TFA_ERR_INVALID, _lib.TFA_ERR_UNSUPPORTED), (kind, n, rc)
         assert not h.value and _err()
-    # inverse STFT: two-sided spectra and too-short hops are refused at plan time
-    rc, _ = _plan(_lib.KIND_STFT, 512, inverse=1, hop=128, flags=_lib.STFT_CENTER)
-    assert rc == _lib.TFA_ERR_UNSUPPORTED
+    # inverse STFT: two-sided spectra at a power-of-two n_fft are accepted, at other n_fft refused;
+    # too-short hops are refused at plan time
+    rc, h = _plan(_lib.KIND_STFT, 512, inverse=1, hop=128, flags=_lib.STFT_CENTER)
+    assert rc == 0 and h.value
+    lib.tfa_plan_destroy(h)
+    rc, _ = _plan(_lib.KIND_STFT, 400, inverse=1, hop=160, flags=_lib.STFT_CENTER)
+    assert rc == _lib.TFA_ERR_UNSUPPORTED and "onesided" in _err()
     rc, _ = _plan(_lib.KIND_STFT, 4096, inverse=1, hop=16, flags=_lib.STFT_ONESIDED)
+    assert rc == _lib.TFA_ERR_UNSUPPORTED and "hop" in _err()
+    # n_fft 4096, hop 512 (halo 7): the onesided tile holds 8 frames, the two-sided one 4
+    rc, h = _plan(_lib.KIND_STFT, 4096, inverse=1, hop=512, flags=_lib.STFT_ONESIDED)
+    assert rc == 0 and h.value
+    lib.tfa_plan_destroy(h)
+    rc, _ = _plan(_lib.KIND_STFT, 4096, inverse=1, hop=512, flags=0)
     assert rc == _lib.TFA_ERR_UNSUPPORTED and "hop" in _err()
     assert lib.tfa_abi_version() >> 16 == 1
 

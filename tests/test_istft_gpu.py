@@ -97,6 +97,65 @@ def test_istft_matches_reference(n_fft, hop, frames, center, normalized, length)
                                        normalized, True, length) is not None
 
 
+# two-sided spectra (n_fft bins, not Hermitian): each frame is the real part of its inverse
+# transform (trnfft/api.py:397-421 with onesided=False); power-of-two n_fft on the fused kernel
+TWO_SIDED_CASES = [
+    # lead, n_fft, hop, frames, center, normalized, length
+    ((3,), 512, 128, 100, True, False, None),
+    ((64,), 512, 256, 626, True, False, None),    # C2's frame count
+    ((2,), 256, 64, 37, True, True, None),
+    ((2,), 1024, 256, 9, True, False, 1500),      # truncation
+    ((2,), 256, 64, 12, True, False, 2000),       # zero fill
+    ((2,), 128, 96, 20, False, False, None),      # hop not dividing n_fft
+    ((2,), 64, 80, 15, False, False, None),       # hop > n_fft: gaps
+    ((2,), 16, 4, 50, True, False, None),
+    ((1,), 4096, 1024, 7, True, False, None),
+    ((2,), 2048, 512, 5, False, True, None),
+    ((2,), 512, 40, 30, True, False, None),       # long halo: the widest tile
+    ((2, 2), 64, 32, 40, True, False, None),      # leading dims
+    ((2,), 512, 126, 60, True, False, 5001),      # one-sample path
+]
+
+
+@pytest.mark.parametrize("lead,n_fft,hop,frames,center,normalized,length", TWO_SIDED_CASES)
+def test_istft_two_sided_matches_reference(lead, n_fft, hop, frames, center, normalized, length):
+    g = torch.Generator().manual_seed(n_fft + hop + frames)
+    re, im = torch.randn(*lead, n_fft, frames, generator=g), torch.randn(*lead, n_fft, frames, generator=g)
+    spec = ComplexTensor(re.cuda(), im.cuda())
+    got = trnfft_amd.istft(spec, n_fft, hop_length=hop, center=center, normalized=normalized, onesided=False,
+                           length=length)
+    ref = oracle.istft((re, im), n_fft, hop_length=hop, center=center, normalized=normalized, onesided=False,
+                       length=length)
+    assert got.shape == ref.shape
+    assert _rel(got, ref) <= 1e-6 * math.log2(n_fft) * 4
+    assert trnfft_amd.api._istft_fused(spec, n_fft, hop, n_fft, None, center, normalized, False, length) is not None
+    # frames-major input (transposed views of (..., frames, n_fft) buffers): the same samples
+    fm = trnfft_amd.istft(ComplexTensor._wrap(re.transpose(-2, -1).contiguous().cuda().transpose(-2, -1),
+                                              im.transpose(-2, -1).contiguous().cuda().transpose(-2, -1)),
+                          n_fft, hop_length=hop, center=center, normalized=normalized, onesided=False, length=length)
+    assert _rel(got, fm) <= 1e-6 * math.log2(n_fft)
+
+
+def test_stft_istft_two_sided_roundtrip():
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(4, 20000, generator=g).cuda()
+    spec = trnfft_amd.stft(x, n_fft=512, hop_length=128, onesided=False)
+    assert spec.real.shape[-2] == 512
+    y = trnfft_amd.istft(spec, n_fft=512, hop_length=128, onesided=False, length=20000)
+    assert _rel(y, x) <= 1e-5
+
+
+def test_istft_two_sided_non_pow2_composes():
+    # two-sided spectra at an n_fft that is not a power of two keep the composed path
+    g = torch.Generator().manual_seed(10)
+    re, im = torch.randn(2, 400, 30, generator=g), torch.randn(2, 400, 30, generator=g)
+    spec = ComplexTensor(re.cuda(), im.cuda())
+    assert trnfft_amd.api._istft_fused(spec, 400, 160, 400, None, True, False, False, None) is None
+    got = trnfft_amd.istft(spec, 400, hop_length=160, onesided=False)
+    ref = oracle.istft((re, im), 400, hop_length=160, onesided=False)
+    assert _rel(got, ref) <= 1e-4
+
+
 def test_istft_window_with_zeros_uses_raw_sum():
     # a symmetric Hann (zero at both ends) without centring: the envelope is zero at the first
     # sample, where the reference returns the raw (unwindowed) overlap-add

@@ -448,15 +448,18 @@ def _istft_fused(spec, n_fft, hop, win_length, window, center, normalized, onesi
     re, im = spec.real, spec.imag
     # power-of-two n_fft in [16, 4096] (two frames per inverse transform), other n_fft in
     # [9, 2048] (one inverse Bluestein chain per frame)
+    # (two-sided spectra: power-of-two n_fft only, the real part of each frame's transform)
     pow2 = n_fft & (n_fft - 1) == 0
-    if (not onesided or (pow2 and not 16 <= n_fft <= 4096) or (not pow2 and not 9 <= n_fft <= 2048)
-            or re.dim() < 2 or re.shape[-2] != n_fft // 2 + 1 or re.shape[-1] < 1 or _ag._grad_on(re, im, window)):
+    bins = n_fft // 2 + 1 if onesided else n_fft
+    if ((not onesided and not pow2) or (pow2 and not 16 <= n_fft <= 4096) or (not pow2 and not 9 <= n_fft <= 2048)
+            or re.dim() < 2 or re.shape[-2] != bins or re.shape[-1] < 1 or _ag._grad_on(re, im, window)):
         return None
     _resolve(None)
     _require_hip("istft")
     dev = target_device(re, im)
     out_dev = re.device
-    flags = _lib.STFT_ONESIDED | (_lib.STFT_CENTER if center else 0) | (_lib.STFT_NORMALIZED if normalized else 0)
+    flags = ((_lib.STFT_ONESIDED if onesided else 0) | (_lib.STFT_CENTER if center else 0)
+             | (_lib.STFT_NORMALIZED if normalized else 0))
     re = to_device_f32(re, dev)
     im = to_device_f32(im, dev)
     frames = re.shape[-1]

@@ -268,7 +268,7 @@ struct RealArgs {
 hipError_t launch_real(int n, const RealArgs& a);
 
 struct IstftArgs {
-  const float* spec_re;  // (batch, n_fft/2+1, n_frames)
+  const float* spec_re;  // (batch, bins, n_frames), bins = n_fft/2+1 (n_fft when two_sided)
   const float* spec_im;
   const float* window;   // n_fft
   float* out;            // (batch, out_pitch)
@@ -288,8 +288,11 @@ struct IstftArgs {
   // hop, start, out_pitch and write_len multiples of 4 and out 16-byte aligned: interior tiles
   // write four consecutive samples per thread (host-checked)
   bool vec4 = false;
-  // input planes (batch, n_frames, n_fft/2+1) instead of (batch, n_fft/2+1, n_frames)
+  // input planes (batch, n_frames, bins) instead of (batch, bins, n_frames)
   bool frames_major = false;
+  // two-sided spectra (bins = n_fft, power-of-two n_fft, not with `adjoint`): each frame is the
+  // real part of its inverse transform; otherwise onesided (bins = n_fft/2 + 1)
+  bool two_sided = false;
   // n_fft that is not a power of two (one inverse Bluestein chain per frame, length m): forward
   // and inverse m-point tables, the inverse chirp (n_fft) and its filter spectrum H/m (m)
   const float2* blue_tw_f = nullptr;
@@ -299,7 +302,7 @@ struct IstftArgs {
   int m = 0;
 };
 hipError_t launch_istft(int n_fft, const IstftArgs& a);
-int istft_frames_per_tile(int n_fft);
+int istft_frames_per_tile(int n_fft, bool two_sided = false);
 hipError_t launch_istft_blue(int n_fft, const IstftArgs& a);  // a.m != 0
 
 struct Fft2Args {

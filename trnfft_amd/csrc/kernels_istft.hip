@@ -5,12 +5,14 @@
 // complex inverse per frame, keeps the real part, and then overlap-adds with index_add into an
 // output, a raw (unwindowed) sum and a window-square envelope before dividing where the envelope
 // exceeds 1e-8 (raw sum elsewhere).  Here one workgroup owns a run of output samples:
-//   1. the onesided bins of FR consecutive frames are staged into LDS (lanes over frames: each
-//      load instruction reads consecutive frames of one bin row of the (batch, bins, frames)
-//      input, the layout the forward STFT writes);
+//   1. the bins of FR consecutive frames are staged into LDS (lanes over frames: each load
+//      instruction reads consecutive frames of one bin row of the (batch, bins, frames) input,
+//      the layout the forward STFT writes; or consecutive bins of the (batch, frames, bins) one);
 //   2. two real frames share one complex inverse transform: Z = X_a + i X_b with X_a, X_b the
-//      Hermitian completions (imaginary parts of bins 0 and n/2 dropped, as the reference's real
-//      part drops them), so IFFT(Z) = x_a + i x_b;
+//      Hermitian completions of onesided spectra (imaginary parts of bins 0 and n/2 dropped, as
+//      the reference's real part drops them), or the Hermitian parts (X[k] + conj X[n-k]) / 2 of
+//      two-sided ones (the reference keeps the real part of each frame's inverse transform), so
+//      IFFT(Z) = x_a + i x_b;
 //   3. every output sample the workgroup owns gathers its covering frames from LDS: the windowed
 //      sum, the raw sum and the envelope, then the normalised sample is written once.
 // A sample is covered by frames t with t*hop <= s < t*hop + n, so a workgroup that owns the
@@ -27,12 +29,14 @@ namespace tfa {
 
 // MAXP caps the frame pairs per workgroup (istft_threads(NFFT) / T in the measured shape; more
 // frames per workgroup cost LDS and resident workgroups without shortening the gather).
-template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = istft_threads(NFFT) / (NFFT / E_)>
+// TS: two-sided spectra (n_fft bins per frame), whose pair regions hold 4 n_fft staged floats.
+template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = istft_threads(NFFT) / (NFFT / E_), bool TS = false>
 struct IstftCfg {
   static constexpr int E = E_;
   static constexpr int T = NFFT / E;
-  static constexpr int F = NFFT / 2 + 1;                    // onesided bins
-  static constexpr int RP = 2 * lds_pad(NFFT) + 4;          // floats per pair region (>= 4F, >= 2n, even)
+  static constexpr int F = TS ? NFFT : NFFT / 2 + 1;        // bins per frame
+  // floats per pair region (>= 4F staged bins, >= 2n exchange and frames; a multiple of 4)
+  static constexpr int RP = TS ? 4 * NFFT + 4 : 2 * lds_pad(NFFT) + 4;
   static constexpr int PAIRS_T = 1024 / T < MAXP ? 1024 / T : MAXP;
   static constexpr int PAIRS_L = (kLdsBytes - NFFT * 4) / (RP * 4);
   static constexpr int PAIRS = PAIRS_T < PAIRS_L ? PAIRS_T : PAIRS_L;
@@ -42,13 +46,14 @@ struct IstftCfg {
 };
 
 template <int NFFT, int E_ = istft_epth(NFFT), int MAXP = istft_threads(NFFT) / (NFFT / E_), bool ADJ = false,
-          bool FM = false>
-__global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_kernel(
+          bool FM = false, bool TS = false>
+__global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP, TS>::THREADS)) void istft_kernel(
     const float* __restrict__ sre, const float* __restrict__ sim, const float* __restrict__ win,
     float* __restrict__ out, const float2* __restrict__ tw, int n_frames, int hop, int halo, int owned,
     int tiles_per_signal, long long expected_len, long long start, long long write_len, long long out_pitch,
     float scale, int vec4) {
-  using C = IstftCfg<NFFT, E_, MAXP>;
+  using C = IstftCfg<NFFT, E_, MAXP, TS>;
+  static_assert(!(ADJ && TS), "the adjoint is of the onesided forward transform");
   constexpr int E = C::E, T = C::T, F = C::F, RP = C::RP, FR = C::FR, THREADS = C::THREADS;
   constexpr bool WL = T <= 64;
   // RP is a multiple of 4: every pair region and frame row is 16-byte aligned
@@ -156,7 +161,15 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int k = tid + T * e;
-    if (k <= NFFT / 2) {  // Z = X_a + i X_b
+    if constexpr (TS) {
+      // two-sided: a frame is Re(IFFT(X)) = IFFT(H) with H[k] = (X[k] + conj X[n-k]) / 2, its
+      // Hermitian part, so two frames still share one transform: Z = H_a + i H_b (the halving is
+      // folded into the scale)
+      const int q = (NFFT - k) & (NFFT - 1);
+      const float har = reg[k] + reg[q], hai = reg[F + k] - reg[F + q];
+      const float hbr = reg[2 * F + k] + reg[2 * F + q], hbi = reg[3 * F + k] - reg[3 * F + q];
+      v[e] = make_float2((har - hbi) * (0.5f * scale), (hai + hbr) * (0.5f * scale));
+    } else if (k <= NFFT / 2) {  // Z = X_a + i X_b
       float ra = reg[k], ia = reg[F + k], rb = reg[2 * F + k], ib = reg[3 * F + k];
       if ((e == 0 || e == E / 2) && tid == 0) {
         // bins 0 and n/2 (k = 0 and T * E / 2): their imaginary parts are dropped; the adjoint
@@ -299,9 +312,9 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP>::THREADS)) void istft_ker
     for (int o = write_len + (int)threadIdx.x; o < out_pitch; o += THREADS) dst[o] = 0.0f;
 }
 
-template <int NFFT, int MAXP>
+template <int NFFT, int MAXP, bool TS>
 static hipError_t launch_istft_cfg(const IstftArgs& a) {
-  using C = IstftCfg<NFFT, istft_epth(NFFT), MAXP>;
+  using C = IstftCfg<NFFT, istft_epth(NFFT), MAXP, TS>;
   const int owned = C::FR - a.halo;
   if (owned < 1) return hipErrorInvalidValue;
   const int tiles = (a.n_frames + owned - 1) / owned;
@@ -313,7 +326,11 @@ static hipError_t launch_istft_cfg(const IstftArgs& a) {
                        (int)a.write_len, (int)a.out_pitch, a.scale, (int)a.vec4);
   };
   constexpr int E = istft_epth(NFFT);
-  if (a.adjoint) {
+  if constexpr (TS) {
+    if (a.adjoint) return hipErrorInvalidValue;  // the adjoint is of the onesided forward transform
+    if (a.frames_major) go(istft_kernel<NFFT, E, MAXP, false, true, true>);
+    else go(istft_kernel<NFFT, E, MAXP, false, false, true>);
+  } else if (a.adjoint) {
     if (a.frames_major) go(istft_kernel<NFFT, E, MAXP, true, true>);
     else go(istft_kernel<NFFT, E, MAXP, true, false>);
   } else {
@@ -325,31 +342,37 @@ static hipError_t launch_istft_cfg(const IstftArgs& a) {
 
 // The measured shape, unless the hop is so short that the recomputed halo frames would be half
 // its tile or more: then the widest tile (1024 threads, as LDS allows), same elements per thread.
-template <int NFFT>
-static hipError_t launch_istft_n(const IstftArgs& a) {
+template <int NFFT, bool TS>
+static hipError_t launch_istft_ts(const IstftArgs& a) {
   constexpr int T = NFFT / istft_epth(NFFT);
   constexpr int FAST = istft_threads(NFFT) / T, WIDE = 1024 / T;
-  if (2 * a.halo <= IstftCfg<NFFT, istft_epth(NFFT), FAST>::FR) return launch_istft_cfg<NFFT, FAST>(a);
-  return launch_istft_cfg<NFFT, WIDE>(a);
+  if (2 * a.halo <= IstftCfg<NFFT, istft_epth(NFFT), FAST, TS>::FR) return launch_istft_cfg<NFFT, FAST, TS>(a);
+  return launch_istft_cfg<NFFT, WIDE, TS>(a);
+}
+
+template <int NFFT>
+static hipError_t launch_istft_n(const IstftArgs& a) {
+  return a.two_sided ? launch_istft_ts<NFFT, true>(a) : launch_istft_ts<NFFT, false>(a);
 }
 
 // frames per tile of the widest shape: the hop bound the plan checks
 template <int NFFT>
-constexpr int istft_wide_fr() {
-  return IstftCfg<NFFT, istft_epth(NFFT), 1024 / (NFFT / istft_epth(NFFT))>::FR;
+constexpr int istft_wide_fr(bool two_sided) {
+  constexpr int W = 1024 / (NFFT / istft_epth(NFFT));
+  return two_sided ? IstftCfg<NFFT, istft_epth(NFFT), W, true>::FR : IstftCfg<NFFT, istft_epth(NFFT), W>::FR;
 }
 
-int istft_frames_per_tile(int n_fft) {
+int istft_frames_per_tile(int n_fft, bool two_sided) {
   switch (n_fft) {
-    case 16: return istft_wide_fr<16>();
-    case 32: return istft_wide_fr<32>();
-    case 64: return istft_wide_fr<64>();
-    case 128: return istft_wide_fr<128>();
-    case 256: return istft_wide_fr<256>();
-    case 512: return istft_wide_fr<512>();
-    case 1024: return istft_wide_fr<1024>();
-    case 2048: return istft_wide_fr<2048>();
-    case 4096: return istft_wide_fr<4096>();
+    case 16: return istft_wide_fr<16>(two_sided);
+    case 32: return istft_wide_fr<32>(two_sided);
+    case 64: return istft_wide_fr<64>(two_sided);
+    case 128: return istft_wide_fr<128>(two_sided);
+    case 256: return istft_wide_fr<256>(two_sided);
+    case 512: return istft_wide_fr<512>(two_sided);
+    case 1024: return istft_wide_fr<1024>(two_sided);
+    case 2048: return istft_wide_fr<2048>(two_sided);
+    case 4096: return istft_wide_fr<4096>(two_sided);
     default: return 0;
   }
 }

@@ -540,7 +540,7 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         }
         if (desc->inverse) {
           if (!(desc->flags & TFA_STFT_ONESIDED)) {
-            rc = fail(TFA_ERR_UNSUPPORTED, "fused inverse STFT takes onesided spectra");
+            rc = fail(TFA_ERR_UNSUPPORTED, "fused inverse STFT at an n_fft that is not a power of two takes onesided spectra");
             break;
           }
           // a halo of more than half the tile recomputes more frames than it owns: the composed
@@ -570,12 +570,9 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         break;
       }
       if (desc->inverse) {
-        // inverse STFT: inverse table in the pair-transform layout of the istft kernel
-        if (!(desc->flags & TFA_STFT_ONESIDED)) {
-          rc = fail(TFA_ERR_UNSUPPORTED, "fused inverse STFT takes onesided spectra");
-          break;
-        }
-        if ((n - 1) / desc->hop >= tfa::istft_frames_per_tile((int)n)) {
+        // inverse STFT (onesided spectra, or two-sided ones: the real part of each frame's inverse
+        // transform): inverse table in the pair-transform layout of the istft kernel
+        if ((n - 1) / desc->hop >= tfa::istft_frames_per_tile((int)n, !(desc->flags & TFA_STFT_ONESIDED))) {
           rc = fail(TFA_ERR_UNSUPPORTED, "hop_length too small for the fused inverse STFT tile");
           break;
         }
@@ -958,9 +955,10 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
   int rc = tfa_istft_length(plan, n_frames, length, &out_len);
   if (rc) return rc;
   const int64_t n_fft = plan->d.n, hop = plan->d.hop;
+  const bool two_sided = !(plan->d.flags & TFA_STFT_ONESIDED);
   const int64_t expected = n_fft + (n_frames - 1) * hop;
   if (expected > INT32_MAX / 2 || n_frames > INT32_MAX / 2 || out_len > INT32_MAX / 2 ||
-      (n_fft / 2 + 1) * n_frames > INT32_MAX)
+      (two_sided ? n_fft : n_fft / 2 + 1) * n_frames > INT32_MAX)
     return fail(TFA_ERR_UNSUPPORTED, "signal too long");
   const int64_t start = (plan->d.flags & TFA_STFT_CENTER) ? n_fft / 2 : 0;
   int64_t cur = expected - start;
@@ -971,6 +969,7 @@ int tfa_istft_execute(const tfa_plan* plan, int64_t batch, int64_t n_frames, con
                    static_cast<hipStream_t>(stream)};
   a.vec4 = vec4_ok(a, out);
   a.frames_major = (plan->d.flags & TFA_STFT_FRAMES_MAJOR) != 0;
+  a.two_sided = two_sided;
   hipError_t e;
   if (!is_pow2(n_fft)) {
     a.blue_tw_f = plan->fwd.tw;
