@@ -450,6 +450,65 @@ def test_istft_gradient_flows():
     assert rel_l2(sr.grad, si.grad, r_r.grad, r_i.grad) <= 1e-4
 
 
+ISTFT_GRAD_CASES = [
+    # lead, n_fft, hop, frames, center, normalized, onesided, length
+    ((2,), 256, 64, 40, True, False, True, 3000),
+    ((2,), 512, 128, 30, False, False, True, None),   # no centring: env[0] = 0, the raw-sum branch
+    ((2, 2), 512, 256, 25, True, True, True, None),   # normalized, leading dims
+    ((2,), 256, 64, 40, True, False, False, 3000),    # two-sided spectra
+    ((1,), 1024, 256, 12, True, False, True, 5000),   # zero fill past the signal
+    ((3,), 64, 16, 50, False, True, False, None),     # two-sided, no centring
+]
+
+
+@pytest.mark.parametrize("lead,n_fft,hop,frames,center,normalized,onesided,length", ISTFT_GRAD_CASES)
+def test_istft_gradient_fused_path(lead, n_fft, hop, frames, center, normalized, onesided, length):
+    # power-of-two n_fft: the fused kernel forward, the spectra gradient as the fused forward STFT of
+    # the envelope-divided gradient; against autograd through the oracle's float64 restatement
+    bins = n_fft // 2 + 1 if onesided else n_fft
+    g = torch.Generator().manual_seed(n_fft + hop + frames)
+    re, im = torch.randn(*lead, bins, frames, generator=g), torch.randn(*lead, bins, frames, generator=g)
+    sr, si = _leaf(re), _leaf(im)
+    y = trnfft_amd.istft(ComplexTensor(sr, si), n_fft, hop_length=hop, center=center, normalized=normalized,
+                         onesided=onesided, length=length)
+    assert type(y.grad_fn).__name__ == "_IstftFnBackward"
+    c, _ = _cotangent(tuple(y.shape), 5)
+    (y * c.float().cuda()).sum().backward()
+    r_r, r_i = re.double().requires_grad_(True), im.double().requires_grad_(True)
+    z = oracle.istft((r_r, r_i), n_fft, hop_length=hop, window=torch.hann_window(n_fft, dtype=torch.float64),
+                     center=center, normalized=normalized, onesided=onesided, length=length)
+    assert tuple(z.shape) == tuple(y.shape)
+    (z * c).sum().backward()
+    # the inverse STFT's own parity bound: the gradient divides by the window envelope, which at
+    # the first kept samples without centring is ~1e-8 (Hann tails), so edge frames carry values
+    # ~1e4 larger than their neighbours, and the STFT pairs two frames per complex transform
+    tol = 4e-6 * math.log2(n_fft)
+    assert rel_l2(sr.grad, si.grad, r_r.grad, r_i.grad) <= tol
+    # frames-major input (transposed views): the same gradient, in the input's shape
+    fr, fi = (_leaf(t.transpose(-2, -1).contiguous()) for t in (re, im))
+    y2 = trnfft_amd.istft(ComplexTensor._wrap(fr.transpose(-2, -1), fi.transpose(-2, -1)), n_fft, hop_length=hop,
+                          center=center, normalized=normalized, onesided=onesided, length=length)
+    (y2 * c.float().cuda()).sum().backward()
+    assert rel_l2(fr.grad.transpose(-2, -1), fi.grad.transpose(-2, -1), r_r.grad, r_i.grad) <= tol
+
+
+def test_istft_window_gradient_composes():
+    # a window that needs a gradient keeps the composed path (its gradient included)
+    g = torch.Generator().manual_seed(41)
+    re, im = torch.randn(2, 129, 30, generator=g), torch.randn(2, 129, 30, generator=g)
+    w = torch.hann_window(256) + 0.1
+    sr, si, aw = _leaf(re), _leaf(im), _leaf(w)
+    y = trnfft_amd.istft(ComplexTensor(sr, si), 256, hop_length=64, window=aw)
+    assert type(y.grad_fn).__name__ != "_IstftFnBackward"
+    c, _ = _cotangent(tuple(y.shape), 6)
+    (y * c.float().cuda()).sum().backward()
+    r_r, r_i, rw = re.double().requires_grad_(True), im.double().requires_grad_(True), w.double().requires_grad_(True)
+    z = oracle.istft((r_r, r_i), 256, hop_length=64, window=rw)
+    (z * c).sum().backward()
+    assert rel_l2(sr.grad, si.grad, r_r.grad, r_i.grad) <= TOL
+    assert _rel(aw.grad, rw.grad) <= TOL
+
+
 def test_reference_named_autograd_entry_points():
     # the names trnfft's NKI autograd module exposes (trnfft/nki/autograd.py:115-116, 158-159,
     # 204-205), here on the HIP kernels: values and gradients against fp64 torch

@@ -225,3 +225,22 @@ def test_complex_matmul_second_derivative(sa, sb):
 
     got, want = _pair(ours, ref, [ar, ai, br, bi], [tuple(out)] * 2, 37)
     assert _rel_all(got, want) <= TOL
+
+
+@pytest.mark.parametrize("n_fft,hop,center,onesided", [(256, 64, True, True), (128, 32, False, False)])
+def test_istft_second_derivative(n_fft, hop, center, onesided):
+    # the fused path's spectra gradient (a forward STFT) recorded under create_graph
+    bins = n_fft // 2 + 1 if onesided else n_fft
+    sr, si = _rand((2, bins, 30), 40), _rand((2, bins, 30), 41)
+
+    def ours(r, i):
+        return (trnfft_amd.istft(ComplexTensor(r, i), n_fft, hop_length=hop, center=center, onesided=onesided),)
+
+    def ref(r, i):
+        return (oracle.istft((r, i), n_fft, hop_length=hop, window=torch.hann_window(n_fft, dtype=torch.float64),
+                             center=center, onesided=onesided),)
+
+    length = (30 - 1) * hop + (0 if center else n_fft)
+    got, want = _pair(ours, ref, [sr, si], [(2, length)], 42)
+    assert _rel_all(got, want) <= TOL
+

@@ -376,11 +376,13 @@ def istft(
 ) -> torch.Tensor:
     """Inverse STFT by overlap-add with window-sum normalisation (trnfft/api.py:368-470).
 
-    Onesided spectra run as one fused kernel (completion, inverse transform -- two frames per
-    transform for power-of-two n_fft in [16, 4096], one inverse Bluestein chain per frame for other
-    n_fft in [9, 2048] -- window, overlap-add, envelope division, trim); when gradients are
-    needed, for two-sided input, other n_fft or hops too short for the kernel's frame tile, the
-    same steps run as a composition of the differentiable kernels.
+    One fused kernel (completion, inverse transform -- two frames per transform for power-of-two
+    n_fft in [16, 4096], onesided or two-sided spectra; one inverse Bluestein chain per frame for
+    other n_fft in [9, 2048], onesided -- window, overlap-add, envelope division, trim), whose
+    spectra gradient at power-of-two n_fft is the fused forward STFT of the envelope-divided
+    gradient; for window gradients, gradients at other n_fft, two-sided spectra at other n_fft or
+    hops too short for the kernel's frame tile, the same steps run as a composition of the
+    differentiable kernels.
     """
     if hop_length is None:
         hop_length = n_fft // 4
@@ -440,50 +442,35 @@ def istft(
 
 
 def _istft_fused(spec, n_fft, hop, win_length, window, center, normalized, onesided, length):
-    """The fused inverse-STFT kernel, or None when its preconditions do not hold."""
-    from . import _lib
-    from .dispatch import ptr, stream_handle
-    from .plan import native_plan
+    """The fused inverse-STFT kernel (differentiable in the spectra at power-of-two n_fft), or None
+    when its preconditions do not hold."""
+    from .dispatch import to_device_f32_strided
 
     re, im = spec.real, spec.imag
-    # power-of-two n_fft in [16, 4096] (two frames per inverse transform), other n_fft in
-    # [9, 2048] (one inverse Bluestein chain per frame)
-    # (two-sided spectra: power-of-two n_fft only, the real part of each frame's transform)
+    # power-of-two n_fft in [16, 4096] (two frames per inverse transform; onesided or two-sided
+    # spectra), other n_fft in [9, 2048] (one inverse Bluestein chain per frame, onesided)
     pow2 = n_fft & (n_fft - 1) == 0
     bins = n_fft // 2 + 1 if onesided else n_fft
     if ((not onesided and not pow2) or (pow2 and not 16 <= n_fft <= 4096) or (not pow2 and not 9 <= n_fft <= 2048)
-            or re.dim() < 2 or re.shape[-2] != bins or re.shape[-1] < 1 or _ag._grad_on(re, im, window)):
+            or re.dim() < 2 or re.shape[-2] != bins or re.shape[-1] < 1):
+        return None
+    # a window that needs a gradient, and gradients through the Bluestein chains, take the composition
+    if _ag._grad_on(window) or (_ag._grad_on(re, im) and not pow2):
         return None
     _resolve(None)
     _require_hip("istft")
     dev = target_device(re, im)
     out_dev = re.device
-    flags = ((_lib.STFT_ONESIDED if onesided else 0) | (_lib.STFT_CENTER if center else 0)
-             | (_lib.STFT_NORMALIZED if normalized else 0))
-    re = to_device_f32(re, dev)
-    im = to_device_f32(im, dev)
-    frames = re.shape[-1]
-    lead = re.shape[:-2]
-    batch = re.numel() // (re.shape[-2] * frames)
-    # either memory order of the (..., bins, frames) planes, without a copy where possible
-    re, im, fm = _fc.stft_planes(re.reshape(batch, re.shape[-2], frames), im.reshape(batch, im.shape[-2], frames))
-    if fm:
-        flags |= _lib.STFT_FRAMES_MAJOR
-    try:
-        plan = native_plan(_lib.KIND_STFT, n_fft, True, dev.index, hop=hop, flags=flags)
-    except NotImplementedError:
-        return None  # hop too small for the kernel's frame tile
+    # either memory order of the (..., bins, frames) planes is taken without a copy
+    re = to_device_f32_strided(re, dev)
+    im = to_device_f32_strided(im, dev)
     win = _effective_window(window.to(dev) if window is not None else None, n_fft, win_length, torch.float32, dev)
     win = to_device_f32(win, dev)
-    out_len = ctypes.c_int64()
-    lib = _lib.lib()
-    req = -1 if length is None else int(length)
-    _lib.check(lib.tfa_istft_length(plan.handle, frames, req, ctypes.byref(out_len)), "tfa_istft_length")
-    out = torch.empty(*lead, out_len.value, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
-        rc = lib.tfa_istft_execute(plan.handle, batch, frames, ptr(re), ptr(im), ptr(win), ptr(out), req,
-                                   stream_handle(dev))
-    _lib.check(rc, "tfa_istft_execute")
+    try:
+        out = _ag.istft(re, im, win, n_fft, hop, center, normalized, onesided, length,
+                        win_length if window is None else None)
+    except NotImplementedError:
+        return None  # hop too small for the kernel's frame tile
     return out if out_dev == dev else out.to(out_dev)
 
 

@@ -32,6 +32,8 @@ gradient can be differentiated again; an ordinary backward keeps the direct kern
 
 from __future__ import annotations
 
+import collections
+import functools
 import math
 
 import torch
@@ -325,6 +327,140 @@ def stft(x, win, n_fft, hop, center, normalized, onesided, num_frames, frames_ma
     else:
         y_re, y_im = _fc.execute_stft(x, win, n_fft, hop, center, normalized, onesided, num_frames, frames_major)
     return ComplexTensor._wrap(y_re, y_im)
+
+
+# ---------------------------------------------------------------------------------------------
+# inverse STFT (power-of-two n_fft, fused kernel forward)
+# ---------------------------------------------------------------------------------------------
+
+
+@functools.lru_cache(maxsize=8)
+def _default_window_envelope(n_fft: int, win_length: int, hop: int, frames: int) -> torch.Tensor:
+    """Window-square envelope (fp32, host) of the default window (periodic Hann of win_length,
+    centred in n_fft) over `frames` frames: it depends on the shape only, so the gradient of a
+    call with the default window reads it (and its raw-sum test) without building it on the
+    device or synchronising with it."""
+    w = torch.zeros(n_fft, dtype=torch.float32)
+    off = (n_fft - win_length) // 2
+    w[off:off + win_length] = torch.hann_window(win_length, dtype=torch.float32)
+    pos = (torch.arange(frames).unsqueeze(1) * hop + torch.arange(n_fft)).reshape(-1)
+    return torch.zeros(n_fft + (frames - 1) * hop, dtype=torch.float32).index_add_(0, pos, (w * w).repeat(frames))
+
+
+_default_inv_env: "collections.OrderedDict" = collections.OrderedDict()  # key -> device 1/env (0 where env <= 1e-8)
+_DEFAULT_INV_ENV_KEEP = 8
+
+
+def _default_window_inv_env(n_fft, win_length, hop, frames, dev):
+    key = (n_fft, win_length, hop, frames, str(dev))
+    inv = _default_inv_env.get(key)
+    if inv is None:
+        env = _default_window_envelope(n_fft, win_length, hop, frames)
+        inv = torch.where(env > 1e-8, 1.0 / env.clamp_min(1e-30), torch.zeros_like(env)).to(dev)
+        _default_inv_env[key] = inv
+        while len(_default_inv_env) > _DEFAULT_INV_ENV_KEEP:
+            _default_inv_env.popitem(last=False)
+    else:
+        _default_inv_env.move_to_end(key)
+    return inv
+
+
+def _pad_product(g2, scale, start, total, rec):
+    """(rows, total) = zero-padded g2 * scale, g2 (rows, m) placed at column start: one product
+    written into the padded buffer (only the pads are cleared); F.pad when recording a graph."""
+    m = g2.shape[-1]
+    if rec:
+        return F.pad(g2 * scale, (start, total - start - m))
+    out = torch.empty(g2.shape[0], total, dtype=g2.dtype, device=g2.device)
+    out[:, :start].zero_()
+    out[:, start + m:].zero_()
+    torch.mul(g2, scale, out=out[:, start:start + m])
+    return out
+
+
+def _istft_adjoint(g, win, n_fft, hop, center, normalized, onesided, frames, length, default_win):
+    """Gradient of the inverse STFT (trnfft/api.py:368-470) with respect to its spectra.  The
+    forward keeps samples [start, start + m) of y[s] = sum_t f_t(s - t hop) w(s - t hop) / env[s]
+    (the raw sum of the frames where env[s] <= 1e-8), f_t the real frames of the spectra X_t.  So
+    the frame gradient is w[j] u1[t hop + j] + u2[t hop + j] with u1 = g / env (env > 1e-8) and
+    u2 = g (elsewhere), g zero-padded back to the untrimmed length: a windowed frame gather and a
+    forward transform, i.e. the STFT without centring, then the adjoint of the frames' completion
+    -- onesided (c2r): r2c / n with bins 1..n/2-1 doubled and no imaginary gradient at 0 and n/2;
+    two-sided (real part of the inverse c2c): the full forward transform / n -- and sqrt(n) when
+    normalized.  The interior factor is folded into the transform's window, the edge bins fixed
+    after it.  Built from the differentiable stft under grad mode (create_graph).
+    default_win: (win_length) of the default window, whose raw-sum test runs on the host."""
+    rec = torch.is_grad_enabled()
+    dev = g.device
+    lead = g.shape[:-1]
+    out_len = g.shape[-1]
+    expected = n_fft + (frames - 1) * hop
+    start = n_fft // 2 if center else 0
+    cur = expected - start
+    if start and cur > start and length is None:
+        cur -= start
+    m = min(cur, out_len)
+    if default_win is not None:
+        inv = _default_window_inv_env(n_fft, default_win, hop, frames, dev)
+        env_h = _default_window_envelope(n_fft, default_win, hop, frames)
+        raw_kept = bool((env_h[start:start + m] <= 1e-8).any())
+        mask = inv > 0 if raw_kept else None
+    else:
+        pos = (torch.arange(frames, device=dev).unsqueeze(1) * hop + torch.arange(n_fft, device=dev)).reshape(-1)
+        env = torch.zeros(expected, dtype=torch.float32, device=dev).index_add(0, pos, (win**2).repeat(frames))
+        mask = env > 1e-8
+        inv = torch.where(mask, 1.0 / torch.where(mask, env, torch.ones_like(env)), torch.zeros_like(env))
+        raw_kept = bool((~mask[start:start + m]).any())  # (one device synchronisation)
+    g2 = g.reshape(-1, out_len)[:, :m]
+    u1 = _pad_product(g2, inv[start:start + m], start, expected, rec)  # the trim's adjoint, / env
+    sc = (math.sqrt(n_fft) if normalized else 1.0) / n_fft
+    f = 2.0 * sc if onesided else sc  # the interior bins' factor, on the window
+    stft_fn = stft if rec else (lambda *a: ComplexTensor._wrap(*_fc.execute_stft(*a)))
+    spec = stft_fn(u1, win * f, n_fft, hop, False, False, onesided, frames)
+    s_re, s_im = spec.real, spec.imag
+    if raw_kept:  # the raw-sum samples inside the kept range: the same transform, window of ones
+        u2 = _pad_product(g2, (~mask[start:start + m]).to(g2.dtype), start, expected, rec)
+        raw = stft_fn(u2, torch.full_like(win, f), n_fft, hop, False, False, onesided, frames)
+        s_re, s_im = s_re + raw.real, s_im + raw.imag
+    if onesided:  # bins 0 and n/2 count once (real part) and carry no imaginary gradient
+        h = n_fft // 2
+        if rec:
+            wr = _bin_weights(s_re.transpose(-2, -1), n_fft, 1.0, 0.5).unsqueeze(-1)
+            wi = _bin_weights(s_im.transpose(-2, -1), n_fft, 1.0, 0.0).unsqueeze(-1)
+            s_re, s_im = s_re * wr, s_im * wi
+        elif h:  # rows 0 and h in one strided op each
+            s_re[..., 0::h, :] *= 0.5
+            s_im[..., 0::h, :] = 0.0
+        else:
+            s_re *= 0.5
+            s_im.zero_()
+    bins = s_re.shape[-2]
+    return s_re.reshape(*lead, bins, frames), s_im.reshape(*lead, bins, frames)
+
+
+class _IstftFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, re, im, win, n_fft, hop, center, normalized, onesided, length, default_win):
+        ctx.save_for_backward(win)
+        ctx.cfg = (n_fft, hop, center, normalized, onesided, re.shape[-1], length, default_win)
+        return _fc.execute_istft(re, im, win, n_fft, hop, center, normalized, onesided, length)
+
+    @staticmethod
+    def backward(ctx, g):
+        (win,) = ctx.saved_tensors
+        n_fft, hop, center, normalized, onesided, frames, length, default_win = ctx.cfg
+        d_re, d_im = _istft_adjoint(g if torch.is_grad_enabled() else g.contiguous(), win, n_fft, hop, center,
+                                    normalized, onesided, frames, length, default_win)
+        return d_re, d_im, None, None, None, None, None, None, None, None
+
+
+def istft(re, im, win, n_fft, hop, center, normalized, onesided, length, default_win=None) -> torch.Tensor:
+    """Fused inverse-STFT kernel on device fp32 spectra and the effective window; differentiable in
+    the spectra (power-of-two n_fft; the window is taken as a constant).  default_win: the
+    win_length of the default (periodic Hann) window when no window was given, else None."""
+    if _grad_on(re, im):
+        return _IstftFn.apply(re, im, win, n_fft, hop, center, normalized, onesided, length, default_win)
+    return _fc.execute_istft(re, im, win, n_fft, hop, center, normalized, onesided, length)
 
 
 # ---------------------------------------------------------------------------------------------

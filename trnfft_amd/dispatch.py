@@ -123,6 +123,16 @@ def to_device_f32(t: torch.Tensor | None, dev: torch.device) -> torch.Tensor | N
     return t.to(dev, non_blocking=False).contiguous()
 
 
+def to_device_f32_strided(t: torch.Tensor | None, dev: torch.device) -> torch.Tensor | None:
+    """fp32 t on dev with its strides kept (no copy when it already is there): for inputs a kernel
+    takes in more than one memory order (the STFT spectra planes)."""
+    if t is None:
+        return None
+    if t.dtype != torch.float32:
+        raise TypeError(f"the HIP backend computes in fp32; got {t.dtype}")
+    return t.to(dev, non_blocking=False)
+
+
 def stream_handle(dev: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 

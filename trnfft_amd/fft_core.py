@@ -250,6 +250,35 @@ def execute_fft2_any(re: torch.Tensor, im: torch.Tensor | None, inverse: bool) -
     return execute_1d(y.real, y.imag, inverse)
 
 
+def execute_istft(re: torch.Tensor, im: torch.Tensor, win: torch.Tensor, n_fft: int, hop: int, center: bool,
+                  normalized: bool, onesided: bool, length: int | None) -> torch.Tensor:
+    """Fused inverse-STFT kernel on device fp32 spectra (..., bins, frames) in either memory order
+    and the effective window (n_fft): the (..., out_len) signal (replaces trnfft/api.py:368-470
+    after its argument handling).  Raises NotImplementedError where the plan refuses the shape
+    (a hop too short for the kernel's frame tile, two-sided spectra at other n_fft)."""
+    flags = ((_lib.STFT_ONESIDED if onesided else 0) | (_lib.STFT_CENTER if center else 0)
+             | (_lib.STFT_NORMALIZED if normalized else 0))
+    dev = re.device
+    frames = re.shape[-1]
+    lead = re.shape[:-2]
+    batch = re.numel() // (re.shape[-2] * frames)
+    re, im, fm = stft_planes(re.reshape(batch, re.shape[-2], frames), im.reshape(batch, im.shape[-2], frames))
+    if fm:
+        flags |= _lib.STFT_FRAMES_MAJOR
+    plan = native_plan(_lib.KIND_STFT, n_fft, True, dev.index, hop=hop, flags=flags)
+    win = win.contiguous()
+    out_len = ctypes.c_int64()
+    lib = _lib.lib()
+    req = -1 if length is None else int(length)
+    _lib.check(lib.tfa_istft_length(plan.handle, frames, req, ctypes.byref(out_len)), "tfa_istft_length")
+    out = torch.empty(*lead, out_len.value, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.tfa_istft_execute(plan.handle, batch, frames, ptr(re), ptr(im), ptr(win), ptr(out), req,
+                                   stream_handle(dev))
+    _lib.check(rc, "tfa_istft_execute")
+    return out
+
+
 def stft_planes(re: torch.Tensor, im: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, bool]:
     """(..., bins, frames) spectrum planes as contiguous buffers for the STFT kernels, without a
     copy where possible: the planes themselves when both are contiguous (the reference's layout,
