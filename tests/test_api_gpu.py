@@ -431,6 +431,33 @@ def test_fft2_real_input(shape):
         assert torch.equal(g[..., w // 2 + 1:], mirrored[..., w // 2 + 1:])
 
 
+# Real-input shapes whose pass 2 takes runs of column tiles with whole-line mirror stores (a
+# workgroup walks its tiles downwards, carrying each tile's first column into the next tile's mirror
+# line), chosen for the run layouts: 1 run per group of 3 tiles (40 x 256^2, 64-column tiles), 2 runs
+# of 4 + 5 tiles (16 x 1024^2), 4 runs of 4-5 of 17 tiles (8 x 2048 x 1024, 32-column tiles), 6
+# uneven runs of 33 tiles (6 x 2048^2), 7 runs of 65 tiles (5 x 2048 x 4096).  Against numpy's
+# float64 FFT (forward and inverse), and the mirrored half equal to the conjugate reflection of the
+# computed one bit for bit, at run boundaries too.
+@pytest.mark.parametrize("shape", [(40, 256, 256), (16, 1024, 1024), (8, 2048, 1024), (6, 2048, 2048),
+                                   (5, 2048, 4096)])
+def test_fft2_real_input_tile_runs(shape):
+    rng = np.random.default_rng(29)
+    x = torch.from_numpy(rng.standard_normal(shape).astype(np.float32))
+    n = shape[-1] * shape[-2]
+    ref = np.fft.fft2(x.double().numpy())
+    got = trnfft_amd.fft2(x.cuda())
+    assert rel_l2(got.real, got.imag, ref.real, ref.imag) <= tol_pow2(n), shape
+    g = torch.complex(got.real, got.imag).cpu()
+    del got
+    mirrored = torch.conj(torch.roll(torch.flip(g, dims=(-2, -1)), shifts=(1, 1), dims=(-2, -1))).resolve_conj()
+    w = shape[-1]
+    assert torch.equal(g[..., w // 2 + 1:], mirrored[..., w // 2 + 1:]), shape
+    del g, mirrored
+    inv = trnfft_amd.ifftn(x.cuda(), dim=(-2, -1))
+    ref_inv = np.fft.ifft2(x.double().numpy())
+    assert rel_l2(inv.real, inv.imag, ref_inv.real, ref_inv.imag) <= tol_pow2(n), shape
+
+
 # every image shape of the single-pass kernel's families (4096 elements per workgroup below
 # 4096, one image at 4096..16384), ragged batches that leave a partial workgroup, complex and
 # real input, forward and inverse

@@ -223,6 +223,164 @@ __global__ __launch_bounds__(C * (HR / E_)) void fft2_pass2_kernel(
   }
 }
 
+// Real input, pass 2 with whole-line mirror stores.  The mirror of the column tile [C*T, C*T + C)
+// is [W - C*T - C + 1, W - C*T]: one column off the line grid.  The aligned run
+// [W - C*T - C, W - C*T) instead holds the mirrors of columns C*T + 1 .. C*T + C, where the last
+// column is the first column of tile T + 1.  So a workgroup takes a run of adjacent tiles of one
+// group in descending order.  Each tile's lane-0 threads keep their column's mirrored values
+// (the "carry", in LDS slots that only the owning thread touches) for the next tile, whose mirror
+// stores then cover whole aligned lines.  The first tile of a run has no carry: its lane 0 stores
+// its own mirrored column instead (the next tile's carry store repeats it), and the first column
+// of its line comes from the run above, which stores its last carry after its loop; those
+// partial lines take plain stores.
+// Column W/2 (lane 0 of the top tile, W/2 being a multiple of C) is its own mirror and is read by
+// the workgroup of its own group, so it is only stored in place, never as a carry (a carry would
+// be written by the workgroup of the mirrored group, which may run first): the line starting at
+// W/2 is split like a run's first line.
+// The tile loop is software-pipelined: the next tile's loads are issued before this tile's
+// stores, and the twiddle table is staged in LDS once, so the transform issues no global loads
+// (gfx9 counts loads and stores in one in-order counter: waiting for a load issued after a store
+// also waits for the store).  The first and last tiles are peeled, so every path into a tile
+// holds the same outstanding loads and stores and the compiler's waits cover the loads only.
+template <int HR, int DIR, int C = fft2_tile(HR), int E_ = fft2_col_epth(HR)>
+__global__ __launch_bounds__(C * (HR / E_)) void fft2_pass2_half_kernel(
+    float* re, float* im, const float2* __restrict__ tw, int W, int tiles_per_group, int runs, float scale) {
+  constexpr int E = E_, T = HR / E;
+  constexpr int PADN = lds_pad(HR) + 1;
+  constexpr int H = 8 * HR;
+  constexpr int NTW = make_shape(HR, E).twoff[make_shape(HR, E).npass];  // twiddle entries
+  __shared__ float2 lds[C * PADN];  // interleaved (re, im) exchange
+  __shared__ float2 carry[2 * T * E];  // lane-0 threads' mirrored column, slot (tile & 1, t, e)
+  __shared__ __attribute__((aligned(16))) float2 twl[NTW > 0 ? NTW : 2];
+  const int c = threadIdx.x % C;
+  const int t = threadIdx.x / C;
+  const unsigned grp = blockIdx.x / (unsigned)runs;  // (image, q2)
+  const int run = (int)(blockIdx.x - grp * (unsigned)runs);
+  const unsigned q2 = grp % 8u;
+  // run r takes tiles [r * TPG / runs, (r + 1) * TPG / runs) (at least two: runs <= TPG / 2)
+  const int lo = run * tiles_per_group / runs;
+  const int hi = (run + 1) * tiles_per_group / runs - 1;
+  const int half = W / 2;
+  const int top = half / C;  // tile of column W/2 (>= 2)
+  // the image's planes (workgroup-uniform bases) and 32-bit byte offsets within the image
+  // (H * W * 4 < 2^32)
+  const size_t img = (size_t)(grp / 8u) * H * W;
+  char* const bre = reinterpret_cast<char*>(re + img);
+  char* const bim = reinterpret_cast<char*>(im + img);
+  const unsigned Wb = 4u * (unsigned)W;
+  const unsigned estep = 8u * T * Wb;  // element e of a thread is 8 T e rows further
+  // row q2 + 8t, and the mirror rows (H - q2 - 8t - 8Te) mod H: only e = 0 can wrap (to row 0)
+  const unsigned row_t0 = (q2 + 8u * (unsigned)t) * Wb;
+  const unsigned mrow_t = (unsigned)H - q2 - 8u * (unsigned)t;
+  const unsigned mrow0_0 = (mrow_t & (unsigned)(H - 1)) * Wb;
+  const unsigned mrow1_0 = mrow_t * Wb;
+  // lanes past column W/2 (top tile only) load, transform and store a copy of column W/2: the
+  // columns transform independently, so they store the same values as lane 0
+  auto load = [&](int tile, float2 (&x)[E]) {
+    const int col = tile * C + c;
+    const unsigned cb = 4u * (unsigned)(col <= half ? col : half);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const unsigned o = row_t0 + e * estep + cb;
+      x[e] = make_float2(__builtin_nontemporal_load(reinterpret_cast<const float*>(bre + o)),
+                         __builtin_nontemporal_load(reinterpret_cast<const float*>(bim + o)));
+    }
+  };
+  float2 nx[E];
+  load(hi, nx);
+  for (int i = threadIdx.x; i < NTW; i += C * T) twl[i] = tw[i];
+  __syncthreads();
+  // one tile: transform the loaded values, request the next tile's (PF), store this one's
+  auto step = [&](int tile, bool pf) {
+    // recomputed per tile (the empty asm hides their loop invariance): the compiler would
+    // otherwise keep the eight elements' row and mirror offsets in registers across the loop
+    // (over 100 VGPRs against ~76)
+    unsigned row_t = row_t0, mrow0 = mrow0_0, mrow1 = mrow1_0;
+    int cc = c;
+    asm volatile("" : "+v"(row_t), "+v"(mrow0), "+v"(mrow1), "+v"(cc));
+    float2 v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = make_float2(nx[e].x * scale, nx[e].y * scale);
+    // the previous tile's transform ended with a barrier after its last LDS reads
+    LdsFft<HR, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, twl, t);
+    // the next tile's loads go out once the transform's temporaries are dead (register pressure)
+    __builtin_amdgcn_sched_barrier(0);
+    if (pf) load(tile - 1, nx);
+    __builtin_amdgcn_sched_barrier(0);
+    const int col = tile * C + cc;
+    const unsigned cb = 4u * (unsigned)(col <= half ? col : half);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const unsigned o = row_t + e * estep + cb;
+      st_stream(reinterpret_cast<float*>(bre + o), v[e].x);
+      st_stream(reinterpret_cast<float*>(bim + o), v[e].y);
+    }
+    // mirror: lane c >= 1 stores column W - col, lane 0 the carry (mirror of column col + C) as
+    // the line's first column W - col - C, or without a carry its own mirror W - col.  The top
+    // tile (column W/2 only: no mirror) repeats its in-place stores instead, so that every tile
+    // issues the same stores; its carry is never used.
+    // The carry slots alternate by tile parity: lane 0 writes its new carry first and then reads
+    // the previous tile's into v (conjugated, as the stores conjugate v), so both never occupy
+    // registers at once.
+    const bool at_top = tile == top;
+    const bool has_carry = tile < hi && tile + 1 < top;
+    const bool use_carry = has_carry && cc == 0;
+    if (cc == 0) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) carry[(tile & 1) * T * E + t * E + e] = make_float2(v[e].x, -v[e].y);
+      if (use_carry) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const float2 y = carry[((tile + 1) & 1) * T * E + t * E + e];
+          v[e] = make_float2(y.x, -y.y);
+        }
+      }
+    }
+    const unsigned mc = 4u * (unsigned)(W - col - (use_carry ? C : 0));
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const unsigned o = at_top ? row_t + e * estep + cb : (e == 0 ? mrow0 : mrow1 - e * estep) + mc;
+      float* pr = reinterpret_cast<float*>(bre + o);
+      float* pi = reinterpret_cast<float*>(bim + o);
+      const float yi = at_top ? v[e].y : -v[e].y;
+      if (has_carry) {  // whole line with lane 0's carry
+        st_stream(pr, v[e].x);
+        st_stream(pi, yi);
+      } else {  // the run's first tile: the line's first column comes from the run above
+        *pr = v[e].x;
+        *pi = yi;
+      }
+    }
+  };
+  step(hi, true);
+  for (int tile = hi - 1; tile > lo; --tile) step(tile, true);
+  step(lo, false);
+  // the last tile's carry (mirror of column C*lo) opens the first mirror line of the run below
+  if (c == 0 && lo >= 1 && lo < top) {
+    const unsigned mc = 4u * (unsigned)(W - lo * C);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float2 y = carry[(lo & 1) * T * E + t * E + e];
+      const unsigned o = (e == 0 ? mrow0_0 : mrow1_0 - e * estep) + mc;
+      *reinterpret_cast<float*>(bre + o) = y.x;
+      *reinterpret_cast<float*>(bim + o) = y.y;
+    }
+  }
+}
+
+// Runs per group of the whole-line pass 2 (0: the one-tile-per-workgroup kernel), from an in-run
+// sweep on MI355X (real input, whole fft2, us; old = one tile per workgroup): one workgroup per
+// CU in all (the kernel holds ~76 VGPRs: one 1024-thread workgroup per CU) was fastest at every
+// shape: 32 x 2048^2 582 (2 runs 599, 4 runs 632; old 622), 16 x 1024^2 73.3 (old 82.2), 64 x 512^2
+// 69.0 (old 80.6), 8 x 2048 x 1024 77.9 (old 83.9).  When that would need runs of fewer than two
+// tiles the old kernel stays (1 x 2048^2: 29.9 against 36.6 with 16 runs).  Tiles must cover at
+// least one 128-byte line, with W/2 a multiple of the tile and at least two tiles below it.
+static int fft2_half_runs(long long groups, int tiles, int c, int w) {
+  if (c < 32 || (w / 2) % c != 0 || w / 2 < 2 * c) return 0;
+  const long long runs = (kNumCUs + groups - 1) / groups;
+  return runs > tiles / 2 ? 0 : (int)runs;
+}
+
 template <int W, int DIR>
 static hipError_t launch_pass1_w(const Fft2Args& a) {
   const long long blocks = a.batch * (a.h / 8);
@@ -241,7 +399,11 @@ static hipError_t launch_pass2_h(const Fft2Args& a) {
   const bool half = a.in_im == nullptr;  // real input: pass 1 wrote columns 0..W/2
   const int tiles = (int)(((half ? a.w / 2 + 1 : a.w) + C - 1) / C);
   const long long blocks = a.batch * 8 * (long long)tiles;
-  if (half)
+  const int runs = half ? fft2_half_runs(a.batch * 8, tiles, C, (int)a.w) : 0;
+  if (runs > 0)
+    hipLaunchKernelGGL((fft2_pass2_half_kernel<HR, DIR>), dim3((unsigned)(a.batch * 8 * runs)), dim3(C * T), 0,
+                       a.stream, a.out_re, a.out_im, a.tw_hr, (int)a.w, tiles, runs, a.scale);
+  else if (half)
     hipLaunchKernelGGL((fft2_pass2_kernel<HR, DIR, true>), dim3((unsigned)blocks), dim3(C * T), 0, a.stream,
                        a.out_re, a.out_im, a.tw_hr, (int)a.w, tiles, a.scale);
   else
