@@ -265,7 +265,20 @@ struct FourStepCfg {
 };
 constexpr int kFourStepNarrow = 8;
 
-template <int N1, int DIR, bool REAL_IN, int CK, int TILE_ = 0>
+// Entries of the W_N^lo / W_N^hi tables the column pass can stage in LDS without lowering its
+// occupancy: the LDS its tile leaves free within its share of the CU (one, two, ... workgroups).
+template <int N1, int TILE_>
+constexpr int fourstep_twl_cap() {
+  using Cfg = FourStepCfg<N1, TILE_>;
+  constexpr long long tile = (Cfg::SPLIT ? 1LL : 2LL) * Cfg::TILE * Cfg::PADN * 4;
+  constexpr long long per_cu = kLdsBytes / tile;  // workgroups per CU by LDS
+  return per_cu > 0 ? (int)((kLdsBytes / per_cu - tile) / 8) : 0;
+}
+
+// TWL: the W_N^lo and W_N^hi tables are staged in LDS at the start (their global loads overlap the
+// tile's), so the twiddle between the passes reads LDS instead of waiting out one L2 round trip per
+// group of factors.
+template <int N1, int DIR, bool REAL_IN, int CK, int TILE_ = 0, bool TWL = false>
 __global__ __launch_bounds__((FourStepCfg<N1, TILE_>::THREADS)) void fourstep_col_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ tw, const float2* __restrict__ tw_lo,
@@ -274,9 +287,16 @@ __global__ __launch_bounds__((FourStepCfg<N1, TILE_>::THREADS)) void fourstep_co
   constexpr int C = Cfg::TILE, E = Cfg::E, T = Cfg::T, THREADS = Cfg::THREADS, PADN = Cfg::PADN;
   constexpr bool SPLIT = Cfg::SPLIT;
   constexpr int TF = E < 4 ? E : 4;  // twiddle factor group
+  constexpr int CAP = TWL ? fourstep_twl_cap<N1, TILE_>() : 1;
   // split planes take turns through one float plane; otherwise interleaved (re, im) entries
   __shared__ float2 lds[SPLIT ? (C * PADN + 1) / 2 : C * PADN];
+  __shared__ float2 twt[CAP > 0 ? CAP : 1];  // TWL: W^lo entries, then W^hi
   float* lre = reinterpret_cast<float*>(lds);
+  const int nlo = 1 << lo_bits;
+  if constexpr (TWL) {
+    const int ntw = nlo + (int)((nmask >> lo_bits) + 1);
+    for (int i = threadIdx.x; i < ntw; i += THREADS) twt[i] = i < nlo ? tw_lo[i] : tw_hi[i - nlo];
+  }
   const int c = threadIdx.x % C;  // column within the tile (fast across lanes: whole lines)
   const int t = threadIdx.x / C;
   const long long tile = xcd_tile_remap(blockIdx.x, gridDim.x);
@@ -301,16 +321,19 @@ __global__ __launch_bounds__((FourStepCfg<N1, TILE_>::THREADS)) void fourstep_co
   // W^lo * W^hi from the two small tables (TF-1 + E/TF table pairs per thread instead of E);
   // the scheduling barrier keeps one group's loads in flight at a time (register pressure)
   const unsigned lomask = (1u << lo_bits) - 1;
+  // (the staged tables were written before the transform, whose exchanges are barriers)
+  const float2* tlo = TWL ? twt : tw_lo;
+  const float2* thi = TWL ? twt + nlo : tw_hi;
   float2 q[TF];
 #pragma unroll
   for (int j = 1; j < TF; ++j) {
     const unsigned m = (col * (unsigned)(T * j)) & nmask;
-    q[j] = cmul(tw_lo[m & lomask], tw_hi[m >> lo_bits]);
+    q[j] = cmul(tlo[m & lomask], thi[m >> lo_bits]);
   }
 #pragma unroll
   for (int a = 0; a < E / TF; ++a) {
     const unsigned m = (col * (unsigned)(t + T * TF * a)) & nmask;
-    const float2 p = cmul(tw_lo[m & lomask], tw_hi[m >> lo_bits]);
+    const float2 p = cmul(tlo[m & lomask], thi[m >> lo_bits]);
     v[TF * a] = cmul(v[TF * a], p);
 #pragma unroll
     for (int j = 1; j < TF; ++j) v[TF * a + j] = cmul(v[TF * a + j], cmul(p, q[j]));
@@ -521,14 +544,18 @@ static hipError_t launch_fourstep_tiles(const FourStepArgs& a) {
   static_assert(N2 % C1::TILE == 0 && N1 % CK == 0, "four-step tiles");
   const unsigned nmask = (unsigned)((long long)N1 * N2 - 1);
   const long long cols = a.batch * (N2 / C1::TILE);
-  if (a.in_im == nullptr)
-    hipLaunchKernelGGL((fourstep_col_kernel<N1, DIR, true, CK, TILE_>), dim3((unsigned)cols), dim3(C1::THREADS), 0,
-                       a.stream, a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, (long long)N2,
-                       N2 / C1::TILE, a.lo_bits, nmask);
-  else
-    hipLaunchKernelGGL((fourstep_col_kernel<N1, DIR, false, CK, TILE_>), dim3((unsigned)cols), dim3(C1::THREADS), 0,
-                       a.stream, a.in_re, a.in_im, a.t_re, a.t_im, a.tw1, a.tw_lo, a.tw_hi, (long long)N2,
-                       N2 / C1::TILE, a.lo_bits, nmask);
+  const bool twl = (1LL << a.lo_bits) + (((long long)N1 * N2) >> a.lo_bits) <= fourstep_twl_cap<N1, TILE_>();
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)cols), dim3(C1::THREADS), 0, a.stream, a.in_re, a.in_im, a.t_re, a.t_im,
+                       a.tw1, a.tw_lo, a.tw_hi, (long long)N2, N2 / C1::TILE, a.lo_bits, nmask);
+  };
+  if (a.in_im == nullptr) {
+    if (twl) go(fourstep_col_kernel<N1, DIR, true, CK, TILE_, true>);
+    else go(fourstep_col_kernel<N1, DIR, true, CK, TILE_, false>);
+  } else {
+    if (twl) go(fourstep_col_kernel<N1, DIR, false, CK, TILE_, true>);
+    else go(fourstep_col_kernel<N1, DIR, false, CK, TILE_, false>);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const long long rows = a.batch * (N1 / CK);
