@@ -378,15 +378,24 @@ __global__ __launch_bounds__((FourStepCfg<N1, TILE_>::THREADS)) void fourstep_co
   }
 }
 
-template <int N2, int DIR, int TILE_ = 0>
+// TWL: the transform's twiddle table is staged in LDS at the start (where it fits beside the tile
+// at the same occupancy), so its table reads do not wait on L2.
+template <int N2, int DIR, int TILE_ = 0, bool TWL = false>
 __global__ __launch_bounds__((FourStepCfg<N2, TILE_>::THREADS)) void fourstep_row_kernel(
     const float* __restrict__ t_re, const float* __restrict__ t_im, float* __restrict__ out_re,
     float* __restrict__ out_im, const float2* __restrict__ tw, int n1_len, float scale) {
   using Cfg = FourStepCfg<N2, TILE_>;
   constexpr int CK = Cfg::TILE, E = Cfg::E, T = Cfg::T, PADN = Cfg::PADN;
   constexpr bool SPLIT = Cfg::SPLIT;
+  constexpr int NTW = make_shape(N2, E).twoff[make_shape(N2, E).npass];
   __shared__ float2 lds[SPLIT ? (CK * PADN + 1) / 2 : CK * PADN];
+  __shared__ __attribute__((aligned(16))) float2 twt[TWL && NTW > 0 ? NTW : 2];
   float* lre = reinterpret_cast<float*>(lds);
+  if constexpr (TWL) {
+    // (read after the transform's first exchange, a barrier)
+    for (int i = threadIdx.x; i < NTW; i += Cfg::THREADS) twt[i] = tw[i];
+  }
+  const float2* twx = TWL ? twt : tw;
   const int r = threadIdx.x % CK;  // row within the tile (fast across lanes)
   const int t = threadIdx.x / CK;
   const int tiles_per_b = n1_len / CK;
@@ -402,9 +411,9 @@ __global__ __launch_bounds__((FourStepCfg<N2, TILE_>::THREADS)) void fourstep_ro
     v[e] = make_float2(t_re[i], t_im[i]);
   }
   if constexpr (SPLIT)
-    LdsFft<N2, E, DIR, false, true>::run(v, lre + r * PADN, nullptr, tw, t);
+    LdsFft<N2, E, DIR, false, true>::run(v, lre + r * PADN, nullptr, twx, t);
   else
-    LdsFft<N2, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + r * PADN), nullptr, tw, t);
+    LdsFft<N2, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + r * PADN), nullptr, twx, t);
   const size_t obase = (size_t)b * N + (size_t)kb * CK + r + (size_t)t * n1_len;
   const size_t ostep = (size_t)T * n1_len;
 #pragma unroll
@@ -559,8 +568,9 @@ static hipError_t launch_fourstep_tiles(const FourStepArgs& a) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const long long rows = a.batch * (N1 / CK);
-  hipLaunchKernelGGL((fourstep_row_kernel<N2, DIR, TILE_>), dim3((unsigned)rows), dim3(C2::THREADS), 0, a.stream,
-                     a.t_re, a.t_im, a.out_re, a.out_im, a.tw2, N1, a.scale);
+  constexpr bool ROW_TWL = make_shape(N2, C2::E).twoff[make_shape(N2, C2::E).npass] <= fourstep_twl_cap<N2, TILE_>();
+  hipLaunchKernelGGL((fourstep_row_kernel<N2, DIR, TILE_, ROW_TWL>), dim3((unsigned)rows), dim3(C2::THREADS), 0,
+                     a.stream, a.t_re, a.t_im, a.out_re, a.out_im, a.tw2, N1, a.scale);
   return hipGetLastError();
 }
 
