@@ -189,6 +189,9 @@ struct BluesteinArgs {
 hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a);
 // Largest wrap (2n - 1 - m) of the fused Bluestein kernel's wrapped-convolution lengths.
 constexpr int kBlueWrapMax = 15;
+// Two-level fused Bluestein kernel (M = 8192): offset of the cross-wave twiddle rows in its tables,
+// after the 512-point wave transform's table.
+constexpr int kBlue2lTwOff = 1024;
 
 // Bluestein down a strided axis (x viewed as (outer, n, stride)), m <= kMaxStridedBlueM.
 constexpr int kMaxStridedBlueM = 4096;

@@ -146,19 +146,168 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   }
 }
 
+// Two-level fused Bluestein at M = 8192 (one row per workgroup: 16 wavefronts x 512 points).
+// The one-level kernel above synchronises the whole workgroup at every radix pass (about ten
+// barriers per row, and waves of a one-row-per-CU launch spend most of their cycles waiting), so
+// here the length splits as M = 16 x 512, n = 512 n_a + n_b, k = k_a + 16 k_b:
+//   forward: each thread (p, n_b) = (tid / 512, tid % 512) holds x[tid + 1024 e] = x[512 (2e + p)
+//     + n_b] and transforms over e in registers (the 8-point half of the 16-point DFT over n_a);
+//     one exchange through LDS gives wave w = k_a = k' + 8q the values Y_0[k'][n_b] + (-1)^q
+//     W_16^k' Y_1[k'][n_b] for all 512 n_b, times W_M^(n_b k_a); a 512-point transform inside the
+//     wave (wave-local exchanges only) leaves X[k_a + 16 k_b] with k_b = lane + 64 e;
+//   the filter spectrum is applied in that order (the plan stores H/M permuted to it), then the
+//     wave's 512-point inverse transform, times W_M^(-n_b k_a);
+//   inverse: one exchange back gives thread (p, n_b) the 16 values Z[k_a][n_b]; the pairs
+//     (Z[k'] +- Z[k' + 8]) times W_16^(-p k') and an 8-point inverse DFT in registers give
+//     y[512 (2e + p) + n_b] = y[tid + 1024 e]: natural order again for the chirp, the wrap
+//     correction and the stores.
+// Two workgroup barriers per row (the two exchanges; the second goes through the waves' own
+// exchange areas).  tw_f / tw_i: the 512-point transform's table (tfa::make_shape(512, 8)),
+// then from entry kBlue2lTwOff the rows W_M^(+-n_b w), w < 16, n_b < 512.
+template <bool REAL_IN, bool WRAP>
+__global__ __launch_bounds__(1024) void bluestein_2l_kernel(
+    const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re, float* out_im,
+    const float2* __restrict__ chirp, const float2* __restrict__ hs, const float2* __restrict__ tw_f,
+    const float2* __restrict__ tw_i, int n, long long batch, float scale, int wrap) {
+  constexpr int M = 8192, T = 1024, E = 8, B = 512, PB = lds_pad(B);
+  __shared__ float2 xbuf[M];        // the two cross-wave exchanges
+  __shared__ float2 warea[16 * PB];  // each wave's 512-point exchange area
+  __shared__ float2 ends[WRAP ? 3 * kBlueWrapMax : 1];  // y[0, wrap), y[L, n), chirp[L, n)
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63;
+  const int p = tid >> 9, nb = tid & 511;
+  const size_t base = (size_t)blockIdx.x * n;
+  const int L = n - wrap;
+  // n <= M/2 (+ up to 8 wrapped): element e of a thread can hold a sample only for e < EH
+  constexpr int EH = E / 2 + (WRAP ? 1 : 0);
+  float2 v[E], ch[EH];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = tid + T * e;
+    float2 y = make_float2(0.0f, 0.0f);
+    if (e < EH) {
+      const float2 c = i < n ? chirp[i] : make_float2(0.0f, 0.0f);
+      ch[e < EH ? e : 0] = c;
+      if (i < n) {
+        const float2 x = make_float2(ld_stream(in_re + base + i), REAL_IN ? 0.0f : ld_stream(in_im + base + i));
+        y = cmul(x, c);
+      }
+      if constexpr (WRAP) {
+        if (i < wrap) ends[i] = y;
+        if (i >= L && i < n) {
+          ends[kBlueWrapMax + i - L] = y;
+          ends[2 * kBlueWrapMax + i - L] = c;
+        }
+      }
+    }
+    v[e] = y;
+  }
+  // the wave's cross twiddles and filter spectrum, requested before the first exchange
+  const int kq = w & 7;
+  float2 tcr[E], hv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    tcr[e] = tw_f[kBlue2lTwOff + w * B + l + 64 * e];
+    hv[e] = hs[tid + T * e];
+  }
+  // 8-point DFT over e (the samples n_a = 2e + p of column n_b), then the exchange
+  Dft<8, -1>::run(v);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) xbuf[(p * 8 + k) * B + nb] = v[k];
+  __syncthreads();
+  // W_16^j = (cos, -sin)(2 pi j / 16) for the forward sign
+  constexpr float kC16[8] = {(float)cos2pi(0, 16), (float)cos2pi(1, 16), (float)cos2pi(2, 16), (float)cos2pi(3, 16),
+                             (float)cos2pi(4, 16), (float)cos2pi(5, 16), (float)cos2pi(6, 16), (float)cos2pi(7, 16)};
+  constexpr float kS16[8] = {(float)sin2pi(0, 16), (float)sin2pi(1, 16), (float)sin2pi(2, 16), (float)sin2pi(3, 16),
+                             (float)sin2pi(4, 16), (float)sin2pi(5, 16), (float)sin2pi(6, 16), (float)sin2pi(7, 16)};
+  {
+    // W_16^k' (forward sign), k' = w mod 8: wave-uniform
+    const float2 w16 = make_float2(kC16[kq], -kS16[kq]);
+    const bool neg = w >= 8;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float2 y0 = xbuf[kq * B + l + 64 * e];
+      const float2 y1 = cmul(xbuf[(8 + kq) * B + l + 64 * e], w16);
+      v[e] = cmul(neg ? csub(y0, y1) : cadd(y0, y1), tcr[e]);
+    }
+  }
+  float* wa = reinterpret_cast<float*>(warea + w * PB);
+  LdsFft<B, E, -1, true, false, true, true>::run(v, wa, nullptr, tw_f, l);
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], hv[e]);
+  LdsFft<B, E, 1, true, false, true, true>::run(v, wa, nullptr, tw_i, l);
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], make_float2(tcr[e].x, -tcr[e].y));
+  // the wave's own exchange area takes its result (its last reads of the area came before the
+  // transform's final wave barrier), so no barrier guards the first exchange's buffer
+#pragma unroll
+  for (int e = 0; e < E; ++e) warea[w * PB + l + 64 * e] = v[e];
+  __syncthreads();
+  {
+    // u[k'] = Z[k'] + Z[k' + 8] (p = 0) or (Z[k'] - Z[k' + 8]) W_16^-k' (p = 1), then the 8-point
+    // inverse DFT over k' gives y[512 (2e + p) + n_b]
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float2 z0 = warea[k * PB + nb], z1 = warea[(k + 8) * PB + nb];
+      if (p == 0) v[k] = cadd(z0, z1);
+      else v[k] = cmul(csub(z0, z1), make_float2(kC16[k], kS16[k]));  // W_16^-k (inverse sign)
+    }
+  }
+  Dft<8, 1>::run(v);
+#pragma unroll
+  for (int e = 0; e < EH; ++e) {
+    const int i = tid + T * e;
+    if (i < n) {
+      float2 cv = v[e];
+      if constexpr (WRAP) {
+        const float2* yl = ends;
+        const float2* yh = ends + kBlueWrapMax;
+        const float2* ct = ends + 2 * kBlueWrapMax;
+        if (i < wrap) {
+          for (int c = i; c < wrap; ++c) {
+            const float2 t = ct[wrap - 1 + i - c];
+            cv = csub(cv, cmul(yh[c], make_float2(t.x, -t.y)));
+          }
+        }
+        if (i >= L) {
+          const int a = i - L;
+          for (int j = 0; j <= a; ++j) {
+            const float2 t = ct[wrap - 1 - a + j];
+            cv = csub(cv, cmul(yl[j], make_float2(t.x, -t.y)));
+          }
+        }
+      }
+      const float2 y = cmul(cv, ch[e]);
+      st_stream(out_re + base + i, y.x * scale);
+      st_stream(out_im + base + i, y.y * scale);
+    }
+  }
+}
+
 template <int M, bool WRAP>
 static hipError_t launch_blue_mw(const BluesteinArgs& a) {
-  using C = BlueCfg<M, blue_epth(M), blue_threads(M)>;
-  const long long blocks = (a.batch + C::XF - 1) / C::XF;
-  if (a.in_im == nullptr)
-    hipLaunchKernelGGL((bluestein_fused_kernel<M, true, WRAP>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
-                       a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i,
-                       a.n, a.batch, a.scale, a.wrap);
-  else
-    hipLaunchKernelGGL((bluestein_fused_kernel<M, false, WRAP>), dim3((unsigned)blocks), dim3(C::THREADS),
-                       0, a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f,
-                       a.tw_i, a.n, a.batch, a.scale, a.wrap);
-  return hipGetLastError();
+  if constexpr (M == 8192) {
+    if (a.batch > 0x7fffffffLL) return hipErrorInvalidValue;
+    if (a.in_im == nullptr)
+      hipLaunchKernelGGL((bluestein_2l_kernel<true, WRAP>), dim3((unsigned)a.batch), dim3(1024), 0, a.stream, a.in_re,
+                         a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i, a.n, a.batch, a.scale, a.wrap);
+    else
+      hipLaunchKernelGGL((bluestein_2l_kernel<false, WRAP>), dim3((unsigned)a.batch), dim3(1024), 0, a.stream, a.in_re,
+                         a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i, a.n, a.batch, a.scale, a.wrap);
+    return hipGetLastError();
+  } else {
+    using C = BlueCfg<M, blue_epth(M), blue_threads(M)>;
+    const long long blocks = (a.batch + C::XF - 1) / C::XF;
+    if (a.in_im == nullptr)
+      hipLaunchKernelGGL((bluestein_fused_kernel<M, true, WRAP>), dim3((unsigned)blocks), dim3(C::THREADS), 0,
+                         a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i,
+                         a.n, a.batch, a.scale, a.wrap);
+    else
+      hipLaunchKernelGGL((bluestein_fused_kernel<M, false, WRAP>), dim3((unsigned)blocks), dim3(C::THREADS),
+                         0, a.stream, a.in_re, a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f,
+                         a.tw_i, a.n, a.batch, a.scale, a.wrap);
+    return hipGetLastError();
+  }
 }
 
 template <int M>

@@ -71,6 +71,28 @@ struct DevBuf {
   void* p = nullptr;
 };
 
+// Tables of the two-level fused Bluestein kernel at M = 8192 (16 wavefronts x 512 points):
+// the 512-point wave transform's table (make_shape(512, 8)), then from entry kBlue2lTwOff the rows
+// W_M^(n_b w) (sign dir), w < 16, n_b < 512.
+std::vector<float2> blue_2l_table(int dir) {
+  std::vector<float2> t = lds_table(512, dir, 8);
+  t.resize((size_t)tfa::kBlue2lTwOff + 16 * 512, make_float2(1.0f, 0.0f));
+  for (int w = 0; w < 16; ++w)
+    for (int nb = 0; nb < 512; ++nb) t[(size_t)tfa::kBlue2lTwOff + w * 512 + nb] = unit_root((int64_t)nb * w, 8192, dir);
+  return t;
+}
+
+// The filter spectrum in the two-level kernel's frequency order: entry tid + 1024 e (wave w =
+// tid / 64, lane l = tid % 64) holds frequency w + 16 (l + 64 e).
+std::vector<float2> blue_2l_permute(const std::vector<float2>& h) {
+  std::vector<float2> out(h.size());
+  for (size_t j = 0; j < h.size(); ++j) {
+    const size_t e = j >> 10, w = (j >> 6) & 15, l = j & 63;
+    out[j] = h[w + 16 * (l + 64 * e)];
+  }
+  return out;
+}
+
 // Power-of-two transform tables for one direction: LDS path (n <= kMaxLdsN) or four-step.
 struct C2cTables {
   int64_t n = 0;
@@ -470,8 +492,13 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         p->fwd.n = p->inv.n = mf;
         p->fwd.dir = -1;
         p->inv.dir = 1;
-        if ((rc = p->upload(lds_table(mf, -1, tfa::blue_epth(mf)), &p->fwd.tw))) break;
-        if ((rc = p->upload(lds_table(mf, 1, tfa::blue_epth(mf)), &p->inv.tw))) break;
+        if (mf == 8192) {  // the two-level kernel's tables (tfa::bluestein_2l_kernel)
+          if ((rc = p->upload(blue_2l_table(-1), &p->fwd.tw))) break;
+          if ((rc = p->upload(blue_2l_table(1), &p->inv.tw))) break;
+        } else {
+          if ((rc = p->upload(lds_table(mf, -1, tfa::blue_epth(mf)), &p->fwd.tw))) break;
+          if ((rc = p->upload(lds_table(mf, 1, tfa::blue_epth(mf)), &p->inv.tw))) break;
+        }
         if (m <= tfa::kMaxStridedBlueM) {  // the strided-axis kernel's layout (tfa::lds_epth)
           if (p->mf == m && tfa::blue_epth((int)m) == tfa::lds_epth((int)m)) {
             p->b_tw_sf = p->fwd.tw;
@@ -486,7 +513,11 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       auto filter_spectrum = [&](int64_t L) { return blue_filter_spectrum(chirp, L); };
       const std::vector<float2> hs = filter_spectrum(m);
       if ((rc = p->upload(chirp, &p->chirp))) break;
-      if ((rc = p->upload(p->blue_fused && p->mf != m ? filter_spectrum(p->mf) : hs, &p->hs))) break;
+      if (p->blue_fused && p->mf == 8192) {
+        if ((rc = p->upload(blue_2l_permute(filter_spectrum(p->mf)), &p->hs))) break;
+      } else if ((rc = p->upload(p->blue_fused && p->mf != m ? filter_spectrum(p->mf) : hs, &p->hs))) {
+        break;
+      }
       if (m <= tfa::kMaxStridedBlueM) {
         if (p->mf == m) p->b_hs_s = p->hs;
         else if ((rc = p->upload(hs, &p->b_hs_s))) break;
