@@ -189,9 +189,11 @@ struct BluesteinArgs {
 hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a);
 // Largest wrap (2n - 1 - m) of the fused Bluestein kernel's wrapped-convolution lengths.
 constexpr int kBlueWrapMax = 15;
-// Two-level fused Bluestein kernel (M = 8192): offset of the cross-wave twiddle rows in its tables,
-// after the 512-point wave transform's table.
+// Two-level fused Bluestein kernel (lengths M = 4096, 8192: M / 512 wavefronts of 512 points per
+// row): offset of the cross-wave twiddle rows in its tables, after the 512-point wave transform's
+// table.
 constexpr int kBlue2lTwOff = 1024;
+__host__ __device__ constexpr bool blue_2l(int m) { return m == 4096 || m == 8192; }
 
 // Bluestein down a strided axis (x viewed as (outer, n, stride)), m <= kMaxStridedBlueM.
 constexpr int kMaxStridedBlueM = 4096;

@@ -146,36 +146,47 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   }
 }
 
-// Two-level fused Bluestein at M = 8192 (one row per workgroup: 16 wavefronts x 512 points).
-// The one-level kernel above synchronises the whole workgroup at every radix pass (about ten
-// barriers per row, and waves of a one-row-per-CU launch spend most of their cycles waiting), so
-// here the length splits as M = 16 x 512, n = 512 n_a + n_b, k = k_a + 16 k_b:
-//   forward: each thread (p, n_b) = (tid / 512, tid % 512) holds x[tid + 1024 e] = x[512 (2e + p)
-//     + n_b] and transforms over e in registers (the 8-point half of the 16-point DFT over n_a);
-//     one exchange through LDS gives wave w = k_a = k' + 8q the values Y_0[k'][n_b] + (-1)^q
-//     W_16^k' Y_1[k'][n_b] for all 512 n_b, times W_M^(n_b k_a); a 512-point transform inside the
-//     wave (wave-local exchanges only) leaves X[k_a + 16 k_b] with k_b = lane + 64 e;
+// Two-level fused Bluestein at M = 4096 and 8192: each row is R = M / 512 wavefronts of 512
+// points.  The one-level kernel above synchronises the whole workgroup at every radix pass
+// (about ten barriers per row at M = 8192, and the waves of a one-row-per-CU launch spend most
+// of their cycles waiting), so here the length splits as M = R x 512, n = 512 n_a + n_b,
+// k = k_a + R k_b:
+//   forward: thread t of the row holds x[t + T e] (T = M / 8) and transforms over the n_a it holds
+//     in registers (R = 8: the whole column n_b = t; R = 16: the samples n_a = 2e + p of column n_b
+//     = t % 512, p = t / 512, the 8-point half of the 16-point DFT); one exchange through LDS gives wave w = k_a its values for all 512 n_b
+//     (for R = 16 the radix-2 half: Y_0[k'] + (-1)^q W_16^k' Y_1[k'], w = k' + 8q), times
+//     W_M^(n_b k_a); a 512-point transform inside the wave (wave-local exchanges only) leaves
+//     X[k_a + R k_b] with k_b = lane + 64 e;
 //   the filter spectrum is applied in that order (the plan stores H/M permuted to it), then the
-//     wave's 512-point inverse transform, times W_M^(-n_b k_a);
-//   inverse: one exchange back gives thread (p, n_b) the 16 values Z[k_a][n_b]; the pairs
-//     (Z[k'] +- Z[k' + 8]) times W_16^(-p k') and an 8-point inverse DFT in registers give
-//     y[512 (2e + p) + n_b] = y[tid + 1024 e]: natural order again for the chirp, the wrap
-//     correction and the stores.
-// Two workgroup barriers per row (the two exchanges; the second goes through the waves' own
-// exchange areas).  tw_f / tw_i: the 512-point transform's table (tfa::make_shape(512, 8)),
-// then from entry kBlue2lTwOff the rows W_M^(+-n_b w), w < 16, n_b < 512.
-template <bool REAL_IN, bool WRAP>
-__global__ __launch_bounds__(1024) void bluestein_2l_kernel(
+//     wave's 512-point inverse transform, times W_M^(-n_b k_a), written into the wave's own
+//     exchange area;
+//   inverse: one exchange back gives each thread the R values Z[k_a][n_b] of its columns; the
+//     inverse DFT over k_a in registers (for R = 16: the pairs (Z[k'] +- Z[k' + 8]) times
+//     W_16^(-p k') and an 8-point inverse DFT) gives y[t + T e]: natural order again for the
+//     chirp, the wrap correction and the stores.
+// Two workgroup barriers per row (one row per workgroup).  tw_f / tw_i: the 512-point transform's
+// table (tfa::make_shape(512, 8)), then from entry kBlue2lTwOff the rows W_M^(+-n_b w), w < R,
+// n_b < 512.  Measured against the one-level kernel (in-run): 256 x 4099 (M = 8192, wrapped) 13.7
+// -> 12.3 us, 256 x 3000 12.4 -> 10.8, 512 x 2000 (4096) 11.2 -> 10.7, 256 x 1700 8.4 -> 7.7; at
+// M = 2048 (four waves per row, two rows per workgroup) it lost at 1024 x 1000 (10.6 -> 10.8 us),
+// so 2048 keeps the one-level kernel.
+template <int M>
+struct Blue2lCfg {
+  static constexpr int R = M / 512, E = 8, T = M / E, B = 512, PB = lds_pad(B);
+};
+template <int M, bool REAL_IN, bool WRAP>
+__global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
     const float* __restrict__ in_re, const float* __restrict__ in_im, float* out_re, float* out_im,
     const float2* __restrict__ chirp, const float2* __restrict__ hs, const float2* __restrict__ tw_f,
     const float2* __restrict__ tw_i, int n, long long batch, float scale, int wrap) {
-  constexpr int M = 8192, T = 1024, E = 8, B = 512, PB = lds_pad(B);
-  __shared__ float2 xbuf[M];        // the two cross-wave exchanges
-  __shared__ float2 warea[16 * PB];  // each wave's 512-point exchange area
+  using C = Blue2lCfg<M>;
+  constexpr int R = C::R, E = C::E, T = C::T, B = C::B, PB = C::PB;
+  static_assert(R == 8 || R == 16, "two-level Bluestein lengths");
+  __shared__ float2 xbuf[M];        // the forward exchange
+  __shared__ float2 warea[R * PB];  // each wave's 512-point exchange area; the inverse exchange
   __shared__ float2 ends[WRAP ? 3 * kBlueWrapMax : 1];  // y[0, wrap), y[L, n), chirp[L, n)
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63;
-  const int p = tid >> 9, nb = tid & 511;
   const size_t base = (size_t)blockIdx.x * n;
   const int L = n - wrap;
   // n <= M/2 (+ up to 8 wrapped): element e of a thread can hold a sample only for e < EH
@@ -203,26 +214,33 @@ __global__ __launch_bounds__(1024) void bluestein_2l_kernel(
     v[e] = y;
   }
   // the wave's cross twiddles and filter spectrum, requested before the first exchange
-  const int kq = w & 7;
   float2 tcr[E], hv[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     tcr[e] = tw_f[kBlue2lTwOff + w * B + l + 64 * e];
     hv[e] = hs[tid + T * e];
   }
-  // 8-point DFT over e (the samples n_a = 2e + p of column n_b), then the exchange
-  Dft<8, -1>::run(v);
-#pragma unroll
-  for (int k = 0; k < 8; ++k) xbuf[(p * 8 + k) * B + nb] = v[k];
-  __syncthreads();
   // W_16^j = (cos, -sin)(2 pi j / 16) for the forward sign
   constexpr float kC16[8] = {(float)cos2pi(0, 16), (float)cos2pi(1, 16), (float)cos2pi(2, 16), (float)cos2pi(3, 16),
                              (float)cos2pi(4, 16), (float)cos2pi(5, 16), (float)cos2pi(6, 16), (float)cos2pi(7, 16)};
   constexpr float kS16[8] = {(float)sin2pi(0, 16), (float)sin2pi(1, 16), (float)sin2pi(2, 16), (float)sin2pi(3, 16),
                              (float)sin2pi(4, 16), (float)sin2pi(5, 16), (float)sin2pi(6, 16), (float)sin2pi(7, 16)};
-  {
-    // W_16^k' (forward sign), k' = w mod 8: wave-uniform
-    const float2 w16 = make_float2(kC16[kq], -kS16[kq]);
+  // forward, in registers over the n_a each thread holds, then the exchange: xbuf[k_a * 512 + n_b]
+  // (R = 16: xbuf[(p * 8 + k') * 512 + n_b] holds the half transform Y_p[k'])
+  if constexpr (R == 16) {
+    Dft<8, -1>::run(v);
+    const int p = tid >> 9, nb = tid & 511;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) xbuf[(p * 8 + k) * B + nb] = v[k];
+  } else {
+    Dft<8, -1>::run(v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) xbuf[k * B + tid] = v[k];
+  }
+  __syncthreads();
+  if constexpr (R == 16) {
+    const int kq = w & 7;
+    const float2 w16 = make_float2(kC16[kq], -kS16[kq]);  // W_16^k' (forward sign), wave-uniform
     const bool neg = w >= 8;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
@@ -230,30 +248,37 @@ __global__ __launch_bounds__(1024) void bluestein_2l_kernel(
       const float2 y1 = cmul(xbuf[(8 + kq) * B + l + 64 * e], w16);
       v[e] = cmul(neg ? csub(y0, y1) : cadd(y0, y1), tcr[e]);
     }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = cmul(xbuf[w * B + l + 64 * e], tcr[e]);
   }
   float* wa = reinterpret_cast<float*>(warea + w * PB);
   LdsFft<B, E, -1, true, false, true, true>::run(v, wa, nullptr, tw_f, l);
 #pragma unroll
   for (int e = 0; e < E; ++e) v[e] = cmul(v[e], hv[e]);
   LdsFft<B, E, 1, true, false, true, true>::run(v, wa, nullptr, tw_i, l);
-#pragma unroll
-  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], make_float2(tcr[e].x, -tcr[e].y));
   // the wave's own exchange area takes its result (its last reads of the area came before the
   // transform's final wave barrier), so no barrier guards the first exchange's buffer
 #pragma unroll
-  for (int e = 0; e < E; ++e) warea[w * PB + l + 64 * e] = v[e];
+  for (int e = 0; e < E; ++e) warea[w * PB + l + 64 * e] = cmul(v[e], make_float2(tcr[e].x, -tcr[e].y));
   __syncthreads();
-  {
+  // inverse over k_a in registers: y[t + T e] into v[e]
+  if constexpr (R == 16) {
     // u[k'] = Z[k'] + Z[k' + 8] (p = 0) or (Z[k'] - Z[k' + 8]) W_16^-k' (p = 1), then the 8-point
     // inverse DFT over k' gives y[512 (2e + p) + n_b]
+    const int p = tid >> 9, nb = tid & 511;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const float2 z0 = warea[k * PB + nb], z1 = warea[(k + 8) * PB + nb];
       if (p == 0) v[k] = cadd(z0, z1);
       else v[k] = cmul(csub(z0, z1), make_float2(kC16[k], kS16[k]));  // W_16^-k (inverse sign)
     }
+    Dft<8, 1>::run(v);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = warea[k * PB + tid];
+    Dft<8, 1>::run(v);
   }
-  Dft<8, 1>::run(v);
 #pragma unroll
   for (int e = 0; e < EH; ++e) {
     const int i = tid + T * e;
@@ -286,14 +311,18 @@ __global__ __launch_bounds__(1024) void bluestein_2l_kernel(
 
 template <int M, bool WRAP>
 static hipError_t launch_blue_mw(const BluesteinArgs& a) {
-  if constexpr (M == 8192) {
-    if (a.batch > 0x7fffffffLL) return hipErrorInvalidValue;
+  if constexpr (blue_2l(M)) {
+    using C2 = Blue2lCfg<M>;
+    const long long blocks = a.batch;  // one row per workgroup
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
     if (a.in_im == nullptr)
-      hipLaunchKernelGGL((bluestein_2l_kernel<true, WRAP>), dim3((unsigned)a.batch), dim3(1024), 0, a.stream, a.in_re,
-                         a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i, a.n, a.batch, a.scale, a.wrap);
+      hipLaunchKernelGGL((bluestein_2l_kernel<M, true, WRAP>), dim3((unsigned)blocks), dim3(C2::T), 0, a.stream,
+                         a.in_re, a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i, a.n, a.batch, a.scale,
+                         a.wrap);
     else
-      hipLaunchKernelGGL((bluestein_2l_kernel<false, WRAP>), dim3((unsigned)a.batch), dim3(1024), 0, a.stream, a.in_re,
-                         a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i, a.n, a.batch, a.scale, a.wrap);
+      hipLaunchKernelGGL((bluestein_2l_kernel<M, false, WRAP>), dim3((unsigned)blocks), dim3(C2::T), 0, a.stream,
+                         a.in_re, a.in_im, a.out_re, a.out_im, a.chirp, a.hs, a.tw_f, a.tw_i, a.n, a.batch, a.scale,
+                         a.wrap);
     return hipGetLastError();
   } else {
     using C = BlueCfg<M, blue_epth(M), blue_threads(M)>;

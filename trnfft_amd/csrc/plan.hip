@@ -71,24 +71,26 @@ struct DevBuf {
   void* p = nullptr;
 };
 
-// Tables of the two-level fused Bluestein kernel at M = 8192 (16 wavefronts x 512 points):
-// the 512-point wave transform's table (make_shape(512, 8)), then from entry kBlue2lTwOff the rows
-// W_M^(n_b w) (sign dir), w < 16, n_b < 512.
-std::vector<float2> blue_2l_table(int dir) {
+// Tables of the two-level fused Bluestein kernel at length m (tfa::blue_2l: m / 512 wavefronts of
+// 512 points per row): the 512-point wave transform's table (make_shape(512, 8)), then from entry
+// kBlue2lTwOff the rows W_m^(n_b w) (sign dir), w < m / 512, n_b < 512.
+std::vector<float2> blue_2l_table(int m, int dir) {
+  const int r = m / 512;
   std::vector<float2> t = lds_table(512, dir, 8);
-  t.resize((size_t)tfa::kBlue2lTwOff + 16 * 512, make_float2(1.0f, 0.0f));
-  for (int w = 0; w < 16; ++w)
-    for (int nb = 0; nb < 512; ++nb) t[(size_t)tfa::kBlue2lTwOff + w * 512 + nb] = unit_root((int64_t)nb * w, 8192, dir);
+  t.resize((size_t)tfa::kBlue2lTwOff + (size_t)r * 512, make_float2(1.0f, 0.0f));
+  for (int w = 0; w < r; ++w)
+    for (int nb = 0; nb < 512; ++nb) t[(size_t)tfa::kBlue2lTwOff + w * 512 + nb] = unit_root((int64_t)nb * w, m, dir);
   return t;
 }
 
-// The filter spectrum in the two-level kernel's frequency order: entry tid + 1024 e (wave w =
-// tid / 64, lane l = tid % 64) holds frequency w + 16 (l + 64 e).
+// The filter spectrum in the two-level kernel's frequency order: entry t + (m / 8) e of a row
+// (wave w = t / 64, lane l = t % 64) holds frequency w + (m / 512) (l + 64 e).
 std::vector<float2> blue_2l_permute(const std::vector<float2>& h) {
-  std::vector<float2> out(h.size());
-  for (size_t j = 0; j < h.size(); ++j) {
-    const size_t e = j >> 10, w = (j >> 6) & 15, l = j & 63;
-    out[j] = h[w + 16 * (l + 64 * e)];
+  const size_t m = h.size(), tt = m / 8, r = m / 512;
+  std::vector<float2> out(m);
+  for (size_t j = 0; j < m; ++j) {
+    const size_t e = j / tt, w = (j % tt) >> 6, l = j & 63;
+    out[j] = h[w + r * (l + 64 * e)];
   }
   return out;
 }
@@ -122,7 +124,7 @@ struct tfa_plan {
   float2* chirp = nullptr;
   float2* hs = nullptr;
   float2 *b_tw_sf = nullptr, *b_tw_si = nullptr;  // Bluestein m <= 4096: strided-axis kernel tables
-  float2* b_hs_s = nullptr;  // Bluestein m <= 4096: strided-axis filter spectrum (length m; hs when mf == m)
+  float2* b_hs_s = nullptr;  // Bluestein m <= 4096: strided-axis filter spectrum (length m, natural order; hs when mf == m and the fused kernel is one-level)
   float2* stft_hs_adj = nullptr;  // forward STFT, n_fft not a power of two: the adjoint chain's filter spectrum
   int blue_wrap = 0;         // Bluestein: 2n - 1 - mf when the fused length wraps the convolution
   C2cTables col;          // FFT2: LDS table for n2/8 (pass 2)
@@ -492,9 +494,9 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
         p->fwd.n = p->inv.n = mf;
         p->fwd.dir = -1;
         p->inv.dir = 1;
-        if (mf == 8192) {  // the two-level kernel's tables (tfa::bluestein_2l_kernel)
-          if ((rc = p->upload(blue_2l_table(-1), &p->fwd.tw))) break;
-          if ((rc = p->upload(blue_2l_table(1), &p->inv.tw))) break;
+        if (tfa::blue_2l(mf)) {  // the two-level kernel's tables (tfa::bluestein_2l_kernel)
+          if ((rc = p->upload(blue_2l_table(mf, -1), &p->fwd.tw))) break;
+          if ((rc = p->upload(blue_2l_table(mf, 1), &p->inv.tw))) break;
         } else {
           if ((rc = p->upload(lds_table(mf, -1, tfa::blue_epth(mf)), &p->fwd.tw))) break;
           if ((rc = p->upload(lds_table(mf, 1, tfa::blue_epth(mf)), &p->inv.tw))) break;
@@ -513,13 +515,15 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
       auto filter_spectrum = [&](int64_t L) { return blue_filter_spectrum(chirp, L); };
       const std::vector<float2> hs = filter_spectrum(m);
       if ((rc = p->upload(chirp, &p->chirp))) break;
-      if (p->blue_fused && p->mf == 8192) {
+      if (p->blue_fused && tfa::blue_2l((int)p->mf)) {
         if ((rc = p->upload(blue_2l_permute(filter_spectrum(p->mf)), &p->hs))) break;
       } else if ((rc = p->upload(p->blue_fused && p->mf != m ? filter_spectrum(p->mf) : hs, &p->hs))) {
         break;
       }
       if (m <= tfa::kMaxStridedBlueM) {
-        if (p->mf == m) p->b_hs_s = p->hs;
+        // (the strided-axis kernel reads H/m in natural order; the two-level fused kernel's copy is
+        // permuted)
+        if (p->mf == m && !tfa::blue_2l((int)p->mf)) p->b_hs_s = p->hs;
         else if ((rc = p->upload(hs, &p->b_hs_s))) break;
       }
       if (p->blue_split) {
