@@ -251,6 +251,21 @@ def test_bluestein_wrapped_lengths_vs_oracle(n, batch, inverse):
     assert e_ends <= 3 * e_all + 1e-6, (n, e_ends, e_all)
 
 
+@pytest.mark.parametrize("n,batch", [(1537, 40), (1700, 257), (2048, 9), (2057, 64), (3000, 130), (4096, 17)])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_bluestein_two_level_lengths_vs_oracle(n, batch, inverse):
+    # convolution lengths 4096 (n = 1537..2048) and 8192 (n = 2057..4096) run the two-level fused
+    # kernel (one exchange into 512-point wave transforms and one back, the filter spectrum in the
+    # waves' frequency order); complex and real input, against the oracle's Bluestein
+    re, im = seeded_complex(batch, n, seed=n + 13)
+    got = _gpu_fft(re, im, inverse)
+    ref = oracle.fft_core(re, im, inverse)
+    assert rel_l2(*got, *ref) <= tol_bluestein(n), (n, inverse)
+    X = trnfft_amd.ifft(re.cuda()) if inverse else trnfft_amd.fft(re.cuda())
+    ref = oracle.fft_core(re, torch.zeros_like(re), inverse)
+    assert rel_l2(X.real, X.imag, *ref) <= tol_bluestein(n), (n, inverse, "real input")
+
+
 @pytest.mark.parametrize("n", [1027, 4099])
 def test_bluestein_wrapped_real_input_and_strided_axis(n):
     # real input through the wrapped fused kernel, and a strided axis (n = 1027: m = 4096 runs the
