@@ -251,12 +251,18 @@ def test_bluestein_wrapped_lengths_vs_oracle(n, batch, inverse):
     assert e_ends <= 3 * e_all + 1e-6, (n, e_ends, e_all)
 
 
-@pytest.mark.parametrize("n,batch", [(1537, 40), (1700, 257), (2048, 9), (2057, 64), (3000, 130), (4096, 17)])
+@pytest.mark.parametrize(
+    "n,batch",
+    [(769, 70), (1000, 33), (1024, 5), (1031, 129), (1537, 40), (1700, 257), (2048, 9), (2057, 64), (3000, 130),
+     (4096, 17)],
+)
 @pytest.mark.parametrize("inverse", [False, True])
 def test_bluestein_two_level_lengths_vs_oracle(n, batch, inverse):
-    # convolution lengths 4096 (n = 1537..2048) and 8192 (n = 2057..4096) run the two-level fused
-    # kernel (one exchange into 512-point wave transforms and one back, the filter spectrum in the
-    # waves' frequency order); complex and real input, against the oracle's Bluestein
+    # convolution lengths 2048 (n = 769..1024, and 1031 wrapped by 13), 4096 (n = 1537..2048) and
+    # 8192 (n = 2057..4096) run the two-level fused kernel (one exchange into 512-point wave
+    # transforms and one back, the filter spectrum in the waves' frequency order, the cross
+    # factors formed from a per-lane and a wave-uniform part); complex and real input, against
+    # the oracle's Bluestein
     re, im = seeded_complex(batch, n, seed=n + 13)
     got = _gpu_fft(re, im, inverse)
     ref = oracle.fft_core(re, im, inverse)

@@ -193,7 +193,7 @@ constexpr int kBlueWrapMax = 15;
 // row): offset of the cross-wave twiddle rows in its tables, after the 512-point wave transform's
 // table.
 constexpr int kBlue2lTwOff = 1024;
-__host__ __device__ constexpr bool blue_2l(int m) { return m == 4096 || m == 8192; }
+__host__ __device__ constexpr bool blue_2l(int m) { return m == 2048 || m == 4096 || m == 8192; }
 
 // Bluestein down a strided axis (x viewed as (outer, n, stride)), m <= kMaxStridedBlueM.
 constexpr int kMaxStridedBlueM = 4096;

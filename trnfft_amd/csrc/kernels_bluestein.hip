@@ -146,15 +146,16 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   }
 }
 
-// Two-level fused Bluestein at M = 4096 and 8192: each row is R = M / 512 wavefronts of 512
+// Two-level fused Bluestein at M = 2048, 4096 and 8192: each row is R = M / 512 wavefronts of 512
 // points.  The one-level kernel above synchronises the whole workgroup at every radix pass
 // (about ten barriers per row at M = 8192, and the waves of a one-row-per-CU launch spend most
 // of their cycles waiting), so here the length splits as M = R x 512, n = 512 n_a + n_b,
 // k = k_a + R k_b:
 //   forward: thread t of the row holds x[t + T e] (T = M / 8) and transforms over the n_a it holds
-//     in registers (R = 8: the whole column n_b = t; R = 16: the samples n_a = 2e + p of column n_b
-//     = t % 512, p = t / 512, the 8-point half of the 16-point DFT); one exchange through LDS gives wave w = k_a its values for all 512 n_b
-//     (for R = 16 the radix-2 half: Y_0[k'] + (-1)^q W_16^k' Y_1[k'], w = k' + 8q), times
+//     in registers (R = 4: two 4-point DFTs, columns n_b = t and t + 256; R = 8: the whole column
+//     n_b = t; R = 16: the samples n_a = 2e + p of column n_b = t % 512, p = t / 512, the 8-point
+//     half of the 16-point DFT); one exchange through LDS gives wave w = k_a its values for all
+//     512 n_b (for R = 16 the radix-2 half: Y_0[k'] + (-1)^q W_16^k' Y_1[k'], w = k' + 8q), times
 //     W_M^(n_b k_a); a 512-point transform inside the wave (wave-local exchanges only) leaves
 //     X[k_a + R k_b] with k_b = lane + 64 e;
 //   the filter spectrum is applied in that order (the plan stores H/M permuted to it), then the
@@ -166,10 +167,17 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
 //     chirp, the wrap correction and the stores.
 // Two workgroup barriers per row (one row per workgroup).  tw_f / tw_i: the 512-point transform's
 // table (tfa::make_shape(512, 8)), then from entry kBlue2lTwOff the rows W_M^(+-n_b w), w < R,
-// n_b < 512.  Measured against the one-level kernel (in-run): 256 x 4099 (M = 8192, wrapped) 13.7
-// -> 12.3 us, 256 x 3000 12.4 -> 10.8, 512 x 2000 (4096) 11.2 -> 10.7, 256 x 1700 8.4 -> 7.7; at
-// M = 2048 (four waves per row, two rows per workgroup) it lost at 1024 x 1000 (10.6 -> 10.8 us),
-// so 2048 keeps the one-level kernel.
+// n_b < 512.  A launch of C3a's 1024 rows at M = 2048 is one workgroup per SIMD, so the row's
+// waits make up the kernel's time, and the loads in flight at the first exchange set the first
+// wait: the cross factor W_M^(w (l + 64 e)) is formed as W_M^(w l) (one vector load) times the
+// wave-uniform W_M^(64 w e) (scalar loads) rather than loaded per element.  Measured (in-run):
+// 256 x 4099 (M = 8192, wrapped) 13.7 -> 12.3 us against the one-level kernel, 11.7 with the
+// formed cross factor; 1024 x 1000 (M = 2048) 10.6 (one-level kernel, or two-level with loaded
+// cross factors) -> 9.8; 512 x 1025 9.3 -> 8.2.  Slower where the launch is one round of
+// workgroups: the 512-point transform's twiddles loaded into registers with the row (1024 x 1000
+// 10.2 us, 256 x 4099 13.3-13.7, either table layout) or staged in LDS (11.3 / 12.6: the staging
+// stores wait for every load issued before them); both win only for many rows per CU
+// (4096 x 800: 28.3-29.4 against 31.9 us).
 template <int M>
 struct Blue2lCfg {
   static constexpr int R = M / 512, E = 8, T = M / E, B = 512, PB = lds_pad(B);
@@ -181,7 +189,7 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
     const float2* __restrict__ tw_i, int n, long long batch, float scale, int wrap) {
   using C = Blue2lCfg<M>;
   constexpr int R = C::R, E = C::E, T = C::T, B = C::B, PB = C::PB;
-  static_assert(R == 8 || R == 16, "two-level Bluestein lengths");
+  static_assert(R == 4 || R == 8 || R == 16, "two-level Bluestein lengths");
   __shared__ float2 xbuf[M];        // the forward exchange
   __shared__ float2 warea[R * PB];  // each wave's 512-point exchange area; the inverse exchange
   __shared__ float2 ends[WRAP ? 3 * kBlueWrapMax : 1];  // y[0, wrap), y[L, n), chirp[L, n)
@@ -214,10 +222,13 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
     v[e] = y;
   }
   // the wave's cross twiddles and filter spectrum, requested before the first exchange
+  // W_M^(w (l + 64 e)) = W_M^(w l) W_M^(64 w e): one vector load, the second factor wave-uniform
   float2 tcr[E], hv[E];
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const float2 tb = tw_f[kBlue2lTwOff + w * B + l];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    tcr[e] = tw_f[kBlue2lTwOff + w * B + l + 64 * e];
+    tcr[e] = e == 0 ? tb : cmul(tb, tw_f[kBlue2lTwOff + wu * B + 64 * e]);
     hv[e] = hs[tid + T * e];
   }
   // W_16^j = (cos, -sin)(2 pi j / 16) for the forward sign
@@ -232,10 +243,18 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
     const int p = tid >> 9, nb = tid & 511;
 #pragma unroll
     for (int k = 0; k < 8; ++k) xbuf[(p * 8 + k) * B + nb] = v[k];
-  } else {
+  } else if constexpr (R == 8) {
     Dft<8, -1>::run(v);
 #pragma unroll
     for (int k = 0; k < 8; ++k) xbuf[k * B + tid] = v[k];
+  } else {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float2 u[4] = {v[c], v[c + 2], v[c + 4], v[c + 6]};
+      Dft<4, -1>::run(u);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xbuf[k * B + tid + 256 * c] = u[k];
+    }
   }
   __syncthreads();
   if constexpr (R == 16) {
@@ -274,10 +293,20 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
       else v[k] = cmul(csub(z0, z1), make_float2(kC16[k], kS16[k]));  // W_16^-k (inverse sign)
     }
     Dft<8, 1>::run(v);
-  } else {
+  } else if constexpr (R == 8) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = warea[k * PB + tid];
     Dft<8, 1>::run(v);
+  } else {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      float2 u[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) u[k] = warea[k * PB + tid + 256 * c];
+      Dft<4, 1>::run(u);
+#pragma unroll
+      for (int a = 0; a < 4; ++a) v[2 * a + c] = u[a];
+    }
   }
 #pragma unroll
   for (int e = 0; e < EH; ++e) {

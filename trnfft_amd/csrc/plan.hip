@@ -502,7 +502,7 @@ int tfa_plan_create(tfa_plan** out, const tfa_plan_desc* desc) {
           if ((rc = p->upload(lds_table(mf, 1, tfa::blue_epth(mf)), &p->inv.tw))) break;
         }
         if (m <= tfa::kMaxStridedBlueM) {  // the strided-axis kernel's layout (tfa::lds_epth)
-          if (p->mf == m && tfa::blue_epth((int)m) == tfa::lds_epth((int)m)) {
+          if (p->mf == m && !tfa::blue_2l((int)m) && tfa::blue_epth((int)m) == tfa::lds_epth((int)m)) {
             p->b_tw_sf = p->fwd.tw;
             p->b_tw_si = p->inv.tw;
           } else {
