@@ -199,18 +199,40 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
   const int L = n - wrap;
   // n <= M/2 (+ up to 8 wrapped): element e of a thread can hold a sample only for e < EH
   constexpr int EH = E / 2 + (WRAP ? 1 : 0);
-  float2 v[E], ch[EH];
+  // the cross factor W_M^(w (l + 64 e)) = W_M^(w l) W_M^(64 w e): one vector load and the
+  // wave-uniform second factors (scalar loads, issued first so they land during the row's loads)
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  float2 cf[E];
+#pragma unroll
+  for (int e = 1; e < E; ++e) cf[e] = tw_f[kBlue2lTwOff + wu * B + 64 * e];
+  // the row's loads at a clamped index, without branches: every element's loads are in flight
+  // before the first wait (a load under `if (i < n)` is waited for before the next one issues)
+  float2 ch[EH], xin[EH];
+#pragma unroll
+  for (int e = 0; e < EH; ++e) {
+    const int i = tid + T * e;
+    const int ic = i < n ? i : n - 1;
+    ch[e] = chirp[ic];
+    xin[e] = make_float2(ld_stream(in_re + base + ic), REAL_IN ? 0.0f : ld_stream(in_im + base + ic));
+  }
+  const float2 tb = tw_f[kBlue2lTwOff + w * B + l];
+  float2 hv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) hv[e] = hs[tid + T * e];
+  // the uniform factors are waited for here, while the vector loads are in flight (left to the
+  // compiler, the wrapped kernels issued them just before the first barrier, which then waited)
+#pragma unroll
+  for (int e = 1; e < E; ++e) asm volatile("" ::"s"(cf[e].x), "s"(cf[e].y));
+  float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int i = tid + T * e;
     float2 y = make_float2(0.0f, 0.0f);
     if (e < EH) {
-      const float2 c = i < n ? chirp[i] : make_float2(0.0f, 0.0f);
+      // (a padded slot multiplies the clamped sample by a zero chirp: zero for finite input)
+      const float2 c = i < n ? ch[e < EH ? e : 0] : make_float2(0.0f, 0.0f);
       ch[e < EH ? e : 0] = c;
-      if (i < n) {
-        const float2 x = make_float2(ld_stream(in_re + base + i), REAL_IN ? 0.0f : ld_stream(in_im + base + i));
-        y = cmul(x, c);
-      }
+      y = cmul(xin[e < EH ? e : 0], c);
       if constexpr (WRAP) {
         if (i < wrap) ends[i] = y;
         if (i >= L && i < n) {
@@ -221,21 +243,17 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
     }
     v[e] = y;
   }
-  // the wave's cross twiddles and filter spectrum, requested before the first exchange
-  // W_M^(w (l + 64 e)) = W_M^(w l) W_M^(64 w e): one vector load, the second factor wave-uniform
-  float2 tcr[E], hv[E];
-  const int wu = __builtin_amdgcn_readfirstlane(w);
-  const float2 tb = tw_f[kBlue2lTwOff + w * B + l];
+  float2 tcr[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    tcr[e] = e == 0 ? tb : cmul(tb, tw_f[kBlue2lTwOff + wu * B + 64 * e]);
-    hv[e] = hs[tid + T * e];
-  }
+  for (int e = 0; e < E; ++e) tcr[e] = e == 0 ? tb : cmul(tb, cf[e]);
   // W_16^j = (cos, -sin)(2 pi j / 16) for the forward sign
   constexpr float kC16[8] = {(float)cos2pi(0, 16), (float)cos2pi(1, 16), (float)cos2pi(2, 16), (float)cos2pi(3, 16),
                              (float)cos2pi(4, 16), (float)cos2pi(5, 16), (float)cos2pi(6, 16), (float)cos2pi(7, 16)};
   constexpr float kS16[8] = {(float)sin2pi(0, 16), (float)sin2pi(1, 16), (float)sin2pi(2, 16), (float)sin2pi(3, 16),
                              (float)sin2pi(4, 16), (float)sin2pi(5, 16), (float)sin2pi(6, 16), (float)sin2pi(7, 16)};
+  // W_16^k' (forward sign) for R = 16, k' = w % 8: wave-uniform, loaded before the first exchange
+  const float2 w16 = make_float2(kC16[wu & 7], -kS16[wu & 7]);
+  if constexpr (R == 16) asm volatile("" ::"s"(w16.x), "s"(w16.y));
   // forward, in registers over the n_a each thread holds, then the exchange: xbuf[k_a * 512 + n_b]
   // (R = 16: xbuf[(p * 8 + k') * 512 + n_b] holds the half transform Y_p[k'])
   if constexpr (R == 16) {
@@ -258,9 +276,8 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
   }
   __syncthreads();
   if constexpr (R == 16) {
-    const int kq = w & 7;
-    const float2 w16 = make_float2(kC16[kq], -kS16[kq]);  // W_16^k' (forward sign), wave-uniform
-    const bool neg = w >= 8;
+    const int kq = wu & 7;
+    const bool neg = wu >= 8;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const float2 y0 = xbuf[kq * B + l + 64 * e];
