@@ -60,6 +60,8 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   const long long b = (long long)blockIdx.x * C::XF + xf;
   const bool valid = b < batch;
   const size_t base = (size_t)b * n;
+  // a slot past the last row reads the last row (its results are not stored)
+  const size_t lbase = (size_t)(valid ? b : batch - 1) * n;
   const int L = n - wrap;
   float2* ends = ends_all + (WRAP ? xf * 3 * kBlueWrapMax : 0);
 
@@ -76,19 +78,31 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   constexpr bool PRE = E <= 8;
   constexpr bool PRE2 = E == 12;
   float2 v[E], ch[PRE ? EH : 1], hv[PRE || PRE2 ? E : 1];
+  // the row's loads at a clamped index and without branches, so that every element's load issues
+  // before the first wait (under `if (i < n)` the compiler waited for each load before issuing
+  // the next one); non-temporal: every row is read and written once (C3b 18.4 -> 17.3 us, C3a
+  // 12.0 -> 11.4)
+  float2 cl[EH], xl[EH];
+#pragma unroll
+  for (int e = 0; e < EH; ++e) {
+    const int i = tid + T * e;
+    const int ic = i < n ? i : n - 1;
+    cl[e] = chirp[ic];
+    xl[e] = make_float2(ld_stream(in_re + lbase + ic), REAL_IN ? 0.0f : ld_stream(in_im + lbase + ic));
+  }
+  if constexpr (PRE || PRE2) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) hv[PRE || PRE2 ? e : 0] = hs[tid + T * e];
+  }
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int i = tid + T * e;
-    if constexpr (PRE || PRE2) hv[e] = hs[i];
     float2 y = make_float2(0.0f, 0.0f);
     if (e < EH) {
-      const float2 c = i < n ? chirp[i] : make_float2(0.0f, 0.0f);
+      // (a padded slot multiplies the clamped sample by a zero chirp: zero for finite input)
+      const float2 c = i < n ? cl[e < EH ? e : 0] : make_float2(0.0f, 0.0f);
       if constexpr (PRE) ch[PRE ? e : 0] = c;
-      if (valid && i < n) {
-        // non-temporal: every row is read and written once (C3b 18.4 -> 17.3 us, C3a 12.0 -> 11.4)
-        const float2 x = make_float2(ld_stream(in_re + base + i), REAL_IN ? 0.0f : ld_stream(in_im + base + i));
-        y = cmul(x, c);
-      }
+      y = cmul(xl[e < EH ? e : 0], c);
       if constexpr (WRAP) {
         // (read after the transforms, whose exchanges synchronise the workgroup)
         if (i < wrap) ends[i] = y;
@@ -418,16 +432,23 @@ __global__ __launch_bounds__(C * (M / lds_epth(M))) void strided_blue_kernel(
   const long long col = (tile % tiles_per_block) * C + c;
   const bool valid = col < stride;
   const size_t base = (size_t)b * n * stride + col;
+  // loads at a clamped column and index, without branches, so that every element's loads issue
+  // before the first wait; the padded slots and the columns past the last take a zero chirp
+  const size_t lbase = (size_t)b * n * stride + (valid ? col : stride - 1);
+  float2 xl[E], cl[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = t + T * e;
+    const int ic = i < n ? i : n - 1;
+    const size_t s = lbase + (size_t)ic * stride;
+    xl[e] = make_float2(in_re[s], REAL_IN ? 0.0f : in_im[s]);
+    cl[e] = chirp[ic];
+  }
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int i = t + T * e;
-    float2 y = make_float2(0.0f, 0.0f);
-    if (valid && i < n) {
-      const size_t s = base + (size_t)i * stride;
-      y = cmul(make_float2(in_re[s], REAL_IN ? 0.0f : in_im[s]), chirp[i]);
-    }
-    v[e] = y;
+    v[e] = cmul(xl[e], valid && i < n ? cl[e] : make_float2(0.0f, 0.0f));
   }
   float* my = reinterpret_cast<float*>(lds + c * PADN);
   // next-pass twiddle prefetch from M = 256 (1000-point columns 49.7 -> 46.2 us, the 480 axis of

@@ -68,7 +68,15 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP, TS>::THREADS)) void istft
   const int ta = t0 - halo > 0 ? t0 - halo : 0;          // first frame of the tile
   const int nf = (t0 + owned < n_frames ? t0 + owned : n_frames) - ta;  // frames in the tile (<= FR)
 
-  for (int i = threadIdx.x; i < NFFT; i += THREADS) wl[i] = win[i];
+  // the window is requested first and written to LDS once the tile's loads are in flight (a
+  // load-then-store here waited out a full memory latency before the first spectrum load issued)
+  constexpr int WI = (NFFT + THREADS - 1) / THREADS;
+  float wv[WI];
+#pragma unroll
+  for (int j = 0; j < WI; ++j) {
+    const int i = (int)threadIdx.x + THREADS * j;
+    wv[j] = win[i < NFFT ? i : NFFT - 1];
+  }
   // 1. stage bins: region of pair p = [re_a | im_a | re_b | im_b], F floats each.  Every load of
   //    the tile is issued before the first LDS write (a load-then-store loop would wait out the
   //    full memory latency once per iteration).
@@ -93,6 +101,9 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP, TS>::THREADS)) void istft
         si[it] = *reinterpret_cast<const float*>(bim + o);
       }
     }
+#pragma unroll
+    for (int j = 0; j < WI; ++j)
+      if ((int)threadIdx.x + THREADS * j < NFFT) wl[threadIdx.x + THREADS * j] = wv[j];
     constexpr int DF = THREADS / F, DK = THREADS % F;
     int f = (int)threadIdx.x / F, k = (int)threadIdx.x - f * F;
 #pragma unroll
@@ -144,6 +155,9 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP, TS>::THREADS)) void istft
         ob += stepb;
       }
     }
+#pragma unroll
+    for (int j = 0; j < WI; ++j)
+      if ((int)threadIdx.x + THREADS * j < NFFT) wl[threadIdx.x + THREADS * j] = wv[j];
     float* sreg = lds + (fs >> 1) * RP + (fs & 1) * 2 * F + k0;
 #pragma unroll
     for (int it = 0; it < SI; ++it) {

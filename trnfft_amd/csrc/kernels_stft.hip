@@ -75,25 +75,24 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS_, E_>::THREADS)) void stft_ker
   const float* x = sig + (size_t)b * length;
   const int start = f0 * hop - pad;  // padded-signal origin of the tile's first frame
   const long long span = (long long)(FR - 1) * hop + NFFT;  // (frames past the end count)
-  float wv[E];
+  // the window times hs is formed after the samples' loads are issued (formed first, the window
+  // loads were waited for before the first sample load)
+  float wr[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) wv[e] = win[tid + T * e] * hs;
+  for (int e = 0; e < E; ++e) wr[e] = win[tid + T * e];
   float2 v[E];
+  float a[E], c[E];
   if (start >= 0 && (long long)start + span <= length) {  // block-uniform: no padding inside the tile
     const float* p0 = x + (start + 2 * pl * hop) + tid;
     const float* p1 = p0 + hop;
-    float a[E], c[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) a[e] = LDNT ? ld_stream(p0 + T * e) : p0[T * e];
 #pragma unroll
     for (int e = 0; e < E; ++e) c[e] = LDNT ? ld_stream(p1 + T * e) : p1[T * e];
-#pragma unroll
-    for (int e = 0; e < E; ++e) v[e] = make_float2(a[e] * wv[e], c[e] * wv[e]);
   } else {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int j = tid + T * e;
-      float s[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         // frames past the end (never stored) read the last frame's samples
@@ -103,10 +102,14 @@ __global__ __launch_bounds__((StftCfg<NFFT, PAIRS_, E_>::THREADS)) void stft_ker
         idx = idx < 0 ? -idx : idx;
         idx = idx >= length ? 2 * (length - 1) - idx : idx;
         idx = idx < 0 ? 0 : (idx >= length ? length - 1 : idx);
-        s[h] = x[idx] * wv[e];
+        (h ? c : a)[e] = x[idx];
       }
-      v[e] = make_float2(s[0], s[1]);
     }
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float wv = wr[e] * hs;
+    v[e] = make_float2(a[e] * wv, c[e] * wv);
   }
   float* my = lds + pl * AREA;
   LdsFft<NFFT, E, -1, (T <= 64), false, true, stft_pf(NFFT)>::run(v, my, nullptr, tw, tid);

@@ -51,22 +51,36 @@ __global__ __launch_bounds__((StftBlueCfg<M, E, FR>::THREADS)) void stft_blue_ke
   // block-uniform: no padding anywhere in the tile's span (64-bit: frames past the end count)
   const long long s0 = (long long)f0 * hop - pad;
   const bool interior = s0 >= 0 && s0 + (long long)(FR - 1) * hop + n <= length;
+  // the frame's loads at clamped indices and without branches, so that every element's loads
+  // issue before the first wait (under a bounds test the compiler waited for each element's loads
+  // before issuing the next); a slot past the frame or past the last frame is multiplied by zero
+  float xs[EIN], ws[EIN];
+  float2 cs[EIN];
+#pragma unroll
+  for (int e = 0; e < EIN; ++e) {
+    const int i = tid + T * e;
+    const int ic = i < n ? i : n - 1;
+    int idx = f * hop + ic - pad;
+    if (!interior) {
+      // reflect without repeating the edge sample (torch.nn.functional.pad mode="reflect")
+      idx = idx < 0 ? -idx : idx;
+      idx = idx >= length ? 2 * (length - 1) - idx : idx;
+      idx = idx < 0 ? 0 : (idx >= length ? length - 1 : idx);
+    }
+    xs[e] = x[idx];
+    ws[e] = win[ic];
+    cs[e] = chirp[ic];
+  }
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int i = tid + T * e;
     float2 y = make_float2(0.0f, 0.0f);
-    if (e < EIN && i < n && f < n_frames) {
-      int idx = f * hop + i - pad;
-      if (!interior) {
-        // reflect without repeating the edge sample (torch.nn.functional.pad mode="reflect")
-        idx = idx < 0 ? -idx : idx;
-        idx = idx >= length ? 2 * (length - 1) - idx : idx;
-        idx = idx < 0 ? 0 : (idx >= length ? length - 1 : idx);
-      }
+    if (e < EIN) {
+      const int i = tid + T * e;
+      const float m = (i < n && f < n_frames) ? 1.0f : 0.0f;
       // the reference's order: frame * window, then * chirp (real input: two products)
-      const float xw = x[idx] * win[i];
-      const float2 c = chirp[i];
+      const float xw = xs[e < EIN ? e : 0] * ws[e < EIN ? e : 0] * m;
+      const float2 c = cs[e < EIN ? e : 0];
       y = make_float2(xw * c.x, xw * c.y);
     }
     v[e] = y;
@@ -219,7 +233,15 @@ __global__ __launch_bounds__((IstftBlueCfg<M, E, FR, ADJ>::THREADS)) void istft_
   const int nf = (t0 + owned < n_frames ? t0 + owned : n_frames) - ta;  // frames in the tile (<= FR)
   const int K = n / 2 + 1;  // onesided bins
 
-  for (int i = threadIdx.x; i < n; i += THREADS) wl[i] = win[i];
+  // the window is requested first and written to LDS after the staging (a load-then-store here
+  // waited out a full memory latency before the first spectrum load issued)
+  constexpr int WI = (C::NW + THREADS - 1) / THREADS;
+  float wv[WI];
+#pragma unroll
+  for (int j = 0; j < WI; ++j) {
+    const int i = (int)threadIdx.x + THREADS * j;
+    wv[j] = win[i < n ? i : n - 1];
+  }
   // 1. stage bins: frame f's area = [re (K) | im (K)]; four loads in flight per thread
   if constexpr (FM) {
     // frames-major input (batch, n_frames, K): the tile's frames are consecutive rows, one
@@ -274,6 +296,9 @@ __global__ __launch_bounds__((IstftBlueCfg<M, E, FR, ADJ>::THREADS)) void istft_
       }
     }
   }
+#pragma unroll
+  for (int j = 0; j < WI; ++j)
+    if ((int)threadIdx.x + THREADS * j < n) wl[threadIdx.x + THREADS * j] = wv[j];
   __syncthreads();
   // 2. completed spectrum times the chirp, Bluestein chain
   const int fl = threadIdx.x / T, tid = threadIdx.x % T;
