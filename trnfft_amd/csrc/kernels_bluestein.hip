@@ -581,17 +581,21 @@ __global__ __launch_bounds__((BlueColCfg<M1>::C * BlueColCfg<M1>::T)) void blue_
   const long long b = tile / tiles;
   const int col = (int)(tile % tiles) * C + c;
   const unsigned m = (unsigned)M1 * (unsigned)m2;
-  float2 v[E];
+  // loads at a clamped index without branches (every element's loads issue before the first
+  // wait); the slots past n take a zero chirp
+  float2 xl[E], cl[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int i = (t + T * e) * m2 + col;
-    float2 y = make_float2(0.0f, 0.0f);
-    if (i < n) {
-      const size_t s = (size_t)b * n + i;
-      y = cmul(make_float2(in_re[s], REAL_IN ? 0.0f : in_im[s]), chirp[i]);
-    }
-    v[e] = y;
+    const int ic = i < n ? i : n - 1;
+    const size_t s = (size_t)b * n + ic;
+    xl[e] = make_float2(in_re[s], REAL_IN ? 0.0f : in_im[s]);
+    cl[e] = chirp[ic];
   }
+  float2 v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    v[e] = cmul(xl[e], (t + T * e) * m2 + col < n ? cl[e] : make_float2(0.0f, 0.0f));
   LdsFft<M1, E, -1, false, false, true, blue_split_pf(M1)>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);
   mul_roots<E, T, false>(v, lo, hi, (unsigned)col, (unsigned)t, m - 1, lo_bits);  // W_m^(col*k1)
 #pragma unroll

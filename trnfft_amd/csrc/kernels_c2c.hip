@@ -96,15 +96,27 @@ __global__ __launch_bounds__(C2cSmallCfg<N>::THREADS) void c2c_small_kernel(
     const float2* __restrict__ tw, long long first, long long batch, float scale) {
   using C = C2cSmallCfg<N>;
   constexpr int XS = C::XS, P = C::P, TPR = C::TPR, E = C::E, THREADS = C::THREADS;
+  static_assert(XS * N == THREADS * E, "the tile's floats per plane are E steps of THREADS");
   __shared__ float2 lds[XS * P];
   const long long r0 = first + (long long)blockIdx.x * XS;
   const int count = TAIL ? (int)(batch - r0 < XS ? batch - r0 : XS) * N : XS * N;  // floats per plane
   const size_t g0 = (size_t)r0 * N;
   const float sc = DIR < 0 ? 1.0f : scale;  // inverse: 1/n applied on input (exact for powers of two)
-  for (int i = threadIdx.x; i < count; i += THREADS) {
-    const float xr = ld_stream(in_re + g0 + i);
-    const float xi = REAL_IN ? 0.0f : ld_stream(in_im + g0 + i);
-    lds[(i / N) * P + C::idx(i % N)] = make_float2(xr * sc, xi * sc);
+  // E loads per thread, all issued before the first LDS write (a load-then-store loop waits out
+  // the memory latency once per step); a ragged tail reads its last element again
+  float xr[E], xi[E];
+#pragma unroll
+  for (int u = 0; u < E; ++u) {
+    const int i = (int)threadIdx.x + THREADS * u;
+    const int ic = TAIL && i >= count ? count - 1 : i;
+    xr[u] = ld_stream(in_re + g0 + ic);
+    xi[u] = REAL_IN ? 0.0f : ld_stream(in_im + g0 + ic);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // (else the scheduler pairs each load with its write)
+#pragma unroll
+  for (int u = 0; u < E; ++u) {
+    const int i = (int)threadIdx.x + THREADS * u;
+    if (!TAIL || i < count) lds[(i / N) * P + C::idx(i % N)] = make_float2(xr[u] * sc, xi[u] * sc);
   }
   __syncthreads();
   const int tid = threadIdx.x % TPR;
@@ -122,10 +134,14 @@ __global__ __launch_bounds__(C2cSmallCfg<N>::THREADS) void c2c_small_kernel(
 #pragma unroll
   for (int e = 0; e < E; ++e) row[C::idx(tid + TPR * e)] = v[e];
   __syncthreads();
-  for (int i = threadIdx.x; i < count; i += THREADS) {
-    const float2 y = lds[(i / N) * P + C::idx(i % N)];
-    st_stream(out_re + g0 + i, y.x);
-    st_stream(out_im + g0 + i, y.y);
+#pragma unroll
+  for (int u = 0; u < E; ++u) {
+    const int i = (int)threadIdx.x + THREADS * u;
+    if (!TAIL || i < count) {
+      const float2 y = lds[(i / N) * P + C::idx(i % N)];
+      st_stream(out_re + g0 + i, y.x);
+      st_stream(out_im + g0 + i, y.y);
+    }
   }
 }
 
@@ -209,12 +225,15 @@ __global__ __launch_bounds__(C * (N1 / lds_epth(N1))) void strided_kernel(
   const long long col = (tile % tiles_per_block) * C + c;
   const bool valid = col < stride;
   const size_t base = (size_t)b * N1 * stride + col;
+  // a column past the last reads the last column (unconditional loads: under `valid ?` the
+  // compiler waited for each load before issuing the next); its results are not stored
+  const size_t lbase = valid ? base : base - (size_t)(col - (stride - 1));
 
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const size_t i = base + (size_t)(t + T * e) * stride;
-    v[e] = valid ? make_float2(ld_stream(in_re + i), REAL_IN ? 0.0f : ld_stream(in_im + i)) : make_float2(0.0f, 0.0f);
+    const size_t i = lbase + (size_t)(t + T * e) * stride;
+    v[e] = make_float2(ld_stream(in_re + i), REAL_IN ? 0.0f : ld_stream(in_im + i));
   }
   if constexpr (IL) {
     LdsFft<N1, E, DIR, false, false, true>::run(v, reinterpret_cast<float*>(lds + c * PADN), nullptr, tw, t);

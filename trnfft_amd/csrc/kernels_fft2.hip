@@ -189,12 +189,16 @@ __global__ __launch_bounds__(C * (HR / E_)) void fft2_pass2_kernel(
   // element r1 (input) and q1 (output) of column col in group q2 both live at row q2 + 8*index
   const size_t base = (size_t)b * (8 * HR) * W + (size_t)q2 * W + col;
   const size_t step = (size_t)8 * W;
+  // a column past the last reads the tile's last column (unconditional loads: under `valid ?`
+  // the compiler waited for each load before issuing the next); its results are not stored
+  const int ncol = HALF ? W / 2 + 1 : W;
+  const size_t lbase = valid ? base : base - (size_t)(col - (ncol - 1));
 
   float2 v[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const size_t i = base + (size_t)(t + T * e) * step;
-    v[e] = valid ? make_float2(ld_stream(re + i) * scale, ld_stream(im + i) * scale) : make_float2(0.0f, 0.0f);
+    const size_t i = lbase + (size_t)(t + T * e) * step;
+    v[e] = make_float2(ld_stream(re + i) * scale, ld_stream(im + i) * scale);
   }
   // every value this workgroup loads is consumed by the transform (whose first exchange is a
   // workgroup barrier) before any thread stores; no other workgroup touches these elements
@@ -444,11 +448,25 @@ __global__ __launch_bounds__(1024) void fft2_small_kernel(
   const int count = TAIL ? (int)((batch - i0 < IMG ? batch - i0 : IMG) * P) : IMG * P;
   const size_t g0 = (size_t)i0 * P;
   const float sc = DIR < 0 ? 1.0f : scale;  // inverse: 1/(h*w) on the input (exact, powers of two)
-  for (int i = threadIdx.x; i < count; i += 1024) {
-    const int img = i / P, r = (i % P) / W, c = i % W;
-    const float xr = ld_stream(in_re + g0 + i);
-    const float xi = REAL_IN ? 0.0f : ld_stream(in_im + g0 + i);
-    lds[(img * H + r) * RW + lds_pad(c)] = make_float2(xr * sc, xi * sc);
+  // E loads per thread, all issued before the first LDS write (a ragged tail rereads its last
+  // element)
+  static_assert(IMG * P == 1024 * E, "the tile's floats per plane are E steps of the workgroup");
+  float xr[E], xi[E];
+#pragma unroll
+  for (int u = 0; u < E; ++u) {
+    const int i = (int)threadIdx.x + 1024 * u;
+    const int ic = TAIL && i >= count ? count - 1 : i;
+    xr[u] = ld_stream(in_re + g0 + ic);
+    xi[u] = REAL_IN ? 0.0f : ld_stream(in_im + g0 + ic);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // (else the scheduler pairs each load with its write)
+#pragma unroll
+  for (int u = 0; u < E; ++u) {
+    const int i = (int)threadIdx.x + 1024 * u;
+    if (!TAIL || i < count) {
+      const int img = i / P, r = (i % P) / W, c = i % W;
+      lds[(img * H + r) * RW + lds_pad(c)] = make_float2(xr[u] * sc, xi[u] * sc);
+    }
   }
   __syncthreads();
   float2 v[E];

@@ -69,10 +69,13 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
   const long long b = b0 + xf;
   const bool valid = !TAIL || b < batch;
   float2* m = lds + xf * C::PADR;
-  const float2* src = reinterpret_cast<const float2*>(x + (size_t)b * (2 * H)) + tid;
+  // a slot past the last row reads the last row (unconditional loads: under `valid ?` the
+  // compiler waited for each load before issuing the next); its results are not stored
+  const long long bl = valid ? b : batch - 1;
+  const float2* src = reinterpret_cast<const float2*>(x + (size_t)bl * (2 * H)) + tid;
   float2 v[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) v[e] = valid ? ld_stream2(src + T * e) : make_float2(0.0f, 0.0f);
+  for (int e = 0; e < E; ++e) v[e] = ld_stream2(src + T * e);
   LdsFft<H, E, -1, WL, false, true, real_pf(H)>::run(v, reinterpret_cast<float*>(m), nullptr, tw, tid);
 #pragma unroll
   for (int e = 0; e < E; ++e) m[lds_pad(tid + T * e)] = v[e];
@@ -142,9 +145,24 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
     const int count = rows * (H + 1);
     const float* prr = in_re + (size_t)b0 * (H + 1);
     const float* pii = in_im + (size_t)b0 * (H + 1);
-    for (int i = threadIdx.x; i < count; i += C::THREADS) {
-      const int r = i / (H + 1), k = i - r * (H + 1);
-      lds[r * C::PADR + lds_pad(k)] = make_float2(ld_stream(prr + i), ld_stream(pii + i));
+    // NS loads per thread, all issued before the first LDS write (a ragged tail rereads its
+    // last bin)
+    constexpr int NS = (C::XF * (H + 1) + C::THREADS - 1) / C::THREADS;
+    float2 bs[NS];
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int i = (int)threadIdx.x + C::THREADS * u;
+      const int ic = i < count ? i : count - 1;
+      bs[u] = make_float2(ld_stream(prr + ic), ld_stream(pii + ic));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // (else the scheduler pairs each load with its write)
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int i = (int)threadIdx.x + C::THREADS * u;
+      if (i < count) {
+        const int r = i / (H + 1), k = i - r * (H + 1);
+        lds[r * C::PADR + lds_pad(k)] = bs[u];
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -154,16 +172,22 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
       a[0].y = 0.0f;           // Im X[0] drops out
     }
   } else {
-    const float* pr = in_re + (size_t)b * (H + 1) + tid;
-    const float* pi = in_im + (size_t)b * (H + 1) + tid;
+    // a slot past the last row reads the last row (unconditional loads: under `valid ?` the
+    // compiler waited for each load before issuing the next) and keeps zeros
+    const long long bl = valid ? b : batch - 1;
+    const float* pr = in_re + (size_t)bl * (H + 1) + tid;
+    const float* pi = in_im + (size_t)bl * (H + 1) + tid;
+#pragma unroll
+    for (int e = 0; e < E; ++e) a[e] = make_float2(ld_stream(pr + T * e), ld_stream(pi + T * e));
+    const float xh = ld_stream(in_re + (size_t)bl * (H + 1) + H);  // Re X[H] (every lane: one address)
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      a[e] = valid ? make_float2(ld_stream(pr + T * e), ld_stream(pi + T * e)) : make_float2(0.0f, 0.0f);
+      if (!valid) a[e] = make_float2(0.0f, 0.0f);
       m[lds_pad(tid + T * e)] = a[e];
     }
     if (tid == 0) {
-      m[lds_pad(H)] = make_float2(valid ? ld_stream(pr + H) : 0.0f, 0.0f);  // Im X[H] is never read
-      a[0].y = 0.0f;                                                        // Im X[0] drops out
+      m[lds_pad(H)] = make_float2(valid ? xh : 0.0f, 0.0f);  // Im X[H] is never read
+      a[0].y = 0.0f;                                          // Im X[0] drops out
     }
   }
   exchange_sync<WL>();
@@ -211,7 +235,23 @@ __global__ __launch_bounds__(kRealSmallRows) void r2c_small_kernel(
   float* lf = reinterpret_cast<float*>(lds);
   const long long r0 = first + (long long)blockIdx.x * XS;
   const int rows = TAIL ? (int)(batch - r0 < XS ? batch - r0 : XS) : XS;
-  for (int i = threadIdx.x; i < rows * N; i += XS) lf[(i / N) * PI + i % N] = ld_stream(x + (size_t)r0 * N + i);
+  // N loads per thread, all issued before the first LDS write (a ragged tail rereads its last
+  // sample)
+  {
+    const int cnt = rows * N;
+    float xs[N];
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      const int i = (int)threadIdx.x + XS * u;
+      xs[u] = ld_stream(x + (size_t)r0 * N + (TAIL && i >= cnt ? cnt - 1 : i));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // (else the scheduler pairs each load with its write)
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      const int i = (int)threadIdx.x + XS * u;
+      if (!TAIL || i < cnt) lf[(i / N) * PI + i % N] = xs[u];
+    }
+  }
   __syncthreads();
   float2 z[H];
   const float* row = lf + threadIdx.x * PI;  // rows past a ragged tail hold stale data, never stored
@@ -247,8 +287,24 @@ __global__ __launch_bounds__(kRealSmallRows) void c2r_small_kernel(
   float* lf = reinterpret_cast<float*>(lds);
   const long long r0 = first + (long long)blockIdx.x * XS;
   const int rows = TAIL ? (int)(batch - r0 < XS ? batch - r0 : XS) : XS;
-  for (int i = threadIdx.x; i < rows * PO; i += XS)
-    lds[i] = make_float2(ld_stream(in_re + (size_t)r0 * PO + i), ld_stream(in_im + (size_t)r0 * PO + i));
+  // PO bins per thread, all loads issued before the first LDS write (a ragged tail rereads its
+  // last bin)
+  {
+    const int cnt = rows * PO;
+    float2 bs[PO];
+#pragma unroll
+    for (int u = 0; u < PO; ++u) {
+      const int i = (int)threadIdx.x + XS * u;
+      const size_t o = (size_t)r0 * PO + (TAIL && i >= cnt ? cnt - 1 : i);
+      bs[u] = make_float2(ld_stream(in_re + o), ld_stream(in_im + o));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // (else the scheduler pairs each load with its write)
+#pragma unroll
+    for (int u = 0; u < PO; ++u) {
+      const int i = (int)threadIdx.x + XS * u;
+      if (!TAIL || i < cnt) lds[i] = bs[u];
+    }
+  }
   __syncthreads();
   float2 a[H + 1];
   const float2* bins = lds + threadIdx.x * PO;
