@@ -188,8 +188,9 @@ def test_bluestein_vs_reference_golden(direction):
                                      # 4104 < n <= 4608 (reference m = 16384; 4097..4104 wrap at
                                      # 8192); 4609 pads to 16384
                                      (4097, 3), (4097, 300), (4200, 9), (4608, 70), (4609, 70), (4609, 5),
-                                     # short rows (m <= 256, staged per workgroup): full tiles plus a
-                                     # ragged one, every padded length 4..256 and real input below
+                                     # short rows (m <= 64 staged through LDS as one run per
+                                     # workgroup): full tiles plus a ragged one, every padded length
+                                     # 4..256 and real input below
                                      (2, 600), (5, 1000), (7, 257), (12, 300), (31, 513), (33, 129),
                                      (60, 200), (100, 130), (127, 65), (129, 3)])
 @pytest.mark.parametrize("inverse", [False, True])

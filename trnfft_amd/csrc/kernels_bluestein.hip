@@ -55,6 +55,16 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
                 "wrapped lengths: the corrected outputs (i < wrap, L <= i < n) lie in elements 0, E/2 - 1 and E/2");
   __shared__ float2 lds[C::XF * C::PADN * C::NBUF];  // interleaved (re, im) exchange
   __shared__ float2 ends_all[WRAP ? C::XF * 3 * kBlueWrapMax : 1];  // per row: y[0, wrap), y[L, n), chirp[L, n)
+  // short rows (M <= 64, up to 8 threads per row): a thread's own loads would touch a different
+  // cache line per lane (rows of n <= 32 samples), so the workgroup's XF rows move between HBM and
+  // LDS as one contiguous run of rows * n floats per plane (row r at r * n), NS coalesced steps
+  constexpr bool STG = T <= 8 && !WRAP;
+  constexpr int NS = (C::XF * (M / 2) + C::THREADS - 1) / C::THREADS;
+  __shared__ float2 stg[STG ? C::XF * (M / 2) : 1];
+  const long long r0 = (long long)blockIdx.x * C::XF;
+  const int srows = STG ? (int)(batch - r0 < C::XF ? batch - r0 : C::XF) : 0;
+  const int scnt = srows * n;
+  const size_t g0 = (size_t)r0 * n;
   const int tid = threadIdx.x % T;
   const int xf = threadIdx.x / T;
   const long long b = (long long)blockIdx.x * C::XF + xf;
@@ -83,12 +93,38 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   // the next one); non-temporal: every row is read and written once (C3b 18.4 -> 17.3 us, C3a
   // 12.0 -> 11.4)
   float2 cl[EH], xl[EH];
+  if constexpr (STG) {
+    float sr[NS], si[NS];
 #pragma unroll
-  for (int e = 0; e < EH; ++e) {
-    const int i = tid + T * e;
-    const int ic = i < n ? i : n - 1;
-    cl[e] = chirp[ic];
-    xl[e] = make_float2(ld_stream(in_re + lbase + ic), REAL_IN ? 0.0f : ld_stream(in_im + lbase + ic));
+    for (int u = 0; u < NS; ++u) {
+      const int i = (int)threadIdx.x + C::THREADS * u;
+      const int ic = i < scnt ? i : scnt - 1;
+      sr[u] = ld_stream(in_re + g0 + ic);
+      si[u] = REAL_IN ? 0.0f : ld_stream(in_im + g0 + ic);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // (else the scheduler pairs each load with its write)
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int i = (int)threadIdx.x + C::THREADS * u;
+      if (i < scnt) stg[i] = make_float2(sr[u], si[u]);
+    }
+    __syncthreads();
+    // (rows past the batch read the staging area's stale entries: transformed, never stored)
+#pragma unroll
+    for (int e = 0; e < EH; ++e) {
+      const int i = tid + T * e;
+      const int ic = i < n ? i : n - 1;
+      cl[e] = chirp[ic];
+      xl[e] = stg[xf * n + ic];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EH; ++e) {
+      const int i = tid + T * e;
+      const int ic = i < n ? i : n - 1;
+      cl[e] = chirp[ic];
+      xl[e] = make_float2(ld_stream(in_re + lbase + ic), REAL_IN ? 0.0f : ld_stream(in_im + lbase + ic));
+    }
   }
   if constexpr (PRE || PRE2) {
 #pragma unroll
@@ -128,6 +164,28 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
     }
   }
   LdsFft<M, E, 1, (T <= 64), false, true, PF, C::DB>::run(v, my, nullptr, tw_i, tid);
+  if constexpr (STG) {
+    __syncthreads();  // every row's staged input is read
+#pragma unroll
+    for (int e = 0; e < EH; ++e) {
+      const int i = tid + T * e;
+      if (i < n) {
+        const float2 y = cmul(v[e], PRE ? ch[PRE ? e : 0] : chirp[i]);
+        stg[xf * n + i] = make_float2(y.x * scale, y.y * scale);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int i = (int)threadIdx.x + C::THREADS * u;
+      if (i < scnt) {
+        const float2 y = stg[i];
+        st_stream(out_re + g0 + i, y.x);
+        st_stream(out_im + g0 + i, y.y);
+      }
+    }
+    return;
+  }
   if (valid) {
 #pragma unroll
     for (int e = 0; e < EH; ++e) {
