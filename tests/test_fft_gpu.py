@@ -186,8 +186,10 @@ def test_bluestein_vs_reference_golden(direction):
 @pytest.mark.parametrize("n,batch", [(1000, 1024), (4099, 256), (3, 5), (17, 33), (8193, 4), (20000, 2),
                                      # the mixed-radix fused length 9216 = 12^2 * 64 covers
                                      # 4104 < n <= 4608 (reference m = 16384; 4097..4104 wrap at
-                                     # 8192); 4609 pads to 16384
+                                     # 8192), 12288 = 24 * 8^3 covers 4608 < n <= 6144 from 28 rows
+                                     # (fewer: the split path at 16384); 6145 pads to 16384
                                      (4097, 3), (4097, 300), (4200, 9), (4608, 70), (4609, 70), (4609, 5),
+                                     (5000, 27), (5000, 28), (6144, 41), (6145, 41),
                                      # short rows (m <= 64 staged through LDS as one run per
                                      # workgroup): full tiles plus a ragged one, every padded length
                                      # 4..256 and real input below
@@ -290,9 +292,10 @@ def test_bluestein_wrapped_real_input_and_strided_axis(n):
 @pytest.mark.parametrize("n", [4099, 6000])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_bluestein_fused_and_split_paths_agree(n, inverse):
-    # n = 6000 (m = 16384) runs the fused one-row-per-workgroup kernel for large batches and the
-    # split three-pass path for small ones; n = 4099 runs the wrapped 8192-point fused kernel at
-    # every batch; rows must agree across batch sizes, and both are checked against the oracle
+    # n = 6000 (m = 16384) runs the fused one-row-per-workgroup kernel at 12288 points for large
+    # batches and the split three-pass path at 16384 for small ones; n = 4099 runs the wrapped
+    # 8192-point fused kernel at every batch; rows must agree across batch sizes, and both are
+    # checked against the oracle
     re, im = seeded_complex(2048, n, seed=11)
     fused = _gpu_fft(re, im, inverse)  # 2048 rows: fused kernel
     small = _gpu_fft(re[:5], im[:5], inverse)  # 5 rows: split path for n = 6000

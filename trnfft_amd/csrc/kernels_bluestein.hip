@@ -579,6 +579,7 @@ hipError_t launch_bluestein_fused(int m, const BluesteinArgs& a) {
     case 1536: return launch_blue_m<1536>(a);
     case 3072: return launch_blue_m<3072>(a);
     case 9216: return launch_blue_m<9216>(a);
+    case 12288: return launch_blue_m<12288>(a);
     default: return hipErrorInvalidValue;
   }
 }

@@ -245,10 +245,12 @@ namespace {
 // transforms and the LDS (two workgroups per CU instead of one).
 // Internal length of the fused Bluestein kernel: the wrapped power of two m/2 where at most
 // kBlueWrapMax outputs need correcting, else the shortest measured-faster mixed-radix length that
-// holds the 2n - 1 point convolution, else the reference's m.
+// holds the 2n - 1 point convolution, else the reference's m.  12288 = 24 x 8^3 (four passes at 24
+// elements per thread, 512 threads) for 4608 < n <= 6144: n = 5000 x 838 rows 102.5 -> 69.0 us,
+// n = 6000 x 699 78.2 -> 53.3 against 16384 points.
 int64_t blue_fused_length(int64_t n, int64_t m) {
   if (tfa::blue_wrap_ok((int)std::min<int64_t>(m / 2, 1 << 30)) && 2 * n - 1 - m / 2 <= tfa::kBlueWrapMax) return m / 2;
-  for (int64_t c : {768, 1536, 3072, 9216})
+  for (int64_t c : {768, 1536, 3072, 9216, 12288})
     if (c >= 2 * n - 1 && c < m) return c;
   return m;
 }
@@ -259,7 +261,10 @@ bool blue_use_split(const tfa_plan* p, int64_t batch) {
   // 9216 points: n = 4099 at 9216 points, 1 row 12.7 vs 13.9 us for the split path at 16384, 16 rows
   // 13.8 vs 16.2, 63 rows 14.7 vs 23.0 (the wrapped 8192-point length: 10.8 us at 1 row).  A wrapped
   // 16384-point row (n = 8193..8200) takes one CU 26-29 us, against 18-21 us for the split path at
-  // 32768 below 64 rows (at 256 rows: 32 against 82 us).
+  // 32768 below 64 rows (at 256 rows: 32 against 82 us).  The 12288-point length (24 x 8^3, for
+  // 4608 < n <= 6144 against the reference's 16384) wins from about 28 rows: n = 5000, 24 rows 17.6
+  // vs 17.1 us split, 32 rows 17.7 vs 18.6, 838 rows 69 vs 103 at 16384 points fused.
+  if (p->mf == 12288) return p->blue_split && batch < 28;
   return p->blue_split && batch < kBlueSplitRows && (p->mf == p->m || p->mf >= 16384);
 }
 
