@@ -104,7 +104,8 @@ __host__ __device__ constexpr bool fft2_small_ok(long long h, long long w) {
 // 1536 (E = 24, 256 threads) n = 600: 57.7 against 62.4 at 2048, n = 700: 46.1 against 55.3;
 // 3072 (E = 12, 256 threads) n = 1300: 57.6 against 62.6 at 4096, n = 1500: 52.0 against 55.2;
 // 12288 (E = 24, 512 threads, 24 x 8^3, 191 VGPRs) n = 5000 x 838: 69.0 against 102.5 at 16384.
-// Slower or no better: 96, 192, 384 (within 3 %), 6144 (84 against 79 us at 8192), E = 12 with
+// Slower or no better: 6144 as 24 x 16^2 (E = 24, 256 threads) against the two-level kernel at
+// 8192 (n = 3000 x 1398 72.6 against 51.6 us, 16 rows 12.7 against 8.8), 96, 192, 384 (within 3 %), 6144 (84 against 79 us at 8192), E = 12 with
 // 512 threads at 1536 and 3072 (70-79 us), E = 6 at 768 (65-89 us).  The plan takes these lengths
 // (blue_fused_length) only where they hold 2n - 1 points and are shorter than m.
 __host__ __device__ constexpr int blue_epth(int m) {
