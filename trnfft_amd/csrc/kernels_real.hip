@@ -31,6 +31,9 @@ struct RealCfg {
   // split lines): rfft n = 256 9.5 -> 8.3 us, n = 512 8.5 -> 8.2, n = 128 7.7 -> 7.5 (4M samples);
   // n = 1024 and 2048 measured 1-3 % slower that way
   static constexpr bool STAGE_OUT = XF > 1 && H <= 256;
+  // r2c at n = 32: the real rows come in the same way, one contiguous run per workgroup (rfft
+  // n = 32 18.4 -> 15.5 us for 8M samples; n = 64 even, n = 128 9 % slower)
+  static constexpr bool STAGE_IN = STAGE && H <= 16;
 };
 
 __device__ __forceinline__ float2 ld_stream2(const float2* p) {
@@ -74,13 +77,42 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
   const long long b = b0 + xf;
   const bool valid = !TAIL || b < batch;
   float2* m = lds + xf * C::PADR;
-  // a slot past the last row reads the last row (unconditional loads: under `valid ?` the
-  // compiler waited for each load before issuing the next); its results are not stored
-  const long long bl = valid ? b : batch - 1;
-  const float2* src = reinterpret_cast<const float2*>(x + (size_t)bl * (2 * H)) + tid;
   float2 v[E];
+  if constexpr (C::STAGE_IN) {
+    // short rows: the workgroup's rows are one contiguous run of rows * 2H floats, loaded as such
+    // (a thread's own float2 loads would cover 32-byte pieces of 16 rows per instruction) into the
+    // bins' staging area, row r at r * (2H + 2) floats (an odd float2 pitch across rows)
+    constexpr int NS = C::XF * 2 * H / C::THREADS;
+    static_assert(NS * C::THREADS == C::XF * 2 * H, "the run is NS steps of the workgroup");
+    const long long left = batch - b0;
+    const int cnt = (TAIL ? (int)(left < C::XF ? left : C::XF) : C::XF) * 2 * H;
+    const float* src0 = x + (size_t)b0 * (2 * H);
+    float xs[NS];
 #pragma unroll
-  for (int e = 0; e < E; ++e) v[e] = ld_stream2(src + T * e);
+    for (int u = 0; u < NS; ++u) {
+      const int i = (int)threadIdx.x + C::THREADS * u;
+      xs[u] = ld_stream(src0 + (TAIL && i >= cnt ? cnt - 1 : i));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // (else the scheduler pairs each load with its write)
+    float* sf = reinterpret_cast<float*>(stage);
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int i = (int)threadIdx.x + C::THREADS * u;
+      if (!TAIL || i < cnt) sf[(i / (2 * H)) * (2 * H + 2) + i % (2 * H)] = xs[u];
+    }
+    __syncthreads();
+    // (rows past the batch read stale entries: transformed, never stored)
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = stage[xf * (H + 1) + tid + T * e];
+    __syncthreads();  // the area takes the bins below
+  } else {
+    // a slot past the last row reads the last row (unconditional loads: under `valid ?` the
+    // compiler waited for each load before issuing the next); its results are not stored
+    const long long bl = valid ? b : batch - 1;
+    const float2* src = reinterpret_cast<const float2*>(x + (size_t)bl * (2 * H)) + tid;
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = ld_stream2(src + T * e);
+  }
   LdsFft<H, E, -1, WL, false, true, real_pf(H)>::run(v, reinterpret_cast<float*>(m), nullptr, tw, tid);
 #pragma unroll
   for (int e = 0; e < E; ++e) m[lds_pad(tid + T * e)] = v[e];
