@@ -113,6 +113,9 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = ld_stream2(src + T * e);
   }
+  // the post-processing root W_N^tid, requested with the row (read where used, its load was
+  // waited for after the transform)
+  const float2 tw0 = twr[tid];
   LdsFft<H, E, -1, WL, false, true, real_pf(H)>::run(v, reinterpret_cast<float*>(m), nullptr, tw, tid);
 #pragma unroll
   for (int e = 0; e < E; ++e) m[lds_pad(tid + T * e)] = v[e];
@@ -121,7 +124,7 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void r2c_kernel(
   float* qr = out_re + (size_t)b * (H + 1) + tid;
   float* qi = out_im + (size_t)b * (H + 1) + tid;
   float2 wk[E];
-  TwRow<E, -1>::fill(wk, twr[tid]);  // W_N^k, k = tid + T e (9.8 -> 9.1 us against E table loads)
+  TwRow<E, -1>::fill(wk, tw0);  // W_N^k, k = tid + T e (9.8 -> 9.1 us against E table loads)
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int k = tid + T * e;
@@ -177,7 +180,11 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
   const long long b = b0 + xf;
   const bool valid = !TAIL || b < batch;
   float2* m = lds + xf * C::PADR;
-  float2 a[E];
+  // tk: the post-processing roots W_N^k requested with the bins from H = 512 (irfft n = 1024
+  // 8.02 -> 7.91 us, n = 2048 8.96 -> 8.83); read where used below that (n = 256 9.4 against 10.2
+  // us requested early, n = 128 7.6 against 8.5)
+  constexpr bool TKP = H >= 512;
+  float2 a[E], tk[TKP ? E : 1];
   if constexpr (C::STAGE) {
     // the rows b0 .. b0 + rows - 1 of bins are one contiguous run of rows * (H + 1) floats per
     // plane: loaded as such into each row's LDS area (bin k of row r at r * PADR + lds_pad(k))
@@ -221,15 +228,19 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
 #pragma unroll
     for (int e = 0; e < E; ++e) a[e] = make_float2(ld_stream(pr + T * e), ld_stream(pi + T * e));
     const float xh = ld_stream(in_re + (size_t)bl * (H + 1) + H);  // Re X[H] (every lane: one address)
+    if constexpr (TKP) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) tk[TKP ? e : 0] = twr[tid + T * e];
+    }
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       if (!valid) a[e] = make_float2(0.0f, 0.0f);
       m[lds_pad(tid + T * e)] = a[e];
     }
-    if (tid == 0) {
-      m[lds_pad(H)] = make_float2(valid ? xh : 0.0f, 0.0f);  // Im X[H] is never read
-      a[0].y = 0.0f;                                          // Im X[0] drops out
-    }
+    // every lane of the row writes the same value (a store under `tid == 0` had the compiler sink
+    // the load into that branch, one more memory round trip); Im X[H] is never read
+    m[lds_pad(H)] = make_float2(valid ? xh : 0.0f, 0.0f);
+    if (tid == 0) a[0].y = 0.0f;  // Im X[0] drops out
   }
   exchange_sync<WL>();
   float2 v[E];
@@ -240,7 +251,8 @@ __global__ __launch_bounds__((RealCfg<H, E_, THR>::THREADS)) void c2r_kernel(
     const float2 z = m[lds_pad(H - k)];
     const float2 c = make_float2(z.x, k == 0 ? 0.0f : -z.y);  // conj X[H-k]
     const float2 sum = cadd(a[e], c);
-    const float2 dif = cmul(csub(a[e], c), make_float2(twr[k].x, -twr[k].y));  // x W_N^-k
+    const float2 t = TKP ? tk[TKP ? e : 0] : twr[k];
+    const float2 dif = cmul(csub(a[e], c), make_float2(t.x, -t.y));  // x W_N^-k
     v[e] = make_float2((sum.x - dif.y) * scale, (sum.y + dif.x) * scale);         // sum + i dif
   }
   exchange_sync<WL>();  // the transform below reuses this transform's LDS
