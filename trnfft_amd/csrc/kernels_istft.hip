@@ -102,8 +102,9 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP, TS>::THREADS)) void istft
       }
     }
 #pragma unroll
-    for (int j = 0; j < WI; ++j)
-      if ((int)threadIdx.x + THREADS * j < NFFT) wl[threadIdx.x + THREADS * j] = wv[j];
+    for (int j = 0; j < WI; ++j)  // (every lane in range when the steps cover the window exactly:
+                                  // no branch for the compiler to sink the window's load into)
+      if (THREADS * WI == NFFT || (int)threadIdx.x + THREADS * j < NFFT) wl[threadIdx.x + THREADS * j] = wv[j];
     constexpr int DF = THREADS / F, DK = THREADS % F;
     int f = (int)threadIdx.x / F, k = (int)threadIdx.x - f * F;
 #pragma unroll
@@ -156,15 +157,20 @@ __global__ __launch_bounds__((IstftCfg<NFFT, E_, MAXP, TS>::THREADS)) void istft
       }
     }
 #pragma unroll
-    for (int j = 0; j < WI; ++j)
-      if ((int)threadIdx.x + THREADS * j < NFFT) wl[threadIdx.x + THREADS * j] = wv[j];
+    for (int j = 0; j < WI; ++j)  // (every lane in range when the steps cover the window exactly:
+                                  // no branch for the compiler to sink the window's load into)
+      if (THREADS * WI == NFFT || (int)threadIdx.x + THREADS * j < NFFT) wl[threadIdx.x + THREADS * j] = wv[j];
     float* sreg = lds + (fs >> 1) * RP + (fs & 1) * 2 * F + k0;
+    // a lane past the last bin row writes its (clamped) values to the pair region's unused tail:
+    // a store under `k < F` had the compiler sink that step's loads into the branch, one more
+    // memory round trip for the workgroup
+    float* spare = lds + (fs >> 1) * RP + 4 * F;
+    static_assert(RP >= 4 * F + 2, "a pair region keeps two spare floats past its bins");
 #pragma unroll
     for (int it = 0; it < SI; ++it) {
-      if (k0 + KS * it < F) {
-        sreg[KS * it] = sr[it];
-        sreg[F + KS * it] = si[it];
-      }
+      const bool in = k0 + KS * it < F;
+      *(in ? sreg + KS * it : spare) = sr[it];
+      *(in ? sreg + F + KS * it : spare + 1) = si[it];
     }
   }
   __syncthreads();
