@@ -257,13 +257,14 @@ def test_bluestein_wrapped_lengths_vs_oracle(n, batch, inverse):
 @pytest.mark.parametrize(
     "n,batch",
     [(769, 70), (1000, 33), (1024, 5), (1031, 129), (1537, 40), (1700, 257), (2048, 9), (2057, 64), (3000, 130),
-     (4096, 17)],
+     (4096, 17), (6145, 40), (7000, 36), (8192, 37), (8193, 9), (8200, 50)],
 )
 @pytest.mark.parametrize("inverse", [False, True])
 def test_bluestein_two_level_lengths_vs_oracle(n, batch, inverse):
-    # convolution lengths 2048 (n = 769..1024, and 1031 wrapped by 13), 4096 (n = 1537..2048) and
-    # 8192 (n = 2057..4096) run the two-level fused kernel (one exchange into 512-point wave
-    # transforms and one back, the filter spectrum in the waves' frequency order, the cross
+    # convolution lengths 2048 (n = 769..1024, and 1031 wrapped by 13), 4096 (n = 1537..2048),
+    # 8192 (n = 2057..4096) and 16384 (n = 6145..8192 from 36 rows, 8193..8200 wrapped at every
+    # batch) run the two-level fused kernel (one exchange into 512-point wave transforms, 1024-point
+    # ones at 16384, and one back, the filter spectrum in the waves' frequency order, the cross
     # factors formed from a per-lane and a wave-uniform part); complex and real input, against
     # the oracle's Bluestein
     re, im = seeded_complex(batch, n, seed=n + 13)
@@ -289,7 +290,7 @@ def test_bluestein_wrapped_real_input_and_strided_axis(n):
         assert rel_l2(Y.real.t(), Y.imag.t(), *ref) <= tol_bluestein(n)
 
 
-@pytest.mark.parametrize("n", [4099, 6000])
+@pytest.mark.parametrize("n", [4099, 6000, 7000])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_bluestein_fused_and_split_paths_agree(n, inverse):
     # n = 6000 (m = 16384) runs the fused one-row-per-workgroup kernel at 12288 points for large

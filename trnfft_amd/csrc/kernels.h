@@ -192,8 +192,13 @@ constexpr int kBlueWrapMax = 15;
 // Two-level fused Bluestein kernel (lengths M = 4096, 8192: M / 512 wavefronts of 512 points per
 // row): offset of the cross-wave twiddle rows in its tables, after the 512-point wave transform's
 // table.
-constexpr int kBlue2lTwOff = 1024;
-__host__ __device__ constexpr bool blue_2l(int m) { return m == 2048 || m == 4096 || m == 8192; }
+__host__ __device__ constexpr bool blue_2l(int m) { return m == 2048 || m == 4096 || m == 8192 || m == 16384; }
+// its wave transform length B and elements per lane (16384 = 16 waves x 1024 points, 16 per lane;
+// the others 512-point waves, 8 per lane), and the entry of its tables where the cross factors
+// W_m^(n_b w) start (after the wave transform's table)
+__host__ __device__ constexpr int blue_2l_b(int m) { return m == 16384 ? 1024 : 512; }
+__host__ __device__ constexpr int blue_2l_e(int m) { return m == 16384 ? 16 : 8; }
+__host__ __device__ constexpr int blue_2l_twoff(int m) { return m == 16384 ? 2048 : 1024; }
 
 // Bluestein down a strided axis (x viewed as (outer, n, stride)), m <= kMaxStridedBlueM.
 constexpr int kMaxStridedBlueM = 4096;

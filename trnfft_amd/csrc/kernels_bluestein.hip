@@ -218,8 +218,11 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
   }
 }
 
-// Two-level fused Bluestein at M = 2048, 4096 and 8192: each row is R = M / 512 wavefronts of 512
-// points.  The one-level kernel above synchronises the whole workgroup at every radix pass
+// Two-level fused Bluestein at M = 2048, 4096, 8192 and 16384: each row is R = M / B wavefronts of
+// B points (B = 512 with 8 elements per lane; at 16384 B = 1024 with 16 per lane, 16 waves, and
+// the filter spectrum and output chirp read where used so that the transforms keep their
+// registers: 80 -> 57.5 us for 680 rows of n = 6145, 56 -> 42 for 300 wrapped rows of 8193,
+// against the one-level kernel).  The one-level kernel above synchronises the whole workgroup at every radix pass
 // (about ten barriers per row at M = 8192, and the waves of a one-row-per-CU launch spend most
 // of their cycles waiting), so here the length splits as M = R x 512, n = 512 n_a + n_b,
 // k = k_a + R k_b:
@@ -252,7 +255,9 @@ __global__ __launch_bounds__((BlueCfg<M, E_, THR>::THREADS)) void bluestein_fuse
 // (4096 x 800: 28.3-29.4 against 31.9 us).
 template <int M>
 struct Blue2lCfg {
-  static constexpr int R = M / 512, E = 8, T = M / E, B = 512, PB = lds_pad(B);
+  static constexpr int B = blue_2l_b(M), E = blue_2l_e(M), R = M / B, T = M / E, PB = lds_pad(B);
+  static constexpr int TWOFF = blue_2l_twoff(M);
+  static_assert(make_shape(B, E).twoff[make_shape(B, E).npass] + 2 <= TWOFF, "the wave table fits before the cross rows");
 };
 template <int M, bool REAL_IN, bool WRAP>
 __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
@@ -261,9 +266,18 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
     const float2* __restrict__ tw_i, int n, long long batch, float scale, int wrap) {
   using C = Blue2lCfg<M>;
   constexpr int R = C::R, E = C::E, T = C::T, B = C::B, PB = C::PB;
-  static_assert(R == 4 || R == 8 || R == 16, "two-level Bluestein lengths");
-  __shared__ float2 xbuf[M];        // the forward exchange
-  __shared__ float2 warea[R * PB];  // each wave's 512-point exchange area; the inverse exchange
+  constexpr int TWOFF = C::TWOFF;
+  // the register DFT over n_a: half of it per thread (R = 2E, two threads per column), all of it
+  // (R = E) or two quarter-length ones (R = E / 2, a thread holds two columns)
+  static_assert((R == 2 * E && E == 8) || R == E || (R * 2 == E && E == 8), "two-level Bluestein lengths");
+  constexpr bool PS = R == 2 * E;  // two threads per column (the radix-2 split of the R-point DFT)
+  // with R <= E wave w reads back only region w of the forward exchange, so the regions are the
+  // waves' own transform areas (stride PB); R = 2E reads two regions per wave (its own buffer)
+  constexpr bool ALIAS = R <= E;
+  constexpr int XS = ALIAS ? PB : B;
+  __shared__ float2 xbuf[ALIAS ? 2 : M];  // the forward exchange (R = 2E)
+  __shared__ float2 warea[R * PB];  // each wave's B-point exchange area; the inverse exchange
+  float2* const xb = ALIAS ? warea : xbuf;
   __shared__ float2 ends[WRAP ? 3 * kBlueWrapMax : 1];  // y[0, wrap), y[L, n), chirp[L, n)
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63;
@@ -276,7 +290,7 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
   const int wu = __builtin_amdgcn_readfirstlane(w);
   float2 cf[E];
 #pragma unroll
-  for (int e = 1; e < E; ++e) cf[e] = tw_f[kBlue2lTwOff + wu * B + 64 * e];
+  for (int e = 1; e < E; ++e) cf[e] = tw_f[TWOFF + wu * B + 64 * e];
   // the row's loads at a clamped index, without branches: every element's loads are in flight
   // before the first wait (a load under `if (i < n)` is waited for before the next one issues)
   float2 ch[EH], xin[EH];
@@ -287,10 +301,15 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
     ch[e] = chirp[ic];
     xin[e] = make_float2(ld_stream(in_re + base + ic), REAL_IN ? 0.0f : ld_stream(in_im + base + ic));
   }
-  const float2 tb = tw_f[kBlue2lTwOff + w * B + l];
-  float2 hv[E];
+  const float2 tb = tw_f[TWOFF + w * B + l];
+  // E = 16: the filter spectrum and the output chirp are read where used and the cross factors
+  // formed where used (held through the transforms, they spilled registers)
+  constexpr bool HOLD = E <= 8;
+  float2 hv[HOLD ? E : 1];
+  if constexpr (HOLD) {
 #pragma unroll
-  for (int e = 0; e < E; ++e) hv[e] = hs[tid + T * e];
+    for (int e = 0; e < E; ++e) hv[HOLD ? e : 0] = hs[tid + T * e];
+  }
   // the uniform factors are waited for here, while the vector loads are in flight (left to the
   // compiler, the wrapped kernels issued them just before the first barrier, which then waited)
 #pragma unroll
@@ -315,9 +334,12 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
     }
     v[e] = y;
   }
-  float2 tcr[E];
+  float2 tcr[HOLD ? E : 1];
+  auto cross = [&](int e) { return e == 0 ? tb : cmul(tb, cf[e]); };
+  if constexpr (HOLD) {
 #pragma unroll
-  for (int e = 0; e < E; ++e) tcr[e] = e == 0 ? tb : cmul(tb, cf[e]);
+    for (int e = 0; e < E; ++e) tcr[HOLD ? e : 0] = cross(e);
+  }
   // W_16^j = (cos, -sin)(2 pi j / 16) for the forward sign
   constexpr float kC16[8] = {(float)cos2pi(0, 16), (float)cos2pi(1, 16), (float)cos2pi(2, 16), (float)cos2pi(3, 16),
                              (float)cos2pi(4, 16), (float)cos2pi(5, 16), (float)cos2pi(6, 16), (float)cos2pi(7, 16)};
@@ -325,56 +347,62 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
                              (float)sin2pi(4, 16), (float)sin2pi(5, 16), (float)sin2pi(6, 16), (float)sin2pi(7, 16)};
   // W_16^k' (forward sign) for R = 16, k' = w % 8: wave-uniform, loaded before the first exchange
   const float2 w16 = make_float2(kC16[wu & 7], -kS16[wu & 7]);
-  if constexpr (R == 16) asm volatile("" ::"s"(w16.x), "s"(w16.y));
-  // forward, in registers over the n_a each thread holds, then the exchange: xbuf[k_a * 512 + n_b]
-  // (R = 16: xbuf[(p * 8 + k') * 512 + n_b] holds the half transform Y_p[k'])
-  if constexpr (R == 16) {
-    Dft<8, -1>::run(v);
-    const int p = tid >> 9, nb = tid & 511;
+  if constexpr (PS) asm volatile("" ::"s"(w16.x), "s"(w16.y));
+  // forward, in registers over the n_a each thread holds, then the exchange: xb[k_a * XS + n_b]
+  // (R = 2E: xb[(p * E + k') * XS + n_b] holds the half transform Y_p[k'])
+  if constexpr (PS) {
+    Dft<E, -1>::run(v);
+    const int p = tid / B, nb = tid % B;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) xbuf[(p * 8 + k) * B + nb] = v[k];
-  } else if constexpr (R == 8) {
-    Dft<8, -1>::run(v);
+    for (int k = 0; k < E; ++k) xb[(p * E + k) * XS + nb] = v[k];
+  } else if constexpr (R == E) {
+    Dft<E, -1>::run(v);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) xbuf[k * B + tid] = v[k];
+    for (int k = 0; k < E; ++k) xb[k * XS + tid] = v[k];
   } else {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       float2 u[4] = {v[c], v[c + 2], v[c + 4], v[c + 6]};
       Dft<4, -1>::run(u);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) xbuf[k * B + tid + 256 * c] = u[k];
+      for (int k = 0; k < 4; ++k) xb[k * XS + tid + T * c] = u[k];
     }
   }
   __syncthreads();
-  if constexpr (R == 16) {
+  if constexpr (PS) {
     const int kq = wu & 7;
     const bool neg = wu >= 8;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const float2 y0 = xbuf[kq * B + l + 64 * e];
-      const float2 y1 = cmul(xbuf[(8 + kq) * B + l + 64 * e], w16);
-      v[e] = cmul(neg ? csub(y0, y1) : cadd(y0, y1), tcr[e]);
+      const float2 y0 = xb[kq * XS + l + 64 * e];
+      const float2 y1 = cmul(xb[(8 + kq) * XS + l + 64 * e], w16);
+      v[e] = cmul(neg ? csub(y0, y1) : cadd(y0, y1), tcr[HOLD ? e : 0]);
     }
   } else {
 #pragma unroll
-    for (int e = 0; e < E; ++e) v[e] = cmul(xbuf[w * B + l + 64 * e], tcr[e]);
+    for (int e = 0; e < E; ++e) v[e] = cmul(xb[w * XS + l + 64 * e], HOLD ? tcr[HOLD ? e : 0] : cross(e));
   }
+  // (aliased: the wave's transform overwrites region w, which only this wave has read since the
+  // barrier)
   float* wa = reinterpret_cast<float*>(warea + w * PB);
-  LdsFft<B, E, -1, true, false, true, true>::run(v, wa, nullptr, tw_f, l);
+  constexpr bool PF = E <= 8;  // the next pass's twiddles prefetched (E = 16: registers)
+  LdsFft<B, E, -1, true, false, true, PF>::run(v, wa, nullptr, tw_f, l);
 #pragma unroll
-  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], hv[e]);
-  LdsFft<B, E, 1, true, false, true, true>::run(v, wa, nullptr, tw_i, l);
+  for (int e = 0; e < E; ++e) v[e] = cmul(v[e], HOLD ? hv[HOLD ? e : 0] : hs[tid + T * e]);
+  LdsFft<B, E, 1, true, false, true, PF>::run(v, wa, nullptr, tw_i, l);
   // the wave's own exchange area takes its result (its last reads of the area came before the
   // transform's final wave barrier), so no barrier guards the first exchange's buffer
 #pragma unroll
-  for (int e = 0; e < E; ++e) warea[w * PB + l + 64 * e] = cmul(v[e], make_float2(tcr[e].x, -tcr[e].y));
+  for (int e = 0; e < E; ++e) {
+    const float2 t = HOLD ? tcr[HOLD ? e : 0] : cross(e);
+    warea[w * PB + l + 64 * e] = cmul(v[e], make_float2(t.x, -t.y));
+  }
   __syncthreads();
   // inverse over k_a in registers: y[t + T e] into v[e]
-  if constexpr (R == 16) {
+  if constexpr (PS) {
     // u[k'] = Z[k'] + Z[k' + 8] (p = 0) or (Z[k'] - Z[k' + 8]) W_16^-k' (p = 1), then the 8-point
-    // inverse DFT over k' gives y[512 (2e + p) + n_b]
-    const int p = tid >> 9, nb = tid & 511;
+    // inverse DFT over k' gives y[B (2e + p) + n_b]
+    const int p = tid / B, nb = tid % B;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const float2 z0 = warea[k * PB + nb], z1 = warea[(k + 8) * PB + nb];
@@ -382,16 +410,16 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
       else v[k] = cmul(csub(z0, z1), make_float2(kC16[k], kS16[k]));  // W_16^-k (inverse sign)
     }
     Dft<8, 1>::run(v);
-  } else if constexpr (R == 8) {
+  } else if constexpr (R == E) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = warea[k * PB + tid];
-    Dft<8, 1>::run(v);
+    for (int k = 0; k < E; ++k) v[k] = warea[k * PB + tid];
+    Dft<E, 1>::run(v);
   } else {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       float2 u[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) u[k] = warea[k * PB + tid + 256 * c];
+      for (int k = 0; k < 4; ++k) u[k] = warea[k * PB + tid + T * c];
       Dft<4, 1>::run(u);
 #pragma unroll
       for (int a = 0; a < 4; ++a) v[2 * a + c] = u[a];
@@ -420,7 +448,7 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
           }
         }
       }
-      const float2 y = cmul(cv, ch[e]);
+      const float2 y = cmul(cv, HOLD ? ch[e] : chirp[i]);  // (E = 16: read again, not held)
       st_stream(out_re + base + i, y.x * scale);
       st_stream(out_im + base + i, y.y * scale);
     }

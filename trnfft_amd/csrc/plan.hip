@@ -71,22 +71,24 @@ struct DevBuf {
   void* p = nullptr;
 };
 
-// Tables of the two-level fused Bluestein kernel at length m (tfa::blue_2l: m / 512 wavefronts of
-// 512 points per row): the 512-point wave transform's table (make_shape(512, 8)), then from entry
-// kBlue2lTwOff the rows W_m^(n_b w) (sign dir), w < m / 512, n_b < 512.
+// Tables of the two-level fused Bluestein kernel at length m (tfa::blue_2l: m / b wavefronts of
+// b = tfa::blue_2l_b(m) points per row, e = tfa::blue_2l_e(m) per lane): the wave transform's
+// table (make_shape(b, e)), then from entry tfa::blue_2l_twoff(m) the rows W_m^(n_b w) (sign dir),
+// w < m / b, n_b < b.
 std::vector<float2> blue_2l_table(int m, int dir) {
-  const int r = m / 512;
-  std::vector<float2> t = lds_table(512, dir, 8);
-  t.resize((size_t)tfa::kBlue2lTwOff + (size_t)r * 512, make_float2(1.0f, 0.0f));
+  const int b = tfa::blue_2l_b(m), r = m / b, off = tfa::blue_2l_twoff(m);
+  std::vector<float2> t = lds_table(b, dir, tfa::blue_2l_e(m));
+  t.resize((size_t)off + (size_t)r * b, make_float2(1.0f, 0.0f));
   for (int w = 0; w < r; ++w)
-    for (int nb = 0; nb < 512; ++nb) t[(size_t)tfa::kBlue2lTwOff + w * 512 + nb] = unit_root((int64_t)nb * w, m, dir);
+    for (int nb = 0; nb < b; ++nb) t[(size_t)off + (size_t)w * b + nb] = unit_root((int64_t)nb * w, m, dir);
   return t;
 }
 
-// The filter spectrum in the two-level kernel's frequency order: entry t + (m / 8) e of a row
-// (wave w = t / 64, lane l = t % 64) holds frequency w + (m / 512) (l + 64 e).
+// The filter spectrum in the two-level kernel's frequency order: entry t + (m / e) j of a row
+// (wave w = t / 64, lane l = t % 64, element j) holds frequency w + (m / b) (l + 64 j).
 std::vector<float2> blue_2l_permute(const std::vector<float2>& h) {
-  const size_t m = h.size(), tt = m / 8, r = m / 512;
+  const int mi = (int)h.size();
+  const size_t m = h.size(), tt = m / tfa::blue_2l_e(mi), r = m / tfa::blue_2l_b(mi);
   std::vector<float2> out(m);
   for (size_t j = 0; j < m; ++j) {
     const size_t e = j / tt, w = (j % tt) >> 6, l = j & 63;
@@ -259,13 +261,16 @@ bool blue_use_split(const tfa_plan* p, int64_t batch) {
   if (!p->blue_fused) return true;
   // With few rows the fused kernel's shorter internal lengths still win where they are at most
   // 9216 points: n = 4099 at 9216 points, 1 row 12.7 vs 13.9 us for the split path at 16384, 16 rows
-  // 13.8 vs 16.2, 63 rows 14.7 vs 23.0 (the wrapped 8192-point length: 10.8 us at 1 row).  A wrapped
-  // 16384-point row (n = 8193..8200) takes one CU 26-29 us, against 18-21 us for the split path at
-  // 32768 below 64 rows (at 256 rows: 32 against 82 us).  The 12288-point length (24 x 8^3, for
-  // 4608 < n <= 6144 against the reference's 16384) wins from about 28 rows: n = 5000, 24 rows 17.6
-  // vs 17.1 us split, 32 rows 17.7 vs 18.6, 838 rows 69 vs 103 at 16384 points fused.
+  // 13.8 vs 16.2, 63 rows 14.7 vs 23.0 (the wrapped 8192-point length: 10.8 us at 1 row).  The
+  // 12288-point length (24 x 8^3, for 4608 < n <= 6144 against the reference's 16384) wins from
+  // about 28 rows: n = 5000, 24 rows 17.6 vs 17.1 us split, 32 rows 17.7 vs 18.6, 838 rows 69 vs
+  // 103 at 16384 points fused.
   if (p->mf == 12288) return p->blue_split && batch < 28;
-  return p->blue_split && batch < kBlueSplitRows && (p->mf == p->m || p->mf >= 16384);
+  // The two-level kernel at 16384 points wins from about 36 rows at the reference's m (n = 7000:
+  // 32 rows 19.1 vs 18.9 us split, 48 rows 19.2 vs 21.1) and at every batch where it wraps
+  // (n = 8193: 8 rows 19.4 vs 20.6 us for the split path at 32768).
+  if (p->mf == 16384) return p->blue_split && p->mf == p->m && batch < 36;
+  return p->blue_split && batch < kBlueSplitRows && p->mf == p->m;
 }
 
 size_t c2c_workspace(const C2cTables& t, int64_t batch) {
