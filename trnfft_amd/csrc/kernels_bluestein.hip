@@ -345,13 +345,21 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
                              (float)cos2pi(4, 16), (float)cos2pi(5, 16), (float)cos2pi(6, 16), (float)cos2pi(7, 16)};
   constexpr float kS16[8] = {(float)sin2pi(0, 16), (float)sin2pi(1, 16), (float)sin2pi(2, 16), (float)sin2pi(3, 16),
                              (float)sin2pi(4, 16), (float)sin2pi(5, 16), (float)sin2pi(6, 16), (float)sin2pi(7, 16)};
-  // W_16^k' (forward sign) for R = 16, k' = w % 8: wave-uniform, loaded before the first exchange
-  const float2 w16 = make_float2(kC16[wu & 7], -kS16[wu & 7]);
-  if constexpr (PS) asm volatile("" ::"s"(w16.x), "s"(w16.y));
   // forward, in registers over the n_a each thread holds, then the exchange: xb[k_a * XS + n_b]
-  // (R = 2E: xb[(p * E + k') * XS + n_b] holds the half transform Y_p[k'])
+  // (R = 2E: xb[(p * E + k') * XS + n_b] holds the half transform Y_p[k'], times W_16^k' for p = 1)
   if constexpr (PS) {
     Dft<E, -1>::run(v);
+    // p = 1 (the upper B-thread half, wave-uniform) applies the combination's twiddle W_16^k'
+    // with compile-time constants here, so the reading waves only add or subtract the halves
+    if (wu >= B / 64) {
+      v[1] = twiddle_const<1, 16, -1>(v[1]);
+      v[2] = twiddle_const<2, 16, -1>(v[2]);
+      v[3] = twiddle_const<3, 16, -1>(v[3]);
+      v[4] = twiddle_const<4, 16, -1>(v[4]);
+      v[5] = twiddle_const<5, 16, -1>(v[5]);
+      v[6] = twiddle_const<6, 16, -1>(v[6]);
+      v[7] = twiddle_const<7, 16, -1>(v[7]);
+    }
     const int p = tid / B, nb = tid % B;
 #pragma unroll
     for (int k = 0; k < E; ++k) xb[(p * E + k) * XS + nb] = v[k];
@@ -370,13 +378,14 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
   }
   __syncthreads();
   if constexpr (PS) {
+    // Y[kq + 8 j] = Y_0[kq] + (-1)^j W_16^kq Y_1[kq] (the twiddle already applied by the writers)
     const int kq = wu & 7;
-    const bool neg = wu >= 8;
+    const float sg = wu >= 8 ? -1.0f : 1.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const float2 y0 = xb[kq * XS + l + 64 * e];
-      const float2 y1 = cmul(xb[(8 + kq) * XS + l + 64 * e], w16);
-      v[e] = cmul(neg ? csub(y0, y1) : cadd(y0, y1), tcr[HOLD ? e : 0]);
+      const float2 y1 = xb[(8 + kq) * XS + l + 64 * e];
+      v[e] = cmul(make_float2(fmaf(sg, y1.x, y0.x), fmaf(sg, y1.y, y0.y)), tcr[HOLD ? e : 0]);
     }
   } else {
 #pragma unroll
