@@ -306,7 +306,13 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
   // formed where used (held through the transforms, they spilled registers)
   constexpr bool HOLD = E <= 8;
   float2 hv[HOLD ? E : 1];
-  if constexpr (HOLD) {
+  // at 8192 points (16 waves, one workgroup per CU) the filter spectrum is requested after the
+  // first exchange: requested with the row, its 64 KB per workgroup doubled the cache traffic of
+  // the load phase that every wave waits for (256 x 4099 11.17 -> 11.02 us, 3000 x 1398 51.7 ->
+  // 50.6); at 2048 / 4096 points (several workgroups per CU, whose phases overlap) that measured
+  // 1-2 % slower
+  constexpr bool HV_LATE = HOLD && M == 8192;
+  if constexpr (HOLD && !HV_LATE) {
 #pragma unroll
     for (int e = 0; e < E; ++e) hv[HOLD ? e : 0] = hs[tid + T * e];
   }
@@ -377,6 +383,10 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
     }
   }
   __syncthreads();
+  if constexpr (HV_LATE) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) hv[HOLD ? e : 0] = hs[tid + T * e];
+  }
   if constexpr (PS) {
     // Y[kq + 8 j] = Y_0[kq] + (-1)^j W_16^kq Y_1[kq] (the twiddle already applied by the writers)
     const int kq = wu & 7;
