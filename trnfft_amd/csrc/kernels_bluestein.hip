@@ -298,8 +298,18 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
   for (int e = 0; e < EH; ++e) {
     const int i = tid + T * e;
     const int ic = i < n ? i : n - 1;
-    ch[e] = chirp[ic];
-    xin[e] = make_float2(ld_stream(in_re + base + ic), REAL_IN ? 0.0f : ld_stream(in_im + base + ic));
+    // at 8192 points (unwrapped) a wave none of whose lanes holds a sample in element e skips its
+    // loads with a wave-uniform branch (n <= 3072 leaves element 3 empty: 2100 x 1997 64.3 ->
+    // 62.2 us); the wrapped kernel (C3b: only its first wave has samples past M/2) measured 1 %
+    // slower with the branches, and at 2048 / 4096 points they kept the scheduler from issuing
+    // the filter spectrum's loads before the row's waits
+    if (M != 8192 || WRAP || e == 0 || T * e + wu * 64 < n) {
+      ch[e] = chirp[ic];
+      xin[e] = make_float2(ld_stream(in_re + base + ic), REAL_IN ? 0.0f : ld_stream(in_im + base + ic));
+    } else {
+      ch[e] = make_float2(0.0f, 0.0f);
+      xin[e] = make_float2(0.0f, 0.0f);
+    }
   }
   const float2 tb = tw_f[TWOFF + w * B + l];
   // E = 16: the filter spectrum and the output chirp are read where used and the cross factors
