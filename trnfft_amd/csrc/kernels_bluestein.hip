@@ -298,12 +298,13 @@ __global__ __launch_bounds__(Blue2lCfg<M>::T) void bluestein_2l_kernel(
   for (int e = 0; e < EH; ++e) {
     const int i = tid + T * e;
     const int ic = i < n ? i : n - 1;
-    // at 8192 points (unwrapped) a wave none of whose lanes holds a sample in element e skips its
-    // loads with a wave-uniform branch (n <= 3072 leaves element 3 empty: 2100 x 1997 64.3 ->
-    // 62.2 us); the wrapped kernel (C3b: only its first wave has samples past M/2) measured 1 %
-    // slower with the branches, and at 2048 / 4096 points they kept the scheduler from issuing
-    // the filter spectrum's loads before the row's waits
-    if (M != 8192 || WRAP || e == 0 || T * e + wu * 64 < n) {
+    // at 8192 and 16384 points (unwrapped) a wave none of whose lanes holds a sample in element e
+    // skips its loads with a wave-uniform branch (n <= 3072 leaves element 3 empty at 8192 points,
+    // n <= 7168 element 7 at 16384: 2100 x 1997 64.3 -> 62.2 us, 6145 x 680 57.5 -> 56.3); the
+    // wrapped kernels (C3b: only the first wave has samples past M/2) measured 1 % slower with the
+    // branches, and at 2048 / 4096 points they kept the scheduler from issuing the filter
+    // spectrum's loads before the row's waits
+    if ((M != 8192 && M != 16384) || WRAP || e == 0 || T * e + wu * 64 < n) {
       ch[e] = chirp[ic];
       xin[e] = make_float2(ld_stream(in_re + base + ic), REAL_IN ? 0.0f : ld_stream(in_im + base + ic));
     } else {
